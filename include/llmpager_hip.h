@@ -1,0 +1,213 @@
+/*
+ * llmpager_hip.h -- C ABI of the MI355X (gfx950) MoE-layer hot path.
+ *
+ * Drop-in boundary for glennswest/llmpager's `llmpager-cuda` crate: the
+ * device runtime (`driver::Cuda`, crates/llmpager-cuda/src/driver.rs), the
+ * hot-path kernel launchers (`kernels::Kernels`, src/kernels.rs) and the
+ * expert-slot bookkeeping the pager runs on (`cache::ExpertCache`,
+ * crates/llmpager-core/src/cache.rs; `pager::Pager`, src/pager.rs).  Paths in
+ * the citations are relative to the reference checkout.
+ *
+ * Conventions (kept from the reference):
+ *   - Device pointers are uint64_t (driver.rs:10 `CUdeviceptr = u64`).
+ *   - Every call returns int: 0 on success, a negative LP_E_* code, or a
+ *     positive hipError_t; lp_last_error() gives this thread's message
+ *     (driver.rs:20-27 turns every failure into an error string).
+ *   - The caller owns every buffer it passes; the library never frees them.
+ *     The context owns only its code objects (decode.rs:756-780 ownership).
+ *   - Launches are asynchronous on the caller's stream; nothing syncs unless
+ *     its name says so (`*_sync`, lp_sync*).
+ *   - A context may be used from several threads after each calls
+ *     lp_bind_thread (driver.rs:125-129).
+ */
+#ifndef LLMPAGER_HIP_H
+#define LLMPAGER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lp_ctx lp_ctx;
+typedef void* lp_stream; /* hipStream_t; NULL is the null stream */
+typedef void* lp_event;  /* hipEvent_t */
+
+enum {
+    LP_OK = 0,
+    LP_E_INVALID = -1,     /* bad argument */
+    LP_E_UNSUPPORTED = -2, /* shape or layout the kernels do not accept */
+    LP_E_LOAD = -3,        /* code object missing or unloadable */
+    LP_E_NOT_READY = -4,   /* (not returned by lp_event_done, which returns 0) */
+    LP_E_DEVICE = -5       /* a kernel reported an error flag */
+};
+
+/* This thread's last error message ("" if none). */
+const char* lp_last_error(void);
+/* Library version string. */
+const char* lp_version(void);
+
+/* ---- device runtime: driver::Cuda (driver.rs:29-304) --------------------- */
+
+/* Cuda::init (driver.rs:66-112) + Kernels::load (kernels.rs:44-68): make
+ * `device` current and load the gfx950 code objects from `hsaco_dir` with
+ * hipModuleLoad (NULL: the directory the library was loaded from). */
+int lp_init(int device, const char* hsaco_dir, lp_ctx** out);
+/* Unload the code objects.  Never frees caller buffers. */
+void lp_destroy(lp_ctx* ctx);
+/* driver.rs:125-129: make the context's device current on this thread. */
+int lp_bind_thread(lp_ctx* ctx);
+/* driver.rs:117-123 */
+int lp_mem_info(lp_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes);
+/* driver.rs:131-141 */
+int lp_alloc_device(lp_ctx* ctx, size_t bytes, uint64_t* out);
+int lp_free_device(lp_ctx* ctx, uint64_t ptr);
+/* driver.rs:143-151 (page-locked host memory, hipHostMalloc) */
+int lp_alloc_pinned(lp_ctx* ctx, size_t bytes, void** out);
+int lp_free_pinned(lp_ctx* ctx, void* p);
+/* driver.rs:153-163, 201-204 */
+int lp_stream_create(lp_ctx* ctx, lp_stream* out);
+int lp_stream_destroy(lp_ctx* ctx, lp_stream s);
+int lp_event_create(lp_ctx* ctx, lp_event* out);
+int lp_event_destroy(lp_ctx* ctx, lp_event e);
+/* driver.rs:165-188: asynchronous copies on `s` */
+int lp_htod_async(lp_ctx* ctx, uint64_t dst, const void* src, size_t bytes, lp_stream s);
+int lp_dtoh_async(lp_ctx* ctx, void* dst, uint64_t src, size_t bytes, lp_stream s);
+int lp_dtod_async(lp_ctx* ctx, uint64_t dst, uint64_t src, size_t bytes, lp_stream s);
+int lp_memset_async(lp_ctx* ctx, uint64_t dst, int value, size_t bytes, lp_stream s);
+/* driver.rs:190-199 */
+int lp_record_event(lp_ctx* ctx, lp_event e, lp_stream s);
+int lp_sync_event(lp_ctx* ctx, lp_event e);
+/* event_done (driver.rs:206-213): 1 complete, 0 pending, <0 error. */
+int lp_event_done(lp_ctx* ctx, lp_event e);
+int lp_event_elapsed_ms(lp_ctx* ctx, lp_event start, lp_event end, float* ms);
+/* driver.rs:216-219 */
+int lp_stream_wait_event(lp_ctx* ctx, lp_stream s, lp_event e);
+/* driver.rs:221-230 */
+int lp_sync_stream(lp_ctx* ctx, lp_stream s);
+int lp_sync(lp_ctx* ctx);
+
+/* ---- hot-path launchers: kernels::Kernels (kernels.rs) ------------------- */
+
+/* q4g64_gemv_batch (kernels.rs:102-127; q4g64.cu:19-81): for e < experts,
+ * y[e*rows + r] = sum_g s[r,g] * sum_{c in g} (q[r,c] - 8) * x[e*x_stride + c],
+ * reading the q4 region at ((u64*)blobs)[e] + region_off.  fp32 accumulation.
+ * group must divide cols and be a multiple of 8. */
+int lp_q4_gemv_batch(lp_ctx* ctx, uint64_t blobs, uint64_t region_off, uint64_t x, int x_stride,
+                     uint64_t y, int rows, int cols, int group, int experts, lp_stream s);
+/* q4g64_gemv (kernels.rs:73-95; q4g64.cu:101-161): one q4 region at `blob`. */
+int lp_q4_gemv(lp_ctx* ctx, uint64_t blob, uint64_t x, uint64_t y, int rows, int cols, int group,
+               lp_stream s);
+/* moe_reduce (kernels.rs:131-144; q4g64.cu:84-99):
+ * out[i] += sum_{e<experts} wts[e] * eouts[e*n + i], summed in order. */
+int lp_moe_reduce(lp_ctx* ctx, uint64_t eouts, uint64_t wts, uint64_t out, int experts, int n,
+                  lp_stream s);
+/* silu_mul (kernels.rs:224-236; decode.cu:117-128): out = g/(1+exp(-g))*u. */
+int lp_silu_mul(lp_ctx* ctx, uint64_t gate, uint64_t up, uint64_t out, int n, lp_stream s);
+/* bf16_gemv (kernels.rs:202-222; decode.cu:80-114): y = W x, W bf16 [rows, cols]. */
+int lp_bf16_gemv(lp_ctx* ctx, uint64_t w, uint64_t x, uint64_t y, int rows, int cols,
+                 lp_stream s);
+/* add (kernels.rs:239-250; decode.cu:131-140): a += b. */
+int lp_add(lp_ctx* ctx, uint64_t a, uint64_t b, int n, lp_stream s);
+
+/* ---- fused MoE layer ------------------------------------------------------ */
+
+enum { LP_GATING_SOFTMAX = 0, LP_GATING_SIGMOID = 1 };
+
+/* One MoE layer as the device sees it.  Blob layout per expert
+ * (crates/llmpager-convert/src/lib.rs:245-286): a 32-byte header, then the
+ * gate [inter, hidden], up [inter, hidden] and down [hidden, inter] q4
+ * regions (quant.rs:1-22: f16 scales [rows, cols/group], then nibbles
+ * [rows, cols/2], value q stored as q + 8).  Expert e lives at
+ * arena_base + slot_table[e] * slot_span (pager.rs:310-318); slot -1 means
+ * not resident. */
+typedef struct lp_moe_layer_desc {
+    int32_t hidden;         /* H (model.rs:34 hidden_size) */
+    int32_t inter;          /* I (moe_intermediate_size) */
+    int32_t experts;        /* E routed experts (<= 1024) */
+    int32_t top_k;          /* k (<= 16) */
+    int32_t group;          /* q4 group (32 or 64, any multiple of 32) */
+    int32_t gating;         /* LP_GATING_SOFTMAX (decode.rs:734-749) or
+                               LP_GATING_SIGMOID (kimi.rs:1155-1186) */
+    int32_t renorm;         /* norm_topk_prob (model.rs:46; kimi.rs:123) */
+    float routed_scaling;   /* sigmoid gating only (kimi.rs:122) */
+    float min_weight;       /* sigmoid gating only (kimi.rs:1181-1183) */
+    int32_t reserved0;
+    uint64_t router_w;      /* device bf16 [E, H] (model.rs:80, 183) */
+    uint64_t router_bias;   /* device f32 [E] (sigmoid gating) or 0 */
+    uint64_t slot_table;    /* device int32 [E] */
+    uint64_t arena_base;    /* device address of slot 0 */
+    uint64_t slot_span;     /* bytes per slot (pager.rs:263) */
+    uint64_t gate_off, up_off, down_off; /* region offsets in a blob (decode.rs:183-185) */
+} lp_moe_layer_desc;
+
+/* Byte offsets of the workspace parts for T tokens (all 256-byte aligned). */
+typedef struct lp_moe_ws_layout {
+    uint64_t logits;  /* f32 [T, E] router logits */
+    uint64_t ids;     /* i32 [T, k] picked expert ids in pick order, -1 past cnt */
+    uint64_t wts;     /* f32 [T, k] routing weights in pick order */
+    uint64_t cnt;     /* i32 [T] picks per token */
+    uint64_t gs;      /* i32 [E+1] dispatch group starts */
+    uint64_t perm;    /* i32 [T*k] pick index t*k+j per dispatch position */
+    uint64_t inv;     /* i32 [T*k] dispatch position per pick, -1 if unused */
+    uint64_t uniq;    /* i32 [E] experts with picks, ascending */
+    uint64_t meta;    /* i32 [16]: [0] unique count, [1] error flags */
+    uint64_t act;     /* f32 [T*k, I] */
+    uint64_t y;       /* f32 [T*k, H] */
+    uint64_t total;   /* bytes */
+} lp_moe_ws_layout;
+
+int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out);
+
+/* Routing for T tokens without the host round trip of decode.rs:305-331:
+ * router GEMV (canonical fp32 FMA order), softmax or sigmoid top-k with
+ * glibc-exact expf (bit-exact with the reference's host routing given the
+ * same logits), and the stable token->expert dispatch.  x: f32 [T, H]. */
+int lp_moe_route(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t workspace,
+                 lp_stream s);
+/* Routing from caller-supplied logits (f32 [T, E], copied into the
+ * workspace): the "given identical fp32 router logits" contract. */
+int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits, int T,
+                        uint64_t workspace, lp_stream s);
+/* Expert half of the layer after lp_moe_route*: grouped gate/up + SiLU,
+ * grouped down, and h[t] += sum_j w[t][j] * y[t][j] in pick order. */
+int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                   uint64_t workspace, lp_stream s);
+/* The whole layer (decode.rs:303-337 for one token, 469-531 for many):
+ * lp_moe_route followed by lp_moe_experts.  h: f32 [T, H], updated in place. */
+int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                   uint64_t workspace, lp_stream s);
+/* Synchronising readback of meta[0..1] (unique count, error flags). */
+int lp_moe_status_sync(lp_ctx* ctx, uint64_t workspace, const lp_moe_layer_desc* d, int T,
+                       lp_stream s, int32_t* unique_count, int32_t* error_flags);
+
+/* ---- blob format and synthetic inputs ------------------------------------ */
+
+/* quant.rs:20-22 */
+uint64_t lp_q4_bytes(int rows, int cols, int group);
+/* Blob size (lib.rs:245-286) and the region offsets decode.rs:161-185 uses. */
+uint64_t lp_blob_bytes(int hidden, int inter, int group);
+void lp_blob_offsets(int hidden, int inter, int group, uint64_t* gate_off, uint64_t* up_off,
+                     uint64_t* down_off);
+/* Synthetic expert blob for (seed, layer, expert): header as lib.rs:276-281;
+ * nibbles uniform 0..15; f16 scales round-to-nearest-even of |N(0, 0.02)|/8.
+ * dst must hold lp_blob_bytes(). Deterministic, independent of threading. */
+int lp_synth_blob(uint8_t* dst, int hidden, int inter, int group, uint64_t seed, int layer,
+                  int expert);
+/* n blobs (experts e0..e0+n-1 of `layer`), `stride` bytes apart, OpenMP-parallel. */
+int lp_synth_blobs(uint8_t* dst, uint64_t stride, int n, int hidden, int inter, int group,
+                   uint64_t seed, int layer, int e0, int threads);
+/* bf16 bits of round-to-nearest-even N(0, std): router weights. */
+int lp_synth_bf16(uint16_t* dst, uint64_t n, float std, uint64_t seed, uint64_t stream);
+/* f32 values that are bf16-exact (RNE of N(0, std)): activations. */
+int lp_synth_f32_bf16(float* dst, uint64_t n, float std, uint64_t seed, uint64_t stream);
+
+/* Host evaluation of the expf routing uses (glibc's bits; see lp_expf.h). */
+float lp_route_expf(float x);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMPAGER_HIP_H */

@@ -1,0 +1,364 @@
+"""llmpager_amd -- MI355X (gfx950) MoE-layer hot path of glennswest/llmpager.
+
+The product is the C-ABI library ``lib/libllmpager_hip.so`` (include/llmpager_hip.h)
+and the gfx950 code objects it loads.  This module is a thin ctypes binding
+whose classes mirror the reference crate's surfaces:
+
+  Cuda     driver::Cuda        (crates/llmpager-cuda/src/driver.rs)
+  Kernels  kernels::Kernels    (crates/llmpager-cuda/src/kernels.rs), hot-path methods
+  MoeLayer the fused layer: router, top-k, dispatch, grouped experts, combine
+
+There is no CPU fallback: if the library or a code object is missing, loading
+raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBDIR = os.path.join(HERE, "lib")
+LIBPATH = os.path.join(LIBDIR, "libllmpager_hip.so")
+
+GATING_SOFTMAX = 0
+GATING_SIGMOID = 1
+
+_lib = None
+
+
+class LpError(RuntimeError):
+    """A non-zero return from the C ABI, with lp_last_error()'s text."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"llmpager_hip error {code}: {msg}")
+        self.code = code
+
+
+class LayerDesc(C.Structure):
+    """lp_moe_layer_desc (include/llmpager_hip.h)."""
+
+    _fields_ = [
+        ("hidden", C.c_int32), ("inter", C.c_int32), ("experts", C.c_int32),
+        ("top_k", C.c_int32), ("group", C.c_int32), ("gating", C.c_int32),
+        ("renorm", C.c_int32), ("routed_scaling", C.c_float), ("min_weight", C.c_float),
+        ("reserved0", C.c_int32),
+        ("router_w", C.c_uint64), ("router_bias", C.c_uint64), ("slot_table", C.c_uint64),
+        ("arena_base", C.c_uint64), ("slot_span", C.c_uint64),
+        ("gate_off", C.c_uint64), ("up_off", C.c_uint64), ("down_off", C.c_uint64),
+    ]
+
+
+class WsLayout(C.Structure):
+    """lp_moe_ws_layout: byte offsets of the workspace parts."""
+
+    _fields_ = [(n, C.c_uint64) for n in (
+        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "act", "y", "total")]
+
+
+def _sig(lib):
+    u64, i32, f32, vp = C.c_uint64, C.c_int, C.c_float, C.c_void_p
+    P = C.POINTER
+    sigs = {
+        "lp_last_error": (C.c_char_p, []),
+        "lp_version": (C.c_char_p, []),
+        "lp_init": (i32, [i32, C.c_char_p, P(vp)]),
+        "lp_destroy": (None, [vp]),
+        "lp_bind_thread": (i32, [vp]),
+        "lp_mem_info": (i32, [vp, P(u64), P(u64)]),
+        "lp_alloc_device": (i32, [vp, C.c_size_t, P(u64)]),
+        "lp_free_device": (i32, [vp, u64]),
+        "lp_alloc_pinned": (i32, [vp, C.c_size_t, P(vp)]),
+        "lp_free_pinned": (i32, [vp, vp]),
+        "lp_stream_create": (i32, [vp, P(vp)]),
+        "lp_stream_destroy": (i32, [vp, vp]),
+        "lp_event_create": (i32, [vp, P(vp)]),
+        "lp_event_destroy": (i32, [vp, vp]),
+        "lp_htod_async": (i32, [vp, u64, vp, C.c_size_t, vp]),
+        "lp_dtoh_async": (i32, [vp, vp, u64, C.c_size_t, vp]),
+        "lp_dtod_async": (i32, [vp, u64, u64, C.c_size_t, vp]),
+        "lp_memset_async": (i32, [vp, u64, i32, C.c_size_t, vp]),
+        "lp_record_event": (i32, [vp, vp, vp]),
+        "lp_sync_event": (i32, [vp, vp]),
+        "lp_event_done": (i32, [vp, vp]),
+        "lp_event_elapsed_ms": (i32, [vp, vp, vp, P(f32)]),
+        "lp_stream_wait_event": (i32, [vp, vp, vp]),
+        "lp_sync_stream": (i32, [vp, vp]),
+        "lp_sync": (i32, [vp]),
+        "lp_q4_gemv_batch": (i32, [vp, u64, u64, u64, i32, u64, i32, i32, i32, i32, vp]),
+        "lp_q4_gemv": (i32, [vp, u64, u64, u64, i32, i32, i32, vp]),
+        "lp_moe_reduce": (i32, [vp, u64, u64, u64, i32, i32, vp]),
+        "lp_silu_mul": (i32, [vp, u64, u64, u64, i32, vp]),
+        "lp_bf16_gemv": (i32, [vp, u64, u64, u64, i32, i32, vp]),
+        "lp_add": (i32, [vp, u64, u64, i32, vp]),
+        "lp_moe_ws_layout_get": (i32, [P(LayerDesc), i32, P(WsLayout)]),
+        "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
+        "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
+        "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
+        "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
+        "lp_moe_status_sync": (i32, [vp, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
+        "lp_q4_bytes": (u64, [i32, i32, i32]),
+        "lp_blob_bytes": (u64, [i32, i32, i32]),
+        "lp_blob_offsets": (None, [i32, i32, i32, P(u64), P(u64), P(u64)]),
+        "lp_synth_blob": (i32, [vp, i32, i32, i32, u64, i32, i32]),
+        "lp_synth_blobs": (i32, [vp, u64, i32, i32, i32, i32, u64, i32, i32, i32]),
+        "lp_synth_bf16": (i32, [vp, u64, f32, u64, u64]),
+        "lp_synth_f32_bf16": (i32, [vp, u64, f32, u64, u64]),
+        "lp_route_expf": (f32, [f32]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def lib() -> C.CDLL:
+    """The loaded C-ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBPATH):
+            raise RuntimeError(
+                f"{LIBPATH} is missing: build it with `python -m llmpager_amd.build` "
+                "(there is no CPU fallback)")
+        _lib = _sig(C.CDLL(LIBPATH))
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise LpError(rc, lib().lp_last_error().decode())
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---- host-only helpers (no device needed) ----------------------------------
+
+def q4_bytes(rows: int, cols: int, group: int) -> int:
+    return int(lib().lp_q4_bytes(rows, cols, group))
+
+
+def blob_bytes(hidden: int, inter: int, group: int) -> int:
+    return int(lib().lp_blob_bytes(hidden, inter, group))
+
+
+def blob_offsets(hidden: int, inter: int, group: int) -> tuple[int, int, int]:
+    g, u, d = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    lib().lp_blob_offsets(hidden, inter, group, C.byref(g), C.byref(u), C.byref(d))
+    return g.value, u.value, d.value
+
+
+def synth_blob(hidden: int, inter: int, group: int, seed: int, layer: int, expert: int) -> np.ndarray:
+    out = np.zeros(blob_bytes(hidden, inter, group), np.uint8)
+    _check(lib().lp_synth_blob(_ptr(out), hidden, inter, group, seed, layer, expert))
+    return out
+
+
+def synth_blobs(n: int, stride: int, hidden: int, inter: int, group: int, seed: int, layer: int,
+                e0: int = 0, threads: int = 0, out: np.ndarray | None = None) -> np.ndarray:
+    if out is None:
+        out = np.zeros(n * stride, np.uint8)
+    threads = threads or min(16, os.cpu_count() or 1)
+    _check(lib().lp_synth_blobs(_ptr(out), stride, n, hidden, inter, group, seed, layer, e0, threads))
+    return out
+
+
+def synth_bf16(n: int, std: float, seed: int, stream: int) -> np.ndarray:
+    out = np.zeros(n, np.uint16)
+    _check(lib().lp_synth_bf16(_ptr(out), n, std, seed, stream))
+    return out
+
+
+def synth_f32_bf16(n: int, std: float, seed: int, stream: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    _check(lib().lp_synth_f32_bf16(_ptr(out), n, std, seed, stream))
+    return out
+
+
+def route_expf(x: float) -> float:
+    return float(lib().lp_route_expf(x))
+
+
+def ws_layout(desc: LayerDesc, T: int) -> WsLayout:
+    lay = WsLayout()
+    _check(lib().lp_moe_ws_layout_get(C.byref(desc), T, C.byref(lay)))
+    return lay
+
+
+# ---- device runtime: driver::Cuda -------------------------------------------
+
+class Cuda:
+    """driver::Cuda (driver.rs:29-304) over the C ABI."""
+
+    def __init__(self, device: int = 0, hsaco_dir: str | None = None):
+        self.ctx = C.c_void_p()
+        d = hsaco_dir.encode() if hsaco_dir else None
+        _check(lib().lp_init(device, d, C.byref(self.ctx)))
+
+    def close(self) -> None:
+        if self.ctx:
+            lib().lp_destroy(self.ctx)
+            self.ctx = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def bind_thread(self) -> None:
+        _check(lib().lp_bind_thread(self.ctx))
+
+    def mem_info(self) -> tuple[int, int]:
+        f, t = C.c_uint64(), C.c_uint64()
+        _check(lib().lp_mem_info(self.ctx, C.byref(f), C.byref(t)))
+        return f.value, t.value
+
+    def alloc_device(self, nbytes: int) -> int:
+        p = C.c_uint64()
+        _check(lib().lp_alloc_device(self.ctx, nbytes, C.byref(p)))
+        return p.value
+
+    def free_device(self, p: int) -> None:
+        _check(lib().lp_free_device(self.ctx, p))
+
+    def alloc_pinned(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        _check(lib().lp_alloc_pinned(self.ctx, nbytes, C.byref(p)))
+        return p.value
+
+    def free_pinned(self, p: int) -> None:
+        _check(lib().lp_free_pinned(self.ctx, p))
+
+    def stream(self) -> int:
+        s = C.c_void_p()
+        _check(lib().lp_stream_create(self.ctx, C.byref(s)))
+        return s.value
+
+    def destroy_stream(self, s: int) -> None:
+        _check(lib().lp_stream_destroy(self.ctx, s))
+
+    def event(self) -> int:
+        e = C.c_void_p()
+        _check(lib().lp_event_create(self.ctx, C.byref(e)))
+        return e.value
+
+    def destroy_event(self, e: int) -> None:
+        _check(lib().lp_event_destroy(self.ctx, e))
+
+    def htod_async(self, dst: int, src: np.ndarray, stream: int | None = None) -> None:
+        src = np.ascontiguousarray(src)
+        _check(lib().lp_htod_async(self.ctx, dst, _ptr(src), src.nbytes, stream))
+
+    def htod_ptr_async(self, dst: int, src_ptr: int, nbytes: int, stream: int | None = None) -> None:
+        _check(lib().lp_htod_async(self.ctx, dst, src_ptr, nbytes, stream))
+
+    def dtoh_async(self, dst: np.ndarray, src: int, stream: int | None = None) -> None:
+        assert dst.flags["C_CONTIGUOUS"]
+        _check(lib().lp_dtoh_async(self.ctx, _ptr(dst), src, dst.nbytes, stream))
+
+    def dtod_async(self, dst: int, src: int, nbytes: int, stream: int | None = None) -> None:
+        _check(lib().lp_dtod_async(self.ctx, dst, src, nbytes, stream))
+
+    def memset_async(self, dst: int, value: int, nbytes: int, stream: int | None = None) -> None:
+        _check(lib().lp_memset_async(self.ctx, dst, value, nbytes, stream))
+
+    def record_event(self, e: int, s: int | None = None) -> None:
+        _check(lib().lp_record_event(self.ctx, e, s))
+
+    def sync_event(self, e: int) -> None:
+        _check(lib().lp_sync_event(self.ctx, e))
+
+    def event_done(self, e: int) -> bool:
+        r = lib().lp_event_done(self.ctx, e)
+        if r < 0:
+            _check(r)
+        return r == 1
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        _check(lib().lp_event_elapsed_ms(self.ctx, a, b, C.byref(ms)))
+        return ms.value
+
+    def stream_wait_event(self, s: int, e: int) -> None:
+        _check(lib().lp_stream_wait_event(self.ctx, s, e))
+
+    def sync_stream(self, s: int | None = None) -> None:
+        _check(lib().lp_sync_stream(self.ctx, s))
+
+    def sync(self) -> None:
+        _check(lib().lp_sync(self.ctx))
+
+    # convenience
+    def upload(self, a: np.ndarray, stream: int | None = None) -> int:
+        a = np.ascontiguousarray(a)
+        p = self.alloc_device(max(a.nbytes, 1))
+        self.htod_async(p, a, stream)
+        return p
+
+    def download(self, p: int, shape, dtype, stream: int | None = None) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self.dtoh_async(out, p, stream)
+        self.sync_stream(stream)
+        return out
+
+
+# ---- hot-path launchers: kernels::Kernels --------------------------------------
+
+class Kernels:
+    """The hot-path methods of kernels::Kernels (kernels.rs), same argument order."""
+
+    def __init__(self, cuda: Cuda):
+        self.cuda = cuda
+
+    def q4g64_gemv_batch(self, blobs: int, region_off: int, x: int, x_stride: int, y: int,
+                         rows: int, cols: int, group: int, experts: int, stream=None) -> None:
+        _check(lib().lp_q4_gemv_batch(self.cuda.ctx, blobs, region_off, x, x_stride, y, rows,
+                                      cols, group, experts, stream))
+
+    def q4g64_gemv(self, blob: int, x: int, y: int, rows: int, cols: int, group: int,
+                   stream=None) -> None:
+        _check(lib().lp_q4_gemv(self.cuda.ctx, blob, x, y, rows, cols, group, stream))
+
+    def moe_reduce(self, eouts: int, wts: int, out: int, experts: int, n: int, stream=None) -> None:
+        _check(lib().lp_moe_reduce(self.cuda.ctx, eouts, wts, out, experts, n, stream))
+
+    def silu_mul(self, gate: int, up: int, out: int, n: int, stream=None) -> None:
+        _check(lib().lp_silu_mul(self.cuda.ctx, gate, up, out, n, stream))
+
+    def bf16_gemv(self, w: int, x: int, y: int, rows: int, cols: int, stream=None) -> None:
+        _check(lib().lp_bf16_gemv(self.cuda.ctx, w, x, y, rows, cols, stream))
+
+    def add(self, a: int, b: int, n: int, stream=None) -> None:
+        _check(lib().lp_add(self.cuda.ctx, a, b, n, stream))
+
+
+# ---- fused MoE layer ----------------------------------------------------------------
+
+class MoeLayer:
+    """The fused layer entry points for one layer descriptor."""
+
+    def __init__(self, cuda: Cuda, desc: LayerDesc):
+        self.cuda = cuda
+        self.desc = desc
+
+    def route(self, x: int, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_route(self.cuda.ctx, C.byref(self.desc), x, T, ws, stream))
+
+    def route_logits(self, logits: int, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_route_logits(self.cuda.ctx, C.byref(self.desc), logits, T, ws, stream))
+
+    def experts(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_experts(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))
+
+    def forward(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_forward(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))
+
+    def status(self, ws: int, T: int, stream=None) -> tuple[int, int]:
+        u, e = C.c_int32(), C.c_int32()
+        _check(lib().lp_moe_status_sync(self.cuda.ctx, ws, C.byref(self.desc), T, stream,
+                                        C.byref(u), C.byref(e)))
+        return u.value, e.value

@@ -1,0 +1,105 @@
+// Kernel argument blocks shared by the host launchers (lp_runtime.cpp) and the
+// gfx950 kernels (kernels/*.hip).  Every kernel takes exactly one of these by
+// value, so hipModuleLaunchKernel is always given a single kernelParams entry
+// and host/device layouts cannot drift apart.
+#pragma once
+#include <stdint.h>
+
+namespace lpk {
+
+// Launch geometry constants the host and the kernels agree on.
+constexpr int kWave = 64;              // CDNA wavefront
+constexpr int kGroupedWaves = 4;       // waves per workgroup in the grouped kernels
+constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x32)
+constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
+constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
+constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
+
+// ---- 1:1 launchers (crates/llmpager-cuda/src/kernels.rs) -------------------
+
+struct Q4GemvBatchArgs {            // kernels.rs:102-127
+    uint64_t blobs;                 // device u64[experts] blob base addresses, or 0:
+    uint64_t region_off;            //   then region_off is the region's device address
+                                    //   (the single-matrix q4g64_gemv, kernels.rs:73-95)
+    uint64_t x;                     // f32
+    int32_t x_stride;
+    int32_t pad0;
+    uint64_t y;                     // f32 [experts, rows]
+    int32_t rows, cols, group, experts;
+};
+
+struct MoeReduceArgs {              // kernels.rs:131-144
+    uint64_t eouts, wts, out;
+    int32_t experts, n;
+};
+
+struct SiluMulArgs {                // kernels.rs:224-236
+    uint64_t gate, up, out;
+    int32_t n, pad0;
+};
+
+struct Bf16GemvArgs {               // kernels.rs:202-222
+    uint64_t w, x, y;
+    int32_t rows, cols;
+};
+
+struct AddArgs {                    // kernels.rs:239-250
+    uint64_t a, b;
+    int32_t n, pad0;
+};
+
+// ---- fused MoE layer ---------------------------------------------------------
+
+// Device-side view of one MoE layer's routing and expert tables.
+struct LayerView {
+    uint64_t router_w;       // bf16 [E, H]
+    uint64_t router_bias;    // f32 [E] or 0
+    uint64_t slot_table;     // int32 [E]: slot within the arena, -1 = absent
+    uint64_t arena_base;     // device base of the layer's slot arena
+    uint64_t slot_span;      // bytes per slot
+    uint64_t gate_off, up_off, down_off;
+    int32_t hidden, inter, experts, top_k, group;
+    int32_t gating;          // 0 softmax, 1 sigmoid + bias
+    int32_t renorm;
+    float routed_scaling, min_weight;
+    int32_t pad0;
+};
+
+// Workspace carve-up for T tokens (offsets in bytes from `ws`).
+struct Workspace {
+    uint64_t logits;     // f32 [T, E]
+    uint64_t ids;        // i32 [T, k]
+    uint64_t wts;        // f32 [T, k]
+    uint64_t cnt;        // i32 [T]
+    uint64_t gs;         // i32 [E + 1] group starts
+    uint64_t perm;       // i32 [T * k] pick (t*k+j) per dispatch position
+    uint64_t inv;        // i32 [T * k] dispatch position per pick (-1 if none)
+    uint64_t uniq;       // i32 [E] experts with picks, ascending
+    uint64_t meta;       // i32 [16]: [0] = unique count, [1] = error flags
+    uint64_t act;        // f32 [T * k, I] expert-major activations
+    uint64_t y;          // f32 [T * k, H] expert-major expert outputs
+};
+
+struct RouteArgs {
+    LayerView L;
+    Workspace W;
+    uint64_t x;          // f32 [T, H]
+    int32_t T, pad0;
+};
+
+struct GroupedArgs {
+    LayerView L;
+    Workspace W;
+    uint64_t x;          // f32 [T, H] (gate/up phase input)
+    uint64_t h;          // f32 [T, H] residual (combine)
+    int32_t T;
+    int32_t phase;       // 0 gate/up/silu, 1 down
+    int32_t lds_per_wave;  // bytes of dynamic LDS per wave
+    int32_t pad0;
+};
+
+// Error flags written into Workspace.meta[1].
+constexpr int kErrMissingExpert = 1;  // a routed expert had no slot
+constexpr int kErrBadShape = 2;
+
+}  // namespace lpk

@@ -1,0 +1,563 @@
+// Host side of the C ABI (include/llmpager_hip.h): device runtime, code-object
+// loading, launch geometry and shape checks for the gfx950 kernels.
+//
+// Mirrors crates/llmpager-cuda/src/driver.rs (Cuda) and src/kernels.rs
+// (Kernels) of the reference.  Kernels are loaded from .hsaco code objects
+// with hipModuleLoad and launched with hipModuleLaunchKernel, each taking one
+// argument block from lp_kargs.h.
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <string>
+
+#include "../../include/llmpager_hip.h"
+#include "lp_expf.h"
+#include "lp_kargs.h"
+
+using namespace lpk;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    g_err = std::string(what) + " failed: " + hipGetErrorString(e) + " (" + std::to_string((int)e) + ")";
+    return (int)e;
+}
+
+#define HIPCHK(expr)                                   \
+    do {                                               \
+        hipError_t e_ = (expr);                        \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+    } while (0)
+
+enum Fn {
+    kQ4Mfma,
+    kQ4Valu,
+    kMoeReduce,
+    kSiluMul,
+    kBf16Gemv,
+    kAdd,
+    kRouter,
+    kTopk,
+    kDispatch,
+    kGrouped,
+    kCombine,
+    kNumFns
+};
+
+struct FnSpec {
+    const char* module;
+    const char* name;
+};
+
+const FnSpec kSpecs[kNumFns] = {
+    {"lp_basic.hsaco", "lp_q4_gemv_mfma"}, {"lp_basic.hsaco", "lp_q4_gemv_valu"},
+    {"lp_basic.hsaco", "lp_moe_reduce"},   {"lp_basic.hsaco", "lp_silu_mul"},
+    {"lp_basic.hsaco", "lp_bf16_gemv"},    {"lp_basic.hsaco", "lp_add"},
+    {"lp_moe.hsaco", "lp_moe_router"},     {"lp_moe.hsaco", "lp_moe_topk"},
+    {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_grouped"},
+    {"lp_moe.hsaco", "lp_moe_combine"},
+};
+
+const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco"};
+constexpr int kNumModules = 2;
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&lp_version), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t cut = p.rfind('/');
+        if (cut != std::string::npos) return p.substr(0, cut);
+    }
+    return ".";
+}
+
+uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+// grid_1d of kernels.rs:39-41: min(ceil(n / 256), 1024), at least 1.
+unsigned grid_1d(int n) {
+    unsigned g = (unsigned)((n + 255) / 256);
+    return std::max(1u, std::min(g, 1024u));
+}
+
+}  // namespace
+
+struct lp_ctx {
+    int device = 0;
+    int cus = 0;
+    size_t max_lds = 0;
+    hipModule_t modules[kNumModules] = {};
+    hipFunction_t fns[kNumFns] = {};
+};
+
+namespace {
+
+template <typename A>
+int launch(lp_ctx* c, Fn f, dim3 grid, dim3 block, size_t lds, lp_stream s, const A& args) {
+    void* params[] = {const_cast<A*>(&args)};
+    hipError_t e = hipModuleLaunchKernel(c->fns[f], grid.x, grid.y, grid.z, block.x, block.y,
+                                         block.z, (unsigned)lds, (hipStream_t)s, params, nullptr);
+    if (e != hipSuccess) return hip_fail(e, kSpecs[f].name);
+    return LP_OK;
+}
+
+int check_ctx(lp_ctx* c) {
+    if (!c) return fail(LP_E_INVALID, "null context");
+    return LP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lp_last_error(void) { return g_err.c_str(); }
+
+const char* lp_version(void) { return "llmpager-hip 0.1.0 (gfx950)"; }
+
+// ---- device runtime ----------------------------------------------------------
+
+int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
+    if (!out) return fail(LP_E_INVALID, "lp_init: null out");
+    *out = nullptr;
+    HIPCHK(hipSetDevice(device));
+    lp_ctx* c = new lp_ctx();
+    c->device = device;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipGetDeviceProperties");
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        delete c;
+        return fail(LP_E_UNSUPPORTED, std::string("device is ") + prop.gcnArchName +
+                                          ", the kernels are built for gfx950 only");
+    }
+    c->cus = prop.multiProcessorCount;
+    c->max_lds = prop.sharedMemPerBlock;
+    const std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
+    for (int m = 0; m < kNumModules; ++m) {
+        const std::string path = dir + "/" + kModules[m];
+        e = hipModuleLoad(&c->modules[m], path.c_str());
+        if (e != hipSuccess) {
+            lp_destroy(c);
+            return fail(LP_E_LOAD, "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
+        }
+    }
+    for (int f = 0; f < kNumFns; ++f) {
+        int m = 0;
+        while (m < kNumModules && strcmp(kModules[m], kSpecs[f].module) != 0) ++m;
+        e = hipModuleGetFunction(&c->fns[f], c->modules[m], kSpecs[f].name);
+        if (e != hipSuccess) {
+            lp_destroy(c);
+            return fail(LP_E_LOAD, std::string("hipModuleGetFunction(") + kSpecs[f].name +
+                                       "): " + hipGetErrorString(e));
+        }
+    }
+    *out = c;
+    return LP_OK;
+}
+
+void lp_destroy(lp_ctx* c) {
+    if (!c) return;
+    for (int m = 0; m < kNumModules; ++m)
+        if (c->modules[m]) (void)hipModuleUnload(c->modules[m]);
+    delete c;
+}
+
+int lp_bind_thread(lp_ctx* c) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipSetDevice(c->device));
+    return LP_OK;
+}
+
+int lp_mem_info(lp_ctx* c, uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (int r = check_ctx(c)) return r;
+    size_t f = 0, t = 0;
+    HIPCHK(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return LP_OK;
+}
+
+int lp_alloc_device(lp_ctx* c, size_t bytes, uint64_t* out) {
+    if (int r = check_ctx(c)) return r;
+    if (!out) return fail(LP_E_INVALID, "lp_alloc_device: null out");
+    void* p = nullptr;
+    HIPCHK(hipMalloc(&p, std::max<size_t>(bytes, 1)));
+    *out = reinterpret_cast<uint64_t>(p);
+    return LP_OK;
+}
+
+int lp_free_device(lp_ctx* c, uint64_t ptr) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipFree(reinterpret_cast<void*>(ptr)));
+    return LP_OK;
+}
+
+int lp_alloc_pinned(lp_ctx* c, size_t bytes, void** out) {
+    if (int r = check_ctx(c)) return r;
+    if (!out) return fail(LP_E_INVALID, "lp_alloc_pinned: null out");
+    HIPCHK(hipHostMalloc(out, std::max<size_t>(bytes, 1), hipHostMallocDefault));
+    return LP_OK;
+}
+
+int lp_free_pinned(lp_ctx* c, void* p) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipHostFree(p));
+    return LP_OK;
+}
+
+int lp_stream_create(lp_ctx* c, lp_stream* out) {
+    if (int r = check_ctx(c)) return r;
+    hipStream_t s;
+    HIPCHK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *out = s;
+    return LP_OK;
+}
+
+int lp_stream_destroy(lp_ctx* c, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipStreamDestroy((hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_event_create(lp_ctx* c, lp_event* out) {
+    if (int r = check_ctx(c)) return r;
+    hipEvent_t e;
+    HIPCHK(hipEventCreate(&e));
+    *out = e;
+    return LP_OK;
+}
+
+int lp_event_destroy(lp_ctx* c, lp_event e) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipEventDestroy((hipEvent_t)e));
+    return LP_OK;
+}
+
+int lp_htod_async(lp_ctx* c, uint64_t dst, const void* src, size_t bytes, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipMemcpyAsync(reinterpret_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice,
+                          (hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_dtoh_async(lp_ctx* c, void* dst, uint64_t src, size_t bytes, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), bytes, hipMemcpyDeviceToHost,
+                          (hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_dtod_async(lp_ctx* c, uint64_t dst, uint64_t src, size_t bytes, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), bytes,
+                          hipMemcpyDeviceToDevice, (hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_memset_async(lp_ctx* c, uint64_t dst, int value, size_t bytes, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipMemsetAsync(reinterpret_cast<void*>(dst), value, bytes, (hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_record_event(lp_ctx* c, lp_event e, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipEventRecord((hipEvent_t)e, (hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_sync_event(lp_ctx* c, lp_event e) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipEventSynchronize((hipEvent_t)e));
+    return LP_OK;
+}
+
+int lp_event_done(lp_ctx* c, lp_event e) {
+    if (int r = check_ctx(c)) return r;
+    hipError_t q = hipEventQuery((hipEvent_t)e);
+    if (q == hipSuccess) return 1;
+    if (q == hipErrorNotReady) return 0;
+    return hip_fail(q, "hipEventQuery");
+}
+
+int lp_event_elapsed_ms(lp_ctx* c, lp_event a, lp_event b, float* ms) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return LP_OK;
+}
+
+int lp_stream_wait_event(lp_ctx* c, lp_stream s, lp_event e) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipStreamWaitEvent((hipStream_t)s, (hipEvent_t)e, 0));
+    return LP_OK;
+}
+
+int lp_sync_stream(lp_ctx* c, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipStreamSynchronize((hipStream_t)s));
+    return LP_OK;
+}
+
+int lp_sync(lp_ctx* c) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipDeviceSynchronize());
+    return LP_OK;
+}
+
+// ---- 1:1 launchers --------------------------------------------------------------
+
+static int q4_gemv_common(lp_ctx* c, uint64_t blobs, uint64_t region_off, uint64_t x, int x_stride,
+                          uint64_t y, int rows, int cols, int group, int experts, lp_stream s,
+                          bool direct) {
+    if (int r = check_ctx(c)) return r;
+    if (rows <= 0 || cols <= 0 || experts <= 0 || group <= 0 || group % 8 != 0 || cols % group != 0)
+        return fail(LP_E_INVALID, "q4 gemv: need group % 8 == 0 and cols % group == 0 (quant.rs:44-46)");
+    Q4GemvBatchArgs a{};
+    a.blobs = direct ? 0 : blobs;
+    a.region_off = region_off;
+    a.x = x;
+    a.x_stride = x_stride;
+    a.y = y;
+    a.rows = rows;
+    a.cols = cols;
+    a.group = group;
+    a.experts = experts;
+    // The MFMA tile needs 32-column sub-groups under one scale, 16-byte
+    // aligned nibble rows and x, and its per-wave fragment area in LDS.
+    const int ng = cols / 32;
+    const size_t frag = (size_t)ng * 272;
+    // (blob bases come from 4096-aligned slot arenas, so only the offset matters)
+    const uint64_t data_off = region_off + (uint64_t)rows * (cols / group) * 2;
+    const bool aligned = (data_off % 16 == 0) && (x % 16 == 0) && ((uint64_t)x_stride * 4 % 16 == 0);
+    int waves = 4;
+    while (waves > 1 && frag * waves > c->max_lds) --waves;
+    if (group % 32 == 0 && aligned && frag <= c->max_lds) {
+        const int tiles = (rows + kTileRows - 1) / kTileRows;
+        const unsigned gx = (unsigned)((tiles + waves - 1) / waves);
+        return launch(c, kQ4Mfma, dim3(gx, experts), dim3(64 * waves), frag * waves, s, a);
+    }
+    return launch(c, kQ4Valu, dim3((rows + 3) / 4, experts), dim3(256), 0, s, a);
+}
+
+int lp_q4_gemv_batch(lp_ctx* c, uint64_t blobs, uint64_t region_off, uint64_t x, int x_stride,
+                     uint64_t y, int rows, int cols, int group, int experts, lp_stream s) {
+    return q4_gemv_common(c, blobs, region_off, x, x_stride, y, rows, cols, group, experts, s, false);
+}
+
+int lp_q4_gemv(lp_ctx* c, uint64_t blob, uint64_t x, uint64_t y, int rows, int cols, int group,
+               lp_stream s) {
+    return q4_gemv_common(c, 0, blob, x, 0, y, rows, cols, group, 1, s, true);
+}
+
+int lp_moe_reduce(lp_ctx* c, uint64_t eouts, uint64_t wts, uint64_t out, int experts, int n,
+                  lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n < 0 || experts < 0) return fail(LP_E_INVALID, "moe_reduce: negative size");
+    MoeReduceArgs a{eouts, wts, out, experts, n};
+    return launch(c, kMoeReduce, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+int lp_silu_mul(lp_ctx* c, uint64_t gate, uint64_t up, uint64_t out, int n, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n < 0) return fail(LP_E_INVALID, "silu_mul: negative size");
+    SiluMulArgs a{gate, up, out, n, 0};
+    return launch(c, kSiluMul, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+int lp_bf16_gemv(lp_ctx* c, uint64_t w, uint64_t x, uint64_t y, int rows, int cols, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (rows <= 0 || cols <= 0) return fail(LP_E_INVALID, "bf16_gemv: empty shape");
+    if (cols % 8 == 0 && (w % 16 != 0 || x % 16 != 0))
+        return fail(LP_E_UNSUPPORTED, "bf16_gemv: w and x must be 16-byte aligned");
+    Bf16GemvArgs a{w, x, y, rows, cols};
+    return launch(c, kBf16Gemv, dim3((rows + 3) / 4), dim3(256), 0, s, a);
+}
+
+int lp_add(lp_ctx* c, uint64_t pa, uint64_t pb, int n, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n < 0) return fail(LP_E_INVALID, "add: negative size");
+    AddArgs a{pa, pb, n, 0};
+    return launch(c, kAdd, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+// ---- fused MoE layer --------------------------------------------------------------
+
+int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out) {
+    if (!d || !out || T <= 0) return fail(LP_E_INVALID, "ws layout: bad arguments");
+    const uint64_t E = (uint64_t)d->experts, k = (uint64_t)d->top_k, H = (uint64_t)d->hidden,
+                   I = (uint64_t)d->inter, t = (uint64_t)T;
+    uint64_t o = 0;
+    auto take = [&](uint64_t bytes) {
+        uint64_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    out->logits = take(t * E * 4);
+    out->ids = take(t * k * 4);
+    out->wts = take(t * k * 4);
+    out->cnt = take(t * 4);
+    out->gs = take((E + 1) * 4);
+    out->perm = take(t * k * 4);
+    out->inv = take(t * k * 4);
+    out->uniq = take(E * 4);
+    out->meta = take(64);
+    out->act = take(t * k * I * 4);
+    out->y = take(t * k * H * 4);
+    out->total = o;
+    return LP_OK;
+}
+
+static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
+    if (int r = check_ctx(c)) return r;
+    if (!d) return fail(LP_E_INVALID, "null layer descriptor");
+    if (T <= 0) return fail(LP_E_INVALID, "T must be >= 1");
+    if (d->experts <= 0 || d->experts > kMaxExperts)
+        return fail(LP_E_UNSUPPORTED, "experts must be in 1..1024");
+    if (d->top_k <= 0 || d->top_k > kMaxTopK) return fail(LP_E_UNSUPPORTED, "top_k must be in 1..16");
+    if (d->hidden <= 0 || d->inter <= 0 || d->hidden % 32 || d->inter % 32)
+        return fail(LP_E_UNSUPPORTED, "hidden and inter must be multiples of 32");
+    if (d->group <= 0 || d->group % 32 || d->hidden % d->group || d->inter % d->group)
+        return fail(LP_E_UNSUPPORTED, "group must be a multiple of 32 dividing hidden and inter");
+    if (d->gating != LP_GATING_SOFTMAX && d->gating != LP_GATING_SIGMOID)
+        return fail(LP_E_INVALID, "unknown gating");
+    if (d->gating == LP_GATING_SIGMOID && !d->router_bias)
+        return fail(LP_E_INVALID, "sigmoid gating needs router_bias");
+    const uint64_t gpr_h = (uint64_t)d->hidden / d->group, gpr_i = (uint64_t)d->inter / d->group;
+    const uint64_t gd = d->gate_off + (uint64_t)d->inter * gpr_h * 2;
+    const uint64_t ud = d->up_off + (uint64_t)d->inter * gpr_h * 2;
+    const uint64_t dd = d->down_off + (uint64_t)d->hidden * gpr_i * 2;
+    if (gd % 16 || ud % 16 || dd % 16 || d->arena_base % 16 || d->slot_span % 16)
+        return fail(LP_E_UNSUPPORTED, "q4 nibble rows must be 16-byte aligned in every slot");
+    if (!d->router_w || !d->slot_table || !d->arena_base)
+        return fail(LP_E_INVALID, "router_w, slot_table and arena_base are required");
+    return LP_OK;
+}
+
+static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView* L, Workspace* W) {
+    *L = LayerView{};
+    L->router_w = d->router_w;
+    L->router_bias = d->router_bias;
+    L->slot_table = d->slot_table;
+    L->arena_base = d->arena_base;
+    L->slot_span = d->slot_span;
+    L->gate_off = d->gate_off;
+    L->up_off = d->up_off;
+    L->down_off = d->down_off;
+    L->hidden = d->hidden;
+    L->inter = d->inter;
+    L->experts = d->experts;
+    L->top_k = d->top_k;
+    L->group = d->group;
+    L->gating = d->gating;
+    L->renorm = d->renorm;
+    L->routed_scaling = d->routed_scaling;
+    L->min_weight = d->min_weight;
+    lp_moe_ws_layout lay;
+    lp_moe_ws_layout_get(d, T, &lay);
+    W->logits = ws + lay.logits;
+    W->ids = ws + lay.ids;
+    W->wts = ws + lay.wts;
+    W->cnt = ws + lay.cnt;
+    W->gs = ws + lay.gs;
+    W->perm = ws + lay.perm;
+    W->inv = ws + lay.inv;
+    W->uniq = ws + lay.uniq;
+    W->meta = ws + lay.meta;
+    W->act = ws + lay.act;
+    W->y = ws + lay.y;
+}
+
+static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
+    const int T = ra.T;
+    if (int r = launch(c, kTopk, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
+    return launch(c, kDispatch, dim3(1), dim3(64), 0, s, ra);
+}
+
+int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws,
+                 lp_stream s) {
+    if (int r = check_desc(c, d, T)) return r;
+    if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
+    RouteArgs ra{};
+    fill_views(d, ws, T, &ra.L, &ra.W);
+    ra.x = x;
+    ra.T = T;
+    dim3 g((unsigned)((d->experts + 3) / 4), (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
+    if (int r = launch(c, kRouter, g, dim3(256), 0, s, ra)) return r;
+    return route_tail(c, ra, s);
+}
+
+int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, int T,
+                        uint64_t ws, lp_stream s) {
+    if (int r = check_desc(c, d, T)) return r;
+    RouteArgs ra{};
+    fill_views(d, ws, T, &ra.L, &ra.W);
+    ra.T = T;
+    if (logits != ra.W.logits)
+        HIPCHK(hipMemcpyAsync(reinterpret_cast<void*>(ra.W.logits), reinterpret_cast<void*>(logits),
+                              (size_t)T * d->experts * 4, hipMemcpyDeviceToDevice, (hipStream_t)s));
+    return route_tail(c, ra, s);
+}
+
+int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                   uint64_t ws, lp_stream s) {
+    if (int r = check_desc(c, d, T)) return r;
+    if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
+    GroupedArgs ga{};
+    fill_views(d, ws, T, &ga.L, &ga.W);
+    ga.x = x;
+    ga.h = h;
+    ga.T = T;
+    const int kmax = std::max(d->hidden, d->inter);
+    const size_t frag = (size_t)(kmax / 32) * 272;
+    int waves = 4;
+    while (waves > 1 && frag * waves > c->max_lds) --waves;
+    if (frag > c->max_lds) return fail(LP_E_UNSUPPORTED, "hidden too large for the LDS fragment area");
+    ga.lds_per_wave = (int)frag;
+    const int maxu = std::min(T * d->top_k, d->experts);
+    for (int phase = 0; phase < 2; ++phase) {
+        ga.phase = phase;
+        const int rows = phase == 0 ? d->inter : d->hidden;
+        const int items = maxu * ((rows + kTileRows - 1) / kTileRows);
+        const int wgs = std::max(1, std::min((items + waves - 1) / waves, 2 * c->cus));
+        if (int r = launch(c, kGrouped, dim3((unsigned)wgs), dim3(64 * waves), frag * waves, s, ga))
+            return r;
+    }
+    return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
+                  s, ga);
+}
+
+int lp_moe_forward(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                   uint64_t ws, lp_stream s) {
+    if (int r = lp_moe_route(c, d, x, T, ws, s)) return r;
+    return lp_moe_experts(c, d, x, h, T, ws, s);
+}
+
+int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T, lp_stream s,
+                       int32_t* unique_count, int32_t* error_flags) {
+    if (int r = check_ctx(c)) return r;
+    lp_moe_ws_layout lay;
+    if (int r = lp_moe_ws_layout_get(d, T, &lay)) return r;
+    int32_t meta[2] = {0, 0};
+    HIPCHK(hipMemcpyAsync(meta, reinterpret_cast<void*>(ws + lay.meta), 8, hipMemcpyDeviceToHost,
+                          (hipStream_t)s));
+    HIPCHK(hipStreamSynchronize((hipStream_t)s));
+    if (unique_count) *unique_count = meta[0];
+    if (error_flags) *error_flags = meta[1];
+    return LP_OK;
+}
+
+float lp_route_expf(float x) { return lp::expf_glibc(x); }
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+"""GPU parity of the fused MoE layer against the CPU oracle.
+
+Bit-exact: router logits (canonical order), routing ids / order / weights
+(decode.rs:734-749, kimi.rs:1155-1186 with glibc expf), dispatch tables.
+Tolerance: the layer output, rel-L2 <= 1e-3 on the MoE delta h' - h (the
+north-star bound, measured on the delta so the residual cannot hide error)."""
+import numpy as np
+import pytest
+
+import llmpager_amd as lp
+import _oracle as O
+from _gpu import DeviceLayer, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_layer(cuda, L: DeviceLayer, T: int, seed: int):
+    H, E, k = L.H, L.E, L.k
+    x = lp.synth_f32_bf16(T * H, 1.0, seed, 1).reshape(T, H)
+    h = lp.synth_f32_bf16(T * H, 1.0, seed, 2).reshape(T, H)
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    dx, dh = cuda.upload(x), cuda.upload(h)
+    L.layer.forward(dx, dh, T, ws)
+    got_h = cuda.download(dh, (T, H), np.float32)
+    dl = lambda off, shape, dt: cuda.download(ws + off, shape, dt)
+    out = dict(
+        h=got_h,
+        logits=dl(lay.logits, (T, E), np.float32),
+        ids=dl(lay.ids, (T, k), np.int32),
+        wts=dl(lay.wts, (T, k), np.float32),
+        cnt=dl(lay.cnt, (T,), np.int32),
+        gs=dl(lay.gs, (E + 1,), np.int32),
+        perm=dl(lay.perm, (T * k,), np.int32),
+        inv=dl(lay.inv, (T * k,), np.int32),
+        uniq=dl(lay.uniq, (E,), np.int32),
+        status=L.layer.status(ws, T),
+    )
+    for p in (ws, dx, dh):
+        cuda.free_device(p)
+    return x, h, out
+
+
+def _check_layer(L: DeviceLayer, x, h, g, T, threads=8):
+    E, k = L.E, L.k
+    want_h, want_logits, want_ids, want_w, want_cnt = O.moe_layer(
+        L.oracle_desc(), L.oracle_blobs(), x, h, threads=threads)
+    # logits: canonical order, identical bits
+    assert np.array_equal(g["logits"].view(np.uint32), want_logits.view(np.uint32))
+    # routing: ids, order, count and weights identical
+    assert np.array_equal(g["cnt"], want_cnt)
+    for t in range(T):
+        c = want_cnt[t]
+        assert np.array_equal(g["ids"][t, :c], want_ids[t, :c]), t
+        assert np.array_equal(g["wts"][t, :c].view(np.uint32), want_w[t, :c].view(np.uint32)), t
+    # dispatch: identical tables
+    perm, gs, inv, uniq = O.moe_dispatch(want_ids, want_cnt, T, k, E)
+    assert np.array_equal(g["gs"], gs)
+    assert np.array_equal(g["perm"][:gs[E]], perm)
+    assert np.array_equal(g["inv"], inv)
+    assert g["status"] == (len(uniq), 0)
+    assert np.array_equal(g["uniq"][:len(uniq)], uniq)
+    # layer output: delta within rel-L2 1e-3
+    assert rel_l2(g["h"] - h, want_h - h) <= 1e-3
+    assert rel_l2(g["h"], want_h) <= 1e-4
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_layer_small(cuda, group, T):
+    # write_test_checkpoint shape (convert/src/lib.rs:341-423): H128/I64/E8/k2
+    L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=group, seed=7, router_std=0.2)
+    x, h, g = _run_layer(cuda, L, T, seed=11 + T)
+    _check_layer(L, x, h, g, T)
+    L.free()
+
+
+@pytest.mark.parametrize("T", [1, 8, 32])
+def test_layer_config1(cuda, T):
+    # Qwen3-30B-A3B shape: H2048, E128, top-8, I768, q4 g32, softmax + renorm
+    L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=0)
+    x, h, g = _run_layer(cuda, L, T, seed=T)
+    _check_layer(L, x, h, g, T)
+    L.free()
+
+
+def test_layer_sigmoid_gating(cuda):
+    # DeepSeek/Kimi-style gating: sigmoid + bias, renorm, scaling, min_weight
+    rng = np.random.default_rng(5)
+    bias = (rng.standard_normal(64) * 0.05).astype(np.float32)
+    L = DeviceLayer(cuda, H=2048, I=1408, E=64, k=6, group=32, seed=3,
+                    gating=lp.GATING_SIGMOID, renorm=True, routed_scaling=2.5,
+                    min_weight=0.3, bias=bias, router_std=0.05)
+    T = 16
+    x, h, g = _run_layer(cuda, L, T, seed=9)
+    _check_layer(L, x, h, g, T)
+    assert (g["cnt"] < 6).any()  # min_weight dropped some picks
+    L.free()
+
+
+def test_layer_missing_expert_flags(cuda):
+    # A routed expert with no slot raises the error flag and contributes 0.
+    slots = np.arange(8, dtype=np.int32)
+    slots[3] = -1
+    L = DeviceLayer(cuda, H=128, I=64, E=8, k=8, group=32, seed=1, slots=slots)
+    T = 2
+    x, h, g = _run_layer(cuda, L, T, seed=1)
+    assert g["status"][1] == 1
+    L.free()
+
+
+def _route_logits(cuda, L: DeviceLayer, logits: np.ndarray):
+    T = logits.shape[0]
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    dlg = cuda.upload(np.ascontiguousarray(logits, np.float32))
+    L.layer.route_logits(dlg, T, ws)
+    ids = cuda.download(ws + lay.ids, (T, L.k), np.int32)
+    wts = cuda.download(ws + lay.wts, (T, L.k), np.float32)
+    cnt = cuda.download(ws + lay.cnt, (T,), np.int32)
+    cuda.free_device(ws)
+    cuda.free_device(dlg)
+    return ids, wts, cnt
+
+
+def _adversarial_logits(E: int, rng) -> np.ndarray:
+    rows = []
+    base = rng.standard_normal(E).astype(np.float32)
+    rows.append(np.zeros(E, np.float32))                       # all equal
+    rows.append(np.full(E, 3.5, np.float32))
+    t = base.copy(); t[[5, 9, 17]] = t.max() + 1.0; rows.append(t)   # exact ties at the top
+    t = base.copy()                                            # neighbours one ulp apart
+    top = np.float32(2.0)
+    for j, e in enumerate([3, 4, 5, 6, 7, 8, 9, 10, 11, 12]):
+        t[e] = np.nextafter(top, np.float32(-10), dtype=np.float32) if j % 2 else top
+        top = np.nextafter(top, np.float32(-10), dtype=np.float32) if j % 3 == 2 else top
+    rows.append(t)
+    rows.append((base * 1e4).astype(np.float32))              # large magnitude
+    rows.append((base * 1e-6).astype(np.float32))             # tiny spread: probability collisions
+    rows.append((base * 40).astype(np.float32))               # underflowing exponentials
+    t = np.linspace(-0.5, 0.5, E).astype(np.float32)[::-1].copy(); rows.append(t)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("E,k", [(128, 8), (64, 6), (8, 2), (4, 2), (300, 16)])
+def test_routing_bit_exact_softmax(cuda, E, k):
+    rng = np.random.default_rng(E * 31 + k)
+    L = DeviceLayer(cuda, H=128, I=64, E=E, k=k, group=32, seed=2)
+    rnd = (rng.standard_normal((2048, E)) * rng.choice([0.01, 1, 8, 30], (2048, 1))).astype(np.float32)
+    logits = np.concatenate([_adversarial_logits(E, rng), rnd])
+    for renorm in (True, False):
+        L.desc.renorm = int(renorm)
+        ids, wts, cnt = _route_logits(cuda, L, logits)
+        for t in range(logits.shape[0]):
+            wi, ww = O.top_k_softmax(logits[t], k, renorm)
+            assert cnt[t] == len(wi)
+            assert np.array_equal(ids[t, :cnt[t]], wi), (t, renorm)
+            assert np.array_equal(wts[t, :cnt[t]].view(np.uint32), ww.view(np.uint32)), (t, renorm)
+    L.free()
+
+
+def test_routing_bit_exact_sigmoid(cuda):
+    E, k = 64, 6
+    rng = np.random.default_rng(77)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    bias[[1, 2]] = 0.0
+    L = DeviceLayer(cuda, H=128, I=64, E=E, k=k, group=32, seed=2, gating=lp.GATING_SIGMOID,
+                    renorm=True, routed_scaling=2.5, min_weight=0.05, bias=bias)
+    logits = np.concatenate([_adversarial_logits(E, rng),
+                             (rng.standard_normal((1024, E)) * 3).astype(np.float32)])
+    for renorm, mw in ((True, 0.05), (False, 0.0), (True, 0.0)):
+        L.desc.renorm, L.desc.min_weight = int(renorm), mw
+        ids, wts, cnt = _route_logits(cuda, L, logits)
+        for t in range(logits.shape[0]):
+            wi, ww = O.sigmoid_topk(logits[t], bias, k, renorm, 2.5, mw)
+            assert cnt[t] == len(wi)
+            assert np.array_equal(ids[t, :cnt[t]], wi), t
+            assert np.array_equal(wts[t, :cnt[t]].view(np.uint32), ww.view(np.uint32)), t
+    L.free()
