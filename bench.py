@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""MoE-layer decode throughput on one MI355X: BASELINE.json config 2.
+
+Workload: the Qwen3-30B-A3B MoE layer shape (hidden 2048, 128 experts, top-8
+softmax with renormalisation, expert FFN 2048->768->2048, q4 group 32) stacked
+to 48 layers; every one of the 48 x 128 experts is resident in a per-layer
+slot arena (16.3 GB of HBM), router weights bf16 N(0, 0.02), activations bf16
+N(0, 1), all synthetic (seed 0).  One step = one lockstep decode of B tokens
+through all 48 layers (router GEMV, top-k, dispatch, grouped q4 gate/up +
+SiLU, grouped down, pick-order combine into the residual), the layer input
+being the residual itself.  B = 1, 8 and 32 are measured; the headline is
+B = 32.
+
+HBM bytes per step are algorithmic: per layer the router (524,288 B), each
+*unique* routed expert's q4 weights once (2,654,208 B incl. scales; unique
+counts are measured, not assumed) and per token 20,480 B of activations.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tok/s + HBM GB/s (% of 8 TB/s), Qwen3-30B-A3B-shape q4 decode"
+H, I, E, K, G, LAYERS = 2048, 768, 128, 8, 32, 48
+ROUTER_BYTES = E * H * 2
+REGION_BYTES = I * (H // G) * 2 + I * H // 2        # 884,736: one q4 projection incl. scales
+EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
+ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
+PEAK_GBPS = 8000.0
+DOMINANT = "lp_moe_gateup"
+KERNELS = ("lp_moe_router", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_gateup", "lp_moe_down",
+           "lp_moe_down_wide", "lp_moe_combine")
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def align(v: int, a: int = 4096) -> int:
+    return (v + a - 1) // a * a
+
+
+class Stack:
+    """The 48-layer expert stack resident on the device."""
+
+    def __init__(self, cuda, stream, layers: int, keep_host: int):
+        import llmpager_amd as lp
+        self.lp, self.cuda, self.s = lp, cuda, stream
+        self.span = align(lp.blob_bytes(H, I, G))
+        self.offsets = lp.blob_offsets(H, I, G)
+        n = E * self.span
+        pin = cuda.alloc_pinned(n)
+        view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(pin))
+        self.descs, self.allocs, self.host, self.router_host = [], [], [], []
+        threads = min(16, os.cpu_count() or 1)
+        for l in range(layers):
+            lp.synth_blobs(E, self.span, H, I, G, 0, l, threads=threads, out=view)
+            arena = cuda.alloc_device(n)
+            cuda.htod_ptr_async(arena, pin, n, stream)
+            rw = lp.synth_bf16(E * H, 0.02, 0, 1000 + l)
+            d_rw = cuda.upload(rw, stream)
+            d_slots = cuda.upload(np.arange(E, dtype=np.int32), stream)
+            cuda.sync_stream(stream)
+            if l < keep_host:
+                self.host.append(view.copy())
+                self.router_host.append(rw)
+            go, uo, do = self.offsets
+            self.descs.append(lp.LayerDesc(
+                hidden=H, inter=I, experts=E, top_k=K, group=G, gating=lp.GATING_SOFTMAX,
+                renorm=1, routed_scaling=1.0, min_weight=0.0, router_w=d_rw, router_bias=0,
+                slot_table=d_slots, arena_base=arena, slot_span=self.span,
+                gate_off=go, up_off=uo, down_off=do))
+            self.allocs += [arena, d_rw, d_slots]
+            if l % 8 == 7:
+                log(f"resident layers {l + 1}/{layers}")
+        cuda.free_pinned(pin)
+        self.layers = [lp.MoeLayer(cuda, d) for d in self.descs]
+
+    def step(self, h: int, T: int, ws: int) -> None:
+        for L in self.layers:
+            L.forward(h, h, T, ws, self.s)
+
+    def unique_counts(self, h: int, T: int, ws: int) -> list[int]:
+        out = []
+        for L in self.layers:
+            L.forward(h, h, T, ws, self.s)
+            out.append(L.status(ws, T, self.s)[0])
+        return out
+
+
+def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
+    """Each step decodes a fresh batch of B tokens: step i works in place on
+    its own resident residual buffer (inputs already in HBM), restored from a
+    saved copy before every pass so the three passes see identical inputs."""
+    import llmpager_amd as lp
+    s = stack.s
+    ws = cuda.alloc_device(lp.ws_layout(stack.descs[0], B).total)
+    n = steps + warmup
+    h0 = lp.synth_f32_bf16(n * B * H, 1.0, 0, 2)
+    tok_bytes = B * H * 4
+    saved = cuda.upload(h0, s)
+    hbuf = cuda.alloc_device(h0.nbytes)
+
+    def restore():
+        cuda.dtod_async(hbuf, saved, h0.nbytes, s)
+        cuda.sync()
+
+    def run(i):
+        stack.step(hbuf + i * tok_bytes, B, ws)
+
+    restore()
+    for i in range(warmup):
+        run(steps + i)
+    e0, e1 = cuda.event(), cuda.event()
+    cuda.sync()
+    cuda.record_event(e0, s)
+    for i in range(steps):
+        run(i)
+    cuda.record_event(e1, s)
+    cuda.sync()
+    ms = cuda.elapsed_ms(e0, e1)
+    # the same steps again, each kernel bracketed by events on its stream
+    restore()
+    cuda.profile_reset()
+    cuda.profile(True)
+    for i in range(steps):
+        run(i)
+    cuda.sync()
+    prof = {k: cuda.profile_read(k) for k in KERNELS}
+    cuda.profile(False)
+    # and once more with a status readback per layer: the measured unique counts
+    restore()
+    uniq = [stack.unique_counts(hbuf + i * tok_bytes, B, ws) for i in range(steps)]
+    for p in (ws, hbuf, saved):
+        cuda.free_device(p)
+    for e in (e0, e1):
+        cuda.destroy_event(e)
+    u = np.array(uniq, np.int64)                       # [steps, layers]
+    step_bytes = float(np.mean(u.sum(1))) * EXPERT_BYTES + LAYERS * (ROUTER_BYTES + B * ACT_BYTES)
+    sec = ms / 1e3 / steps
+    # dominant kernel: grouped gate/up (two of the three projections of every
+    # unique expert); its algorithmic bytes are U x 2 x 884,736 per launch
+    gu_bytes = float(u.sum()) * 2 * REGION_BYTES
+    dom_ms, dom_n = prof[DOMINANT]
+    dom_gbps = gu_bytes / (dom_ms / 1e3) / 1e9 if dom_ms > 0 else 0.0
+    dn_ms = prof["lp_moe_down"][0] + prof["lp_moe_down_wide"][0]
+    dn_gbps = float(u.sum()) * REGION_BYTES / (dn_ms / 1e3) / 1e9 if dn_ms > 0 else 0.0
+    res = dict(
+        batch=B, tok_s=B / sec, ms_per_step=sec * 1e3, unique_experts_per_layer=float(u.mean()),
+        bytes_per_step=step_bytes, hbm_gbps=step_bytes / sec / 1e9,
+        hbm_frac=step_bytes / sec / 1e9 / PEAK_GBPS,
+        dominant=dict(kernel=DOMINANT, launches=dom_n, avg_us=dom_ms * 1e3 / max(dom_n, 1),
+                      bytes_per_launch=gu_bytes / max(dom_n, 1), gbps=dom_gbps,
+                      frac=dom_gbps / PEAK_GBPS),
+        down_gbps=dn_gbps,
+        kernels_avg_us={k: v[0] * 1e3 / max(v[1], 1) for k, v in prof.items() if v[1]},
+    )
+    log(f"B={B}: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step, "
+        f"{res['hbm_gbps']:.0f} GB/s step, gate/up {dom_gbps:.0f} GB/s, down {dn_gbps:.0f} GB/s, "
+        f"U={res['unique_experts_per_layer']:.1f}")
+    return res
+
+
+def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
+    """The oracle (oracle/, the CPU restatement of the reference path) on the
+    host cores: the first layers kept in host memory, B tokens, repeated until
+    about budget_s seconds of work; scaled to the 48-layer stack."""
+    import llmpager_amd as lp
+    path = os.path.join(ROOT, "oracle", "liblp_oracle.so")
+    lib = C.CDLL(path)
+
+    class Layer(C.Structure):
+        _fields_ = [
+            ("hidden", C.c_int), ("inter", C.c_int), ("experts", C.c_int), ("top_k", C.c_int),
+            ("group", C.c_int), ("gating", C.c_int), ("renorm", C.c_int),
+            ("routed_scaling", C.c_float), ("min_weight", C.c_float),
+            ("router_w", C.c_void_p), ("router_bias", C.c_void_p), ("blobs", C.c_void_p),
+            ("gate_off", C.c_uint64), ("up_off", C.c_uint64), ("down_off", C.c_uint64),
+            ("shared_blob", C.c_void_p), ("shared_inter", C.c_int), ("shared_group", C.c_int),
+            ("sh_gate_off", C.c_uint64), ("sh_up_off", C.c_uint64), ("sh_down_off", C.c_uint64)]
+
+    vp = C.c_void_p
+    lib.lpo_moe_layer.argtypes = [C.POINTER(Layer), vp, vp, C.c_int, vp, vp, vp, vp, vp, C.c_int,
+                                  C.c_int]
+    lib.lpo_moe_layer.restype = C.c_int
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    layers = []
+    go, uo, do = stack.offsets
+    for hb, rw in zip(stack.host, stack.router_host):
+        ptrs = (C.c_void_p * E)(*[hb.ctypes.data + e * stack.span for e in range(E)])
+        layers.append((Layer(hidden=H, inter=I, experts=E, top_k=K, group=G, gating=0, renorm=1,
+                             routed_scaling=1.0, min_weight=0.0, router_w=rw.ctypes.data,
+                             blobs=C.cast(ptrs, vp), gate_off=go, up_off=uo, down_off=do), ptrs))
+    h = lp.synth_f32_bf16(B * H, 1.0, 0, 2).reshape(B, H)
+    x = np.empty_like(h)
+    t0 = time.perf_counter()
+    n_layer_passes = 0
+    while True:
+        for L, _ in layers:
+            x[:] = h
+            rc = lib.lpo_moe_layer(C.byref(L), x.ctypes.data, h.ctypes.data, B, None, None, None,
+                                   None, None, 0, threads)
+            assert rc == 0
+            n_layer_passes += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    per_step = dt / n_layer_passes * LAYERS
+    log(f"cpu baseline: {n_layer_passes} layer passes of B={B} in {dt:.1f}s on {threads} threads")
+    return dict(value=B / per_step, unit="tok/s", cores=threads, kind="port",
+                sample=f"oracle lpo_moe_layer (reference semantics, OpenMP over rows) on "
+                       f"{n_layer_passes} layer passes of batch {B} over the first "
+                       f"{len(layers)} layers, scaled to the 48-layer stack")
+
+
+def main() -> int:
+    global LAYERS
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batches", default="1,8,32")
+    ap.add_argument("--headline", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: this build's MoE path runs on a single MI355X "
+              f"(the multi-GPU expert-parallel split is a design, not built); got --gpus {a.gpus}",
+              file=sys.stderr)
+        return 2
+    LAYERS = a.layers
+    batches = [int(b) for b in a.batches.split(",")]
+    if a.headline not in batches:
+        batches.append(a.headline)
+
+    import llmpager_amd as lp
+    cuda = lp.Cuda(0)
+    s = cuda.stream()
+    log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
+    stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu else 2)
+    results = {}
+    for B in batches:
+        results[B] = run_batch(cuda, stack, B, a.steps, a.warmup)
+    hl = results[a.headline]
+    cpu = None if a.no_cpu else cpu_baseline(stack, a.headline, a.cpu_seconds)
+    dom = hl["dominant"]
+    line = {
+        "metric": METRIC,
+        "value": round(hl["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(hl["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 x bf16-split -> fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config2: {LAYERS}-layer Qwen3-30B-A3B-shape MoE stack, lockstep decode "
+                        f"batch {a.headline}, all {LAYERS * E} experts resident",
+            "hidden": H, "inter": I, "experts": E, "top_k": K, "group": G, "layers": LAYERS,
+            "batch": a.headline, "parallelism": "none (one GPU)",
+        },
+        "hbm_gbps": round(hl["hbm_gbps"], 1),
+        "hbm_frac": round(hl["hbm_frac"], 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": DOMINANT,
+            "bytes_per_launch": round(dom["bytes_per_launch"]),
+            "achieved": round(dom["gbps"], 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dom["frac"], 4),
+            "traffic": None,
+            "avg_us": round(dom["avg_us"], 3),
+        },
+        "cpu_baseline": cpu,
+        "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
+                             for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
+                    | {"gateup_gbps": round(r["dominant"]["gbps"], 1),
+                       "gateup_avg_us": round(r["dominant"]["avg_us"], 3),
+                       "kernels_avg_us": {k: round(v, 3) for k, v in r["kernels_avg_us"].items()}}
+                    for b, r in results.items()},
+    }
+    print(json.dumps(line), flush=True)
+    cuda.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -182,6 +182,53 @@ int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t
 int lp_moe_status_sync(lp_ctx* ctx, uint64_t workspace, const lp_moe_layer_desc* d, int T,
                        lp_stream s, int32_t* unique_count, int32_t* error_flags);
 
+/* ---- expert-slot bookkeeping: cache::ExpertCache (cache.rs:58-241) -------- */
+
+typedef struct lp_cache lp_cache;
+enum { LP_LOOKUP_HIT = 0, LP_LOOKUP_MISS = 1, LP_LOOKUP_STALLED = 2 };
+
+/* cache.rs:71-73 (ExpertCache::new) and :78-102 (partitioned).  NULL on a
+ * zero argument (the reference asserts). */
+lp_cache* lp_cache_new(uint16_t num_layers, uint32_t slots_per_layer, uint32_t decay_interval);
+lp_cache* lp_cache_partitioned(uint32_t partitions, uint32_t ids_per_partition,
+                               uint32_t slots_per_partition, uint32_t decay_interval);
+void lp_cache_free(lp_cache* c);
+/* cache.rs:106-108 */
+uint32_t lp_cache_fold(uint16_t layer, uint16_t expert, uint32_t experts_per_layer);
+/* cache.rs:112-118 */
+uint32_t lp_cache_slots_per_partition(const lp_cache* c);
+uint32_t lp_cache_total_slots(const lp_cache* c);
+/* cache.rs:132-179: returns LP_LOOKUP_HIT / MISS / STALLED; the slot is
+ * pinned on HIT and MISS; *evicted is the displaced id or -1. */
+int lp_cache_acquire(lp_cache* c, uint32_t id, uint32_t* slot, int64_t* evicted);
+/* cache.rs:184-195: 1 (pinned hit on a published slot) or 0. */
+int lp_cache_lookup_ready(lp_cache* c, uint32_t id, uint32_t* slot);
+/* cache.rs:198-204 */
+int lp_cache_publish(lp_cache* c, uint32_t slot);
+int lp_cache_is_ready(const lp_cache* c, uint32_t slot);
+/* cache.rs:207-211: LP_E_INVALID for a release without a matching acquire. */
+int lp_cache_release(lp_cache* c, uint32_t slot);
+/* cache.rs:218-225 */
+int lp_cache_decay_all(lp_cache* c);
+/* cache.rs:229-236: 1 when every slot the id could use is pinned and ready. */
+int lp_cache_is_wedged(const lp_cache* c, uint32_t id);
+/* cache.rs:238-240 */
+int lp_cache_stats(const lp_cache* c, uint64_t* hits, uint64_t* misses);
+/* The id a slot holds, or -1 (no counterpart in the reference: lets a caller
+ * rebuild a layer's device slot table from the cache). */
+int64_t lp_cache_slot_id(const lp_cache* c, uint32_t slot);
+
+/* ---- measurement ------------------------------------------------------------ */
+
+/* When enabled, every kernel launch through this context is bracketed by a
+ * pair of hipEvents on its stream (a measurement aid; it adds two event
+ * records per launch).  lp_profile_read_sync waits for the recorded work and
+ * returns, for the kernel named `kernel` (e.g. "lp_moe_grouped"), the summed
+ * elapsed milliseconds and launch count since the last reset. */
+int lp_profile_enable(lp_ctx* ctx, int enable);
+int lp_profile_reset(lp_ctx* ctx);
+int lp_profile_read_sync(lp_ctx* ctx, const char* kernel, double* total_ms, int64_t* launches);
+
 /* ---- blob format and synthetic inputs ------------------------------------ */
 
 /* quant.rs:20-22 */
@@ -205,6 +252,8 @@ int lp_synth_f32_bf16(float* dst, uint64_t n, float std, uint64_t seed, uint64_t
 
 /* Host evaluation of the expf routing uses (glibc's bits; see lp_expf.h). */
 float lp_route_expf(float x);
+/* out[i] = lp_route_expf(bits_to_float(first + i*stride)), i < n. */
+void lp_route_expf_sweep(uint32_t first, uint32_t stride, uint64_t n, float* out);
 
 #ifdef __cplusplus
 }

@@ -105,7 +105,11 @@ def _sig(lib):
         "lp_synth_blobs": (i32, [vp, u64, i32, i32, i32, i32, u64, i32, i32, i32]),
         "lp_synth_bf16": (i32, [vp, u64, f32, u64, u64]),
         "lp_synth_f32_bf16": (i32, [vp, u64, f32, u64, u64]),
+        "lp_profile_enable": (i32, [vp, i32]),
+        "lp_profile_reset": (i32, [vp]),
+        "lp_profile_read_sync": (i32, [vp, C.c_char_p, P(C.c_double), P(C.c_int64)]),
         "lp_route_expf": (f32, [f32]),
+        "lp_route_expf_sweep": (None, [C.c_uint32, C.c_uint32, u64, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -180,6 +184,12 @@ def synth_f32_bf16(n: int, std: float, seed: int, stream: int) -> np.ndarray:
 
 def route_expf(x: float) -> float:
     return float(lib().lp_route_expf(x))
+
+
+def route_expf_sweep(first: int, stride: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    lib().lp_route_expf_sweep(first, stride, n, _ptr(out))
+    return out
 
 
 def ws_layout(desc: LayerDesc, T: int) -> WsLayout:
@@ -291,6 +301,18 @@ class Cuda:
 
     def sync(self) -> None:
         _check(lib().lp_sync(self.ctx))
+
+    # measurement (lp_profile_*)
+    def profile(self, enable: bool) -> None:
+        _check(lib().lp_profile_enable(self.ctx, int(enable)))
+
+    def profile_reset(self) -> None:
+        _check(lib().lp_profile_reset(self.ctx))
+
+    def profile_read(self, kernel: str) -> tuple[float, int]:
+        ms, n = C.c_double(), C.c_int64()
+        _check(lib().lp_profile_read_sync(self.ctx, kernel.encode(), C.byref(ms), C.byref(n)))
+        return ms.value, n.value
 
     # convenience
     def upload(self, a: np.ndarray, stream: int | None = None) -> int:

@@ -10,48 +10,38 @@ using namespace lpk;
 // q4 GEMV, batched over experts (kernels.rs:102-127, q4g64.cu:19-81 semantics):
 //   y[e*rows + r] = sum_g s[r, g] * sum_{c in g} (q[r, c] - 8) * x_e[c],
 //   x_e = x + e*x_stride, region = blobs[e] + region_off.
-// MFMA path: grid (waves-per-expert/4, experts), 4 waves per workgroup, each
-// wave stages x_e once into its LDS fragment area and walks 16-row tiles.
-// Requires group % 32 == 0, 16-byte aligned nibble rows and x (host checks).
-// Dynamic LDS: one fragment area (frag_lds_bytes) per wave.
+// MFMA path: grid (workgroups per expert, experts); the workgroup stages x_e
+// once into an LDS fragment pair, then each wave walks 16-row tiles.
+// Requires group = 32 * 2^r, 16-byte aligned nibble rows and x (host checks).
+// Dynamic LDS: frag_pair_bytes(cols / 32).
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(256) lp_q4_gemv_mfma(const Q4GemvBatchArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int wave = threadIdx.x >> 6;
+    const int wpb = blockDim.x >> 6;
+    const int lane = lane_id();
     const int e = blockIdx.y;
     const int ng = a.cols >> 5;
-    FragLds F;
-    uint8_t* base = lds + (size_t)wave * frag_lds_bytes(ng);
-    F.frag = reinterpret_cast<uint4*>(base);
-    F.off = reinterpret_cast<float*>(base + (size_t)ng * 256);
-    F.ng = ng;
-    const uint64_t blob = a.blobs ? reinterpret_cast<const uint64_t*>(a.blobs)[e] : a.region_off;
-    const uint8_t* region = reinterpret_cast<const uint8_t*>(a.blobs ? blob + a.region_off : blob);
+    const uint64_t region = a.blobs ? gptr<uint64_t>(a.blobs)[e] + a.region_off : a.region_off;
     const float* x = reinterpret_cast<const float*>(a.x) + (size_t)e * a.x_stride;
     float* y = reinterpret_cast<float*>(a.y) + (size_t)e * a.rows;
-
-    stage_frags(F, x, nullptr);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-
+    const Frags F = frags_at(lds, ng, 1);
+    stage_rows(F, 1, [&](int) { return x; }, threadIdx.x, blockDim.x);
+    __syncthreads();
     const int tiles = (a.rows + kTileRows - 1) / kTileRows;
     const int S = tile_steps(a.cols);
-    const int lane = lane_id();
-    const int wpb = blockDim.x >> 6;
+    const int rs = ilog2_pow2(a.group >> 5);
     for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
         const int n0 = tile * kTileRows;
-        float acc0 = 0.0f, acc1 = 0.0f;
-        TileRegs<8> A, B;
-        tile_load(A, region, a.rows, a.cols, a.group, n0, 0);
+        float acc[1][2] = {{0.0f, 0.0f}};
+        WRegs<16> R;
         for (int c0 = 0; c0 < S; c0 += 16) {
-            if (c0 + 8 < S) tile_load(B, region, a.rows, a.cols, a.group, n0, c0 + 8);
-            tile_mma(A, F, a.cols, c0, acc0, acc1);
-            if (c0 + 16 < S) tile_load(A, region, a.rows, a.cols, a.group, n0, c0 + 16);
-            if (c0 + 8 < S) tile_mma(B, F, a.cols, c0 + 8, acc0, acc1);
+            wload(R, region, a.rows, a.cols, rs, n0, c0);
+            wmma(R, F, a.cols, c0, 1, acc);
         }
-        acc0 = tile_reduce(acc0);
+        const float v = tile_reduce(acc[0][0]);
         const int row = n0 + (lane & 15);
-        if (lane < 16 && row < a.rows) y[row] = acc0;
+        if (lane < 16 && row < a.rows) y[row] = v;
     }
 }
 

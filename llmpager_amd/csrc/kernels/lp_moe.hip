@@ -296,136 +296,186 @@ extern "C" __global__ void __launch_bounds__(64) lp_moe_dispatch(const RouteArgs
 }
 
 // ---------------------------------------------------------------------------
-// Grouped expert projections.  Work item = (unique expert, 16-row tile); each
-// wave takes items round-robin and serves the expert's tokens two at a time.
-//   phase 0: act[pos][r] = silu(gate_e . x_t)[r] * (up_e . x_t)[r], rows r < I
-//   phase 1: y[pos][r]   = (down_e . act[pos])[r], rows r < H
-// pos = dispatch position of the (token, pick) pair; the blob of expert e is
+// Grouped expert projections.  A workgroup of W waves takes one work item =
+// (unique expert, run of rows); every wave owns 16-row tiles of that run and
+// the workgroup stages the expert's tokens into shared LDS fragments, up to
+// `pairs_cap` token pairs at a time.  Weight loads are issued before the
+// fragments are staged, and each dequantised weight word serves every staged
+// token pair.
+//   gate/up: act[pos][r] = silu(gate_e . x_t)[r] * (up_e . x_t)[r], r < I
+//   down:    y[pos][r]   = (down_e . act[pos])[r], r < H
+// pos = dispatch position of the (token, pick) pair; expert e's blob sits at
 // arena_base + slot_table[e] * slot_span (the per-layer slot arena of
 // pager.rs:310-318).  An expert without a slot raises kErrMissingExpert in
-// meta[1] and contributes zeros.
+// meta[1] and its outputs are zero.
 // ---------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(256) lp_moe_grouped(const GroupedArgs a) {
+namespace {
+
+struct Item {
+    int e, slot, p0, ntok, chunk;
+    bool live;
+};
+
+__device__ __forceinline__ Item item_of(const GroupedArgs& a, int chunks) {
+    Item it;
+    const int nu = gptr<int>(a.W.meta)[0];
+    const int u = blockIdx.x / chunks;
+    it.live = u < nu;
+    if (!it.live) return it;
+    it.chunk = blockIdx.x - u * chunks;
+    it.e = gptr<int>(a.W.uniq)[u];
+    it.slot = gptr<int>(a.L.slot_table)[it.e];
+    it.p0 = gptr<int>(a.W.gs)[it.e];
+    it.ntok = gptr<int>(a.W.gs)[it.e + 1] - it.p0;
+    return it;
+}
+
+__device__ __forceinline__ void missing_expert(const GroupedArgs& a, const Item& it, float* out,
+                                               int stride, int rows, int row_lo, int row_hi) {
+    if (threadIdx.x == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
+    for (int p = 0; p < it.ntok; ++p)
+        for (int r = row_lo + (int)threadIdx.x; r < row_hi && r < rows; r += blockDim.x)
+            out[(size_t)(it.p0 + p) * stride + r] = 0.0f;
+}
+
+template <int NS, int PMAX>
+__device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int wave = threadIdx.x >> 6;
-    const int lane = lane_id();
     const LayerView& L = a.L;
     const int H = L.hidden, I = L.inter, k = L.top_k;
-    const int phase = a.phase;
-    const int rows = phase == 0 ? I : H;
-    const int cols = phase == 0 ? H : I;
-    const int ng = cols >> 5;
-    FragLds F;
-    uint8_t* lbase = lds + (size_t)wave * a.lds_per_wave;
-    F.frag = reinterpret_cast<uint4*>(lbase);
-    F.off = reinterpret_cast<float*>(lbase + (size_t)ng * 256);
-    F.ng = ng;
-
-    const int* meta = dptr<const int>(a.W.meta);
-    const int* uniq = dptr<const int>(a.W.uniq);
-    const int* gs = dptr<const int>(a.W.gs);
-    const int* perm = dptr<const int>(a.W.perm);
-    const int* slots = dptr<const int>(L.slot_table);
-    const float* x = dptr<const float>(a.x);
+    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6, lane = lane_id();
+    const int ng = H >> 5;
+    const int run = kTileRows * W;
+    const int chunks = (I + run - 1) / run;
+    const Item it = item_of(a, chunks);
+    if (!it.live) return;
     float* act = dptr<float>(a.W.act);
-    float* y = dptr<float>(a.W.y);
-
-    const int nu = meta[0];
-    const int tiles = (rows + kTileRows - 1) / kTileRows;
-    const int total = nu * tiles;
-    const int S = tile_steps(cols);
-    int staged0 = -2, staged1 = -2;
-
-    const int wpb = blockDim.x >> 6;
-    for (int item = blockIdx.x * wpb + wave; item < total; item += gridDim.x * wpb) {
-        const int u = item / tiles;
-        const int n0 = (item - u * tiles) * kTileRows;
-        const int e = uniq[u];
-        const int slot = slots[e];
-        const int p0 = gs[e], p1 = gs[e + 1];
-        const int row = n0 + (lane & 15);
-        if (slot < 0) {
-            if (lane == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
-            for (int p = p0; p < p1; ++p) {
-                float* out = phase == 0 ? act + (size_t)p * I : y + (size_t)p * H;
-                if (lane < 16 && row < rows) out[row] = 0.0f;
+    if (it.slot < 0) {
+        missing_expert(a, it, act, I, I, it.chunk * run, it.chunk * run + run);
+        return;
+    }
+    const uint64_t blob = L.arena_base + (uint64_t)it.slot * L.slot_span;
+    const uint64_t rg = blob + L.gate_off, ru = blob + L.up_off;
+    const int rs = ilog2_pow2(L.group >> 5);
+    const int S = tile_steps(H);
+    const int n0 = it.chunk * run + kTileRows * wave;
+    const int row = n0 + (lane & 15);
+    const int cap = min(PMAX, a.pairs_cap);
+    const Frags F = frags_at(lds, ng, cap);
+    const bool one = S <= NS;
+    WRegs<NS> G, U;
+    if (one) {
+        wload(G, rg, I, H, rs, n0, 0);
+        wload(U, ru, I, H, rs, n0, 0);
+    }
+    const int* perm = dptr<const int>(a.W.perm);
+    const float* x = dptr<const float>(a.x);
+    for (int tb = 0; tb < it.ntok; tb += 2 * cap) {
+        const int nt = min(2 * cap, it.ntok - tb);
+        const int pairs = (nt + 1) >> 1;
+        if (tb > 0) __syncthreads();
+        stage_rows(F, nt, [&](int t) { return x + (size_t)(perm[it.p0 + tb + t] / k) * H; },
+                   threadIdx.x, blockDim.x);
+        __syncthreads();
+        float ag[PMAX][2], au[PMAX][2];
+#pragma unroll
+        for (int p = 0; p < PMAX; ++p) ag[p][0] = ag[p][1] = au[p][0] = au[p][1] = 0.0f;
+        for (int c0 = 0; c0 < S; c0 += NS) {
+            if (!one) {
+                wload(G, rg, I, H, rs, n0, c0);
+                wload(U, ru, I, H, rs, n0, c0);
             }
-            continue;
+            wmma(G, F, H, c0, pairs, ag);
+            wmma(U, F, H, c0, pairs, au);
         }
-        const uint8_t* blob = dptr<const uint8_t>(L.arena_base + (uint64_t)slot * L.slot_span);
-        for (int q0 = p0; q0 < p1; q0 += 2) {
-            const int q1 = q0 + 1 < p1 ? q0 + 1 : -1;
-            int key0, key1;
-            const float *x0, *x1;
-            if (phase == 0) {
-                key0 = perm[q0] / k;
-                key1 = q1 >= 0 ? perm[q1] / k : -1;
-                x0 = x + (size_t)key0 * H;
-                x1 = key1 >= 0 ? x + (size_t)key1 * H : nullptr;
-            } else {
-                key0 = q0;
-                key1 = q1;
-                x0 = act + (size_t)q0 * I;
-                x1 = q1 >= 0 ? act + (size_t)q1 * I : nullptr;
-            }
-            if (key0 != staged0 || key1 != staged1) {
-                wave_sync_lds();
-                stage_frags(F, x0, x1);
-                wave_sync_lds();
-                staged0 = key0;
-                staged1 = key1;
-            }
-            if (phase == 0) {
-                const uint8_t* rg = blob + L.gate_off;
-                const uint8_t* ru = blob + L.up_off;
-                float g0 = 0.0f, g1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
-                TileRegs<8> GA, UA, GB, UB;
-                tile_load(GA, rg, I, H, L.group, n0, 0);
-                tile_load(UA, ru, I, H, L.group, n0, 0);
-                for (int c0 = 0; c0 < S; c0 += 16) {
-                    if (c0 + 8 < S) {
-                        tile_load(GB, rg, I, H, L.group, n0, c0 + 8);
-                        tile_load(UB, ru, I, H, L.group, n0, c0 + 8);
-                    }
-                    tile_mma(GA, F, H, c0, g0, g1);
-                    tile_mma(UA, F, H, c0, u0, u1);
-                    if (c0 + 16 < S) {
-                        tile_load(GA, rg, I, H, L.group, n0, c0 + 16);
-                        tile_load(UA, ru, I, H, L.group, n0, c0 + 16);
-                    }
-                    if (c0 + 8 < S) {
-                        tile_mma(GB, F, H, c0 + 8, g0, g1);
-                        tile_mma(UB, F, H, c0 + 8, u0, u1);
-                    }
-                }
-                g0 = tile_reduce(g0);
-                g1 = tile_reduce(g1);
-                u0 = tile_reduce(u0);
-                u1 = tile_reduce(u1);
-                if (row < I) {
-                    if (lane < 16) act[(size_t)q0 * I + row] = g0 / (1.0f + expf(-g0)) * u0;
-                    else if (lane < 32 && q1 >= 0) act[(size_t)q1 * I + row] = g1 / (1.0f + expf(-g1)) * u1;
-                }
-            } else {
-                const uint8_t* rd = blob + L.down_off;
-                float y0 = 0.0f, y1 = 0.0f;
-                TileRegs<8> DA, DB;
-                tile_load(DA, rd, H, I, L.group, n0, 0);
-                for (int c0 = 0; c0 < S; c0 += 16) {
-                    if (c0 + 8 < S) tile_load(DB, rd, H, I, L.group, n0, c0 + 8);
-                    tile_mma(DA, F, I, c0, y0, y1);
-                    if (c0 + 16 < S) tile_load(DA, rd, H, I, L.group, n0, c0 + 16);
-                    if (c0 + 8 < S) tile_mma(DB, F, I, c0 + 8, y0, y1);
-                }
-                y0 = tile_reduce(y0);
-                y1 = tile_reduce(y1);
-                if (row < H) {
-                    if (lane < 16) y[(size_t)q0 * H + row] = y0;
-                    else if (lane < 32 && q1 >= 0) y[(size_t)q1 * H + row] = y1;
+#pragma unroll
+        for (int p = 0; p < PMAX; ++p) {
+            if (p < pairs) {
+                const float g0 = tile_reduce(ag[p][0]), g1 = tile_reduce(ag[p][1]);
+                const float u0 = tile_reduce(au[p][0]), u1 = tile_reduce(au[p][1]);
+                const int t = tb + 2 * p + (lane >> 4);
+                if (row < I && lane < 32 && t < it.ntok) {
+                    const float g = lane < 16 ? g0 : g1;
+                    const float u = lane < 16 ? u0 : u1;
+                    act[(size_t)(it.p0 + t) * I + row] = g / (1.0f + expf(-g)) * u;
                 }
             }
         }
     }
+}
+
+template <int NS, int TW, int PMAX>
+__device__ __forceinline__ void down_body(const GroupedArgs& a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LayerView& L = a.L;
+    const int H = L.hidden, I = L.inter;
+    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6, lane = lane_id();
+    const int ng = I >> 5;
+    const int run = kTileRows * W * TW;
+    const int chunks = (H + run - 1) / run;
+    const Item it = item_of(a, chunks);
+    if (!it.live) return;
+    float* y = dptr<float>(a.W.y);
+    if (it.slot < 0) {
+        missing_expert(a, it, y, H, H, it.chunk * run, it.chunk * run + run);
+        return;
+    }
+    const uint64_t rd = L.arena_base + (uint64_t)it.slot * L.slot_span + L.down_off;
+    const int rs = ilog2_pow2(L.group >> 5);
+    const int S = tile_steps(I);
+    const int cap = min(PMAX, a.pairs_cap);
+    const Frags F = frags_at(lds, ng, cap);
+    const bool one = S <= NS;
+    WRegs<NS> D[TW];
+    int n0[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        n0[t] = it.chunk * run + kTileRows * (wave + W * t);
+        if (one) wload(D[t], rd, H, I, rs, n0[t], 0);
+    }
+    const float* act = dptr<const float>(a.W.act);
+    for (int tb = 0; tb < it.ntok; tb += 2 * cap) {
+        const int nt = min(2 * cap, it.ntok - tb);
+        const int pairs = (nt + 1) >> 1;
+        if (tb > 0) __syncthreads();
+        stage_rows(F, nt, [&](int t) { return act + (size_t)(it.p0 + tb + t) * I; },
+                   threadIdx.x, blockDim.x);
+        __syncthreads();
+#pragma unroll
+        for (int tw = 0; tw < TW; ++tw) {
+            float acc[PMAX][2];
+#pragma unroll
+            for (int p = 0; p < PMAX; ++p) acc[p][0] = acc[p][1] = 0.0f;
+            for (int c0 = 0; c0 < S; c0 += NS) {
+                if (!one) wload(D[tw], rd, H, I, rs, n0[tw], c0);
+                wmma(D[tw], F, I, c0, pairs, acc);
+            }
+            const int row = n0[tw] + (lane & 15);
+#pragma unroll
+            for (int p = 0; p < PMAX; ++p) {
+                if (p < pairs) {
+                    const float v0 = tile_reduce(acc[p][0]), v1 = tile_reduce(acc[p][1]);
+                    const int t = tb + 2 * p + (lane >> 4);
+                    if (row < H && lane < 32 && t < it.ntok)
+                        y[(size_t)(it.p0 + t) * H + row] = lane < 16 ? v0 : v1;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_gateup(const GroupedArgs a) {
+    gateup_body<16, kMaxPairs>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_down(const GroupedArgs a) {
+    down_body<8, 2, kMaxPairs>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_down_wide(const GroupedArgs a) {
+    down_body<16, 1, kMaxPairs>(a);
 }
 
 // ---------------------------------------------------------------------------

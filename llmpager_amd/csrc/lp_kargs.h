@@ -14,6 +14,8 @@ constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
+constexpr int kFragBytesPerSubgroup = 4 * 4 * 16 + 16;  // LDS per token pair per 32 columns
+constexpr int kMaxPairs = 4;           // token pairs the grouped kernels stage at once
 
 // ---- 1:1 launchers (crates/llmpager-cuda/src/kernels.rs) -------------------
 
@@ -93,9 +95,7 @@ struct GroupedArgs {
     uint64_t x;          // f32 [T, H] (gate/up phase input)
     uint64_t h;          // f32 [T, H] residual (combine)
     int32_t T;
-    int32_t phase;       // 0 gate/up/silu, 1 down
-    int32_t lds_per_wave;  // bytes of dynamic LDS per wave
-    int32_t pad0;
+    int32_t pairs_cap;   // token pairs the dynamic LDS holds at once
 };
 
 // Error flags written into Workspace.meta[1].

@@ -11,7 +11,9 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/llmpager_hip.h"
 #include "lp_expf.h"
@@ -49,7 +51,9 @@ enum Fn {
     kRouter,
     kTopk,
     kDispatch,
-    kGrouped,
+    kGateup,
+    kDown,
+    kDownWide,
     kCombine,
     kNumFns
 };
@@ -64,7 +68,8 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_basic.hsaco", "lp_moe_reduce"},   {"lp_basic.hsaco", "lp_silu_mul"},
     {"lp_basic.hsaco", "lp_bf16_gemv"},    {"lp_basic.hsaco", "lp_add"},
     {"lp_moe.hsaco", "lp_moe_router"},     {"lp_moe.hsaco", "lp_moe_topk"},
-    {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_grouped"},
+    {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_gateup"},
+    {"lp_moe.hsaco", "lp_moe_down"},       {"lp_moe.hsaco", "lp_moe_down_wide"},
     {"lp_moe.hsaco", "lp_moe_combine"},
 };
 
@@ -91,21 +96,71 @@ unsigned grid_1d(int n) {
 
 }  // namespace
 
+struct ProfRec {
+    int fn;
+    hipEvent_t start, end;
+};
+
 struct lp_ctx {
     int device = 0;
     int cus = 0;
     size_t max_lds = 0;
     hipModule_t modules[kNumModules] = {};
     hipFunction_t fns[kNumFns] = {};
+    // measurement (lp_profile_*)
+    bool prof = false;
+    std::mutex prof_mu;
+    std::vector<ProfRec> prof_recs;
+    std::vector<hipEvent_t> prof_pool;
+    double prof_ms[kNumFns] = {};
+    int64_t prof_n[kNumFns] = {};
 };
 
 namespace {
 
+hipEvent_t prof_event(lp_ctx* c) {
+    if (!c->prof_pool.empty()) {
+        hipEvent_t e = c->prof_pool.back();
+        c->prof_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Fold completed records into the per-kernel sums (caller holds prof_mu and
+// has synchronised the device).
+void prof_drain(lp_ctx* c) {
+    for (const ProfRec& r : c->prof_recs) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.start, r.end) == hipSuccess) {
+            c->prof_ms[r.fn] += ms;
+            c->prof_n[r.fn] += 1;
+        }
+        c->prof_pool.push_back(r.start);
+        c->prof_pool.push_back(r.end);
+    }
+    c->prof_recs.clear();
+}
+
 template <typename A>
 int launch(lp_ctx* c, Fn f, dim3 grid, dim3 block, size_t lds, lp_stream s, const A& args) {
     void* params[] = {const_cast<A*>(&args)};
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (c->prof) {
+        std::lock_guard<std::mutex> g(c->prof_mu);
+        e0 = prof_event(c);
+        e1 = prof_event(c);
+        if (e0) (void)hipEventRecord(e0, (hipStream_t)s);
+    }
     hipError_t e = hipModuleLaunchKernel(c->fns[f], grid.x, grid.y, grid.z, block.x, block.y,
                                          block.z, (unsigned)lds, (hipStream_t)s, params, nullptr);
+    if (c->prof && e0 && e1) {
+        std::lock_guard<std::mutex> g(c->prof_mu);
+        (void)hipEventRecord(e1, (hipStream_t)s);
+        c->prof_recs.push_back(ProfRec{(int)f, e0, e1});
+    }
     if (e != hipSuccess) return hip_fail(e, kSpecs[f].name);
     return LP_OK;
 }
@@ -169,6 +224,11 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
 
 void lp_destroy(lp_ctx* c) {
     if (!c) return;
+    for (const ProfRec& r : c->prof_recs) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.end);
+    }
+    for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
     for (int m = 0; m < kNumModules; ++m)
         if (c->modules[m]) (void)hipModuleUnload(c->modules[m]);
     delete c;
@@ -334,19 +394,18 @@ static int q4_gemv_common(lp_ctx* c, uint64_t blobs, uint64_t region_off, uint64
     a.cols = cols;
     a.group = group;
     a.experts = experts;
-    // The MFMA tile needs 32-column sub-groups under one scale, 16-byte
-    // aligned nibble rows and x, and its per-wave fragment area in LDS.
-    const int ng = cols / 32;
-    const size_t frag = (size_t)ng * 272;
-    // (blob bases come from 4096-aligned slot arenas, so only the offset matters)
+    // The MFMA tile needs 32-column sub-groups (a power-of-two number of them
+    // under one scale), 16-byte aligned nibble rows and x, and one LDS
+    // fragment pair.
     const uint64_t data_off = region_off + (uint64_t)rows * (cols / group) * 2;
     const bool aligned = (data_off % 16 == 0) && (x % 16 == 0) && ((uint64_t)x_stride * 4 % 16 == 0);
-    int waves = 4;
-    while (waves > 1 && frag * waves > c->max_lds) --waves;
-    if (group % 32 == 0 && aligned && frag <= c->max_lds) {
+    const bool pow2 = group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0;
+    const size_t frag = (size_t)(cols / 32) * kFragBytesPerSubgroup;
+    if (pow2 && aligned && frag <= c->max_lds) {
         const int tiles = (rows + kTileRows - 1) / kTileRows;
+        const int waves = std::min(4, tiles);
         const unsigned gx = (unsigned)((tiles + waves - 1) / waves);
-        return launch(c, kQ4Mfma, dim3(gx, experts), dim3(64 * waves), frag * waves, s, a);
+        return launch(c, kQ4Mfma, dim3(gx, experts), dim3(64 * waves), frag, s, a);
     }
     return launch(c, kQ4Valu, dim3((rows + 3) / 4, experts), dim3(256), 0, s, a);
 }
@@ -519,19 +578,38 @@ int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
     ga.x = x;
     ga.h = h;
     ga.T = T;
-    const int kmax = std::max(d->hidden, d->inter);
-    const size_t frag = (size_t)(kmax / 32) * 272;
-    int waves = 4;
-    while (waves > 1 && frag * waves > c->max_lds) --waves;
-    if (frag > c->max_lds) return fail(LP_E_UNSUPPORTED, "hidden too large for the LDS fragment area");
-    ga.lds_per_wave = (int)frag;
+    const int H = d->hidden, I = d->inter;
     const int maxu = std::min(T * d->top_k, d->experts);
-    for (int phase = 0; phase < 2; ++phase) {
-        ga.phase = phase;
-        const int rows = phase == 0 ? d->inter : d->hidden;
-        const int items = maxu * ((rows + kTileRows - 1) / kTileRows);
-        const int wgs = std::max(1, std::min((items + waves - 1) / waves, 2 * c->cus));
-        if (int r = launch(c, kGrouped, dim3((unsigned)wgs), dim3(64 * waves), frag * waves, s, ga))
+    // Token pairs staged at once: enough for T tokens on one expert, bounded
+    // by kMaxPairs and by the LDS the fragments need.
+    const size_t fr_h = (size_t)(H / 32) * kFragBytesPerSubgroup;
+    const size_t fr_i = (size_t)(I / 32) * kFragBytesPerSubgroup;
+    int cap = std::min(kMaxPairs, (T + 1) / 2);
+    while (cap > 1 && (size_t)cap * std::max(fr_h, fr_i) > c->max_lds) --cap;
+    if (fr_h > c->max_lds || fr_i > c->max_lds)
+        return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
+    ga.pairs_cap = cap;
+    // Workgroup width: the widest (more rows per staged fragment set) that
+    // still yields about two work items per CU.
+    auto pick_w = [&](int rows, int tw) {
+        for (int w = 4; w > 1; w >>= 1)
+            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= 2L * c->cus)
+                return w;
+        return 1;
+    };
+    {
+        const int w = pick_w(I, 1);
+        const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
+        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w), cap * fr_h, s, ga))
+            return r;
+    }
+    {
+        const int steps = ((I / 32) + 3) / 4;
+        const Fn f = steps <= 8 ? kDown : kDownWide;
+        const int tw = steps <= 8 ? 2 : 1;
+        const int w = pick_w(H, tw);
+        const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
+        if (int r = launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), cap * fr_i, s, ga))
             return r;
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
@@ -558,6 +636,49 @@ int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T
     return LP_OK;
 }
 
+int lp_profile_enable(lp_ctx* c, int enable) {
+    if (int r = check_ctx(c)) return r;
+    c->prof = enable != 0;
+    return LP_OK;
+}
+
+int lp_profile_reset(lp_ctx* c) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> g(c->prof_mu);
+    prof_drain(c);
+    for (int f = 0; f < kNumFns; ++f) {
+        c->prof_ms[f] = 0.0;
+        c->prof_n[f] = 0;
+    }
+    return LP_OK;
+}
+
+int lp_profile_read_sync(lp_ctx* c, const char* kernel, double* total_ms, int64_t* launches) {
+    if (int r = check_ctx(c)) return r;
+    if (!kernel) return fail(LP_E_INVALID, "null kernel name");
+    HIPCHK(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> g(c->prof_mu);
+    prof_drain(c);
+    for (int f = 0; f < kNumFns; ++f) {
+        if (strcmp(kSpecs[f].name, kernel) == 0) {
+            if (total_ms) *total_ms = c->prof_ms[f];
+            if (launches) *launches = c->prof_n[f];
+            return LP_OK;
+        }
+    }
+    return fail(LP_E_INVALID, std::string("unknown kernel ") + kernel);
+}
+
 float lp_route_expf(float x) { return lp::expf_glibc(x); }
+
+void lp_route_expf_sweep(uint32_t first, uint32_t stride, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t b = first + (uint32_t)(i * stride);
+        float f;
+        memcpy(&f, &b, 4);
+        out[i] = lp::expf_glibc(f);
+    }
+}
 
 }  // extern "C"

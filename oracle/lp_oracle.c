@@ -93,6 +93,10 @@ float lpo_bf16_to_f32(uint16_t h) { return u2f(((uint32_t)h) << 16); }
 
 float lpo_expf(float x) { return expf(x); }
 
+void lpo_expf_sweep(uint32_t first, uint32_t stride, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = expf(u2f(first + (uint32_t)(i * stride)));
+}
+
 /* Rust's f32 `Iterator::sum` folds from -0.0 (rustc >= 1.81); starting there
  * only changes the sign of an all-zero sum. */
 #define RUST_SUM_INIT (-0.0f)

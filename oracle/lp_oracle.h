@@ -38,6 +38,9 @@ float lpo_bf16_to_f32(uint16_t h);
 
 /* libm expf: what Rust's f32::exp lowers to on the reference host (glibc). */
 float lpo_expf(float x);
+/* out[i] = expf(bits_to_float(first + i*stride)) for i < n: the checker for
+ * exhaustive / strided sweeps over float bit patterns. */
+void lpo_expf_sweep(uint32_t first, uint32_t stride, size_t n, float* out);
 
 /* ---- q4 group-wise format (quant.rs) ----------------------------------- */
 

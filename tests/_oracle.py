@@ -44,6 +44,7 @@ def lib():
             "lpo_bf16_rne": (C.c_uint16, [f32]),
             "lpo_bf16_to_f32": (f32, [C.c_uint16]),
             "lpo_expf": (f32, [f32]),
+            "lpo_expf_sweep": (None, [C.c_uint32, C.c_uint32, sz, vp]),
             "lpo_q4_bytes": (sz, [sz, sz, sz]),
             "lpo_q4_quantize": (i32, [vp, sz, sz, sz, vp, sz, C.POINTER(f32)]),
             "lpo_q4_store_group": (None, [vp, sz, sz, sz, sz, sz, f32, vp]),
@@ -82,6 +83,12 @@ def f16_to_f32(h: int) -> float:
 
 def expf(x: float) -> float:
     return lib().lpo_expf(x)
+
+
+def expf_sweep(first: int, stride: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    lib().lpo_expf_sweep(first, stride, n, out.ctypes.data)
+    return out
 
 
 def q4_bytes(rows, cols, group):

@@ -90,7 +90,7 @@ def test_layer_sigmoid_gating(cuda):
     bias = (rng.standard_normal(64) * 0.05).astype(np.float32)
     L = DeviceLayer(cuda, H=2048, I=1408, E=64, k=6, group=32, seed=3,
                     gating=lp.GATING_SIGMOID, renorm=True, routed_scaling=2.5,
-                    min_weight=0.3, bias=bias, router_std=0.05)
+                    min_weight=0.41, bias=bias, router_std=0.05)
     T = 16
     x, h, g = _run_layer(cuda, L, T, seed=9)
     _check_layer(L, x, h, g, T)
@@ -128,11 +128,11 @@ def _adversarial_logits(E: int, rng) -> np.ndarray:
     base = rng.standard_normal(E).astype(np.float32)
     rows.append(np.zeros(E, np.float32))                       # all equal
     rows.append(np.full(E, 3.5, np.float32))
-    t = base.copy(); t[[5, 9, 17]] = t.max() + 1.0; rows.append(t)   # exact ties at the top
+    t = base.copy(); t[[5 % E, 9 % E, 17 % E]] = t.max() + 1.0; rows.append(t)  # exact ties at the top
     t = base.copy()                                            # neighbours one ulp apart
     top = np.float32(2.0)
-    for j, e in enumerate([3, 4, 5, 6, 7, 8, 9, 10, 11, 12]):
-        t[e] = np.nextafter(top, np.float32(-10), dtype=np.float32) if j % 2 else top
+    for j in range(min(10, E)):
+        t[(3 + j) % E] = np.nextafter(top, np.float32(-10), dtype=np.float32) if j % 2 else top
         top = np.nextafter(top, np.float32(-10), dtype=np.float32) if j % 3 == 2 else top
     rows.append(t)
     rows.append((base * 1e4).astype(np.float32))              # large magnitude
