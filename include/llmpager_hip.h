@@ -153,6 +153,7 @@ typedef struct lp_moe_ws_layout {
     uint64_t inv;     /* i32 [T*k] dispatch position per pick, -1 if unused */
     uint64_t uniq;    /* i32 [E] experts with picks, ascending */
     uint64_t meta;    /* i32 [16]: [0] unique count, [1] error flags */
+    uint64_t et;      /* 32-byte expert entries [E] for the grouped kernels */
     uint64_t act;     /* f32 [T*k, I] */
     uint64_t y;       /* f32 [T*k, H] */
     uint64_t total;   /* bytes */

@@ -54,7 +54,8 @@ class WsLayout(C.Structure):
     """lp_moe_ws_layout: byte offsets of the workspace parts."""
 
     _fields_ = [(n, C.c_uint64) for n in (
-        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "act", "y", "total")]
+        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y",
+        "total")]
 
 
 def _sig(lib):

@@ -13,35 +13,50 @@ using namespace lpk;
 // MFMA path: grid (workgroups per expert, experts); the workgroup stages x_e
 // once into an LDS fragment pair, then each wave walks 16-row tiles.
 // Requires group = 32 * 2^r, 16-byte aligned nibble rows and x (host checks).
-// Dynamic LDS: frag_pair_bytes(cols / 32).
+// Dynamic LDS: lpk::frag_lds_bytes(cols, 1).
 // ---------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(256) lp_q4_gemv_mfma(const Q4GemvBatchArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
+template <int RS>
+__device__ __forceinline__ void q4_gemv_tiles(const Q4GemvBatchArgs& a, const Frags& F, uint64_t region,
+                                              float* y) {
     const int wave = threadIdx.x >> 6;
     const int wpb = blockDim.x >> 6;
     const int lane = lane_id();
+    const int tiles = (a.rows + kTileRows - 1) / kTileRows;
+    const int S = tile_steps(a.cols);
+    for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
+        const int n0 = tile * kTileRows;
+        const WTile<RS> T = wtile<RS>(region, a.rows, a.cols, n0);
+        float acc[1][1][2] = {{{0.0f, 0.0f}}};
+        WRegs<kStepChunk> R[1];
+        wload(R[0], T, 0);
+#pragma nounroll
+        for (int c0 = 0;;) {
+            const ABase B[1] = {abase(F, 0, c0)};
+            wmma(R, B, F.lds, S - c0, acc);
+            c0 += kStepChunk;
+            if (c0 >= S) break;
+            wload(R[0], T, c0);
+        }
+        const float v = tile_reduce(acc[0][0][0]);
+        const int row = n0 + (lane & 15);
+        if (lane < 16 && row < a.rows) y[row] = v;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) lp_q4_gemv_mfma(const Q4GemvBatchArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
     const int e = blockIdx.y;
-    const int ng = a.cols >> 5;
     const uint64_t region = a.blobs ? gptr<uint64_t>(a.blobs)[e] + a.region_off : a.region_off;
     const float* x = reinterpret_cast<const float*>(a.x) + (size_t)e * a.x_stride;
     float* y = reinterpret_cast<float*>(a.y) + (size_t)e * a.rows;
-    const Frags F = frags_at(lds, ng, 1);
+    const Frags F = frags_at(lds, a.cols);
+    zero_block(F, threadIdx.x, blockDim.x);
     stage_rows(F, 1, [&](int) { return x; }, threadIdx.x, blockDim.x);
     __syncthreads();
-    const int tiles = (a.rows + kTileRows - 1) / kTileRows;
-    const int S = tile_steps(a.cols);
-    const int rs = ilog2_pow2(a.group >> 5);
-    for (int tile = blockIdx.x * wpb + wave; tile < tiles; tile += gridDim.x * wpb) {
-        const int n0 = tile * kTileRows;
-        float acc[1][2] = {{0.0f, 0.0f}};
-        WRegs<16> R;
-        for (int c0 = 0; c0 < S; c0 += 16) {
-            wload(R, region, a.rows, a.cols, rs, n0, c0);
-            wmma(R, F, a.cols, c0, 1, acc);
-        }
-        const float v = tile_reduce(acc[0][0]);
-        const int row = n0 + (lane & 15);
-        if (lane < 16 && row < a.rows) y[row] = v;
+    switch (ilog2_pow2(a.group >> 5)) {
+        case 0: q4_gemv_tiles<0>(a, F, region, y); break;
+        case 1: q4_gemv_tiles<1>(a, F, region, y); break;
+        default: q4_gemv_tiles<2>(a, F, region, y); break;
     }
 }
 

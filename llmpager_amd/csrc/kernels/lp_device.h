@@ -47,12 +47,18 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // last place is 1, so OR-ing a nibble into the low mantissa bits adds it
 // exactly.  Element i = 2v + h of the result holds value p = v + 4h, so the
 // activation fragment must be laid out in the same order (see frag_col).
+// v_bitop3_b32 computes (b & mask) | magic in one instruction (truth table
+// 0xEA = (S0 & S1) | S2).
+__device__ __forceinline__ uint32_t and_or(uint32_t b, uint32_t m, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(b, m, c, 0xEA);
+}
+
 __device__ __forceinline__ bf16x8_t q4_word_to_bf16x8(uint32_t b) {
     u32x4_t t;
-    t[0] = (b & 0x000F000Fu) | 0x43004300u;
-    t[1] = ((b >> 4) & 0x000F000Fu) | 0x43004300u;
-    t[2] = ((b >> 8) & 0x000F000Fu) | 0x43004300u;
-    t[3] = ((b >> 12) & 0x000F000Fu) | 0x43004300u;
+    t[0] = and_or(b, 0x000F000Fu, 0x43004300u);
+    t[1] = and_or(b >> 4, 0x000F000Fu, 0x43004300u);
+    t[2] = and_or(b >> 8, 0x000F000Fu, 0x43004300u);
+    t[3] = and_or(b >> 12, 0x000F000Fu, 0x43004300u);
     return __builtin_bit_cast(bf16x8_t, t);
 }
 
@@ -62,6 +68,10 @@ __device__ __forceinline__ int frag_col(int d, int i) { return 8 * d + (i >> 1) 
 // Global-address-space views: loads through these compile to global_load_*
 // (tracked by vmcnt only), not flat_load_*, so many can be in flight at once.
 #define LP_GLOBAL __attribute__((address_space(1)))
+
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family parts: 32-bit
+// data format, no swizzle; out-of-range loads return zero.
+constexpr int kBufferWord3 = 0x00020000;
 
 template <typename T>
 __device__ __forceinline__ const LP_GLOBAL T* gptr(uint64_t a) {
@@ -76,7 +86,7 @@ __device__ __forceinline__ LP_GLOBAL T* gptr_w(uint64_t a) {
 // ---------------------------------------------------------------------------
 // The grouped q4 tile.
 //
-// One wave computes, for a 16-row tile of a q4 region [rows, cols] and for
+// One wave computes, for a 16-row tile of a q4 region [rows, cols] and for P
 // pairs of tokens, y[t][row] = sum_g s[row, g >> rs] * sum_{c in sub-group g}
 // (q[row, c] - 8) * x[t][c] in fp32.  Sub-groups are 32 columns; one f16
 // scale covers 2^rs sub-groups (rs = log2(group / 32)).
@@ -88,7 +98,8 @@ __device__ __forceinline__ LP_GLOBAL T* gptr_w(uint64_t a) {
 //   A (activations): row m = 4*slot + th, th = 2*token + part, part 0 =
 //     bf16(x), part 1 = bf16(x - bf16(x)).  Element (m, k = 8*kbA + i) is
 //     non-zero only when slot == kbA, so the 16 MFMA output rows keep four
-//     sub-groups x four (token, part) apart.
+//     sub-groups x four (token, part) apart.  Lanes whose slot is not their
+//     kb read a zero block, so every LDS read is unconditional.
 //   C: lane l holds C[4*(l/16) + i][l % 16]: its own sub-group (slot = kb),
 //     th = i.  With n = q + 8 the stored nibble, the weight operand is
 //     128 + n, so sum_k (128 + n_k) x_k = sum_k (n_k - 8) x_k + 136 sum_k x_k;
@@ -96,41 +107,54 @@ __device__ __forceinline__ LP_GLOBAL T* gptr_w(uint64_t a) {
 // Products of bf16 values are exact in fp32 and x = part0 + part1 to 16
 // significant bits, so the only roundings are the fp32 accumulations.
 //
-// Activation fragments live in LDS, per token pair p:
-//   frag[p][th][g][d] : uint4 (8 bf16 in element order i), th 0..3
+// LDS (see lpk::frag_lds_bytes): zero block, then per token pair p
+//   frag[p][th][g][d] : uint4 (8 bf16 in element order i), g < ngp
 //   off [p][g][th]    : float, -136 * sum of the th part over sub-group g
 // ---------------------------------------------------------------------------
 
 struct Frags {
-    uint4* frag;   // [pairs][4][ng][4]
-    float* off;    // [pairs][ng][4]
-    int ng;        // sub-groups (cols / 32)
+    uint8_t* lds;  // start of the fragment area (zero block first)
+    int ng;        // sub-groups with data (cols / 32)
+    int ngp;       // padded sub-groups (multiple of 4)
 };
 
-__device__ __forceinline__ size_t frag_pair_bytes(int ng) { return (size_t)ng * lpk::kFragBytesPerSubgroup; }
-
-__device__ __forceinline__ Frags frags_at(uint8_t* base, int ng, int pairs) {
+__device__ __forceinline__ Frags frags_at(uint8_t* lds, int cols) {
     Frags F;
-    F.frag = reinterpret_cast<uint4*>(base);
-    F.off = reinterpret_cast<float*>(base + (size_t)pairs * ng * 256);
-    F.ng = ng;
+    F.lds = lds;
+    F.ng = cols >> 5;
+    F.ngp = lpk::frag_ngp(cols);
     return F;
+}
+
+__device__ __forceinline__ uint8_t* frag_ptr(const Frags& F, int p, int th, int g) {
+    return F.lds + lpk::kZeroBytes + p * lpk::frag_pair_bytes(F.ngp) + th * lpk::frag_th_stride(F.ngp) + g * 64;
+}
+
+__device__ __forceinline__ float* off_ptr(const Frags& F, int p, int g) {
+    return reinterpret_cast<float*>(F.lds + lpk::kZeroBytes + p * lpk::frag_pair_bytes(F.ngp) +
+                                    4 * lpk::frag_th_stride(F.ngp) + g * 16);
+}
+
+// Zero the idle-lane block (once per workgroup, before the first barrier).
+__device__ __forceinline__ void zero_block(const Frags& F, int tid, int nthreads) {
+    for (int i = tid; i < lpk::kZeroBytes / 16; i += nthreads)
+        reinterpret_cast<uint4*>(F.lds)[i] = make_uint4(0, 0, 0, 0);
 }
 
 // Stage ntok activation rows into fragment pairs 0 .. ceil(ntok/2)-1.
 // row_of(t) returns the f32 row of token t.  Work units (token, sub-group)
-// are spread over the `nthreads` participating threads (tid < nthreads); a
-// missing second token of the last pair is written as zeros.
+// are spread over the `nthreads` participating threads; a missing second
+// token of the last pair and the padding sub-groups are written as zeros.
 template <typename RowOf>
 __device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int tid, int nthreads) {
-    const int units = ((ntok + 1) & ~1) * F.ng;
+    const int units = ((ntok + 1) & ~1) * F.ngp;
     for (int u = tid; u < units; u += nthreads) {
-        const int t = u / F.ng;
-        const int g = u - t * F.ng;
+        const int t = u / F.ngp;
+        const int g = u - t * F.ngp;
         const int pair = t >> 1, tk = t & 1;
+        const bool live = t < ntok && g < F.ng;
         const LP_GLOBAL float4* p =
-            t < ntok ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr;
-        uint4* fr = F.frag + (size_t)pair * 4 * F.ng * 4;
+            live ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr;
         float shi = 0.0f, slo = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -153,14 +177,14 @@ __device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int ti
                 shi += bf16_to_f32(hi[q]);
                 slo += bf16_to_f32(lo[q]);
             }
-            const uint4 a = make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16),
-                                       hi[2] | (hi[6] << 16), hi[3] | (hi[7] << 16));
-            const uint4 b = make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16),
-                                       lo[2] | (lo[6] << 16), lo[3] | (lo[7] << 16));
-            fr[((size_t)(2 * tk + 0) * F.ng + g) * 4 + d] = a;
-            fr[((size_t)(2 * tk + 1) * F.ng + g) * 4 + d] = b;
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 0, g) + d * 16) =
+                make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
+                           hi[3] | (hi[7] << 16));
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 1, g) + d * 16) =
+                make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
+                           lo[3] | (lo[7] << 16));
         }
-        float* of = F.off + ((size_t)pair * F.ng + g) * 4;
+        float* of = off_ptr(F, pair, g);
         of[2 * tk + 0] = -136.0f * shi;
         of[2 * tk + 1] = -136.0f * slo;
     }
@@ -168,85 +192,135 @@ __device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int ti
 
 __device__ __forceinline__ int tile_steps(int cols) { return ((cols >> 5) + 3) >> 2; }
 
-// Raw weight registers for steps [c0, c0 + NS) of one 16-row tile.
+// One 16-row tile of a q4 region [rows, cols] (scales then nibbles, the blob
+// layout), read through a raw buffer resource that covers exactly the
+// region: loads past its end return zeros instead of faulting, so no lane
+// ever needs a clamped address.  Lane (n, kb) owns row n0 + n and, at step c,
+// sub-group 4c + kb (64 contiguous bytes per row and step over the four kb
+// lanes).  One f16 scale covers 2^RS sub-groups (group = 32 << RS, RS <= 2).
+template <int RS>
+struct WTile {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t dofs;  // lane's nibble byte offset at step 0
+    uint32_t sofs;  // lane's scale byte offset at step 0
+    int last;       // steps c with 4c + kb < cols / 32
+    bool ok;        // row inside the matrix
+};
+
+template <int RS>
+__device__ __forceinline__ WTile<RS> wtile(uint64_t region, int rows, int cols, int n0) {
+    const int lane = lane_id();
+    const int n = lane & 15, kb = lane >> 4;
+    const uint32_t ng = (uint32_t)cols >> 5, gpr = ng >> RS;
+    const uint32_t sbytes = (uint32_t)rows * gpr * 2;
+    const uint32_t row = (uint32_t)(n0 + n);
+    WTile<RS> T;
+    T.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(region), (short)0,
+                                               (int)(sbytes + (uint32_t)rows * ng * 16), kBufferWord3);
+    T.dofs = sbytes + (row * ng + kb) * 16;
+    T.sofs = (row * gpr + (kb >> RS)) * 2;
+    T.last = ((int)ng - kb + 3) >> 2;
+    T.ok = (int)row < rows;
+    return T;
+}
+
+// Raw weight registers for steps [c0, c0 + NS) of one tile.
 template <int NS>
 struct WRegs {
     uint4 w[NS];
     uint32_t s[NS];  // f16 bits of the lane's sub-group scale
+    bool ok;         // row inside the matrix (scales of other rows count as 0)
+    int last;        // chunk steps >= last carry no data for this lane
 };
 
-// Issue the tile's loads: lane (n, kb) loads sub-group 4c + kb of row n0 + n.
-template <int NS>
-__device__ __forceinline__ void wload(WRegs<NS>& R, uint64_t region, int rows, int cols, int rs,
-                                      int n0, int c0) {
-    const int lane = lane_id();
-    const int n = lane & 15, kb = lane >> 4;
-    const int ng = cols >> 5;
-    const int row = n0 + n;
-    const int gpr = ng >> rs;
-    const bool rowok = row < rows;
-    const LP_GLOBAL uint4* data = gptr<uint4>(region + (uint64_t)rows * gpr * 2) +
-                                  (size_t)row * (cols >> 5);
-    const LP_GLOBAL uint16_t* sc = gptr<uint16_t>(region) + (size_t)row * gpr;
+// Issue the tile's loads for steps c0 .. c0 + NS - 1: one per-lane offset
+// plus an immediate per step (64 B of nibbles, 8 >> RS B of scales).  The
+// loads are unconditional, so the compiler keeps them together ahead of
+// their use.  Steps past the lane's last sub-group read whatever follows in
+// the region (or zeros past its end); wmma gives them a zero scale.
+template <int NS, int RS>
+__device__ __forceinline__ void wload(WRegs<NS>& R, const WTile<RS>& T, int c0) {
+    R.ok = T.ok;
+    R.last = T.last - c0;
+    const uint32_t d = T.dofs + 64u * (uint32_t)c0;
+    const uint32_t sc = T.sofs + (8u >> RS) * (uint32_t)c0;
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int g = 4 * (c0 + j) + kb;
-        if (rowok && g < ng) {
-            R.w[j] = data[g];
-            R.s[j] = sc[g >> rs];
-        } else {
-            R.w[j] = make_uint4(0, 0, 0, 0);
-            R.s[j] = 0u;
-        }
+        R.w[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(T.rsrc, (int)(d + 64u * j), 0, 0));
+        R.s[j] = __builtin_amdgcn_raw_buffer_load_b16(T.rsrc, (int)(sc + (8u >> RS) * j), 0, 0);
     }
 }
 
-// MFMAs for steps [c0, c0 + NS) against `pairs` staged token pairs
-// (pairs <= PMAX), accumulating acc[p][0..1] (tokens 2p, 2p+1) per lane.
-template <int NS, int PMAX>
-__device__ __forceinline__ void wmma(const WRegs<NS>& R, const Frags& F, int cols, int c0, int pairs,
-                                     float (&acc)[PMAX][2]) {
+// Per-lane LDS bases for the A operand and the accumulator seeds of pair p
+// at step chunk c0 (steps are 256 B apart in frag, 64 B apart in off).
+struct ABase {
+    const uint8_t* a;
+    const uint8_t* o;
+};
+
+__device__ __forceinline__ ABase abase(const Frags& F, int p, int c0) {
     const int lane = lane_id();
-    const int kb = lane >> 4;
-    const int m = lane & 15;
-    const int ng = cols >> 5;
-    const int S = tile_steps(cols);
-    const bool aact = (m >> 2) == kb;   // A lane (m, kb) is live when its slot m/4 == kb
-    const int th = m & 3;
+    const int kb = lane >> 4, m = lane & 15;
+    const bool live = (m >> 2) == kb;  // A lane (m, kb) is live when its slot m/4 == kb
+    ABase b;
+    b.a = live ? frag_ptr(F, p, m & 3, 4 * c0 + kb) : F.lds;
+    b.o = reinterpret_cast<const uint8_t*>(off_ptr(F, p, 4 * c0 + kb));
+    return b;
+}
+
+// MFMAs of one loaded chunk for M weight tiles that share the same staged
+// activations (gate and up of one expert, or several row tiles of one
+// matrix) against P token pairs: acc[m][p][0..1] += tokens 2p, 2p+1 of tile
+// m.  Every step reads the A fragments once for all M tiles, and the M
+// independent MFMA chains interleave.  Steps j >= rem (past the tile) read
+// the zero block and carry a zero scale, so the chunk is straight-line code.
+template <int NS, int P, int M>
+__device__ __forceinline__ void wmma(const WRegs<NS> (&R)[M], const ABase (&B)[P], const uint8_t* zero,
+                                     int rem, float (&acc)[M][P][2]) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int c = c0 + j;
-        if (c >= S) break;
-        const int g = 4 * c + kb;
-        const bool gok = g < ng;
-        const int gs = gok ? g : 0;
-        const float s = f16_bits_to_f32(R.s[j]);
-        bf16x8_t bv[4];
-        bv[0] = q4_word_to_bf16x8(R.w[j].x);
-        bv[1] = q4_word_to_bf16x8(R.w[j].y);
-        bv[2] = q4_word_to_bf16x8(R.w[j].z);
-        bv[3] = q4_word_to_bf16x8(R.w[j].w);
+        const bool in = j < rem;  // uniform
+        float s[M];
+        bf16x8_t bv[M][4];
 #pragma unroll
-        for (int p = 0; p < PMAX; ++p) {
-            if (p < pairs) {
-                const float4 o = *reinterpret_cast<const float4*>(F.off + ((size_t)p * ng + gs) * 4);
-                f32x4_t cacc;
-                cacc[0] = o.x;
-                cacc[1] = o.y;
-                cacc[2] = o.z;
-                cacc[3] = o.w;
-                const uint4* fr = F.frag + (((size_t)p * 4 + th) * ng + gs) * 4;
+        for (int m = 0; m < M; ++m) {
+            s[m] = (R[m].ok && j < R[m].last) ? f16_bits_to_f32(R[m].s[j]) : 0.0f;
+            bv[m][0] = q4_word_to_bf16x8(R[m].w[j].x);
+            bv[m][1] = q4_word_to_bf16x8(R[m].w[j].y);
+            bv[m][2] = q4_word_to_bf16x8(R[m].w[j].z);
+            bv[m][3] = q4_word_to_bf16x8(R[m].w[j].w);
+        }
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    uint4 a = make_uint4(0, 0, 0, 0);
-                    if (aact && gok) a = fr[d];
-                    cacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8_t, a), bv[d], cacc, 0, 0, 0);
-                }
-                acc[p][0] = __builtin_fmaf(s, cacc[0] + cacc[1], acc[p][0]);
-                acc[p][1] = __builtin_fmaf(s, cacc[2] + cacc[3], acc[p][1]);
+        for (int p = 0; p < P; ++p) {
+            const uint8_t* pa = in ? B[p].a : zero;
+            const uint8_t* po = in ? B[p].o : zero;
+            const float4 o = *reinterpret_cast<const float4*>(po + j * 64);
+            uint4 a[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) a[d] = *reinterpret_cast<const uint4*>(pa + j * 256 + d * 16);
+            f32x4_t c[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                c[m][0] = o.x;
+                c[m][1] = o.y;
+                c[m][2] = o.z;
+                c[m][3] = o.w;
+            }
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                    c[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[d]),
+                                                                   bv[m][d], c[m], 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                acc[m][p][0] = __builtin_fmaf(s[m], c[m][0] + c[m][1], acc[m][p][0]);
+                acc[m][p][1] = __builtin_fmaf(s[m], c[m][2] + c[m][3], acc[m][p][1]);
             }
         }
+        // keep each step's LDS reads next to their MFMAs: hoisting all of them
+        // to the top of the chunk costs more registers than the latency saves
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

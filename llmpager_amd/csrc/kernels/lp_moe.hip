@@ -216,20 +216,49 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch (one wave): the (t, j) picks stably grouped by expert id, then t
-// ascending.  Writes group starts gs[E+1], perm[pos] = t*k + j, inv[t*k + j] =
-// pos (-1 for unused pick slots), uniq[] (experts with picks, ascending) and
-// meta[0] = unique count; clears meta[1] (error flags).  Stability comes from
-// ranking each pick by the tokens before it inside a 64-token block (one bit
-// per lane) plus a running per-expert base across blocks.
+// Dispatch (one workgroup of 256): the (t, j) picks stably grouped by expert
+// id, then t ascending.  Writes group starts gs[E+1], perm[pos] = t*k + j,
+// inv[t*k + j] = pos (-1 for unused pick slots), uniq[] (experts with picks,
+// ascending), meta[0] = unique count (meta[1], the error flags, cleared), and
+// the expert table et[u] for u < min(T*k, E) that the grouped kernels read
+// (blob address through the slot table, positions, first two tokens).
+// Stability comes from ranking each pick by the tokens before it inside a
+// 64-token block (one bit per lane) plus a running per-expert base.
 // ---------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(64) lp_moe_dispatch(const RouteArgs a) {
+namespace {
+
+// Exclusive scan of one int per thread over a 256-thread workgroup.
+__device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    int x = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) sh[wave] = x;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+    for (int w = 0; w < 4; ++w) {
+        wbase += w < wave ? sh[w] : 0;
+        tot += sh[w];
+    }
+    *total = tot;
+    __syncthreads();
+    return wbase + x - v;
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
     __shared__ int cnt_e[kMaxExperts];
     __shared__ int base[kMaxExperts];
     __shared__ int gsl[kMaxExperts + 1];
+    __shared__ int uniq_l[kMaxExperts];
+    __shared__ int tok01[kMaxExperts][2];
     __shared__ uint32_t mlo[kMaxExperts];
     __shared__ uint32_t mhi[kMaxExperts];
-    const int lane = lane_id();
+    __shared__ int scan_sh[4];
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int E = a.L.experts, k = a.L.top_k, T = a.T;
     const int* ids = dptr<const int>(a.W.ids);
     const int* cnt = dptr<const int>(a.W.cnt);
@@ -237,245 +266,360 @@ extern "C" __global__ void __launch_bounds__(64) lp_moe_dispatch(const RouteArgs
     int* inv = dptr<int>(a.W.inv);
     int* meta = dptr<int>(a.W.meta);
 
-    for (int e = lane; e < E; e += 64) {
+    for (int e = tid; e < E; e += 256) {
         cnt_e[e] = 0;
         base[e] = 0;
+        tok01[e][0] = tok01[e][1] = -1;
     }
     __syncthreads();
-    for (int p = lane; p < T * k; p += 64) {
+    for (int p = tid; p < T * k; p += 256) {
         const int t = p / k, j = p - t * k;
         if (j < cnt[t]) atomicAdd(&cnt_e[ids[p]], 1);
     }
     __syncthreads();
-    if (lane == 0) {
-        int* uniq = dptr<int>(a.W.uniq);
-        int nu = 0;
-        gsl[0] = 0;
-        for (int e = 0; e < E; ++e) {
-            gsl[e + 1] = gsl[e] + cnt_e[e];
-            if (cnt_e[e] > 0) uniq[nu++] = e;
+    // group starts and the unique list: thread i covers experts 4i .. 4i+3
+    {
+        int c[4], f[4], sc = 0, sf = 0;
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            c[q] = e < E ? cnt_e[e] : 0;
+            f[q] = c[q] > 0;
+            sc += c[q];
+            sf += f[q];
         }
-        meta[0] = nu;
-        meta[1] = 0;
+        int tot_c, tot_f;
+        int oc = block_excl_scan(sc, scan_sh, &tot_c);
+        int of = block_excl_scan(sf, scan_sh, &tot_f);
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            if (e < E) {
+                gsl[e] = oc;
+                if (f[q]) uniq_l[of++] = e;
+            }
+            oc += c[q];
+        }
+        if (tid == 0) {
+            gsl[E] = tot_c;
+            meta[0] = tot_f;
+            meta[1] = 0;
+        }
     }
     __syncthreads();
     int* gs = dptr<int>(a.W.gs);
-    for (int e = lane; e <= E; e += 64) gs[e] = gsl[e];
+    for (int e = tid; e <= E; e += 256) gs[e] = gsl[e];
+    const int nu = meta[0];
+    int* uniq = dptr<int>(a.W.uniq);
+    for (int u = tid; u < nu; u += 256) uniq[u] = uniq_l[u];
 
     for (int tb = 0; tb < T; tb += 64) {
-        for (int e = lane; e < E; e += 64) {
+        for (int e = tid; e < E; e += 256) {
             mlo[e] = 0u;
             mhi[e] = 0u;
         }
         __syncthreads();
         const int t = tb + lane;
-        const int c = t < T ? cnt[t] : 0;
+        const int c = (wave == 0 && t < T) ? cnt[t] : 0;
         for (int j = 0; j < c; ++j) {
             const int e = ids[t * k + j];
             atomicOr(lane < 32 ? &mlo[e] : &mhi[e], 1u << (lane & 31));
         }
         __syncthreads();
-        if (t < T) {
+        if (wave == 0 && t < T) {
             for (int j = 0; j < k; ++j) {
                 if (j < c) {
                     const int e = ids[t * k + j];
                     const uint64_t mask = (uint64_t)mlo[e] | ((uint64_t)mhi[e] << 32);
                     const uint64_t below = lane == 0 ? 0ull : (mask & ((1ull << lane) - 1ull));
-                    const int pos = gsl[e] + base[e] + __popcll(below);
+                    const int rank = base[e] + __popcll(below);
+                    const int pos = gsl[e] + rank;
                     perm[pos] = t * k + j;
                     inv[t * k + j] = pos;
+                    if (rank < 2) tok01[e][rank] = t;
                 } else {
                     inv[t * k + j] = -1;
                 }
             }
         }
         __syncthreads();
-        for (int e = lane; e < E; e += 64) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
+        for (int e = tid; e < E; e += 256) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
         __syncthreads();
+    }
+    // the expert table for the grouped kernels
+    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    const int* slots = dptr<const int>(a.L.slot_table);
+    const int maxu = min(T * k, E);
+    for (int u = tid; u < maxu; u += 256) {
+        ExpertEntry x;
+        x.pad0 = 0;
+        if (u < nu) {
+            const int e = uniq_l[u];
+            const int slot = slots[e];
+            x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
+            x.p0 = gsl[e];
+            x.ntok = cnt_e[e];
+            x.tok0 = tok01[e][0];
+            x.tok1 = tok01[e][1];
+            x.e = e;
+        } else {
+            x.blob = 0ull;
+            x.p0 = 0;
+            x.ntok = 0;
+            x.tok0 = x.tok1 = -1;
+            x.e = -1;
+        }
+        et[u] = x;
     }
 }
 
 // ---------------------------------------------------------------------------
 // Grouped expert projections.  A workgroup of W waves takes one work item =
-// (unique expert, run of rows); every wave owns 16-row tiles of that run and
+// (routed expert u, run of rows); every wave owns 16-row tiles of that run and
 // the workgroup stages the expert's tokens into shared LDS fragments, up to
-// `pairs_cap` token pairs at a time.  Weight loads are issued before the
+// kMaxPairs token pairs at a time.  The item's only dependent load is its
+// expert-table entry; the first chunk of weights is in flight while the
 // fragments are staged, and each dequantised weight word serves every staged
-// token pair.
+// token pair.  Small per-wave state keeps several workgroups resident per CU
+// so one item's latency hides behind another's work.
 //   gate/up: act[pos][r] = silu(gate_e . x_t)[r] * (up_e . x_t)[r], r < I
 //   down:    y[pos][r]   = (down_e . act[pos])[r], r < H
-// pos = dispatch position of the (token, pick) pair; expert e's blob sits at
-// arena_base + slot_table[e] * slot_span (the per-layer slot arena of
-// pager.rs:310-318).  An expert without a slot raises kErrMissingExpert in
-// meta[1] and its outputs are zero.
+// pos = dispatch position of the (token, pick) pair.  An expert without a
+// slot raises kErrMissingExpert in meta[1] and its outputs are zero.
 // ---------------------------------------------------------------------------
 namespace {
 
-struct Item {
-    int e, slot, p0, ntok, chunk;
-    bool live;
-};
-
-__device__ __forceinline__ Item item_of(const GroupedArgs& a, int chunks) {
-    Item it;
-    const int nu = gptr<int>(a.W.meta)[0];
-    const int u = blockIdx.x / chunks;
-    it.live = u < nu;
-    if (!it.live) return it;
-    it.chunk = blockIdx.x - u * chunks;
-    it.e = gptr<int>(a.W.uniq)[u];
-    it.slot = gptr<int>(a.L.slot_table)[it.e];
-    it.p0 = gptr<int>(a.W.gs)[it.e];
-    it.ntok = gptr<int>(a.W.gs)[it.e + 1] - it.p0;
-    return it;
+__device__ __forceinline__ ExpertEntry entry_of(const GroupedArgs& a, int u) {
+    const LP_GLOBAL uint4* p = gptr<uint4>(a.W.et + (uint64_t)u * sizeof(ExpertEntry));
+    const uint4 lo = p[0], hi = p[1];
+    ExpertEntry x;
+    x.blob = (uint64_t)lo.x | ((uint64_t)lo.y << 32);
+    x.p0 = (int)lo.z;
+    x.ntok = (int)lo.w;
+    x.tok0 = (int)hi.x;
+    x.tok1 = (int)hi.y;
+    x.e = (int)hi.z;
+    x.pad0 = 0;
+    return x;
 }
 
-__device__ __forceinline__ void missing_expert(const GroupedArgs& a, const Item& it, float* out,
+__device__ __forceinline__ void missing_expert(const GroupedArgs& a, const ExpertEntry& x, float* out,
                                                int stride, int rows, int row_lo, int row_hi) {
     if (threadIdx.x == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
-    for (int p = 0; p < it.ntok; ++p)
+    for (int p = 0; p < x.ntok; ++p)
         for (int r = row_lo + (int)threadIdx.x; r < row_hi && r < rows; r += blockDim.x)
-            out[(size_t)(it.p0 + p) * stride + r] = 0.0f;
+            out[(size_t)(x.p0 + p) * stride + r] = 0.0f;
 }
 
-template <int NS, int PMAX>
+// gate/up MFMAs for one staged token group of P pairs, then SiLU * up into
+// act.  GU (gate, up) holds the first chunk on entry; later chunks are loaded
+// right after the previous one's MFMAs.  When `next` is set the first chunk
+// is loaded again for the following token group before the epilogue, so its
+// latency overlaps the stores and the restaging.
+template <int P, int RS>
+__device__ __forceinline__ void gateup_group(const Frags& F, WRegs<kStepChunk> (&GU)[2],
+                                             const WTile<RS>& TG, const WTile<RS>& TU, int I,
+                                             int n0, int S, int t0, int ntok, int p0, bool next,
+                                             float* act) {
+    float acc[2][P][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc[m][p][0] = acc[m][p][1] = 0.0f;
+#pragma nounroll
+    for (int c0 = 0;;) {
+        ABase B[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
+        wmma(GU, B, F.lds, S - c0, acc);
+        c0 += kStepChunk;
+        if (c0 >= S) break;
+        wload(GU[0], TG, c0);
+        wload(GU[1], TU, c0);
+    }
+    if (next) {
+        wload(GU[0], TG, 0);
+        wload(GU[1], TU, 0);
+    }
+    const int lane = lane_id();
+    const int row = n0 + (lane & 15);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const float g0 = tile_reduce(acc[0][p][0]), g1 = tile_reduce(acc[0][p][1]);
+        const float u0 = tile_reduce(acc[1][p][0]), u1 = tile_reduce(acc[1][p][1]);
+        const int t = t0 + 2 * p + (lane >> 4);
+        if (row < I && lane < 32 && t < ntok) {
+            const float g = lane < 16 ? g0 : g1;
+            const float u = lane < 16 ? u0 : u1;
+            act[(size_t)(p0 + t) * I + row] = g / (1.0f + expf(-g)) * u;
+        }
+    }
+}
+
+template <int RS>
 __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
     const int H = L.hidden, I = L.inter, k = L.top_k;
-    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6, lane = lane_id();
-    const int ng = H >> 5;
+    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int run = kTileRows * W;
     const int chunks = (I + run - 1) / run;
-    const Item it = item_of(a, chunks);
-    if (!it.live) return;
+    const int u = blockIdx.x / chunks;
+    const int chunk = blockIdx.x - u * chunks;
+    const ExpertEntry x = entry_of(a, u);
+    if (x.ntok == 0) return;
     float* act = dptr<float>(a.W.act);
-    if (it.slot < 0) {
-        missing_expert(a, it, act, I, I, it.chunk * run, it.chunk * run + run);
+    if (x.blob == 0) {
+        missing_expert(a, x, act, I, I, chunk * run, chunk * run + run);
         return;
     }
-    const uint64_t blob = L.arena_base + (uint64_t)it.slot * L.slot_span;
-    const uint64_t rg = blob + L.gate_off, ru = blob + L.up_off;
-    const int rs = ilog2_pow2(L.group >> 5);
     const int S = tile_steps(H);
-    const int n0 = it.chunk * run + kTileRows * wave;
-    const int row = n0 + (lane & 15);
-    const int cap = min(PMAX, a.pairs_cap);
-    const Frags F = frags_at(lds, ng, cap);
-    const bool one = S <= NS;
-    WRegs<NS> G, U;
-    if (one) {
-        wload(G, rg, I, H, rs, n0, 0);
-        wload(U, ru, I, H, rs, n0, 0);
-    }
+    const int n0 = chunk * run + kTileRows * wave;
+    const Frags F = frags_at(lds, H);
+    const WTile<RS> TG = wtile<RS>(x.blob + L.gate_off, I, H, n0);
+    const WTile<RS> TU = wtile<RS>(x.blob + L.up_off, I, H, n0);
+    WRegs<kStepChunk> GU[2];
+    wload(GU[0], TG, 0);
+    wload(GU[1], TU, 0);
+    zero_block(F, threadIdx.x, blockDim.x);
     const int* perm = dptr<const int>(a.W.perm);
-    const float* x = dptr<const float>(a.x);
-    for (int tb = 0; tb < it.ntok; tb += 2 * cap) {
-        const int nt = min(2 * cap, it.ntok - tb);
-        const int pairs = (nt + 1) >> 1;
+    const float* xs = dptr<const float>(a.x);
+    const int cap = min(kMaxPairs, a.pairs_cap);
+    for (int tb = 0; tb < x.ntok; tb += 2 * cap) {
+        const int nt = min(2 * cap, x.ntok - tb);
+        const bool next = tb + nt < x.ntok;
         if (tb > 0) __syncthreads();
-        stage_rows(F, nt, [&](int t) { return x + (size_t)(perm[it.p0 + tb + t] / k) * H; },
-                   threadIdx.x, blockDim.x);
+        stage_rows(F, nt, [&](int t) {
+            const int i = tb + t;
+            const int tok = i == 0 ? x.tok0 : i == 1 ? x.tok1 : perm[x.p0 + i] / k;
+            return xs + (size_t)tok * H;
+        }, threadIdx.x, blockDim.x);
         __syncthreads();
-        float ag[PMAX][2], au[PMAX][2];
-#pragma unroll
-        for (int p = 0; p < PMAX; ++p) ag[p][0] = ag[p][1] = au[p][0] = au[p][1] = 0.0f;
-        for (int c0 = 0; c0 < S; c0 += NS) {
-            if (!one) {
-                wload(G, rg, I, H, rs, n0, c0);
-                wload(U, ru, I, H, rs, n0, c0);
+        if constexpr (kMaxPairs > 1) {
+            if (nt > 2) {
+                gateup_group<2>(F, GU, TG, TU, I, n0, S, tb, x.ntok, x.p0, next, act);
+                continue;
             }
-            wmma(G, F, H, c0, pairs, ag);
-            wmma(U, F, H, c0, pairs, au);
         }
+        gateup_group<1>(F, GU, TG, TU, I, n0, S, tb, x.ntok, x.p0, next, act);
+    }
+}
+
+// down MFMAs for one staged token group of P pairs over TW row tiles, into
+// y; D holds the first chunk on entry (as for gateup_group).
+template <int P, int TW, int RS>
+__device__ __forceinline__ void down_group(const Frags& F, WRegs<kStepChunk> (&D)[TW],
+                                           const WTile<RS> (&TD)[TW], int H, const int (&n0)[TW],
+                                           int S, int t0, int ntok, int p0, bool next, float* y) {
+    const int lane = lane_id();
+    float acc[TW][P][2];
 #pragma unroll
-        for (int p = 0; p < PMAX; ++p) {
-            if (p < pairs) {
-                const float g0 = tile_reduce(ag[p][0]), g1 = tile_reduce(ag[p][1]);
-                const float u0 = tile_reduce(au[p][0]), u1 = tile_reduce(au[p][1]);
-                const int t = tb + 2 * p + (lane >> 4);
-                if (row < I && lane < 32 && t < it.ntok) {
-                    const float g = lane < 16 ? g0 : g1;
-                    const float u = lane < 16 ? u0 : u1;
-                    act[(size_t)(it.p0 + t) * I + row] = g / (1.0f + expf(-g)) * u;
-                }
-            }
+    for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc[tw][p][0] = acc[tw][p][1] = 0.0f;
+#pragma nounroll
+    for (int c0 = 0;;) {
+        ABase B[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
+        wmma(D, B, F.lds, S - c0, acc);
+        c0 += kStepChunk;
+        if (c0 >= S) break;
+#pragma unroll
+        for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], c0);
+    }
+    if (next) {
+#pragma unroll
+        for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], 0);
+    }
+#pragma unroll
+    for (int tw = 0; tw < TW; ++tw) {
+        const int row = n0[tw] + (lane & 15);
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const float v0 = tile_reduce(acc[tw][p][0]), v1 = tile_reduce(acc[tw][p][1]);
+            const int t = t0 + 2 * p + (lane >> 4);
+            if (row < H && lane < 32 && t < ntok) y[(size_t)(p0 + t) * H + row] = lane < 16 ? v0 : v1;
         }
     }
 }
 
-template <int NS, int TW, int PMAX>
+template <int TW, int RS>
 __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
     const int H = L.hidden, I = L.inter;
-    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6, lane = lane_id();
-    const int ng = I >> 5;
+    const int wave = threadIdx.x >> 6, W = blockDim.x >> 6;
     const int run = kTileRows * W * TW;
     const int chunks = (H + run - 1) / run;
-    const Item it = item_of(a, chunks);
-    if (!it.live) return;
+    const int u = blockIdx.x / chunks;
+    const int chunk = blockIdx.x - u * chunks;
+    const ExpertEntry x = entry_of(a, u);
+    if (x.ntok == 0) return;
     float* y = dptr<float>(a.W.y);
-    if (it.slot < 0) {
-        missing_expert(a, it, y, H, H, it.chunk * run, it.chunk * run + run);
+    if (x.blob == 0) {
+        missing_expert(a, x, y, H, H, chunk * run, chunk * run + run);
         return;
     }
-    const uint64_t rd = L.arena_base + (uint64_t)it.slot * L.slot_span + L.down_off;
-    const int rs = ilog2_pow2(L.group >> 5);
     const int S = tile_steps(I);
-    const int cap = min(PMAX, a.pairs_cap);
-    const Frags F = frags_at(lds, ng, cap);
-    const bool one = S <= NS;
-    WRegs<NS> D[TW];
+    const Frags F = frags_at(lds, I);
+    WRegs<kStepChunk> D[TW];
+    WTile<RS> TD[TW];
     int n0[TW];
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
-        n0[t] = it.chunk * run + kTileRows * (wave + W * t);
-        if (one) wload(D[t], rd, H, I, rs, n0[t], 0);
+        n0[t] = chunk * run + kTileRows * (wave + W * t);
+        TD[t] = wtile<RS>(x.blob + L.down_off, H, I, n0[t]);
+        wload(D[t], TD[t], 0);
     }
+    zero_block(F, threadIdx.x, blockDim.x);
     const float* act = dptr<const float>(a.W.act);
-    for (int tb = 0; tb < it.ntok; tb += 2 * cap) {
-        const int nt = min(2 * cap, it.ntok - tb);
-        const int pairs = (nt + 1) >> 1;
+    const int cap = min(kMaxPairs, a.pairs_cap);
+    for (int tb = 0; tb < x.ntok; tb += 2 * cap) {
+        const int nt = min(2 * cap, x.ntok - tb);
+        const bool next = tb + nt < x.ntok;
         if (tb > 0) __syncthreads();
-        stage_rows(F, nt, [&](int t) { return act + (size_t)(it.p0 + tb + t) * I; },
+        stage_rows(F, nt, [&](int t) { return act + (size_t)(x.p0 + tb + t) * I; },
                    threadIdx.x, blockDim.x);
         __syncthreads();
-#pragma unroll
-        for (int tw = 0; tw < TW; ++tw) {
-            float acc[PMAX][2];
-#pragma unroll
-            for (int p = 0; p < PMAX; ++p) acc[p][0] = acc[p][1] = 0.0f;
-            for (int c0 = 0; c0 < S; c0 += NS) {
-                if (!one) wload(D[tw], rd, H, I, rs, n0[tw], c0);
-                wmma(D[tw], F, I, c0, pairs, acc);
-            }
-            const int row = n0[tw] + (lane & 15);
-#pragma unroll
-            for (int p = 0; p < PMAX; ++p) {
-                if (p < pairs) {
-                    const float v0 = tile_reduce(acc[p][0]), v1 = tile_reduce(acc[p][1]);
-                    const int t = tb + 2 * p + (lane >> 4);
-                    if (row < H && lane < 32 && t < it.ntok)
-                        y[(size_t)(it.p0 + t) * H + row] = lane < 16 ? v0 : v1;
-                }
+        if constexpr (kMaxPairs > 1) {
+            if (nt > 2) {
+                down_group<2, TW>(F, D, TD, H, n0, S, tb, x.ntok, x.p0, next, y);
+                continue;
             }
         }
+        down_group<1, TW>(F, D, TD, H, n0, S, tb, x.ntok, x.p0, next, y);
     }
 }
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_gateup(const GroupedArgs a) {
-    gateup_body<16, kMaxPairs>(a);
+// Scale granularity (group = 32 << RS) is a template parameter so that every
+// load offset of a chunk is an immediate.
+#define LP_BY_RS(group, call)               \
+    switch (ilog2_pow2((group) >> 5)) {      \
+        case 0: call(0); break;              \
+        case 1: call(1); break;              \
+        default: call(2); break;             \
+    }
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup(const GroupedArgs a) {
+#define LP_GATEUP(rs) gateup_body<rs>(a)
+    LP_BY_RS(a.L.group, LP_GATEUP)
+#undef LP_GATEUP
 }
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_down(const GroupedArgs a) {
-    down_body<8, 2, kMaxPairs>(a);
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_down(const GroupedArgs a) {
+#define LP_DOWN(rs) down_body<2, rs>(a)
+    LP_BY_RS(a.L.group, LP_DOWN)
+#undef LP_DOWN
 }
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_down_wide(const GroupedArgs a) {
-    down_body<16, 1, kMaxPairs>(a);
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_down_wide(const GroupedArgs a) {
+#define LP_DOWN(rs) down_body<1, rs>(a)
+    LP_BY_RS(a.L.group, LP_DOWN)
+#undef LP_DOWN
 }
 
 // ---------------------------------------------------------------------------

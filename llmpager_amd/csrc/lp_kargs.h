@@ -5,6 +5,12 @@
 #pragma once
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define LPK_HD __host__ __device__
+#else
+#define LPK_HD
+#endif
+
 namespace lpk {
 
 // Launch geometry constants the host and the kernels agree on.
@@ -14,8 +20,20 @@ constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
-constexpr int kFragBytesPerSubgroup = 4 * 4 * 16 + 16;  // LDS per token pair per 32 columns
-constexpr int kMaxPairs = 4;           // token pairs the grouped kernels stage at once
+constexpr int kMaxPairs = 1;           // token pairs the grouped kernels stage at once
+constexpr int kStepChunk = 8;          // MFMA steps (4 sub-groups each) per register chunk
+constexpr int kZeroBytes = 256 * kStepChunk;  // LDS zero block read by idle MFMA lanes
+
+// LDS bytes of the fragment area for `pairs` token pairs over `cols` columns:
+// a zero block, then per pair four (token, part) blocks of ngp sub-groups x
+// 64 B (+16 B to stagger banks) and ngp x 16 B of accumulator seeds, with
+// ngp = 4 * ceil(cols / 128) sub-groups (zero padded).
+LPK_HD constexpr int frag_ngp(int cols) { return 4 * (((cols >> 5) + 3) >> 2); }
+LPK_HD constexpr int frag_th_stride(int ngp) { return ngp * 64 + 16; }
+LPK_HD constexpr int frag_pair_bytes(int ngp) { return 4 * frag_th_stride(ngp) + ngp * 16; }
+LPK_HD constexpr int frag_lds_bytes(int cols, int pairs) {
+    return kZeroBytes + pairs * frag_pair_bytes(frag_ngp(cols));
+}
 
 // ---- 1:1 launchers (crates/llmpager-cuda/src/kernels.rs) -------------------
 
@@ -67,6 +85,17 @@ struct LayerView {
     int32_t pad0;
 };
 
+// One routed expert as the grouped kernels see it, written by the dispatch
+// kernel for u < min(T*k, E) (ntok = 0 past the unique count).
+struct ExpertEntry {
+    uint64_t blob;       // device address of the expert's blob (0 if not resident)
+    int32_t p0;          // first dispatch position of its (token, pick) pairs
+    int32_t ntok;        // number of those pairs
+    int32_t tok0, tok1;  // tokens of the first two pairs (-1 if absent)
+    int32_t e;           // expert id
+    int32_t pad0;
+};
+
 // Workspace carve-up for T tokens (offsets in bytes from `ws`).
 struct Workspace {
     uint64_t logits;     // f32 [T, E]
@@ -78,6 +107,7 @@ struct Workspace {
     uint64_t inv;        // i32 [T * k] dispatch position per pick (-1 if none)
     uint64_t uniq;       // i32 [E] experts with picks, ascending
     uint64_t meta;       // i32 [16]: [0] = unique count, [1] = error flags
+    uint64_t et;         // ExpertEntry [E]
     uint64_t act;        // f32 [T * k, I] expert-major activations
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
 };

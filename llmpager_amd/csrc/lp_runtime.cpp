@@ -400,7 +400,7 @@ static int q4_gemv_common(lp_ctx* c, uint64_t blobs, uint64_t region_off, uint64
     const uint64_t data_off = region_off + (uint64_t)rows * (cols / group) * 2;
     const bool aligned = (data_off % 16 == 0) && (x % 16 == 0) && ((uint64_t)x_stride * 4 % 16 == 0);
     const bool pow2 = group % 32 == 0 && ((group / 32) & (group / 32 - 1)) == 0;
-    const size_t frag = (size_t)(cols / 32) * kFragBytesPerSubgroup;
+    const size_t frag = (size_t)frag_lds_bytes(cols, 1);
     if (pow2 && aligned && frag <= c->max_lds) {
         const int tiles = (rows + kTileRows - 1) / kTileRows;
         const int waves = std::min(4, tiles);
@@ -472,6 +472,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->inv = take(t * k * 4);
     out->uniq = take(E * 4);
     out->meta = take(64);
+    out->et = take(E * sizeof(ExpertEntry));
     out->act = take(t * k * I * 4);
     out->y = take(t * k * H * 4);
     out->total = o;
@@ -534,6 +535,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->inv = ws + lay.inv;
     W->uniq = ws + lay.uniq;
     W->meta = ws + lay.meta;
+    W->et = ws + lay.et;
     W->act = ws + lay.act;
     W->y = ws + lay.y;
 }
@@ -541,7 +543,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
     if (int r = launch(c, kTopk, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
-    return launch(c, kDispatch, dim3(1), dim3(64), 0, s, ra);
+    return launch(c, kDispatch, dim3(1), dim3(256), 0, s, ra);
 }
 
 int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws,
@@ -582,13 +584,13 @@ int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
     const int maxu = std::min(T * d->top_k, d->experts);
     // Token pairs staged at once: enough for T tokens on one expert, bounded
     // by kMaxPairs and by the LDS the fragments need.
-    const size_t fr_h = (size_t)(H / 32) * kFragBytesPerSubgroup;
-    const size_t fr_i = (size_t)(I / 32) * kFragBytesPerSubgroup;
     int cap = std::min(kMaxPairs, (T + 1) / 2);
-    while (cap > 1 && (size_t)cap * std::max(fr_h, fr_i) > c->max_lds) --cap;
-    if (fr_h > c->max_lds || fr_i > c->max_lds)
+    auto lds_for = [&](int p) { return (size_t)std::max(frag_lds_bytes(H, p), frag_lds_bytes(I, p)); };
+    while (cap > 1 && lds_for(cap) > c->max_lds) --cap;
+    if (lds_for(1) > c->max_lds)
         return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
     ga.pairs_cap = cap;
+    const size_t fr_h = (size_t)frag_lds_bytes(H, cap), fr_i = (size_t)frag_lds_bytes(I, cap);
     // Workgroup width: the widest (more rows per staged fragment set) that
     // still yields about two work items per CU.
     auto pick_w = [&](int rows, int tw) {
@@ -600,16 +602,16 @@ int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
     {
         const int w = pick_w(I, 1);
         const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
-        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w), cap * fr_h, s, ga))
+        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w), fr_h, s, ga))
             return r;
     }
     {
         const int steps = ((I / 32) + 3) / 4;
-        const Fn f = steps <= 8 ? kDown : kDownWide;
-        const int tw = steps <= 8 ? 2 : 1;
+        const Fn f = steps <= kStepChunk ? kDown : kDownWide;
+        const int tw = steps <= kStepChunk ? 2 : 1;
         const int w = pick_w(H, tw);
         const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
-        if (int r = launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), cap * fr_i, s, ga))
+        if (int r = launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), fr_i, s, ga))
             return r;
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
