@@ -156,6 +156,7 @@ typedef struct lp_moe_ws_layout {
     uint64_t et;      /* 32-byte expert entries [E] for the grouped kernels */
     uint64_t act;     /* f32 [T*k, I] */
     uint64_t y;       /* f32 [T*k, H] */
+    uint64_t xf;      /* [T] bf16 hi/lo fragment images of x for the grouped gate/up */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;
 
@@ -171,12 +172,14 @@ int lp_moe_route(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, int T, uin
  * workspace): the "given identical fp32 router logits" contract. */
 int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits, int T,
                         uint64_t workspace, lp_stream s);
-/* Expert half of the layer after lp_moe_route*: grouped gate/up + SiLU,
- * grouped down, and h[t] += sum_j w[t][j] * y[t][j] in pick order. */
+/* Expert half of the layer after lp_moe_route*: fragment images of x,
+ * grouped gate/up + SiLU, grouped down, and h[t] += sum_j w[t][j] * y[t][j]
+ * in pick order. */
 int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
 /* The whole layer (decode.rs:303-337 for one token, 469-531 for many):
- * lp_moe_route followed by lp_moe_experts.  h: f32 [T, H], updated in place. */
+ * lp_moe_route followed by lp_moe_experts, with the fragment images of x
+ * written by the router kernel.  h: f32 [T, H], updated in place. */
 int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
 /* Synchronising readback of meta[0..1] (unique count, error flags). */

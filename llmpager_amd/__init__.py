@@ -54,7 +54,7 @@ class WsLayout(C.Structure):
     """lp_moe_ws_layout: byte offsets of the workspace parts."""
 
     _fields_ = [(n, C.c_uint64) for n in (
-        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y",
+        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y", "xf",
         "total")]
 
 

@@ -27,13 +27,13 @@ __device__ __forceinline__ void q4_gemv_tiles(const Q4GemvBatchArgs& a, const Fr
         const int n0 = tile * kTileRows;
         const WTile<RS> T = wtile<RS>(region, a.rows, a.cols, n0);
         float acc[1][1][2] = {{{0.0f, 0.0f}}};
-        WRegs<kStepChunk> R[1];
+        WRegs<kGemvChunk> R[1];
         wload(R[0], T, 0);
 #pragma nounroll
         for (int c0 = 0;;) {
             const ABase B[1] = {abase(F, 0, c0)};
-            wmma(R, B, F.lds, S - c0, acc);
-            c0 += kStepChunk;
+            wmma(R, B, S - c0, 1, acc);
+            c0 += kGemvChunk;
             if (c0 >= S) break;
             wload(R[0], T, c0);
         }

@@ -141,6 +141,46 @@ __device__ __forceinline__ void zero_block(const Frags& F, int tid, int nthreads
         reinterpret_cast<uint4*>(F.lds)[i] = make_uint4(0, 0, 0, 0);
 }
 
+// One 32-column sub-group of an fp32 row as fragment words: the bf16 parts
+// hi = bf16(x) and lo = bf16(x - hi) in fragment order (32-bit word w of
+// uint4 d pairs columns 8d + w and 8d + w + 4) and each part's sum.  p == 0
+// gives zeros (padding sub-groups, missing tokens).
+struct GroupFrag {
+    uint4 hi[4], lo[4];
+    float shi, slo;
+};
+
+__device__ __forceinline__ GroupFrag convert_group(const LP_GLOBAL float4* p) {
+    GroupFrag q;
+    q.shi = 0.0f;
+    q.slo = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        float v[8];
+        if (p) {
+            const float4 f0 = p[2 * d], f1 = p[2 * d + 1];
+            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+            v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            hi[i] = f32_to_bf16_rne(v[i]);
+            lo[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hi[i]));
+            q.shi += bf16_to_f32(hi[i]);
+            q.slo += bf16_to_f32(lo[i]);
+        }
+        q.hi[d] = make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
+                             hi[3] | (hi[7] << 16));
+        q.lo[d] = make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
+                             lo[3] | (lo[7] << 16));
+    }
+    return q;
+}
+
 // Stage ntok activation rows into fragment pairs 0 .. ceil(ntok/2)-1.
 // row_of(t) returns the f32 row of token t.  Work units (token, sub-group)
 // are spread over the `nthreads` participating threads; a missing second
@@ -153,41 +193,64 @@ __device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int ti
         const int g = u - t * F.ngp;
         const int pair = t >> 1, tk = t & 1;
         const bool live = t < ntok && g < F.ng;
-        const LP_GLOBAL float4* p =
-            live ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr;
-        float shi = 0.0f, slo = 0.0f;
+        const GroupFrag q =
+            convert_group(live ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr);
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            // columns 8d .. 8d+7; fragment element i holds column frag_col(d, i),
-            // so 32-bit word w pairs columns 8d + w and 8d + w + 4
-            float v[8];
-            if (p) {
-                const float4 f0 = p[2 * d], f1 = p[2 * d + 1];
-                v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
-                v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) v[q] = 0.0f;
-            }
-            uint32_t hi[8], lo[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                hi[q] = f32_to_bf16_rne(v[q]);
-                lo[q] = f32_to_bf16_rne(v[q] - bf16_to_f32(hi[q]));
-                shi += bf16_to_f32(hi[q]);
-                slo += bf16_to_f32(lo[q]);
-            }
-            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 0, g) + d * 16) =
-                make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
-                           hi[3] | (hi[7] << 16));
-            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 1, g) + d * 16) =
-                make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
-                           lo[3] | (lo[7] << 16));
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 0, g) + d * 16) = q.hi[d];
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 1, g) + d * 16) = q.lo[d];
         }
         float* of = off_ptr(F, pair, g);
-        of[2 * tk + 0] = -136.0f * shi;
-        of[2 * tk + 1] = -136.0f * slo;
+        of[2 * tk + 0] = -136.0f * q.shi;
+        of[2 * tk + 1] = -136.0f * q.slo;
     }
+}
+
+// Sub-group g of an fp32 row of `cols` columns into the row's fragment image
+// (lpk::image_bytes layout): part blocks [2][ngp][64 B], then seeds [ngp][2].
+__device__ __forceinline__ void write_image_group(const float* row, int cols, int g, uint8_t* img) {
+    const int ng = cols >> 5, ngp = lpk::frag_ngp(cols);
+    const GroupFrag q =
+        convert_group(g < ng ? gptr<float4>(reinterpret_cast<uint64_t>(row + (size_t)g * 32)) : nullptr);
+    uint4* hi = reinterpret_cast<uint4*>(img + (size_t)g * 64);
+    uint4* lo = reinterpret_cast<uint4*>(img + (size_t)ngp * 64 + (size_t)g * 64);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        hi[d] = q.hi[d];
+        lo[d] = q.lo[d];
+    }
+    reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * q.shi, -136.0f * q.slo);
+}
+
+// Copy the fragment images of nt tokens (img_of(t): device address of token
+// t's image) into fragment pairs 0 .. ceil(nt/2)-1.  Part blocks go straight
+// from memory into LDS (global_load_lds_dwordx4: 64 lanes fill 1 KB of LDS
+// per instruction, no registers, no LDS store), one instruction per wave in
+// turn; the seeds go through registers.  Ends with every load of the calling
+// thread complete; the caller's barrier then publishes the copy.  The second
+// token of an odd last pair is left as it is: its MFMA output rows are
+// separate and never stored.
+template <typename ImgOf>
+__device__ inline void load_images(const Frags& F, int nt, ImgOf img_of) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const int q4 = 4 * F.ngp;          // 16-byte units per part block
+    const int ipb = (q4 + 63) >> 6;    // DMA instructions per part block
+    for (int i = wave; i < 2 * nt * ipb; i += W) {
+        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + part
+        const int t = blk >> 1, part = blk & 1;
+        const int q = r * 64 + lane;
+        const uint64_t src = img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)q * 16;
+        uint8_t* dst = frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024;
+        if (q < q4)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const LP_GLOBAL void*>(src),
+                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    }
+    for (int f = threadIdx.x; f < nt * F.ngp; f += blockDim.x) {
+        const int t = f / F.ngp, g = f - t * F.ngp;
+        const uint2 sd = gptr<uint2>(img_of(t) + (uint64_t)F.ngp * 128)[g];
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(off_ptr(F, t >> 1, g)) + (t & 1) * 8) = sd;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct loads have landed
 }
 
 __device__ __forceinline__ int tile_steps(int cols) { return ((cols >> 5) + 3) >> 2; }
@@ -203,8 +266,7 @@ struct WTile {
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t dofs;  // lane's nibble byte offset at step 0
     uint32_t sofs;  // lane's scale byte offset at step 0
-    int last;       // steps c with 4c + kb < cols / 32
-    bool ok;        // row inside the matrix
+    bool lastok;    // the lane's sub-group exists at the tile's last step
 };
 
 template <int RS>
@@ -219,18 +281,18 @@ __device__ __forceinline__ WTile<RS> wtile(uint64_t region, int rows, int cols, 
                                                (int)(sbytes + (uint32_t)rows * ng * 16), kBufferWord3);
     T.dofs = sbytes + (row * ng + kb) * 16;
     T.sofs = (row * gpr + (kb >> RS)) * 2;
-    T.last = ((int)ng - kb + 3) >> 2;
-    T.ok = (int)row < rows;
+    T.lastok = (ng & 3) == 0 || kb < (int)(ng & 3);
     return T;
 }
 
-// Raw weight registers for steps [c0, c0 + NS) of one tile.
+// Raw weight registers for steps [c0, c0 + NS) of one tile.  Rows past the
+// matrix read zero nibbles (past the buffer) and garbage scales; their
+// outputs are never stored, so they need no mask.
 template <int NS>
 struct WRegs {
     uint4 w[NS];
     uint32_t s[NS];  // f16 bits of the lane's sub-group scale
-    bool ok;         // row inside the matrix (scales of other rows count as 0)
-    int last;        // chunk steps >= last carry no data for this lane
+    bool lastok;     // the lane's sub-group exists at the tile's last step
 };
 
 // Issue the tile's loads for steps c0 .. c0 + NS - 1: one per-lane offset
@@ -240,14 +302,30 @@ struct WRegs {
 // the region (or zeros past its end); wmma gives them a zero scale.
 template <int NS, int RS>
 __device__ __forceinline__ void wload(WRegs<NS>& R, const WTile<RS>& T, int c0) {
-    R.ok = T.ok;
-    R.last = T.last - c0;
-    const uint32_t d = T.dofs + 64u * (uint32_t)c0;
-    const uint32_t sc = T.sofs + (8u >> RS) * (uint32_t)c0;
+    R.lastok = T.lastok;
+    uint32_t d = T.dofs + 64u * (uint32_t)c0;
+    uint32_t sc = T.sofs + (8u >> RS) * (uint32_t)c0;
+    // opaque per-chunk bases: every step is then base + immediate, and the
+    // compiler cannot hoist NS separate step addresses out of a chunk loop
+    asm volatile("" : "+v"(d), "+v"(sc));
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         R.w[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(T.rsrc, (int)(d + 64u * j), 0, 0));
         R.s[j] = __builtin_amdgcn_raw_buffer_load_b16(T.rsrc, (int)(sc + (8u >> RS) * j), 0, 0);
+    }
+}
+
+// Make a chunk's registers opaque to the optimiser.  Called where a chunk
+// is reused (each token group of a tile that stays in registers): without
+// it the decoded bf16 weights, invariant across the groups, are hoisted out
+// of the group loop and take four registers per loaded one.  Emits no code;
+// the loads must already be complete (they are, after load_images).
+template <int NS>
+__device__ __forceinline__ void opaque(WRegs<NS>& R) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        asm volatile("" : "+v"(R.w[j].x), "+v"(R.w[j].y), "+v"(R.w[j].z), "+v"(R.w[j].w));
+        asm volatile("" : "+v"(R.s[j]));
     }
 }
 
@@ -270,52 +348,55 @@ __device__ __forceinline__ ABase abase(const Frags& F, int p, int c0) {
 
 // MFMAs of one loaded chunk for M weight tiles that share the same staged
 // activations (gate and up of one expert, or several row tiles of one
-// matrix) against P token pairs: acc[m][p][0..1] += tokens 2p, 2p+1 of tile
-// m.  Every step reads the A fragments once for all M tiles, and the M
-// independent MFMA chains interleave.  Steps j >= rem (past the tile) read
-// the zero block and carry a zero scale, so the chunk is straight-line code.
+// matrix) against the first np (<= P) token pairs: acc[m][p][0..1] +=
+// tokens 2p, 2p+1 of tile m.  Every step reads the A fragments once for all
+// M tiles, and the M independent MFMA chains interleave.  rem = steps left
+// in the tile from this chunk: steps j >= rem are skipped (uniform branch),
+// and at step rem - 1 lanes without a sub-group (cols % 128 != 0) take a
+// zero scale.  One code path serves every np, so the loaded chunk keeps its
+// registers whatever the token count.
 template <int NS, int P, int M>
-__device__ __forceinline__ void wmma(const WRegs<NS> (&R)[M], const ABase (&B)[P], const uint8_t* zero,
-                                     int rem, float (&acc)[M][P][2]) {
+__device__ __forceinline__ void wmma(const WRegs<NS> (&R)[M], const ABase (&B)[P], int rem, int np,
+                                     float (&acc)[M][P][2]) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const bool in = j < rem;  // uniform
-        float s[M];
-        bf16x8_t bv[M][4];
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            s[m] = (R[m].ok && j < R[m].last) ? f16_bits_to_f32(R[m].s[j]) : 0.0f;
-            bv[m][0] = q4_word_to_bf16x8(R[m].w[j].x);
-            bv[m][1] = q4_word_to_bf16x8(R[m].w[j].y);
-            bv[m][2] = q4_word_to_bf16x8(R[m].w[j].z);
-            bv[m][3] = q4_word_to_bf16x8(R[m].w[j].w);
-        }
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const uint8_t* pa = in ? B[p].a : zero;
-            const uint8_t* po = in ? B[p].o : zero;
-            const float4 o = *reinterpret_cast<const float4*>(po + j * 64);
-            uint4 a[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) a[d] = *reinterpret_cast<const uint4*>(pa + j * 256 + d * 16);
-            f32x4_t c[M];
+        if (j < rem) {  // uniform
+            float s[M];
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                c[m][0] = o.x;
-                c[m][1] = o.y;
-                c[m][2] = o.z;
-                c[m][3] = o.w;
+                s[m] = f16_bits_to_f32(R[m].s[j]);
+                if (j == rem - 1 && !R[m].lastok) s[m] = 0.0f;
             }
 #pragma unroll
-            for (int d = 0; d < 4; ++d)
+            for (int p = 0; p < P; ++p) {
+                if (p > 0 && p >= np) break;  // uniform: pairs staged in this token group
+                const float4 o = *reinterpret_cast<const float4*>(B[p].o + j * 64);
+                f32x4_t c[M];
 #pragma unroll
-                for (int m = 0; m < M; ++m)
-                    c[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[d]),
-                                                                   bv[m][d], c[m], 0, 0, 0);
+                for (int m = 0; m < M; ++m) {
+                    c[m][0] = o.x;
+                    c[m][1] = o.y;
+                    c[m][2] = o.z;
+                    c[m][3] = o.w;
+                }
+                // one A fragment and one decoded weight word per MFMA keeps
+                // the step's temporaries to a few registers beside the chunk
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                acc[m][p][0] = __builtin_fmaf(s[m], c[m][0] + c[m][1], acc[m][p][0]);
-                acc[m][p][1] = __builtin_fmaf(s[m], c[m][2] + c[m][3], acc[m][p][1]);
+                for (int d = 0; d < 4; ++d) {
+                    const uint4 a = *reinterpret_cast<const uint4*>(B[p].a + j * 256 + d * 16);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const uint32_t w = d == 0 ? R[m].w[j].x : d == 1 ? R[m].w[j].y
+                                         : d == 2 ? R[m].w[j].z : R[m].w[j].w;
+                        c[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8_t, a), q4_word_to_bf16x8(w), c[m], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    acc[m][p][0] = __builtin_fmaf(s[m], c[m][0] + c[m][1], acc[m][p][0]);
+                    acc[m][p][1] = __builtin_fmaf(s[m], c[m][2] + c[m][3], acc[m][p][1]);
+                }
             }
         }
         // keep each step's LDS reads next to their MFMAs: hoisting all of them

@@ -37,16 +37,32 @@ __device__ __forceinline__ float div_rn(float a, float b) { return (float)((doub
 // Router GEMV: logits[t][e] = W_r[e, :] . x[t, :] (bf16 x f32, fp32 FMAs) in the
 // canonical order: lane l takes 8-column chunks l, l+64, ... with fused
 // multiply-adds, then a butterfly over the 64 lanes.  One wave per expert row,
-// kRouterTokBlock tokens per wave.  Grid (ceil(E/4), ceil(T/8)).
+// kRouterTokBlock tokens per wave.  Grid (ceil(E/4), ceil(T/8)).  With
+// make_xf the workgroups of a token block also write those tokens' fragment
+// images (one token per workgroup, round robin), which the grouped gate/up
+// kernel copies straight into LDS.
 // ---------------------------------------------------------------------------
+namespace {
+
+__device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
+    const int H = a.L.hidden;
+    const float* row = dptr<const float>(a.x) + (size_t)t * H;
+    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
+    for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) write_image_group(row, H, g, img);
+}
+
+}  // namespace
+
 extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) {
     const int wave = threadIdx.x >> 6;
     const int lane = lane_id();
     const int E = a.L.experts, H = a.L.hidden;
     const int e = blockIdx.x * 4 + wave;
     const int t0 = blockIdx.y * kRouterTokBlock;
-    if (e >= E) return;
     const int nt = min(kRouterTokBlock, a.T - t0);
+    if (a.make_xf)
+        for (int t = t0 + (int)blockIdx.x; t < t0 + nt; t += gridDim.x) write_image(a, t);
+    if (e >= E) return;
     const uint16_t* w = dptr<const uint16_t>(a.L.router_w) + (size_t)e * H;
     const float* x = dptr<const float>(a.x) + (size_t)t0 * H;
     float acc[kRouterTokBlock];
@@ -84,6 +100,12 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs 
         for (int o = 32; o >= 1; o >>= 1) v += shfl_xor(v, o);
         if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * E + e] = v;
     }
+}
+
+// Fragment images of x alone, for callers that route from their own logits.
+// Grid (T), 256 threads.
+extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs a) {
+    write_image(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -221,7 +243,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a)
 // inv[t*k + j] = pos (-1 for unused pick slots), uniq[] (experts with picks,
 // ascending), meta[0] = unique count (meta[1], the error flags, cleared), and
 // the expert table et[u] for u < min(T*k, E) that the grouped kernels read
-// (blob address through the slot table, positions, first two tokens).
+// (blob address through the slot table, positions, first kEntryToks tokens).
 // Stability comes from ranking each pick by the tokens before it inside a
 // 64-token block (one bit per lane) plus a running per-expert base.
 // ---------------------------------------------------------------------------
@@ -254,7 +276,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
     __shared__ int base[kMaxExperts];
     __shared__ int gsl[kMaxExperts + 1];
     __shared__ int uniq_l[kMaxExperts];
-    __shared__ int tok01[kMaxExperts][2];
+    __shared__ int tokf[kMaxExperts][kEntryToks];
     __shared__ uint32_t mlo[kMaxExperts];
     __shared__ uint32_t mhi[kMaxExperts];
     __shared__ int scan_sh[4];
@@ -269,7 +291,8 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
     for (int e = tid; e < E; e += 256) {
         cnt_e[e] = 0;
         base[e] = 0;
-        tok01[e][0] = tok01[e][1] = -1;
+#pragma unroll
+        for (int q = 0; q < kEntryToks; ++q) tokf[e][q] = -1;
     }
     __syncthreads();
     for (int p = tid; p < T * k; p += 256) {
@@ -334,7 +357,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
                     const int pos = gsl[e] + rank;
                     perm[pos] = t * k + j;
                     inv[t * k + j] = pos;
-                    if (rank < 2) tok01[e][rank] = t;
+                    if (rank < kEntryToks) tokf[e][rank] = t;
                 } else {
                     inv[t * k + j] = -1;
                 }
@@ -350,22 +373,20 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
     const int maxu = min(T * k, E);
     for (int u = tid; u < maxu; u += 256) {
         ExpertEntry x;
-        x.pad0 = 0;
         if (u < nu) {
             const int e = uniq_l[u];
             const int slot = slots[e];
             x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
             x.p0 = gsl[e];
             x.ntok = cnt_e[e];
-            x.tok0 = tok01[e][0];
-            x.tok1 = tok01[e][1];
-            x.e = e;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = tokf[e][q];
         } else {
             x.blob = 0ull;
             x.p0 = 0;
             x.ntok = 0;
-            x.tok0 = x.tok1 = -1;
-            x.e = -1;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = -1;
         }
         et[u] = x;
     }
@@ -394,11 +415,18 @@ __device__ __forceinline__ ExpertEntry entry_of(const GroupedArgs& a, int u) {
     x.blob = (uint64_t)lo.x | ((uint64_t)lo.y << 32);
     x.p0 = (int)lo.z;
     x.ntok = (int)lo.w;
-    x.tok0 = (int)hi.x;
-    x.tok1 = (int)hi.y;
-    x.e = (int)hi.z;
-    x.pad0 = 0;
+    x.tok[0] = (int)hi.x;
+    x.tok[1] = (int)hi.y;
+    x.tok[2] = (int)hi.z;
+    x.tok[3] = (int)hi.w;
     return x;
+}
+
+// Token of the expert's i-th (token, pick) pair: from the entry for the first
+// kEntryToks (no dependent load), else through the dispatch permutation.
+__device__ __forceinline__ int pair_token(const ExpertEntry& x, int i, const int* perm, int k) {
+    static_assert(kEntryToks == 4, "select chain below");
+    return i == 0 ? x.tok[0] : i == 1 ? x.tok[1] : i == 2 ? x.tok[2] : i == 3 ? x.tok[3] : perm[x.p0 + i] / k;
 }
 
 __device__ __forceinline__ void missing_expert(const GroupedArgs& a, const ExpertEntry& x, float* out,
@@ -410,34 +438,45 @@ __device__ __forceinline__ void missing_expert(const GroupedArgs& a, const Exper
 }
 
 // gate/up MFMAs for one staged token group of P pairs, then SiLU * up into
-// act.  GU (gate, up) holds the first chunk on entry; later chunks are loaded
-// right after the previous one's MFMAs.  When `next` is set the first chunk
-// is loaded again for the following token group before the epilogue, so its
-// latency overlaps the stores and the restaging.
-template <int P, int RS>
-__device__ __forceinline__ void gateup_group(const Frags& F, WRegs<kStepChunk> (&GU)[2],
-                                             const WTile<RS>& TG, const WTile<RS>& TU, int I,
-                                             int n0, int S, int t0, int ntok, int p0, bool next,
-                                             float* act) {
+// act.  GU (gate, up) holds the tile's first chunk on entry.  A tile of one
+// chunk (ONE: S <= NS) is straight-line code and simply stays in registers
+// for the next token group.  Longer tiles load each further chunk right
+// after the previous one's MFMAs and, when another token group follows
+// (`reload`), the first chunk again before the epilogue, so that latency
+// overlaps the stores and the next group's image copy.
+template <int P, int NS, bool ONE, int RS>
+__device__ __forceinline__ void gateup_group(const Frags& F, WRegs<NS> (&GU)[2], const WTile<RS>& TG,
+                                             const WTile<RS>& TU, int I, int n0, int S, int t0,
+                                             int nt, int p0, bool reload, float* act) {
+    const int np = (nt + 1) >> 1;
     float acc[2][P][2];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
         for (int p = 0; p < P; ++p) acc[m][p][0] = acc[m][p][1] = 0.0f;
-#pragma nounroll
-    for (int c0 = 0;;) {
+    if constexpr (ONE) {
+        opaque(GU[0]);
+        opaque(GU[1]);
         ABase B[P];
 #pragma unroll
-        for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
-        wmma(GU, B, F.lds, S - c0, acc);
-        c0 += kStepChunk;
-        if (c0 >= S) break;
-        wload(GU[0], TG, c0);
-        wload(GU[1], TU, c0);
-    }
-    if (next) {
-        wload(GU[0], TG, 0);
-        wload(GU[1], TU, 0);
+        for (int p = 0; p < P; ++p) B[p] = abase(F, p, 0);
+        wmma(GU, B, S, np, acc);
+    } else {
+#pragma nounroll
+        for (int c0 = 0;;) {
+            ABase B[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
+            wmma(GU, B, S - c0, np, acc);
+            c0 += NS;
+            if (c0 >= S) break;
+            wload(GU[0], TG, c0);
+            wload(GU[1], TU, c0);
+        }
+        if (reload) {
+            wload(GU[0], TG, 0);
+            wload(GU[1], TU, 0);
+        }
     }
     const int lane = lane_id();
     const int row = n0 + (lane & 15);
@@ -445,16 +484,16 @@ __device__ __forceinline__ void gateup_group(const Frags& F, WRegs<kStepChunk> (
     for (int p = 0; p < P; ++p) {
         const float g0 = tile_reduce(acc[0][p][0]), g1 = tile_reduce(acc[0][p][1]);
         const float u0 = tile_reduce(acc[1][p][0]), u1 = tile_reduce(acc[1][p][1]);
-        const int t = t0 + 2 * p + (lane >> 4);
-        if (row < I && lane < 32 && t < ntok) {
+        const int t = 2 * p + (lane >> 4);  // within the group
+        if (row < I && lane < 32 && t < nt) {
             const float g = lane < 16 ? g0 : g1;
             const float u = lane < 16 ? u0 : u1;
-            act[(size_t)(p0 + t) * I + row] = g / (1.0f + expf(-g)) * u;
+            act[(size_t)(p0 + t0 + t) * I + row] = g / (1.0f + expf(-g)) * u;
         }
     }
 }
 
-template <int RS>
+template <int NS, bool ONE, int RS>
 __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -476,59 +515,61 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     const Frags F = frags_at(lds, H);
     const WTile<RS> TG = wtile<RS>(x.blob + L.gate_off, I, H, n0);
     const WTile<RS> TU = wtile<RS>(x.blob + L.up_off, I, H, n0);
-    WRegs<kStepChunk> GU[2];
+    WRegs<NS> GU[2];
     wload(GU[0], TG, 0);
     wload(GU[1], TU, 0);
     zero_block(F, threadIdx.x, blockDim.x);
     const int* perm = dptr<const int>(a.W.perm);
-    const float* xs = dptr<const float>(a.x);
+    const uint64_t xf = a.W.xf;
+    const uint64_t ib = (uint64_t)image_bytes(H);
     const int cap = min(kMaxPairs, a.pairs_cap);
     for (int tb = 0; tb < x.ntok; tb += 2 * cap) {
         const int nt = min(2 * cap, x.ntok - tb);
-        const bool next = tb + nt < x.ntok;
+        const bool reload = tb + nt < x.ntok;
         if (tb > 0) __syncthreads();
-        stage_rows(F, nt, [&](int t) {
-            const int i = tb + t;
-            const int tok = i == 0 ? x.tok0 : i == 1 ? x.tok1 : perm[x.p0 + i] / k;
-            return xs + (size_t)tok * H;
-        }, threadIdx.x, blockDim.x);
+        load_images(F, nt, [&](int t) { return xf + (uint64_t)pair_token(x, tb + t, perm, k) * ib; });
         __syncthreads();
-        if constexpr (kMaxPairs > 1) {
-            if (nt > 2) {
-                gateup_group<2>(F, GU, TG, TU, I, n0, S, tb, x.ntok, x.p0, next, act);
-                continue;
-            }
-        }
-        gateup_group<1>(F, GU, TG, TU, I, n0, S, tb, x.ntok, x.p0, next, act);
+        gateup_group<kMaxPairs, NS, ONE>(F, GU, TG, TU, I, n0, S, tb, nt, x.p0, reload, act);
     }
 }
 
 // down MFMAs for one staged token group of P pairs over TW row tiles, into
-// y; D holds the first chunk on entry (as for gateup_group).
-template <int P, int TW, int RS>
-__device__ __forceinline__ void down_group(const Frags& F, WRegs<kStepChunk> (&D)[TW],
+// y; D holds the first chunk on entry, and ONE / reload mean what they do
+// for gateup_group.
+template <int P, int TW, int NS, bool ONE, int RS>
+__device__ __forceinline__ void down_group(const Frags& F, WRegs<NS> (&D)[TW],
                                            const WTile<RS> (&TD)[TW], int H, const int (&n0)[TW],
-                                           int S, int t0, int ntok, int p0, bool next, float* y) {
+                                           int S, int t0, int nt, int p0, bool reload, float* y) {
+    const int np = (nt + 1) >> 1;
     const int lane = lane_id();
     float acc[TW][P][2];
 #pragma unroll
     for (int tw = 0; tw < TW; ++tw)
 #pragma unroll
         for (int p = 0; p < P; ++p) acc[tw][p][0] = acc[tw][p][1] = 0.0f;
-#pragma nounroll
-    for (int c0 = 0;;) {
+    if constexpr (ONE) {
+#pragma unroll
+        for (int tw = 0; tw < TW; ++tw) opaque(D[tw]);
         ABase B[P];
 #pragma unroll
-        for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
-        wmma(D, B, F.lds, S - c0, acc);
-        c0 += kStepChunk;
-        if (c0 >= S) break;
+        for (int p = 0; p < P; ++p) B[p] = abase(F, p, 0);
+        wmma(D, B, S, np, acc);
+    } else {
+#pragma nounroll
+        for (int c0 = 0;;) {
+            ABase B[P];
 #pragma unroll
-        for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], c0);
-    }
-    if (next) {
+            for (int p = 0; p < P; ++p) B[p] = abase(F, p, c0);
+            wmma(D, B, S - c0, np, acc);
+            c0 += NS;
+            if (c0 >= S) break;
 #pragma unroll
-        for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], 0);
+            for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], c0);
+        }
+        if (reload) {
+#pragma unroll
+            for (int tw = 0; tw < TW; ++tw) wload(D[tw], TD[tw], 0);
+        }
     }
 #pragma unroll
     for (int tw = 0; tw < TW; ++tw) {
@@ -536,13 +577,13 @@ __device__ __forceinline__ void down_group(const Frags& F, WRegs<kStepChunk> (&D
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const float v0 = tile_reduce(acc[tw][p][0]), v1 = tile_reduce(acc[tw][p][1]);
-            const int t = t0 + 2 * p + (lane >> 4);
-            if (row < H && lane < 32 && t < ntok) y[(size_t)(p0 + t) * H + row] = lane < 16 ? v0 : v1;
+            const int t = 2 * p + (lane >> 4);  // within the group
+            if (row < H && lane < 32 && t < nt) y[(size_t)(p0 + t0 + t) * H + row] = lane < 16 ? v0 : v1;
         }
     }
 }
 
-template <int TW, int RS>
+template <int TW, int NS, bool ONE, int RS>
 __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -561,7 +602,7 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     }
     const int S = tile_steps(I);
     const Frags F = frags_at(lds, I);
-    WRegs<kStepChunk> D[TW];
+    WRegs<NS> D[TW];
     WTile<RS> TD[TW];
     int n0[TW];
 #pragma unroll
@@ -575,18 +616,12 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     const int cap = min(kMaxPairs, a.pairs_cap);
     for (int tb = 0; tb < x.ntok; tb += 2 * cap) {
         const int nt = min(2 * cap, x.ntok - tb);
-        const bool next = tb + nt < x.ntok;
+        const bool reload = tb + nt < x.ntok;
         if (tb > 0) __syncthreads();
         stage_rows(F, nt, [&](int t) { return act + (size_t)(x.p0 + tb + t) * I; },
                    threadIdx.x, blockDim.x);
         __syncthreads();
-        if constexpr (kMaxPairs > 1) {
-            if (nt > 2) {
-                down_group<2, TW>(F, D, TD, H, n0, S, tb, x.ntok, x.p0, next, y);
-                continue;
-            }
-        }
-        down_group<1, TW>(F, D, TD, H, n0, S, tb, x.ntok, x.p0, next, y);
+        down_group<kMaxPairs, TW, NS, ONE>(F, D, TD, H, n0, S, tb, nt, x.p0, reload, y);
     }
 }
 
@@ -601,25 +636,43 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
         default: call(2); break;             \
     }
 
+// Gate/up: a tile of at most kGateupChunk steps is loaded in one piece and
+// kept in registers; longer tiles stream kGateupLoopChunk steps at a time.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_gateup(const GroupedArgs a) {
-#define LP_GATEUP(rs) gateup_body<rs>(a)
-    LP_BY_RS(a.L.group, LP_GATEUP)
+    if (tile_steps(a.L.hidden) <= kGateupChunk) {
+#define LP_GATEUP(rs) gateup_body<kGateupChunk, true, rs>(a)
+        LP_BY_RS(a.L.group, LP_GATEUP)
 #undef LP_GATEUP
+    } else {
+#define LP_GATEUP(rs) gateup_body<kGateupLoopChunk, false, rs>(a)
+        LP_BY_RS(a.L.group, LP_GATEUP)
+#undef LP_GATEUP
+    }
 }
 
+// Down, two row tiles per wave: tiles of at most kDownChunk steps (the host
+// picks this kernel only for those), loaded in one piece.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down(const GroupedArgs a) {
-#define LP_DOWN(rs) down_body<2, rs>(a)
+#define LP_DOWN(rs) down_body<2, kDownChunk, true, rs>(a)
     LP_BY_RS(a.L.group, LP_DOWN)
 #undef LP_DOWN
 }
 
+// Down, one row tile per wave: up to kDownWideChunk steps in one piece,
+// longer tiles streamed kDownLoopChunk steps at a time.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down_wide(const GroupedArgs a) {
-#define LP_DOWN(rs) down_body<1, rs>(a)
-    LP_BY_RS(a.L.group, LP_DOWN)
+    if (tile_steps(a.L.inter) <= kDownWideChunk) {
+#define LP_DOWN(rs) down_body<1, kDownWideChunk, true, rs>(a)
+        LP_BY_RS(a.L.group, LP_DOWN)
 #undef LP_DOWN
+    } else {
+#define LP_DOWN(rs) down_body<1, kDownLoopChunk, false, rs>(a)
+        LP_BY_RS(a.L.group, LP_DOWN)
+#undef LP_DOWN
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -20,9 +20,15 @@ constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
-constexpr int kMaxPairs = 1;           // token pairs the grouped kernels stage at once
-constexpr int kStepChunk = 8;          // MFMA steps (4 sub-groups each) per register chunk
-constexpr int kZeroBytes = 256 * kStepChunk;  // LDS zero block read by idle MFMA lanes
+constexpr int kMaxPairs = 2;           // token pairs the grouped kernels stage at once
+constexpr int kMaxChunk = 16;          // most MFMA steps (4 sub-groups each) one register chunk holds
+constexpr int kGateupChunk = 16;       // gate/up tiles up to this many steps load in one piece
+constexpr int kGateupLoopChunk = 8;    // steps per chunk of longer gate/up tiles
+constexpr int kDownChunk = 8;          // steps per chunk in the two-tile grouped down kernel
+constexpr int kDownWideChunk = 16;     // one-tile down: tiles up to this many steps in one piece
+constexpr int kDownLoopChunk = 8;      // steps per chunk of longer one-tile down tiles
+constexpr int kGemvChunk = 8;          // steps per chunk in the 1:1 q4 GEMV
+constexpr int kZeroBytes = 256 * kMaxChunk;  // LDS zero block read by idle MFMA lanes
 
 // LDS bytes of the fragment area for `pairs` token pairs over `cols` columns:
 // a zero block, then per pair four (token, part) blocks of ngp sub-groups x
@@ -34,6 +40,12 @@ LPK_HD constexpr int frag_pair_bytes(int ngp) { return 4 * frag_th_stride(ngp) +
 LPK_HD constexpr int frag_lds_bytes(int cols, int pairs) {
     return kZeroBytes + pairs * frag_pair_bytes(frag_ngp(cols));
 }
+
+// A token row's fragment image in device memory, the form the grouped gate/up
+// kernel copies straight into LDS: part 0 (bf16(x)) and part 1
+// (bf16(x - bf16(x))) as [ngp][64 B] blocks in fragment order, then the
+// accumulator seeds [ngp][2] f32 (-136 * the part's sum over the sub-group).
+LPK_HD constexpr int image_bytes(int cols) { return 136 * frag_ngp(cols); }
 
 // ---- 1:1 launchers (crates/llmpager-cuda/src/kernels.rs) -------------------
 
@@ -87,14 +99,15 @@ struct LayerView {
 
 // One routed expert as the grouped kernels see it, written by the dispatch
 // kernel for u < min(T*k, E) (ntok = 0 past the unique count).
+constexpr int kEntryToks = 4;  // tokens an entry names directly (2 * kMaxPairs)
 struct ExpertEntry {
-    uint64_t blob;       // device address of the expert's blob (0 if not resident)
-    int32_t p0;          // first dispatch position of its (token, pick) pairs
-    int32_t ntok;        // number of those pairs
-    int32_t tok0, tok1;  // tokens of the first two pairs (-1 if absent)
-    int32_t e;           // expert id
-    int32_t pad0;
+    uint64_t blob;             // device address of the expert's blob (0 if not resident)
+    int32_t p0;                // first dispatch position of its (token, pick) pairs
+    int32_t ntok;              // number of those pairs
+    int32_t tok[kEntryToks];   // tokens of the first pairs (-1 if absent)
 };
+static_assert(sizeof(ExpertEntry) == 32, "two 16-byte loads per entry");
+static_assert(2 * kMaxPairs <= kEntryToks, "the first token group comes from the entry");
 
 // Workspace carve-up for T tokens (offsets in bytes from `ws`).
 struct Workspace {
@@ -110,13 +123,15 @@ struct Workspace {
     uint64_t et;         // ExpertEntry [E]
     uint64_t act;        // f32 [T * k, I] expert-major activations
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
+    uint64_t xf;         // [T] fragment images of the layer input (image_bytes(H) each)
 };
 
 struct RouteArgs {
     LayerView L;
     Workspace W;
     uint64_t x;          // f32 [T, H]
-    int32_t T, pad0;
+    int32_t T;
+    int32_t make_xf;     // router: also write the fragment images of x into W.xf
 };
 
 struct GroupedArgs {

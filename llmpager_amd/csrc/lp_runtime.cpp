@@ -55,6 +55,7 @@ enum Fn {
     kDown,
     kDownWide,
     kCombine,
+    kXImage,
     kNumFns
 };
 
@@ -70,7 +71,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_router"},     {"lp_moe.hsaco", "lp_moe_topk"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_gateup"},
     {"lp_moe.hsaco", "lp_moe_down"},       {"lp_moe.hsaco", "lp_moe_down_wide"},
-    {"lp_moe.hsaco", "lp_moe_combine"},
+    {"lp_moe.hsaco", "lp_moe_combine"},    {"lp_moe.hsaco", "lp_moe_ximage"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco"};
@@ -475,6 +476,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->et = take(E * sizeof(ExpertEntry));
     out->act = take(t * k * I * 4);
     out->y = take(t * k * H * 4);
+    out->xf = take(t * (uint64_t)image_bytes((int)H));
     out->total = o;
     return LP_OK;
 }
@@ -538,6 +540,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->et = ws + lay.et;
     W->act = ws + lay.act;
     W->y = ws + lay.y;
+    W->xf = ws + lay.xf;
 }
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
@@ -554,6 +557,7 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.x = x;
     ra.T = T;
+    ra.make_xf = 1;
     dim3 g((unsigned)((d->experts + 3) / 4), (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
     if (int r = launch(c, kRouter, g, dim3(256), 0, s, ra)) return r;
     return route_tail(c, ra, s);
@@ -571,10 +575,20 @@ int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, 
     return route_tail(c, ra, s);
 }
 
-int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                   uint64_t ws, lp_stream s) {
+// The grouped expert kernels and the combine; the fragment images of x are
+// written first unless the router kernel of lp_moe_forward already did.
+static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                        uint64_t ws, lp_stream s, bool have_images) {
     if (int r = check_desc(c, d, T)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
+    if (!have_images) {
+        RouteArgs ra{};
+        fill_views(d, ws, T, &ra.L, &ra.W);
+        ra.x = x;
+        ra.T = T;
+        ra.make_xf = 1;
+        if (int r = launch(c, kXImage, dim3((unsigned)T), dim3(256), 0, s, ra)) return r;
+    }
     GroupedArgs ga{};
     fill_views(d, ws, T, &ga.L, &ga.W);
     ga.x = x;
@@ -607,8 +621,8 @@ int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
     }
     {
         const int steps = ((I / 32) + 3) / 4;
-        const Fn f = steps <= kStepChunk ? kDown : kDownWide;
-        const int tw = steps <= kStepChunk ? 2 : 1;
+        const Fn f = steps <= kDownChunk ? kDown : kDownWide;
+        const int tw = steps <= kDownChunk ? 2 : 1;
         const int w = pick_w(H, tw);
         const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
         if (int r = launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), fr_i, s, ga))
@@ -618,10 +632,15 @@ int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
                   s, ga);
 }
 
+int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                   uint64_t ws, lp_stream s) {
+    return experts_impl(c, d, x, h, T, ws, s, false);
+}
+
 int lp_moe_forward(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t ws, lp_stream s) {
     if (int r = lp_moe_route(c, d, x, T, ws, s)) return r;
-    return lp_moe_experts(c, d, x, h, T, ws, s);
+    return experts_impl(c, d, x, h, T, ws, s, true);
 }
 
 int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T, lp_stream s,
