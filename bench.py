@@ -39,7 +39,8 @@ EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 DOMINANT = "lp_moe_gateup"
-KERNELS = ("lp_moe_router", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_gateup", "lp_moe_down",
+KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_ximage",
+           "lp_moe_gateup", "lp_moe_down",
            "lp_moe_down_wide", "lp_moe_combine")
 
 

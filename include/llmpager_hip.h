@@ -258,6 +258,10 @@ int lp_synth_f32_bf16(float* dst, uint64_t n, float std, uint64_t seed, uint64_t
 float lp_route_expf(float x);
 /* out[i] = lp_route_expf(bits_to_float(first + i*stride)), i < n. */
 void lp_route_expf_sweep(uint32_t first, uint32_t stride, uint64_t n, float* out);
+/* The same sweep evaluated on the device the way the routing kernels do
+ * (table in registers, whole waves); out: device f32 [n]. */
+int lp_route_expf_device(lp_ctx* ctx, uint32_t first, uint32_t stride, uint64_t n, uint64_t out,
+                         lp_stream s);
 
 #ifdef __cplusplus
 }

@@ -111,6 +111,7 @@ def _sig(lib):
         "lp_profile_read_sync": (i32, [vp, C.c_char_p, P(C.c_double), P(C.c_int64)]),
         "lp_route_expf": (f32, [f32]),
         "lp_route_expf_sweep": (None, [C.c_uint32, C.c_uint32, u64, vp]),
+        "lp_route_expf_device": (i32, [vp, C.c_uint32, C.c_uint32, u64, u64, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)

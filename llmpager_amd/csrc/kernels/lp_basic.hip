@@ -155,3 +155,14 @@ extern "C" __global__ void __launch_bounds__(256) lp_bf16_gemv(const Bf16GemvArg
     for (int o = 32; o >= 1; o >>= 1) acc += shfl_xor(acc, o);
     if (lane == 0) reinterpret_cast<float*>(a.y)[row] = acc;
 }
+
+// expf over float bit patterns, the way routing evaluates it on the device
+// (expf_glibc_wave: table in registers, whole waves): out[i] =
+// expf(bits(first + i * stride)), i < n.  For parity checks against glibc.
+extern "C" __global__ void __launch_bounds__(256) lp_expf_wave(const ExpfSweepArgs a) {
+    const uint64_t tabv = exp2tab_lane();
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t bits = a.first + (uint32_t)(i * a.stride);
+    const float y = expf_glibc_wave(__uint_as_float(bits), tabv);  // every lane, in or out of range
+    if (i < a.n) reinterpret_cast<float*>(a.out)[i] = y;
+}

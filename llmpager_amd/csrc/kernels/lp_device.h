@@ -34,12 +34,31 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    for (int o = 32; o >= 1; o >>= 1) {
-        uint64_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
+// Wave-wide reduction of a 32-bit value through DPP (gfx9 row shifts and row
+// broadcasts, no LDS traffic); every lane gets the result.  ident is the
+// identity of op, read where a lane has no source.  Lane i of each row first
+// gathers lanes i-3..i of the original value, then i-7..i and i-15..i of the
+// running value; row broadcasts fold rows 0+1 into lane 31 and all four rows
+// into lane 63.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v0, uint32_t ident, Op op) {
+    const int id = (int)ident;
+    uint32_t v = op(v0, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v0, 0x111, 0xf, 0xf, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v0, 0x112, 0xf, 0xf, false));  // row_shr:2
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v0, 0x113, 0xf, 0xf, false));  // row_shr:3
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x114, 0xf, 0xe, false));   // row_shr:4
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x118, 0xf, 0xc, false));   // row_shr:8
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xa, 0xf, false));   // row_bcast:15
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xc, 0xf, false));   // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    return wave_reduce_u32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    return wave_reduce_u32(v, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
 }
 
 // Eight q4 values (one 32-bit word, value p at bits [4p, 4p+4), stored as q+8)

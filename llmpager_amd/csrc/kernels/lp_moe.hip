@@ -51,9 +51,8 @@ __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
     for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) write_image_group(row, H, g, img);
 }
 
-}  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) {
+__device__ __forceinline__ void router_rows(const RouteArgs& a) {
     const int wave = threadIdx.x >> 6;
     const int lane = lane_id();
     const int E = a.L.experts, H = a.L.hidden;
@@ -102,6 +101,10 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs 
     }
 }
 
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) { router_rows(a); }
+
 // Fragment images of x alone, for callers that route from their own logits.
 // Grid (T), 256 threads.
 extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs a) {
@@ -119,122 +122,156 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs 
 // expf is glibc's (lp_expf.h); every f32 operation is the reference's, in its
 // order, so ids, order and weights match the host path bit for bit.
 // ---------------------------------------------------------------------------
-extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a) {
-    __shared__ float sh_v[4][kMaxExperts];
-    const int wave = threadIdx.x >> 6;
-    const int lane = lane_id();
-    const int t = blockIdx.x * 4 + wave;
-    if (t >= a.T) return;
-    const int E = a.L.experts, k = a.L.top_k;
-    constexpr int PER = kMaxExperts / 64;
-    const float* lg = dptr<const float>(a.W.logits) + (size_t)t * E;
-    float* sv = sh_v[wave];
-    uint32_t key[PER];
+namespace {
 
+// Top-k of token t by the calling wave, PER candidates per lane (expert
+// i = lane + 64 q); sv is the wave's LDS row of kMaxExperts floats (the
+// probabilities, read back for the picks).  The in-order sum runs as a
+// chain of adds over v_readlane values; each pick is two DPP reductions:
+// the largest ordered key, then the lowest id holding it.
+template <int PER>
+__device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv, int* ids_l, int* cnt_l) {
+    const int lane = lane_id();
+    const int E = a.L.experts, k = a.L.top_k;
+    const float* lg = dptr<const float>(a.W.logits) + (size_t)t * E;
+    const uint64_t tabv = exp2tab_lane();  // glibc's 2^(i/32) table, one entry per lane
+    uint32_t key[PER];
+    float v[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int i = lane + 64 * q;
+        v[q] = i < E ? lg[i] : 0.0f;
+        key[q] = 0u;
+    }
     if (a.L.gating == 0) {
-        float m = -3.40282347e+38f;  // f32::MIN
+        uint32_t mk = 0u;  // max over the ordered keys = the largest logit (f32::MIN start)
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (lane + 64 * q < E) mk = mk > ordered_key(v[q]) ? mk : ordered_key(v[q]);
+        mk = wave_max_u32(mk);
+        float m = __uint_as_float((mk & 0x80000000u) ? (mk & 0x7fffffffu) : ~mk);
+        m = fmaxf(m, -3.40282347e+38f);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const float ex = expf_glibc_wave(v[q] - m, tabv);  // every lane takes part
+            v[q] = lane + 64 * q < E ? ex : 0.0f;
+        }
+        // z = e_0 + e_1 + ... in id order, from -0.0 (the reference's fold):
+        // a chain of adds over lane values read with v_readlane
+        float z = -0.0f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (64 * q >= E) break;  // uniform
+            const int n = E - 64 * q;
+#pragma unroll 8
+            for (int l = 0; l < 64; ++l)
+                if (l < n) z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+        }
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int i = lane + 64 * q;
-            if (i < E) m = fmaxf(m, lg[i]);
-        }
-        m = wave_max(m);
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = lane + 64 * q;
-            if (i < E) sv[i] = expf_glibc(lg[i] - m);
-        }
-        wave_sync_lds();
-        float z = 0.0f;
-        if (lane == 0) {
-            z = -0.0f;
-            for (int i = 0; i < E; ++i) z = z + sv[i];
-        }
-        z = __shfl(z, 0, 64);
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = lane + 64 * q;
-            key[q] = 0u;
             if (i < E) {
-                const float p = div_rn(sv[i], z);
+                const float p = div_rn(v[q], z);
                 key[q] = ordered_key(p);
+                sv[i] = p;
             }
-        }
-        wave_sync_lds();
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = lane + 64 * q;
-            if (i < E) sv[i] = div_rn(sv[i], z);
         }
     } else {
         const float* bias = dptr<const float>(a.L.router_bias);
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int i = lane + 64 * q;
-            key[q] = 0u;
+            const float ex = expf_glibc_wave(-v[q], tabv);  // every lane takes part
             if (i < E) {
-                const float d = 1.0f + expf_glibc(-lg[i]);
-                const float s = div_rn(1.0f, d);
-                sv[i] = s;
-                key[q] = ordered_key((s + bias[i]) + 0.0f);  // -0 ranks equal to +0
+                const float d = 1.0f + ex;
+                const float sg = div_rn(1.0f, d);
+                sv[i] = sg;
+                key[q] = ordered_key((sg + bias[i]) + 0.0f);  // -0 ranks equal to +0
             }
         }
     }
     wave_sync_lds();
 
     const int n = k < E ? k : E;
-    uint32_t picked = 0u;
     int ids[kMaxTopK];
     float val[kMaxTopK];
-    for (int j = 0; j < n; ++j) {
-        uint64_t best = 0;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = lane + 64 * q;
-            if (i < E && !((picked >> q) & 1u)) {
-                const uint64_t c = ((uint64_t)key[q] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-                best = c > best ? c : best;
-            }
-        }
-        best = wave_max_u64(best);
-        const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-        if ((id & 63) == lane) picked |= 1u << (id >> 6);
+    for (int j = 0; j < kMaxTopK; ++j) {
+        ids[j] = -1;
+        val[j] = 0.0f;
+        if (j >= n) continue;
+        uint32_t bk = 0u;  // keys of live candidates are >= 1 (ordered_key(+0) = 0x80000000)
+#pragma unroll
+        for (int q = 0; q < PER; ++q) bk = key[q] > bk ? key[q] : bk;
+        const uint32_t M = wave_max_u32(bk);
+        uint32_t bid = 0xffffffffu;
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (key[q] == M && key[q] != 0u) bid = min(bid, (uint32_t)(lane + 64 * q));
+        const int id = (int)wave_min_u32(bid);
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (lane + 64 * q == id) key[q] = 0u;  // picked
         ids[j] = id;
         val[j] = sv[id];
     }
 
-    int kept = n;
-    float w[kMaxTopK];
     float s = -0.0f;
-    for (int j = 0; j < n; ++j) s = s + val[j];
-    if (a.L.gating == 0) {
-        for (int j = 0; j < n; ++j) w[j] = a.L.renorm ? div_rn(val[j], s) : val[j];
-    } else {
-        for (int j = 0; j < n; ++j) {
-            float v = val[j];
-            if (a.L.renorm && s > 0.0f) v = div_rn(v, s);
-            w[j] = v * a.L.routed_scaling;
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+        if (j < n) s = s + val[j];
+    // weights in pick order; lane j keeps pick j (min_weight compacts the
+    // survivors: pick j lands in slot kept-so-far)
+    int kept = 0;
+    int my_id = -1;
+    float my_w = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+        if (j >= n) continue;
+        float wj;
+        if (a.L.gating == 0) {
+            wj = a.L.renorm ? div_rn(val[j], s) : val[j];
+        } else {
+            wj = val[j];
+            if (a.L.renorm && s > 0.0f) wj = div_rn(wj, s);
+            wj = wj * a.L.routed_scaling;
+            if (a.L.min_weight > 0.0f && !(wj >= a.L.min_weight)) continue;
         }
-        if (a.L.min_weight > 0.0f) {
-            kept = 0;
-            for (int j = 0; j < n; ++j) {
-                if (w[j] >= a.L.min_weight) {
-                    ids[kept] = ids[j];
-                    w[kept] = w[j];
-                    ++kept;
-                }
-            }
+        if (lane == kept) {
+            my_id = ids[j];
+            my_w = wj;
         }
+        ++kept;
+    }
+    if (lane < k) {
+        dptr<int>(a.W.ids)[(size_t)t * k + lane] = my_id;
+        dptr<float>(a.W.wts)[(size_t)t * k + lane] = my_w;
+        if (ids_l) ids_l[t * k + lane] = my_id;
     }
     if (lane == 0) {
-        int* gids = dptr<int>(a.W.ids) + (size_t)t * k;
-        float* gw = dptr<float>(a.W.wts) + (size_t)t * k;
-        for (int j = 0; j < k; ++j) {
-            gids[j] = j < kept ? ids[j] : -1;
-            gw[j] = j < kept ? w[j] : 0.0f;
-        }
         dptr<int>(a.W.cnt)[t] = kept;
+        if (cnt_l) cnt_l[t] = kept;
     }
+}
+
+// Top-k of token t with the candidate count per lane the expert count needs;
+// ids_l / cnt_l (may be null) receive LDS copies of the picks.
+__device__ __forceinline__ void topk_any(const RouteArgs& a, int t, float* sv, int* ids_l = nullptr,
+                                         int* cnt_l = nullptr) {
+    if (a.L.experts <= 128)
+        topk_token<2>(a, t, sv, ids_l, cnt_l);
+    else if (a.L.experts <= 256)
+        topk_token<4>(a, t, sv, ids_l, cnt_l);
+    else
+        topk_token<kMaxExperts / 64>(a, t, sv, ids_l, cnt_l);
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a) {
+    __shared__ float sh_v[4][kMaxExperts];
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t < a.T) topk_any(a, t, sh_v[threadIdx.x >> 6]);
 }
 
 // ---------------------------------------------------------------------------
@@ -249,9 +286,9 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a)
 // ---------------------------------------------------------------------------
 namespace {
 
-// Exclusive scan of one int per thread over a 256-thread workgroup.
+// Exclusive scan of one int per thread over the workgroup (<= 16 waves).
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
-    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int lane = lane_id(), wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int x = v;
     for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(x, o, 64);
@@ -260,7 +297,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
     if (lane == 63) sh[wave] = x;
     __syncthreads();
     int wbase = 0, tot = 0;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < nw; ++w) {
         wbase += w < wave ? sh[w] : 0;
         tot += sh[w];
     }
@@ -269,33 +306,37 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
     return wbase + x - v;
 }
 
-}  // namespace
+// LDS of dispatch_all, carved from one buffer so that the single-workgroup
+// top-k + dispatch kernel can share it with its top-k phase.
+constexpr int kDispatchSmem = 4 * (kMaxExperts * 6 + (kMaxExperts + 4) + kMaxExperts * kEntryToks + 16);
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
-    __shared__ int cnt_e[kMaxExperts];
-    __shared__ int base[kMaxExperts];
-    __shared__ int gsl[kMaxExperts + 1];
-    __shared__ int uniq_l[kMaxExperts];
-    __shared__ int tokf[kMaxExperts][kEntryToks];
-    __shared__ uint32_t mlo[kMaxExperts];
-    __shared__ uint32_t mhi[kMaxExperts];
-    __shared__ int scan_sh[4];
+// ids / cnt: the picks (global, or LDS copies from the same workgroup);
+// slots: the slot table (global, or an LDS copy).
+__device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids,
+                                             const int* cnt, const int* slots) {
+    int* cnt_e = reinterpret_cast<int*>(sm);
+    int* base = cnt_e + kMaxExperts;
+    int* gsl = base + kMaxExperts;                       // kMaxExperts + 1 used
+    int* uniq_l = gsl + kMaxExperts + 4;
+    int (*tokf)[kEntryToks] = reinterpret_cast<int (*)[kEntryToks]>(uniq_l + kMaxExperts);
+    uint32_t* mlo = reinterpret_cast<uint32_t*>(uniq_l + kMaxExperts + kMaxExperts * kEntryToks);
+    uint32_t* mhi = mlo + kMaxExperts;
+    int* scan_sh = reinterpret_cast<int*>(mhi + kMaxExperts);
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const int nth = blockDim.x;  // 256 .. 1024; 4 * nth >= kMaxExperts
     const int E = a.L.experts, k = a.L.top_k, T = a.T;
-    const int* ids = dptr<const int>(a.W.ids);
-    const int* cnt = dptr<const int>(a.W.cnt);
     int* perm = dptr<int>(a.W.perm);
     int* inv = dptr<int>(a.W.inv);
     int* meta = dptr<int>(a.W.meta);
 
-    for (int e = tid; e < E; e += 256) {
+    for (int e = tid; e < E; e += nth) {
         cnt_e[e] = 0;
         base[e] = 0;
 #pragma unroll
         for (int q = 0; q < kEntryToks; ++q) tokf[e][q] = -1;
     }
     __syncthreads();
-    for (int p = tid; p < T * k; p += 256) {
+    for (int p = tid; p < T * k; p += nth) {
         const int t = p / k, j = p - t * k;
         if (j < cnt[t]) atomicAdd(&cnt_e[ids[p]], 1);
     }
@@ -329,13 +370,14 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
     }
     __syncthreads();
     int* gs = dptr<int>(a.W.gs);
-    for (int e = tid; e <= E; e += 256) gs[e] = gsl[e];
-    const int nu = meta[0];
+    for (int e = tid; e <= E; e += nth) gs[e] = gsl[e];
+    int nu = 0;
+    for (int e = 0; e < E; e += 64) nu += __popcll(__ballot(e + lane < E && cnt_e[e + lane] > 0));
     int* uniq = dptr<int>(a.W.uniq);
-    for (int u = tid; u < nu; u += 256) uniq[u] = uniq_l[u];
+    for (int u = tid; u < nu; u += nth) uniq[u] = uniq_l[u];
 
     for (int tb = 0; tb < T; tb += 64) {
-        for (int e = tid; e < E; e += 256) {
+        for (int e = tid; e < E; e += nth) {
             mlo[e] = 0u;
             mhi[e] = 0u;
         }
@@ -364,14 +406,13 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
             }
         }
         __syncthreads();
-        for (int e = tid; e < E; e += 256) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
+        for (int e = tid; e < E; e += nth) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
         __syncthreads();
     }
     // the expert table for the grouped kernels
     ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
-    const int* slots = dptr<const int>(a.L.slot_table);
     const int maxu = min(T * k, E);
-    for (int u = tid; u < maxu; u += 256) {
+    for (int u = tid; u < maxu; u += nth) {
         ExpertEntry x;
         if (u < nu) {
             const int e = uniq_l[u];
@@ -390,6 +431,37 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
         }
         et[u] = x;
     }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
+    __shared__ __align__(16) uint8_t sm[kDispatchSmem];
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
+                 dptr<const int>(a.L.slot_table));
+}
+
+// ---------------------------------------------------------------------------
+// Top-k and dispatch in one workgroup of 1024 threads, for decode-sized
+// batches (the host uses it for T <= kTopkDispatchMaxT): wave w ranks tokens
+// w, w + 16, ..., then the whole workgroup builds the dispatch tables.  One
+// launch less than lp_moe_topk + lp_moe_dispatch, and no cross-workgroup
+// synchronisation.
+// ---------------------------------------------------------------------------
+extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const RouteArgs a) {
+    constexpr int kTopkLds = 16 * kMaxExperts * 4;
+    __shared__ __align__(16) uint8_t sm[kDispatchSmem > kTopkLds ? kDispatchSmem : kTopkLds];
+    __shared__ int ids_l[kTopkDispatchMaxT * kMaxTopK];
+    __shared__ int cnt_l[kTopkDispatchMaxT];
+    __shared__ int slots_l[kMaxExperts];
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    // the slot table comes in while the picks are made
+    const int* slots = dptr<const int>(a.L.slot_table);
+    for (int e = threadIdx.x; e < a.L.experts; e += blockDim.x) slots_l[e] = slots[e];
+    float* sv = reinterpret_cast<float*>(sm) + wave * kMaxExperts;
+    for (int t = wave; t < a.T; t += nw) topk_any(a, t, sv, ids_l, cnt_l);
+    __syncthreads();
+    dispatch_all(a, sm, ids_l, cnt_l, slots_l);
 }
 
 // ---------------------------------------------------------------------------

@@ -66,7 +66,10 @@ static const uint64_t kExp2Tab[32] = {
 __device__ inline uint64_t exp2tab(uint32_t i) { return kExp2Tab[i]; }
 #endif
 
-LP_HD inline float expf_glibc(float x) {
+// The normal-range arithmetic of expf_glibc, with the table read through
+// tab(i).  Specials (|x| >= ~88, inf, nan) are the callers' business.
+template <typename Tab>
+LP_HD inline float expf_glibc_core(float x, Tab tab) {
 #if defined(__clang__)
 #pragma clang fp contract(off)
 #endif
@@ -75,24 +78,12 @@ LP_HD inline float expf_glibc(float x) {
     const double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
     const double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-    const uint32_t ux = expf_float_to_bits(x);
-    const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                      // |x| >= 88 or x is inf/nan
-        if (ux == 0xff800000u) return 0.0f;      // -inf
-        if (abstop >= 0x7f8u) return x + x;      // +inf or nan
-        if (x > 0x1.62e42ep6f) return __builtin_inff();   // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;              // underflow
-    }
     const double xd = (double)x;
     double kd = __builtin_fma(kInvLn2N, xd, kShift);
     const uint64_t ki = expf_double_to_bits(kd);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-#if defined(__HIP_DEVICE_COMPILE__)
-    const uint64_t t = exp2tab((uint32_t)(ki % 32)) + (ki << 47);
-#else
-    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
-#endif
+    const uint64_t t = tab((uint32_t)(ki % 32)) + (ki << 47);
     const double s = expf_bits_to_double(t);
     const double z = __builtin_fma(kC0, r, kC1);
     const double r2 = r * r;
@@ -101,5 +92,51 @@ LP_HD inline float expf_glibc(float x) {
     y = y * s;
     return (float)y;
 }
+
+LP_HD inline float expf_glibc(float x) {
+    const uint32_t ux = expf_float_to_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                      // |x| >= 88 or x is inf/nan
+        if (ux == 0xff800000u) return 0.0f;      // -inf
+        if (abstop >= 0x7f8u) return x + x;      // +inf or nan
+        if (x > 0x1.62e42ep6f) return __builtin_inff();   // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;              // underflow
+    }
+#if defined(__HIP_DEVICE_COMPILE__)
+    return expf_glibc_core(x, [](uint32_t i) { return exp2tab(i); });
+#else
+    return expf_glibc_core(x, [](uint32_t i) { return kExp2Tab[i]; });
+#endif
+}
+
+#if defined(__HIPCC__)
+// Wave form of expf_glibc: the table lives in registers (lanes 0..31 hold
+// entry `lane`, from exp2tab_lane()) and is read with cross-lane shuffles,
+// so no lookup waits on memory.  Every lane of the wave must call it
+// together (no lane may sit out under a branch); specials are selected after
+// the normal-range arithmetic, which is harmless for them.  Bit-identical
+// to expf_glibc.
+__device__ inline uint64_t exp2tab_lane() {
+    const uint32_t l = __lane_id();
+    return l < 32 ? exp2tab(l) : 0ull;
+}
+
+__device__ inline float expf_glibc_wave(float x, uint64_t tabv) {
+    const int lo = (int)(uint32_t)tabv, hi = (int)(uint32_t)(tabv >> 32);
+    const float y = expf_glibc_core(x, [&](uint32_t i) {
+        return (uint64_t)(uint32_t)__shfl(lo, (int)i, 64) | ((uint64_t)(uint32_t)__shfl(hi, (int)i, 64) << 32);
+    });
+    const uint32_t ux = expf_float_to_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    float r = y;
+    if (abstop >= 0x42bu) {
+        if (x < -0x1.9fe368p6f) r = 0.0f;
+        if (x > 0x1.62e42ep6f) r = __builtin_inff();
+        if (abstop >= 0x7f8u) r = x + x;
+        if (ux == 0xff800000u) r = 0.0f;
+    }
+    return r;
+}
+#endif
 
 }  // namespace lp

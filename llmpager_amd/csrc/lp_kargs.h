@@ -20,6 +20,7 @@ constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
+constexpr int kTopkDispatchMaxT = 64;  // largest T routed by the one-workgroup top-k + dispatch
 constexpr int kMaxPairs = 2;           // token pairs the grouped kernels stage at once
 constexpr int kMaxChunk = 16;          // most MFMA steps (4 sub-groups each) one register chunk holds
 constexpr int kGateupChunk = 16;       // gate/up tiles up to this many steps load in one piece
@@ -78,6 +79,12 @@ struct Bf16GemvArgs {               // kernels.rs:202-222
 struct AddArgs {                    // kernels.rs:239-250
     uint64_t a, b;
     int32_t n, pad0;
+};
+
+struct ExpfSweepArgs {              // device expf check (no reference counterpart)
+    uint64_t out;                   // f32 [n]
+    uint64_t n;
+    uint32_t first, stride;
 };
 
 // ---- fused MoE layer ---------------------------------------------------------

@@ -56,6 +56,8 @@ enum Fn {
     kDownWide,
     kCombine,
     kXImage,
+    kTopkDispatch,
+    kExpfWave,
     kNumFns
 };
 
@@ -72,6 +74,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_gateup"},
     {"lp_moe.hsaco", "lp_moe_down"},       {"lp_moe.hsaco", "lp_moe_down_wide"},
     {"lp_moe.hsaco", "lp_moe_combine"},    {"lp_moe.hsaco", "lp_moe_ximage"},
+    {"lp_moe.hsaco", "lp_moe_topk_dispatch"}, {"lp_basic.hsaco", "lp_expf_wave"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco"};
@@ -545,6 +548,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
+    if (T <= kTopkDispatchMaxT) return launch(c, kTopkDispatch, dim3(1), dim3(1024), 0, s, ra);
     if (int r = launch(c, kTopk, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
     return launch(c, kDispatch, dim3(1), dim3(256), 0, s, ra);
 }
@@ -692,6 +696,14 @@ int lp_profile_read_sync(lp_ctx* c, const char* kernel, double* total_ms, int64_
 }
 
 float lp_route_expf(float x) { return lp::expf_glibc(x); }
+
+int lp_route_expf_device(lp_ctx* c, uint32_t first, uint32_t stride, uint64_t n, uint64_t out,
+                         lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (!out || n == 0) return fail(LP_E_INVALID, "lp_route_expf_device: bad arguments");
+    ExpfSweepArgs a{out, n, first, stride};
+    return launch(c, kExpfWave, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+}
 
 void lp_route_expf_sweep(uint32_t first, uint32_t stride, uint64_t n, float* out) {
     for (uint64_t i = 0; i < n; ++i) {

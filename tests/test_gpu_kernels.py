@@ -98,3 +98,31 @@ def test_silu_add_reduce(cuda):
     assert np.array_equal(got, O.moe_reduce(eo, wt, h))
     for p in (da, db, dout, deo, dwt, dh):
         cuda.free_device(p)
+
+
+def _device_expf(cuda, first, stride, n):
+    out = cuda.alloc_device(n * 4)
+    assert lp.lib().lp_route_expf_device(cuda.ctx, first, stride, n, out, None) == 0
+    got = cuda.download(out, (n,), np.float32)
+    cuda.free_device(out)
+    return got
+
+
+@pytest.mark.parametrize("first,stride,n", [
+    (0, 9973, (1 << 32) // 9973),     # a spread over every float
+    (0x42b00000 - 2048, 1, 4096),     # around 88.0 (the special-case cut)
+    (0x42b17218 - 2048, 1, 4096),     # around the overflow threshold
+    (0xc2cff1b4 - 2048, 1, 4096),     # around the underflow threshold
+    (0x7f800000 - 2048, 1, 4096),     # largest finite, +inf, NaNs
+    (0xff800000 - 2048, 1, 4096),     # most negative finite, -inf, NaNs
+    (0x00000000, 1, 8192),            # +0 and denormals
+    (0x80000000, 1, 8192),            # -0 and negative denormals
+    (0x3f800000 - 4096, 1, 8192),     # around 1.0
+])
+def test_device_expf_matches_glibc(cuda, first, stride, n):
+    # The routing kernels' expf (glibc's method, table in registers) against
+    # this host's glibc expf, bit for bit.
+    got = _device_expf(cuda, first, stride, n)
+    want = O.expf_sweep(first, stride, n)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), hex((first + stride * int(np.argmin(same))) & 0xffffffff)

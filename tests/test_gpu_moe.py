@@ -177,3 +177,65 @@ def test_routing_bit_exact_sigmoid(cuda):
             assert np.array_equal(ids[t, :cnt[t]], wi), t
             assert np.array_equal(wts[t, :cnt[t]].view(np.uint32), ww.view(np.uint32)), t
     L.free()
+
+
+def _check_route(cuda, L: DeviceLayer, T: int, seed: int, stream=None):
+    """lp_moe_route on fresh x against the oracle: logits, routing, dispatch
+    tables and the expert table the grouped kernels read."""
+    H, E, k = L.H, L.E, L.k
+    x = lp.synth_f32_bf16(T * H, 1.0, seed, 1).reshape(T, H)
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    dx = cuda.upload(x)
+    L.layer.route(dx, T, ws, stream)
+    cuda.sync()
+    dl = lambda off, shape, dt: cuda.download(ws + off, shape, dt)
+    logits = dl(lay.logits, (T, E), np.float32)
+    ids, wts, cnt = dl(lay.ids, (T, k), np.int32), dl(lay.wts, (T, k), np.float32), dl(lay.cnt, (T,), np.int32)
+    gs, perm, inv = dl(lay.gs, (E + 1,), np.int32), dl(lay.perm, (T * k,), np.int32), dl(lay.inv, (T * k,), np.int32)
+    maxu = min(T * k, E)
+    et = dl(lay.et, (maxu * 32,), np.uint8)
+    cuda.free_device(ws)
+    cuda.free_device(dx)
+
+    want_logits = np.stack([O.router_logits(L.router_w, x[t], E, H) for t in range(T)])
+    assert np.array_equal(logits.view(np.uint32), want_logits.view(np.uint32)), T
+    want_ids = np.full((T, k), -1, np.int32)
+    want_cnt = np.zeros(T, np.int32)
+    for t in range(T):
+        wi, ww = O.top_k_softmax(want_logits[t], k, True)
+        want_cnt[t] = len(wi)
+        want_ids[t, :len(wi)] = wi
+        assert np.array_equal(ids[t, :len(wi)], wi), (T, t)
+        assert np.array_equal(wts[t, :len(wi)].view(np.uint32), ww.view(np.uint32)), (T, t)
+    assert np.array_equal(cnt, want_cnt)
+    wperm, wgs, winv, uniq = O.moe_dispatch(want_ids, want_cnt, T, k, E)
+    assert np.array_equal(gs, wgs) and np.array_equal(perm[:wgs[E]], wperm) and np.array_equal(inv, winv)
+    # expert table: blob address, first position, pair count, first four tokens
+    blob = et.view(np.uint64)[0::4]
+    i32 = et.view(np.int32).reshape(maxu, 8)
+    for u in range(maxu):
+        if u < len(uniq):
+            e = uniq[u]
+            p0, n = wgs[e], wgs[e + 1] - wgs[e]
+            assert blob[u] == L.arena + int(L.slots[e]) * L.span
+            assert (i32[u, 2], i32[u, 3]) == (p0, n)
+            toks = [wperm[p0 + i] // k if i < n else -1 for i in range(4)]
+            assert list(i32[u, 4:8]) == toks, (T, u)
+        else:
+            assert i32[u, 3] == 0
+
+
+def test_route_sequence(cuda):
+    # One context and workspace shape after shape, on either side of the
+    # one-workgroup top-k + dispatch limit (T <= 64) and on two streams.
+    L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=4, router_std=0.05)
+    for i, T in enumerate((1, 9, 64, 3, 200, 8, 1)):
+        _check_route(cuda, L, T, seed=100 + i)
+    # and on a second stream (its own counter slice)
+    s = cuda.stream()
+    for i, T in enumerate((5, 33)):
+        _check_route(cuda, L, T, seed=200 + i, stream=s)
+    cuda.sync()
+    cuda.destroy_stream(s)
+    L.free()
