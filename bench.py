@@ -39,6 +39,12 @@ EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 DOMINANT = "lp_moe_gateup"
+CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
+# HBM bytes per lp_moe_gateup launch at B = 32 (FETCH_SIZE + WRITE_SIZE, each
+# scaled by the factor the same counter reads for the calibration copy), from
+# the rocprofv3 --pmc runs recorded in profiles/lp_moe_gateup_config2_b32.md.
+# Re-measure whenever the kernel changes.
+GATEUP_TRAFFIC_B32 = 180_659_514
 KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_ximage",
            "lp_moe_gateup", "lp_moe_down",
            "lp_moe_down_wide", "lp_moe_combine")
@@ -250,6 +256,13 @@ def main() -> int:
     import llmpager_amd as lp
     cuda = lp.Cuda(0)
     s = cuda.stream()
+    # a plain device-to-device copy of CALIB_BYTES (outside every timed region):
+    # under rocprofv3 --pmc it calibrates FETCH_SIZE / WRITE_SIZE per byte
+    ca, cb = cuda.alloc_device(CALIB_BYTES), cuda.alloc_device(CALIB_BYTES)
+    cuda.dtod_async(cb, ca, CALIB_BYTES, s)
+    cuda.sync()
+    cuda.free_device(ca)
+    cuda.free_device(cb)
     log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
     stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu else 2)
     results = {}
@@ -269,7 +282,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4 x bf16-split -> fp32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
             "workload": f"config2: {LAYERS}-layer Qwen3-30B-A3B-shape MoE stack, lockstep decode "
@@ -287,7 +300,7 @@ def main() -> int:
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dom["frac"], 4),
-            "traffic": None,
+            "traffic": GATEUP_TRAFFIC_B32 if a.headline == 32 else None,
             "avg_us": round(dom["avg_us"], 3),
         },
         "cpu_baseline": cpu,
