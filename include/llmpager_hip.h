@@ -140,6 +140,13 @@ typedef struct lp_moe_layer_desc {
     uint64_t arena_base;    /* device address of slot 0 */
     uint64_t slot_span;     /* bytes per slot (pager.rs:263) */
     uint64_t gate_off, up_off, down_off; /* region offsets in a blob (decode.rs:183-185) */
+    /* The always-on shared MLP (kimi.rs:739-744, added unweighted after the
+     * routed part at kimi.rs:779; one MLP whose width is the shared experts'
+     * combined intermediate size, kimi.rs:274-291).  shared_blob = 0: none. */
+    uint64_t shared_blob;   /* device address of the shared MLP's blob */
+    int32_t shared_inter;   /* its intermediate size */
+    int32_t shared_group;   /* its q4 group */
+    uint64_t sh_gate_off, sh_up_off, sh_down_off; /* region offsets in that blob */
 } lp_moe_layer_desc;
 
 /* Byte offsets of the workspace parts for T tokens (all 256-byte aligned). */
@@ -157,6 +164,10 @@ typedef struct lp_moe_ws_layout {
     uint64_t act;     /* f32 [T*k, I] */
     uint64_t y;       /* f32 [T*k, H] */
     uint64_t xf;      /* [T] bf16 hi/lo fragment images of x for the grouped gate/up */
+    uint64_t sh_et;   /* shared MLP: its expert entry (size 0 without one) */
+    uint64_t sh_perm; /* shared MLP: i32 [T] identity token list */
+    uint64_t sh_act;  /* shared MLP: f32 [T, shared_inter] */
+    uint64_t sh_y;    /* shared MLP: f32 [T, H] */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;
 

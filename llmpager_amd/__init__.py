@@ -47,6 +47,8 @@ class LayerDesc(C.Structure):
         ("router_w", C.c_uint64), ("router_bias", C.c_uint64), ("slot_table", C.c_uint64),
         ("arena_base", C.c_uint64), ("slot_span", C.c_uint64),
         ("gate_off", C.c_uint64), ("up_off", C.c_uint64), ("down_off", C.c_uint64),
+        ("shared_blob", C.c_uint64), ("shared_inter", C.c_int32), ("shared_group", C.c_int32),
+        ("sh_gate_off", C.c_uint64), ("sh_up_off", C.c_uint64), ("sh_down_off", C.c_uint64),
     ]
 
 
@@ -55,7 +57,7 @@ class WsLayout(C.Structure):
 
     _fields_ = [(n, C.c_uint64) for n in (
         "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y", "xf",
-        "total")]
+        "sh_et", "sh_perm", "sh_act", "sh_y", "total")]
 
 
 def _sig(lib):

@@ -409,6 +409,19 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
         for (int e = tid; e < E; e += nth) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
         __syncthreads();
     }
+    // the shared MLP (if any) takes every token: one entry, identity token list
+    if (a.L.shared_blob) {
+        for (int t = tid; t < T; t += nth) dptr<int>(a.W.sh_perm)[t] = t;
+        if (tid == 0) {
+            ExpertEntry x;
+            x.blob = a.L.shared_blob;
+            x.p0 = 0;
+            x.ntok = T;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
+            *dptr<ExpertEntry>(a.W.sh_et) = x;
+        }
+    }
     // the expert table for the grouped kernels
     ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
     const int maxu = min(T * k, E);
@@ -749,7 +762,8 @@ lp_moe_down_wide(const GroupedArgs a) {
 
 // ---------------------------------------------------------------------------
 // Combine: h[t][i] += sum_j w[t][j] * y[inv[t*k+j]][i], j in pick order with
-// fused multiply-adds, then one add (q4g64.cu:84-99).  Grid (ceil(H/256), T).
+// fused multiply-adds, then one add (q4g64.cu:84-99); with a shared MLP its
+// output is added after that, unweighted (kimi.rs:779).  Grid (ceil(H/256), T).
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedArgs a) {
     const int t = blockIdx.y;
@@ -763,5 +777,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
     float acc = 0.0f;
     for (int j = 0; j < c; ++j) acc = __builtin_fmaf(w[j], y[(size_t)inv[j] * H + i], acc);
     float* h = dptr<float>(a.h) + (size_t)t * H;
-    h[i] += acc;
+    float v = h[i] + acc;
+    if (a.L.shared_blob) v = v + dptr<const float>(a.W.sh_y)[(size_t)t * H + i];
+    h[i] = v;
 }

@@ -102,6 +102,9 @@ struct LayerView {
     int32_t renorm;
     float routed_scaling, min_weight;
     int32_t pad0;
+    uint64_t shared_blob;    // the always-on shared MLP's blob, or 0
+    uint64_t sh_gate_off, sh_up_off, sh_down_off;
+    int32_t shared_inter, shared_group;
 };
 
 // One routed expert as the grouped kernels see it, written by the dispatch
@@ -131,6 +134,10 @@ struct Workspace {
     uint64_t act;        // f32 [T * k, I] expert-major activations
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
     uint64_t xf;         // [T] fragment images of the layer input (image_bytes(H) each)
+    uint64_t sh_et;      // shared MLP: one ExpertEntry (all T tokens)
+    uint64_t sh_perm;    // shared MLP: i32 [T], t
+    uint64_t sh_act;     // shared MLP: f32 [T, shared_inter]
+    uint64_t sh_y;       // shared MLP: f32 [T, H]
 };
 
 struct RouteArgs {

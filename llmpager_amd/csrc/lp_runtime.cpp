@@ -480,6 +480,12 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->act = take(t * k * I * 4);
     out->y = take(t * k * H * 4);
     out->xf = take(t * (uint64_t)image_bytes((int)H));
+    const bool sh = d->shared_blob != 0;
+    const uint64_t Is = sh ? (uint64_t)d->shared_inter : 0;
+    out->sh_et = take(sh ? sizeof(ExpertEntry) : 0);
+    out->sh_perm = take(sh ? t * 4 : 0);
+    out->sh_act = take(t * Is * 4);
+    out->sh_y = take(sh ? t * H * 4 : 0);
     out->total = o;
     return LP_OK;
 }
@@ -493,8 +499,9 @@ static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
     if (d->top_k <= 0 || d->top_k > kMaxTopK) return fail(LP_E_UNSUPPORTED, "top_k must be in 1..16");
     if (d->hidden <= 0 || d->inter <= 0 || d->hidden % 32 || d->inter % 32)
         return fail(LP_E_UNSUPPORTED, "hidden and inter must be multiples of 32");
-    if (d->group <= 0 || d->group % 32 || d->hidden % d->group || d->inter % d->group)
-        return fail(LP_E_UNSUPPORTED, "group must be a multiple of 32 dividing hidden and inter");
+    if (d->group <= 0 || d->group % 32 || ((d->group / 32) & (d->group / 32 - 1)) || d->group > 128 ||
+        d->hidden % d->group || d->inter % d->group)
+        return fail(LP_E_UNSUPPORTED, "group must be 32, 64 or 128 and divide hidden and inter");
     if (d->gating != LP_GATING_SOFTMAX && d->gating != LP_GATING_SIGMOID)
         return fail(LP_E_INVALID, "unknown gating");
     if (d->gating == LP_GATING_SIGMOID && !d->router_bias)
@@ -507,6 +514,17 @@ static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
         return fail(LP_E_UNSUPPORTED, "q4 nibble rows must be 16-byte aligned in every slot");
     if (!d->router_w || !d->slot_table || !d->arena_base)
         return fail(LP_E_INVALID, "router_w, slot_table and arena_base are required");
+    if (d->shared_blob) {
+        const int Is = d->shared_inter, gs = d->shared_group;
+        if (Is <= 0 || Is % 32) return fail(LP_E_UNSUPPORTED, "shared_inter must be a multiple of 32");
+        if (gs <= 0 || gs % 32 || ((gs / 32) & (gs / 32 - 1)) || gs > 128 || d->hidden % gs || Is % gs)
+            return fail(LP_E_UNSUPPORTED, "shared_group must be 32, 64 or 128 and divide hidden and shared_inter");
+        const uint64_t sgd = d->sh_gate_off + (uint64_t)Is * (d->hidden / gs) * 2;
+        const uint64_t sud = d->sh_up_off + (uint64_t)Is * (d->hidden / gs) * 2;
+        const uint64_t sdd = d->sh_down_off + (uint64_t)d->hidden * (Is / gs) * 2;
+        if ((d->shared_blob | sgd | sud | sdd) % 16)
+            return fail(LP_E_UNSUPPORTED, "shared MLP nibble rows must be 16-byte aligned");
+    }
     return LP_OK;
 }
 
@@ -529,6 +547,12 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     L->renorm = d->renorm;
     L->routed_scaling = d->routed_scaling;
     L->min_weight = d->min_weight;
+    L->shared_blob = d->shared_blob;
+    L->shared_inter = d->shared_inter;
+    L->shared_group = d->shared_group;
+    L->sh_gate_off = d->sh_gate_off;
+    L->sh_up_off = d->sh_up_off;
+    L->sh_down_off = d->sh_down_off;
     lp_moe_ws_layout lay;
     lp_moe_ws_layout_get(d, T, &lay);
     W->logits = ws + lay.logits;
@@ -544,6 +568,10 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->act = ws + lay.act;
     W->y = ws + lay.y;
     W->xf = ws + lay.xf;
+    W->sh_et = ws + lay.sh_et;
+    W->sh_perm = ws + lay.sh_perm;
+    W->sh_act = ws + lay.sh_act;
+    W->sh_y = ws + lay.sh_y;
 }
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
@@ -579,6 +607,33 @@ int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, 
     return route_tail(c, ra, s);
 }
 
+// Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
+// (maxu entries): workgroup width chosen so that there are about two work
+// items per CU, down with two tiles per wave when the inner size allows.
+static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga, int maxu, lp_stream s) {
+    const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
+    auto pick_w = [&](int rows, int tw) {
+        for (int w = 4; w > 1; w >>= 1)
+            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= 2L * c->cus)
+                return w;
+        return 1;
+    };
+    {
+        const int w = pick_w(I, 1);
+        const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
+        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w),
+                           (size_t)frag_lds_bytes(H, cap), s, ga))
+            return r;
+    }
+    const int steps = ((I / 32) + 3) / 4;
+    const Fn f = steps <= kDownChunk ? kDown : kDownWide;
+    const int tw = steps <= kDownChunk ? 2 : 1;
+    const int w = pick_w(H, tw);
+    const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
+    return launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), (size_t)frag_lds_bytes(I, cap), s,
+                  ga);
+}
+
 // The grouped expert kernels and the combine; the fragment images of x are
 // written first unless the router kernel of lp_moe_forward already did.
 static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
@@ -598,39 +653,34 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     ga.x = x;
     ga.h = h;
     ga.T = T;
-    const int H = d->hidden, I = d->inter;
-    const int maxu = std::min(T * d->top_k, d->experts);
+    const int H = d->hidden;
+    const int Is = d->shared_blob ? d->shared_inter : 0;
     // Token pairs staged at once: enough for T tokens on one expert, bounded
     // by kMaxPairs and by the LDS the fragments need.
     int cap = std::min(kMaxPairs, (T + 1) / 2);
-    auto lds_for = [&](int p) { return (size_t)std::max(frag_lds_bytes(H, p), frag_lds_bytes(I, p)); };
+    auto lds_for = [&](int p) {
+        return (size_t)std::max({frag_lds_bytes(H, p), frag_lds_bytes(d->inter, p), frag_lds_bytes(std::max(Is, 32), p)});
+    };
     while (cap > 1 && lds_for(cap) > c->max_lds) --cap;
     if (lds_for(1) > c->max_lds)
         return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
     ga.pairs_cap = cap;
-    const size_t fr_h = (size_t)frag_lds_bytes(H, cap), fr_i = (size_t)frag_lds_bytes(I, cap);
-    // Workgroup width: the widest (more rows per staged fragment set) that
-    // still yields about two work items per CU.
-    auto pick_w = [&](int rows, int tw) {
-        for (int w = 4; w > 1; w >>= 1)
-            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= 2L * c->cus)
-                return w;
-        return 1;
-    };
-    {
-        const int w = pick_w(I, 1);
-        const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
-        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w), fr_h, s, ga))
-            return r;
-    }
-    {
-        const int steps = ((I / 32) + 3) / 4;
-        const Fn f = steps <= kDownChunk ? kDown : kDownWide;
-        const int tw = steps <= kDownChunk ? 2 : 1;
-        const int w = pick_w(H, tw);
-        const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
-        if (int r = launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), fr_i, s, ga))
-            return r;
+    if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), s)) return r;
+    if (d->shared_blob) {
+        // the shared MLP through the same kernels: its own width, group and
+        // regions, one expert entry covering every token (written by dispatch)
+        GroupedArgs gs = ga;
+        gs.L.inter = Is;
+        gs.L.group = d->shared_group;
+        gs.L.gate_off = d->sh_gate_off;
+        gs.L.up_off = d->sh_up_off;
+        gs.L.down_off = d->sh_down_off;
+        gs.L.top_k = 1;
+        gs.W.et = ga.W.sh_et;
+        gs.W.perm = ga.W.sh_perm;
+        gs.W.act = ga.W.sh_act;
+        gs.W.y = ga.W.sh_y;
+        if (int r = grouped_ffn(c, gs, 1, s)) return r;
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
                   s, ga);

@@ -18,7 +18,8 @@ class DeviceLayer:
     def __init__(self, cuda: lp.Cuda, H: int, I: int, E: int, k: int, group: int, seed: int = 0,
                  layer: int = 0, gating: int = lp.GATING_SOFTMAX, renorm: bool = True,
                  routed_scaling: float = 1.0, min_weight: float = 0.0, router_std: float = 0.02,
-                 bias: np.ndarray | None = None, slots: np.ndarray | None = None):
+                 bias: np.ndarray | None = None, slots: np.ndarray | None = None,
+                 shared: tuple[int, int] | None = None):
         self.cuda = cuda
         self.H, self.I, self.E, self.k, self.group = H, I, E, k, group
         self.blob_bytes = lp.blob_bytes(H, I, group)
@@ -40,6 +41,16 @@ class DeviceLayer:
             renorm=int(renorm), routed_scaling=routed_scaling, min_weight=min_weight,
             router_w=self.d_router, router_bias=self.d_bias, slot_table=self.d_slots,
             arena_base=self.arena, slot_span=self.span, gate_off=go, up_off=uo, down_off=do)
+        # the always-on shared MLP (kimi.rs:739-744, 779): (inter, group) or None
+        self.shared = None
+        if shared is not None:
+            si, sg = shared
+            blob = lp.synth_blob(H, si, sg, seed, layer, 1 << 20)
+            self.shared = dict(blob=blob, inter=si, group=sg, offsets=lp.blob_offsets(H, si, sg))
+            self.d_shared = cuda.upload(blob)
+            self.desc.shared_blob = self.d_shared
+            self.desc.shared_inter, self.desc.shared_group = si, sg
+            self.desc.sh_gate_off, self.desc.sh_up_off, self.desc.sh_down_off = self.shared["offsets"]
         self.layer = lp.MoeLayer(cuda, self.desc)
         cuda.sync()
 
@@ -61,6 +72,8 @@ class DeviceLayer:
             self.cuda.free_device(p)
         if self.d_bias:
             self.cuda.free_device(self.d_bias)
+        if self.shared is not None:
+            self.cuda.free_device(self.d_shared)
 
 
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:

@@ -44,7 +44,7 @@ def _run_layer(cuda, L: DeviceLayer, T: int, seed: int):
 def _check_layer(L: DeviceLayer, x, h, g, T, threads=8):
     E, k = L.E, L.k
     want_h, want_logits, want_ids, want_w, want_cnt = O.moe_layer(
-        L.oracle_desc(), L.oracle_blobs(), x, h, threads=threads)
+        L.oracle_desc(), L.oracle_blobs(), x, h, threads=threads, shared_blob=L.shared)
     # logits: canonical order, identical bits
     assert np.array_equal(g["logits"].view(np.uint32), want_logits.view(np.uint32))
     # routing: ids, order, count and weights identical
@@ -95,6 +95,28 @@ def test_layer_sigmoid_gating(cuda):
     x, h, g = _run_layer(cuda, L, T, seed=9)
     _check_layer(L, x, h, g, T)
     assert (g["cnt"] < 6).any()  # min_weight dropped some picks
+    L.free()
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_layer_shared_expert(cuda, T):
+    # Config 5's MoE half (DeepSeek-V2-Lite style): 64 routed experts top-6 of
+    # width 1408 plus the always-on shared MLP (2 x 1408 = 2816 wide), added
+    # unweighted after the routed part (kimi.rs:739-744, 779).
+    rng = np.random.default_rng(11)
+    bias = (rng.standard_normal(64) * 0.05).astype(np.float32)
+    L = DeviceLayer(cuda, H=2048, I=1408, E=64, k=6, group=32, seed=5, gating=lp.GATING_SIGMOID,
+                    renorm=True, routed_scaling=1.0, bias=bias, router_std=0.05, shared=(2816, 32))
+    x, h, g = _run_layer(cuda, L, T, seed=40 + T)
+    _check_layer(L, x, h, g, T)
+    L.free()
+
+
+def test_layer_shared_expert_g64_softmax(cuda):
+    # a g64 shared MLP beside g32 routed experts, softmax gating, small shape
+    L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=32, seed=8, router_std=0.2, shared=(128, 64))
+    x, h, g = _run_layer(cuda, L, 5, seed=3)
+    _check_layer(L, x, h, g, 5)
     L.free()
 
 
