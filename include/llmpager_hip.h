@@ -188,6 +188,11 @@ int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits
  * in pick order. */
 int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
+/* Paged flow (decode.rs:305-331 order: route, then request the picks, then
+ * compute): after lp_moe_route* and the pager's requests for the picked
+ * experts, re-resolve the expert table's blob addresses through the layer's
+ * now-current slot table, before lp_moe_experts. */
+int lp_moe_resolve(lp_ctx* ctx, const lp_moe_layer_desc* d, int T, uint64_t workspace, lp_stream s);
 /* The whole layer (decode.rs:303-337 for one token, 469-531 for many):
  * lp_moe_route followed by lp_moe_experts, with the fragment images of x
  * written by the router kernel.  h: f32 [T, H], updated in place. */
@@ -232,6 +237,65 @@ int lp_cache_stats(const lp_cache* c, uint64_t* hits, uint64_t* misses);
 /* The id a slot holds, or -1 (no counterpart in the reference: lets a caller
  * rebuild a layer's device slot table from the cache). */
 int64_t lp_cache_slot_id(const lp_cache* c, uint32_t slot);
+
+/* ---- expert pager: pager::Pager (crates/llmpager-cuda/src/pager.rs) ------ */
+
+typedef struct lp_pager lp_pager;
+
+typedef struct lp_pager_config {
+    uint32_t layers;            /* pack layers (pager.rs:263-264) */
+    uint32_t experts_per_layer; /* ids fold (layer, expert) on this (pager.rs:224-226) */
+    uint32_t slots_per_layer;   /* PagerConfig::slots_per_layer (pager.rs:34) */
+    uint32_t decay_interval;    /* per-layer pools: halve counters every this many inserts (:37) */
+    uint64_t blob_bytes;        /* bytes copied per miss */
+    uint64_t span;              /* VRAM bytes per slot; 0 = blob_bytes rounded up to 4096 (:263) */
+    const void* host_blobs;     /* pinned host memory: blob (l, e) at host_blobs + (l*E + e)*host_stride */
+    uint64_t host_stride;
+    int32_t copy_streams;       /* 1..8 copy streams (the io_threads' role, :35) */
+    int32_t global_pool;        /* one pool for every layer (LLMPAGER_GLOBAL_POOL, :296-318) */
+    uint32_t pool_decay_tokens; /* global pool: decay every this many ticks; 0 = 4 (:361-365) */
+    uint32_t reserved0;
+} lp_pager_config;
+
+typedef struct lp_pager_metrics {
+    uint64_t hits, misses, bytes_fetched, fetches, stalls; /* pager.rs:568-589 (Metrics) */
+} lp_pager_metrics;
+
+/* Pager::new (pager.rs:260-388): one arena of layers x slots_per_layer slots,
+ * per-layer device slot tables (expert -> global slot, -1 absent), copy streams. */
+int lp_pager_new(lp_ctx* ctx, const lp_pager_config* cfg, lp_pager** out);
+/* Drop (pager.rs:606-620): waits for copies in flight, frees the arena. */
+void lp_pager_free(lp_pager* p);
+/* The arena base (the layer desc's arena_base), the slot span (its
+ * slot_span) and layer l's device slot table (its slot_table). */
+uint64_t lp_pager_arena(const lp_pager* p);
+uint64_t lp_pager_span(const lp_pager* p);
+uint64_t lp_pager_slot_table(const lp_pager* p, uint32_t layer);
+uint32_t lp_pager_slots_per_layer(const lp_pager* p);
+/* Pager::request + wait_stream (pager.rs:402-460, 499-503): pin n experts of
+ * `layer`; misses are copied from the host blobs on a copy stream; `compute`
+ * waits for every fill still in flight and gets the layer's slot table
+ * refreshed in its own order.  Never blocks for I/O; blocks only while every
+ * slot of the pool is pinned and a release is pending; errors (expert cache
+ * deadlock) when none is.  slots_out: n global slot numbers (may be NULL). */
+int lp_pager_request(lp_pager* p, uint16_t layer, const uint16_t* experts, int n, lp_stream compute,
+                     uint32_t* slots_out);
+/* Pager::release (pager.rs:505-510): unpin now (the GPU is done with them). */
+int lp_pager_release(lp_pager* p, const uint32_t* slots, int n);
+/* The deferred release of decode.rs:621-649: unpin once `compute` has passed
+ * this point. */
+int lp_pager_release_after(lp_pager* p, const uint32_t* slots, int n, lp_stream compute);
+/* Pager::prefetch (pager.rs:464-486): best effort, never blocks; the fill's
+ * pin drops when it lands. */
+int lp_pager_prefetch(lp_pager* p, uint16_t layer, const uint16_t* experts, int n);
+/* Pager::wait (pager.rs:489-496): block until the slot's last fill landed. */
+int lp_pager_wait(lp_pager* p, uint32_t slot);
+/* Pager::tick (pager.rs:524-533): end of a forward pass (global-pool decay). */
+int lp_pager_tick(lp_pager* p);
+/* Wait for every copy in flight and hand back every deferred release. */
+int lp_pager_sync(lp_pager* p);
+/* Pager::metrics (pager.rs:568-589). */
+int lp_pager_get_metrics(lp_pager* p, lp_pager_metrics* out);
 
 /* ---- measurement ------------------------------------------------------------ */
 

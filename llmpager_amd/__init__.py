@@ -99,6 +99,7 @@ def _sig(lib):
         "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
         "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
         "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
+        "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, vp]),
         "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
         "lp_moe_status_sync": (i32, [vp, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
         "lp_q4_bytes": (u64, [i32, i32, i32]),
@@ -114,6 +115,20 @@ def _sig(lib):
         "lp_route_expf": (f32, [f32]),
         "lp_route_expf_sweep": (None, [C.c_uint32, C.c_uint32, u64, vp]),
         "lp_route_expf_device": (i32, [vp, C.c_uint32, C.c_uint32, u64, u64, vp]),
+        "lp_pager_new": (i32, [vp, vp, P(vp)]),
+        "lp_pager_free": (None, [vp]),
+        "lp_pager_arena": (u64, [vp]),
+        "lp_pager_span": (u64, [vp]),
+        "lp_pager_slot_table": (u64, [vp, C.c_uint32]),
+        "lp_pager_slots_per_layer": (C.c_uint32, [vp]),
+        "lp_pager_request": (i32, [vp, C.c_uint16, vp, i32, vp, vp]),
+        "lp_pager_release": (i32, [vp, vp, i32]),
+        "lp_pager_release_after": (i32, [vp, vp, i32, vp]),
+        "lp_pager_prefetch": (i32, [vp, C.c_uint16, vp, i32]),
+        "lp_pager_wait": (i32, [vp, C.c_uint32]),
+        "lp_pager_tick": (i32, [vp]),
+        "lp_pager_sync": (i32, [vp]),
+        "lp_pager_get_metrics": (i32, [vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -364,6 +379,80 @@ class Kernels:
 
 # ---- fused MoE layer ----------------------------------------------------------------
 
+class PagerConfig(C.Structure):
+    """lp_pager_config (include/llmpager_hip.h)."""
+
+    _fields_ = [
+        ("layers", C.c_uint32), ("experts_per_layer", C.c_uint32), ("slots_per_layer", C.c_uint32),
+        ("decay_interval", C.c_uint32), ("blob_bytes", C.c_uint64), ("span", C.c_uint64),
+        ("host_blobs", C.c_void_p), ("host_stride", C.c_uint64), ("copy_streams", C.c_int32),
+        ("global_pool", C.c_int32), ("pool_decay_tokens", C.c_uint32), ("reserved0", C.c_uint32),
+    ]
+
+
+class PagerMetrics(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "bytes_fetched", "fetches", "stalls")]
+
+
+class Pager:
+    """pager::Pager (pager.rs) over the C ABI: VRAM expert slots, misses filled
+    from pinned host blobs on copy streams."""
+
+    def __init__(self, cuda: "Cuda", cfg: PagerConfig):
+        self.cuda, self.cfg = cuda, cfg
+        p = C.c_void_p()
+        _check(lib().lp_pager_new(cuda.ctx, C.byref(cfg), C.byref(p)))
+        self.p = p.value
+
+    @property
+    def arena(self) -> int:
+        return int(lib().lp_pager_arena(self.p))
+
+    @property
+    def span(self) -> int:
+        return int(lib().lp_pager_span(self.p))
+
+    def slot_table(self, layer: int) -> int:
+        return int(lib().lp_pager_slot_table(self.p, layer))
+
+    def request(self, layer: int, experts, stream=None) -> np.ndarray:
+        ex = np.ascontiguousarray(experts, np.uint16)
+        out = np.zeros(len(ex), np.uint32)
+        _check(lib().lp_pager_request(self.p, layer, _ptr(ex), len(ex), stream, _ptr(out)))
+        return out
+
+    def release(self, slots) -> None:
+        sl = np.ascontiguousarray(slots, np.uint32)
+        _check(lib().lp_pager_release(self.p, _ptr(sl), len(sl)))
+
+    def release_after(self, slots, stream=None) -> None:
+        sl = np.ascontiguousarray(slots, np.uint32)
+        _check(lib().lp_pager_release_after(self.p, _ptr(sl), len(sl), stream))
+
+    def prefetch(self, layer: int, experts) -> None:
+        ex = np.ascontiguousarray(experts, np.uint16)
+        _check(lib().lp_pager_prefetch(self.p, layer, _ptr(ex), len(ex)))
+
+    def wait(self, slot: int) -> None:
+        _check(lib().lp_pager_wait(self.p, slot))
+
+    def tick(self) -> None:
+        _check(lib().lp_pager_tick(self.p))
+
+    def sync(self) -> None:
+        _check(lib().lp_pager_sync(self.p))
+
+    def metrics(self) -> dict:
+        m = PagerMetrics()
+        _check(lib().lp_pager_get_metrics(self.p, C.byref(m)))
+        return {n: getattr(m, n) for n, _ in PagerMetrics._fields_}
+
+    def close(self) -> None:
+        if self.p:
+            lib().lp_pager_free(self.p)
+            self.p = None
+
+
 class MoeLayer:
     """The fused layer entry points for one layer descriptor."""
 
@@ -376,6 +465,9 @@ class MoeLayer:
 
     def route_logits(self, logits: int, T: int, ws: int, stream=None) -> None:
         _check(lib().lp_moe_route_logits(self.cuda.ctx, C.byref(self.desc), logits, T, ws, stream))
+
+    def resolve(self, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_resolve(self.cuda.ctx, C.byref(self.desc), T, ws, stream))
 
     def experts(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
         _check(lib().lp_moe_experts(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))

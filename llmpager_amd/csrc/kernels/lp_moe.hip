@@ -454,6 +454,22 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArg
                  dptr<const int>(a.L.slot_table));
 }
 
+// Re-resolve the expert table's blob addresses through the layer's current
+// slot table: the paged flow routes first, asks the pager for the picked
+// experts (whose slots the pager then writes into the table), and only then
+// runs the expert kernels.  One workgroup.
+extern "C" __global__ void __launch_bounds__(256) lp_moe_resolve(const RouteArgs a) {
+    const int maxu = min(a.T * a.L.top_k, a.L.experts);
+    const int nu = dptr<const int>(a.W.meta)[0];
+    const int* uniq = dptr<const int>(a.W.uniq);
+    const int* slots = dptr<const int>(a.L.slot_table);
+    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    for (int u = threadIdx.x; u < maxu && u < nu; u += blockDim.x) {
+        const int slot = slots[uniq[u]];
+        et[u].blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Top-k and dispatch in one workgroup of 1024 threads, for decode-sized
 // batches (the host uses it for T <= kTopkDispatchMaxT): wave w ranks tokens

@@ -17,6 +17,7 @@
 
 #include "../../include/llmpager_hip.h"
 #include "lp_expf.h"
+#include "lp_internal.h"
 #include "lp_kargs.h"
 
 using namespace lpk;
@@ -29,6 +30,12 @@ int fail(int code, const std::string& msg) {
     g_err = msg;
     return code;
 }
+
+}  // namespace
+
+int lpi::set_error(int code, const std::string& msg) { return fail(code, msg); }
+
+namespace {
 
 int hip_fail(hipError_t e, const char* what) {
     g_err = std::string(what) + " failed: " + hipGetErrorString(e) + " (" + std::to_string((int)e) + ")";
@@ -58,6 +65,7 @@ enum Fn {
     kXImage,
     kTopkDispatch,
     kExpfWave,
+    kResolve,
     kNumFns
 };
 
@@ -75,6 +83,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_down"},       {"lp_moe.hsaco", "lp_moe_down_wide"},
     {"lp_moe.hsaco", "lp_moe_combine"},    {"lp_moe.hsaco", "lp_moe_ximage"},
     {"lp_moe.hsaco", "lp_moe_topk_dispatch"}, {"lp_basic.hsaco", "lp_expf_wave"},
+    {"lp_moe.hsaco", "lp_moe_resolve"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco"};
@@ -684,6 +693,14 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
                   s, ga);
+}
+
+int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, lp_stream s) {
+    if (int r = check_desc(c, d, T)) return r;
+    RouteArgs ra{};
+    fill_views(d, ws, T, &ra.L, &ra.W);
+    ra.T = T;
+    return launch(c, kResolve, dim3(1), dim3(256), 0, s, ra);
 }
 
 int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,

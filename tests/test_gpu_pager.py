@@ -1,0 +1,189 @@
+"""The expert pager (pager.rs) on the GPU: fills are byte-exact copies of the
+host blobs, cache decisions are the ExpertCache's (cache.rs), and a paged
+layer stack computes what the all-resident oracle computes."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import llmpager_amd as lp
+import _oracle as O
+from _gpu import align, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K, G = 128, 64, 8, 2, 32
+
+
+class HostPack:
+    """Every (layer, expert) blob in pinned host memory, span-strided."""
+
+    def __init__(self, cuda, layers: int, seed: int):
+        self.cuda, self.layers = cuda, layers
+        self.blob = lp.blob_bytes(H, I, G)
+        self.span = align(self.blob)
+        n = layers * E * self.span
+        self.pin = cuda.alloc_pinned(n)
+        self.view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(self.pin))
+        for l in range(layers):
+            lp.synth_blobs(E, self.span, H, I, G, seed, l, out=self.view[l * E * self.span:(l + 1) * E * self.span])
+
+    def blob_of(self, l: int, e: int) -> np.ndarray:
+        o = (l * E + e) * self.span
+        return self.view[o:o + self.blob]
+
+    def pager(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256) -> lp.Pager:
+        cfg = lp.PagerConfig(layers=self.layers, experts_per_layer=E, slots_per_layer=slots,
+                             decay_interval=decay, blob_bytes=self.blob, span=0, host_blobs=self.pin,
+                             host_stride=self.span, copy_streams=streams, global_pool=glob)
+        return lp.Pager(self.cuda, cfg)
+
+    def free(self):
+        self.cuda.free_pinned(self.pin)
+
+
+def _cache_model(layers: int, slots: int, glob: bool):
+    # the pager's cache: per-layer pools decaying every 256 insertions, or one
+    # pool that only decays on ticks (pager.rs:331-343)
+    L = lp.lib()
+    L.lp_cache_partitioned.restype = C.c_void_p
+    L.lp_cache_partitioned.argtypes = [C.c_uint32] * 4
+    if glob:
+        return L.lp_cache_partitioned(1, E, slots * layers, 0xffffffff)
+    return L.lp_cache_partitioned(layers, E, slots, 256)
+
+
+def test_pager_fills_are_byte_exact(cuda):
+    pk = HostPack(cuda, 2, seed=3)
+    pg = pk.pager(slots=3)
+    s = cuda.stream()
+    slots = pg.request(1, [3, 5, 1], s)
+    cuda.sync_stream(s)
+    for e, sl in zip((3, 5, 1), slots):
+        got = cuda.download(pg.arena + int(sl) * pg.span, (pk.blob,), np.uint8)
+        assert np.array_equal(got, pk.blob_of(1, e)), (e, sl)
+    table = cuda.download(pg.slot_table(1), (E,), np.int32)
+    assert [table[e] for e in (3, 5, 1)] == list(slots)
+    assert (np.delete(table, [3, 5, 1]) == -1).all()
+    assert pg.metrics()["misses"] == 3
+    pg.release_after(slots, s)
+    pg.sync()
+    pg.close()
+    cuda.destroy_stream(s)
+    pk.free()
+
+
+def test_pager_prefetch_then_hit(cuda):
+    pk = HostPack(cuda, 1, seed=4)
+    pg = pk.pager(slots=4)
+    pg.prefetch(0, [6, 2])
+    s = cuda.stream()
+    slots = pg.request(0, [2, 6, 7], s)   # two hits (prefetched), one miss
+    cuda.sync_stream(s)
+    m = pg.metrics()
+    assert (m["hits"], m["misses"]) == (2, 3)
+    for e, sl in zip((2, 6, 7), slots):
+        assert np.array_equal(cuda.download(pg.arena + int(sl) * pg.span, (pk.blob,), np.uint8),
+                              pk.blob_of(0, e))
+    pg.release(slots)
+    pg.sync()
+    pg.close()
+    cuda.destroy_stream(s)
+    pk.free()
+
+
+def test_pager_deadlock_is_an_error(cuda):
+    # every slot pinned and nothing pending: the reference bails out rather than
+    # hang (pager.rs:430-451); so does the C ABI
+    pk = HostPack(cuda, 1, seed=5)
+    pg = pk.pager(slots=2)
+    s = cuda.stream()
+    pg.request(0, [0, 1], s)
+    with pytest.raises(RuntimeError, match="deadlock"):
+        pg.request(0, [2], s)
+    with pytest.raises(RuntimeError):
+        pg.request(0, [0, 1, 2], s)     # more than the pool holds (pager.rs:405-413)
+    cuda.sync_stream(s)
+    pg.close()
+    cuda.destroy_stream(s)
+    pk.free()
+
+
+@pytest.mark.parametrize("glob", [0, 1])
+def test_paged_stack_matches_the_oracle(cuda, glob):
+    # Two layers, 4 of 8 expert slots per layer (8 in one pool when glob): each
+    # decode step routes on the device, reads the picks back, asks the pager for
+    # them (misses copied on the copy streams), re-resolves the expert table and
+    # runs the experts -- the reference's order (decode.rs:305-337) with the
+    # routing on the GPU.  Hits and misses must be those of the ExpertCache fed
+    # the same requests, and h must match the oracle with every expert resident.
+    layers, slots, steps = 2, 4, 10
+    pk = HostPack(cuda, layers, seed=6)
+    pg = pk.pager(slots=slots, glob=glob)
+    model = _cache_model(layers, slots, bool(glob))
+    Lc = lp.lib()
+    Lc.lp_cache_acquire.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_int64)]
+    Lc.lp_cache_release.argtypes = [C.c_void_p, C.c_uint32]
+    Lc.lp_cache_stats.argtypes = [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+    Lc.lp_cache_free.argtypes = [C.c_void_p]
+    Lc.lp_cache_decay_all.argtypes = [C.c_void_p]
+    s = cuda.stream()
+    routers = [lp.synth_bf16(E * H, 0.2, 6, 1000 + l) for l in range(layers)]
+    d_routers = [cuda.upload(r) for r in routers]
+    go, uo, do = lp.blob_offsets(H, I, G)
+    descs = [lp.LayerDesc(hidden=H, inter=I, experts=E, top_k=K, group=G, gating=lp.GATING_SOFTMAX,
+                          renorm=1, routed_scaling=1.0, router_w=d_routers[l], slot_table=pg.slot_table(l),
+                          arena_base=pg.arena, slot_span=pg.span, gate_off=go, up_off=uo, down_off=do)
+             for l in range(layers)]
+    moe = [lp.MoeLayer(cuda, d) for d in descs]
+    lay = lp.ws_layout(descs[0], 1)
+    ws = cuda.alloc_device(lay.total)
+    h0 = lp.synth_f32_bf16(steps * H, 1.0, 6, 2).reshape(steps, H)
+    dh = cuda.upload(h0)
+    for t in range(steps):
+        ht = dh + t * H * 4
+        for l in range(layers):
+            moe[l].route(ht, 1, ws, s)
+            cuda.sync_stream(s)
+            ids = cuda.download(ws + lay.ids, (K,), np.int32)
+            cnt = int(cuda.download(ws + lay.cnt, (1,), np.int32)[0])
+            picks = sorted(set(int(e) for e in ids[:cnt]))
+            got = pg.request(l, picks, s)
+            ref_slots = []
+            for e in picks:
+                sl, ev = C.c_uint32(), C.c_int64()
+                Lc.lp_cache_acquire(model, l * E + e, C.byref(sl), C.byref(ev))
+                ref_slots.append(sl.value)
+            assert list(got) == ref_slots, (t, l)
+            moe[l].resolve(1, ws, s)
+            moe[l].experts(ht, ht, 1, ws, s)
+            pg.release_after(got, s)
+            for sl in ref_slots:
+                Lc.lp_cache_release(model, sl)
+        pg.tick()
+        if glob and (t + 1) % 4 == 0:   # pool_decay_tokens defaults to 4
+            Lc.lp_cache_decay_all(model)
+    cuda.sync_stream(s)
+    got_h = cuda.download(dh, (steps, H), np.float32)
+    hits, misses = C.c_uint64(), C.c_uint64()
+    Lc.lp_cache_stats(model, C.byref(hits), C.byref(misses))
+    m = pg.metrics()
+    assert (m["hits"], m["misses"]) == (hits.value, misses.value)
+    assert m["misses"] > slots and m["hits"] > 0        # evictions happened, and hits
+    # the oracle with every expert resident
+    want = h0.copy()
+    for t in range(steps):
+        for l in range(layers):
+            desc = dict(hidden=H, inter=I, experts=E, top_k=K, group=G, gating=0, renorm=True,
+                        routed_scaling=1.0, min_weight=0.0, router_w=routers[l], router_bias=None,
+                        offsets=(go, uo, do))
+            x = want[t:t + 1].copy()
+            want[t:t + 1] = O.moe_layer(desc, [pk.blob_of(l, e) for e in range(E)], x, want[t:t + 1].copy())[0]
+    assert rel_l2(got_h - h0, want - h0) <= 1e-3
+    Lc.lp_cache_free(model)
+    pg.sync()
+    pg.close()
+    for p in d_routers + [ws, dh]:
+        cuda.free_device(p)
+    cuda.destroy_stream(s)
+    pk.free()
