@@ -168,6 +168,8 @@ typedef struct lp_moe_ws_layout {
     uint64_t sh_perm; /* shared MLP: i32 [T] identity token list */
     uint64_t sh_act;  /* shared MLP: f32 [T, shared_inter] */
     uint64_t sh_y;    /* shared MLP: f32 [T, H] */
+    uint64_t tiles;   /* prefill GEMM tile list (size 0 on the decode path) */
+    uint64_t actimg;  /* prefill GEMM: images of the act rows (size 0 on the decode path) */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;
 

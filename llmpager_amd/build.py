@@ -1,7 +1,8 @@
 """Build the gfx950 code objects and the C-ABI host library, in-tree.
 
 Outputs (under llmpager_amd/lib/):
-  lp_basic.hsaco, lp_moe.hsaco   kernels, hipcc --genco --offload-arch=gfx950
+  lp_basic.hsaco, lp_moe.hsaco,
+  lp_gemm.hsaco                   kernels, hipcc --genco --offload-arch=gfx950
   libllmpager_hip.so              host runtime (g++), loads the code objects
                                   with hipModuleLoad at lp_init
 
@@ -22,7 +23,7 @@ OUT = os.path.join(HERE, "lib")
 ROOT = os.path.dirname(HERE)
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip"]
+KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip", "lp_gemm.hip"]
 HOST_SOURCES = ["lp_runtime.cpp", "lp_synth.cpp", "lp_cache.cpp", "lp_pager.cpp"]
 
 # Packed-FP32 instructions stay off (the code is written for scalar fp32).

@@ -138,6 +138,8 @@ struct Workspace {
     uint64_t sh_perm;    // shared MLP: i32 [T], t
     uint64_t sh_act;     // shared MLP: f32 [T, shared_inter]
     uint64_t sh_y;       // shared MLP: f32 [T, H]
+    uint64_t tiles;      // prefill GEMM: i32 tile list
+    uint64_t actimg;     // prefill GEMM: [T*k] images of act rows (image_bytes(I) each)
 };
 
 struct RouteArgs {
@@ -155,6 +157,31 @@ struct GroupedArgs {
     uint64_t h;          // f32 [T, H] residual (combine)
     int32_t T;
     int32_t pairs_cap;   // token pairs the dynamic LDS holds at once
+};
+
+// Prefill grouped GEMM (lp_gemm.hip).
+constexpr int kGemmBM = 64;            // tokens per tile
+constexpr int kGemmRows = 128;         // weight rows per tile (gate/up: 64 gate + the same 64 up)
+constexpr int kGemmMinPairsPerExpert = 16;  // the experts path switches to the GEMM at this average
+
+// LDS of one GEMM pipeline stage (one 32-column sub-group of K).
+constexpr int kGemmStageA = 2 * kGemmBM * 64;          // hi / lo bf16 fragments, 64 B per token
+constexpr int kGemmStageSeeds = 2 * kGemmBM * 4;       // -136 * part sums
+constexpr int kGemmStageB = kGemmRows * 64;            // dequantised bf16 weights, 64 B per row
+constexpr int kGemmStageScales = kGemmRows * 4;        // f32 scales
+constexpr int kGemmStage = kGemmStageA + kGemmStageSeeds + kGemmStageB + kGemmStageScales;
+constexpr int kGemmLds = 2 * kGemmStage + kGemmBM * 8; // two stages + the tile rows' image addresses
+
+struct GemmArgs {
+    LayerView L;
+    Workspace W;
+    uint64_t a_img;      // A images: gate/up = W.xf (token rows through perm); down = act images
+    uint64_t out;        // gate/up: act f32 [T*k, I]; down: y f32 [T*k, H]
+    uint64_t tiles;      // i32 [max_tiles]: (expert entry << 16) | token block; count in meta[2]
+    int32_t T;
+    int32_t max_tiles;
+    int32_t nblocks;     // weight-row blocks per tile row
+    int32_t pad0;
 };
 
 // Error flags written into Workspace.meta[1].

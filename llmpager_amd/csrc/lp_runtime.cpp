@@ -66,6 +66,10 @@ enum Fn {
     kTopkDispatch,
     kExpfWave,
     kResolve,
+    kGemmTiles,
+    kGemmGateup,
+    kGemmActImg,
+    kGemmDown,
     kNumFns
 };
 
@@ -84,10 +88,12 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_combine"},    {"lp_moe.hsaco", "lp_moe_ximage"},
     {"lp_moe.hsaco", "lp_moe_topk_dispatch"}, {"lp_basic.hsaco", "lp_expf_wave"},
     {"lp_moe.hsaco", "lp_moe_resolve"},
+    {"lp_gemm.hsaco", "lp_gemm_tiles"},    {"lp_gemm.hsaco", "lp_gemm_gateup"},
+    {"lp_gemm.hsaco", "lp_gemm_actimg"},   {"lp_gemm.hsaco", "lp_gemm_down"},
 };
 
-const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco"};
-constexpr int kNumModules = 2;
+const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
+constexpr int kNumModules = 3;
 
 std::string library_dir() {
     Dl_info info;
@@ -466,6 +472,18 @@ int lp_add(lp_ctx* c, uint64_t pa, uint64_t pb, int n, lp_stream s) {
 
 // ---- fused MoE layer --------------------------------------------------------------
 
+// Prefill: the grouped GEMM takes over from the decode kernels once routed
+// experts average kGemmMinPairsPerExpert (token, pick) pairs.
+static bool use_gemm(const lp_moe_layer_desc* d, int T) {
+    const long pairs = (long)T * d->top_k;
+    return pairs >= (long)kGemmMinPairsPerExpert * std::min<long>(d->experts, pairs);
+}
+
+static int gemm_max_tiles(const lp_moe_layer_desc* d, int T) {
+    const int pairs = T * d->top_k;
+    return pairs / kGemmBM + std::min(d->experts, pairs) + 1;
+}
+
 int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out) {
     if (!d || !out || T <= 0) return fail(LP_E_INVALID, "ws layout: bad arguments");
     const uint64_t E = (uint64_t)d->experts, k = (uint64_t)d->top_k, H = (uint64_t)d->hidden,
@@ -495,6 +513,9 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->sh_perm = take(sh ? t * 4 : 0);
     out->sh_act = take(t * Is * 4);
     out->sh_y = take(sh ? t * H * 4 : 0);
+    const bool gemm = use_gemm(d, T);
+    out->tiles = take(gemm ? (uint64_t)gemm_max_tiles(d, T) * 4 : 0);
+    out->actimg = take(gemm ? t * k * (uint64_t)image_bytes((int)I) : 0);
     out->total = o;
     return LP_OK;
 }
@@ -581,6 +602,8 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->sh_perm = ws + lay.sh_perm;
     W->sh_act = ws + lay.sh_act;
     W->sh_y = ws + lay.sh_y;
+    W->tiles = ws + lay.tiles;
+    W->actimg = ws + lay.actimg;
 }
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
@@ -674,7 +697,30 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     if (lds_for(1) > c->max_lds)
         return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
     ga.pairs_cap = cap;
-    if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), s)) return r;
+    if (use_gemm(d, T)) {
+        if ((size_t)kGemmLds > c->max_lds) return fail(LP_E_UNSUPPORTED, "GEMM stages exceed the LDS");
+        GemmArgs gm{};
+        gm.L = ga.L;
+        gm.W = ga.W;
+        gm.T = T;
+        gm.tiles = ga.W.tiles;
+        gm.max_tiles = gemm_max_tiles(d, T);
+        if (int r = launch(c, kGemmTiles, dim3(1), dim3(256), 0, s, gm)) return r;
+        gm.a_img = ga.W.xf;
+        gm.out = ga.W.act;
+        gm.nblocks = (d->inter + kGemmRows / 2 - 1) / (kGemmRows / 2);
+        if (int r = launch(c, kGemmGateup, dim3((unsigned)(gm.max_tiles * gm.nblocks)), dim3(256), kGemmLds, s, gm))
+            return r;
+        if (int r = launch(c, kGemmActImg, dim3((unsigned)((T * d->top_k + 7) / 8)), dim3(256), 0, s, gm))
+            return r;
+        gm.a_img = ga.W.actimg;
+        gm.out = ga.W.y;
+        gm.nblocks = (d->hidden + kGemmRows - 1) / kGemmRows;
+        if (int r = launch(c, kGemmDown, dim3((unsigned)(gm.max_tiles * gm.nblocks)), dim3(256), kGemmLds, s, gm))
+            return r;
+    } else if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), s)) {
+        return r;
+    }
     if (d->shared_blob) {
         // the shared MLP through the same kernels: its own width, group and
         // regions, one expert entry covering every token (written by dispatch)
