@@ -179,6 +179,115 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
     return res
 
 
+PREFILL_T = 2048
+PREFILL_KERNELS = ("lp_moe_router", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_ximage", "lp_gemm_tiles",
+                   "lp_gemm_gateup", "lp_gemm_actimg", "lp_gemm_down", "lp_moe_combine")
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
+    """a 2048-token chunk through one Qwen3-30B-A3B-shape
+    layer whose router logits carry a Zipf(1.1) per-expert offset
+    (v_e += -1.1 ln rank_e, rank a seeded permutation of 1..128), so expert
+    loads are skewed (the top expert takes ~23% of the picks).
+
+    The logits are the device router's own (lp_moe_route on the chunk), biased
+    once on the host and kept resident; a step is lp_moe_route_logits (top-k
+    + dispatch from those logits) + lp_moe_experts (activation images, the
+    grouped MFMA GEMMs, combine into the residual), and the router GEMV's
+    measured time over the same chunk is added to it for tok/s."""
+    import llmpager_amd as lp
+    T = PREFILL_T
+    span = align(lp.blob_bytes(H, I, G))
+    host = lp.synth_blobs(E, span, H, I, G, 0, 0, threads=min(16, os.cpu_count() or 1))
+    arena = cuda.upload(host, s)
+    rw = lp.synth_bf16(E * H, 0.02, 0, 1000)
+    d_rw = cuda.upload(rw, s)
+    d_slots = cuda.upload(np.arange(E, dtype=np.int32), s)
+    go, uo, do = lp.blob_offsets(H, I, G)
+    desc = lp.LayerDesc(hidden=H, inter=I, experts=E, top_k=K, group=G, gating=lp.GATING_SOFTMAX,
+                        renorm=1, routed_scaling=1.0, min_weight=0.0, router_w=d_rw, router_bias=0,
+                        slot_table=d_slots, arena_base=arena, slot_span=span,
+                        gate_off=go, up_off=uo, down_off=do)
+    layer = lp.MoeLayer(cuda, desc)
+    lay = lp.ws_layout(desc, T)
+    assert lay.tiles != lay.actimg, "config 3 must take the grouped-GEMM path"
+    ws = cuda.alloc_device(lay.total)
+    x, h = lp.synth_f32_bf16(T * H, 1.0, 0, 3), lp.synth_f32_bf16(T * H, 1.0, 0, 4)
+    dx, dh = cuda.upload(x, s), cuda.upload(h, s)
+    cuda.sync_stream(s)     # the host copies above may go once the uploads are done
+    del host
+    layer.route(dx, T, ws, s)
+    logits = cuda.download(ws + lay.logits, (T, E), np.float32, s)
+    rank = np.random.default_rng(0).permutation(E) + 1
+    biased = np.ascontiguousarray(logits + (-1.1 * np.log(rank)).astype(np.float32), np.float32)
+    dl = cuda.upload(biased, s)
+    cuda.sync_stream(s)
+
+    def step():
+        layer.route_logits(dl, T, ws, s)
+        layer.experts(dx, dh, T, ws, s)
+
+    for _ in range(warmup):
+        step()
+    e0, e1 = cuda.event(), cuda.event()
+    cuda.sync()
+    cuda.record_event(e0, s)
+    for _ in range(steps):
+        step()
+    cuda.record_event(e1, s)
+    cuda.sync()
+    ms = cuda.elapsed_ms(e0, e1) / steps
+    cuda.profile_reset()
+    cuda.profile(True)
+    for _ in range(steps):
+        step()
+    for _ in range(steps):
+        layer.route(dx, T, ws, s)     # the router GEMV over the same chunk
+    cuda.sync()
+    prof = {k: cuda.profile_read(k) for k in PREFILL_KERNELS}
+    cuda.profile(False)
+    step()
+    gs = cuda.download(ws + lay.gs, (E + 1,), np.int32, s)
+    uniq, err = layer.status(ws, T, s)
+    for p in (ws, dx, dh, dl, arena, d_rw, d_slots):
+        cuda.free_device(p)
+    for e in (e0, e1):
+        cuda.destroy_event(e)
+    assert err == 0, f"prefill step reported error flags {err}"
+    avg = {k: v[0] / max(v[1], 1) for k, v in prof.items() if v[1]}   # ms per launch
+    load = np.diff(gs)
+    pairs = int(gs[-1])
+    router_ms = avg.get("lp_moe_router", 0.0)
+    step_ms = ms + router_ms
+    gu_flop = 2.0 * pairs * (2 * I) * H
+    dn_flop = 2.0 * pairs * H * I
+    rt_flop = 2.0 * T * E * H
+
+    def tf(flop, t_ms):
+        return flop / (t_ms / 1e3) / 1e12 if t_ms > 0 else 0.0
+
+    gu_ms, dn_ms = avg["lp_gemm_gateup"], avg["lp_gemm_down"]
+    gemm_tf = tf(gu_flop + dn_flop, gu_ms + dn_ms)
+    res = dict(
+        tokens=T, tok_s=T / (step_ms / 1e3), ms_per_step=step_ms, route_experts_ms=ms,
+        flop_per_step=gu_flop + dn_flop + rt_flop, pairs=pairs, unique_experts=uniq,
+        max_expert_load=int(load.max()), top_expert_share=float(load.max() / max(pairs, 1)),
+        gemm=dict(gateup_us=gu_ms * 1e3, down_us=dn_ms * 1e3,
+                  gateup_tflops=tf(gu_flop, gu_ms), down_tflops=tf(dn_flop, dn_ms),
+                  tflops=gemm_tf, mfma_util=gemm_tf / MFMA_PEAK_TFLOPS),
+        layer_tflops=tf(gu_flop + dn_flop + rt_flop, step_ms),
+        dispatch_us=(avg.get("lp_moe_topk", 0) + avg.get("lp_moe_dispatch", 0)) * 1e3,
+        combine_us=avg.get("lp_moe_combine", 0) * 1e3,
+        kernels_avg_us={k: v * 1e3 for k, v in avg.items()},
+    )
+    log(f"prefill T={T}: {res['tok_s']:.0f} tok/s, {step_ms:.3f} ms/layer, GEMMs "
+        f"{gemm_tf:.0f} TFLOP/s ({100 * res['gemm']['mfma_util']:.1f}% of bf16 MFMA), gate/up "
+        f"{gu_ms * 1e3:.1f} us, down {dn_ms * 1e3:.1f} us, dispatch {res['dispatch_us']:.1f} us, "
+        f"combine {res['combine_us']:.1f} us, top expert {res['top_expert_share']:.3f} of picks")
+    return res
+
+
 def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
     """The oracle (oracle/, the CPU restatement of the reference path) on the
     host cores: the first layers kept in host memory, B tokens, repeated until
@@ -231,6 +340,12 @@ def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
                        f"{len(layers)} layers, scaled to the 48-layer stack")
 
 
+def _rounded(d):
+    if isinstance(d, dict):
+        return {k: _rounded(v) for k, v in d.items()}
+    return round(d, 4) if isinstance(d, float) else d
+
+
 def main() -> int:
     global LAYERS
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -242,6 +357,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill leg")
+    ap.add_argument("--prefill-only", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: this build's MoE path runs on a single MI355X "
@@ -263,6 +380,11 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
+    prefill = None if a.no_prefill else run_prefill(cuda, s, a.steps, a.warmup)
+    if a.prefill_only:
+        print(json.dumps({"prefill": prefill}), flush=True)
+        cuda.close()
+        return 0
     log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
     stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu else 2)
     results = {}
@@ -304,6 +426,7 @@ def main() -> int:
             "avg_us": round(dom["avg_us"], 3),
         },
         "cpu_baseline": cpu,
+        "prefill": None if prefill is None else _rounded(prefill),
         "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
                              for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
                     | {"gateup_gbps": round(r["dominant"]["gbps"], 1),

@@ -170,6 +170,7 @@ typedef struct lp_moe_ws_layout {
     uint64_t sh_y;    /* shared MLP: f32 [T, H] */
     uint64_t tiles;   /* prefill GEMM tile list (size 0 on the decode path) */
     uint64_t actimg;  /* prefill GEMM: images of the act rows (size 0 on the decode path) */
+    uint64_t xlo;     /* i32 [T]: 1 when a token's image in xf has a non-zero lo part */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;
 

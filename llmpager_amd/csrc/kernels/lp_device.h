@@ -226,8 +226,12 @@ __device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int ti
 }
 
 // Sub-group g of an fp32 row of `cols` columns into the row's fragment image
-// (lpk::image_bytes layout): part blocks [2][ngp][64 B], then seeds [ngp][2].
-__device__ __forceinline__ void write_image_group(const float* row, int cols, int g, uint8_t* img) {
+// (lpk::image_bytes layout): part blocks [2][ngp][64 B], then seeds [ngp][2]:
+// [0] = -136 * sum(hi) + -136 * sum(lo), the whole sub-group's seed, and
+// [1] = 0 (a consumer that keeps the parts in separate accumulator rows seeds
+// the hi row with [0] and the lo row with [1]).  Returns whether any lo
+// element is non-zero.
+__device__ __forceinline__ bool write_image_group(const float* row, int cols, int g, uint8_t* img) {
     const int ng = cols >> 5, ngp = lpk::frag_ngp(cols);
     const GroupFrag q =
         convert_group(g < ng ? gptr<float4>(reinterpret_cast<uint64_t>(row + (size_t)g * 32)) : nullptr);
@@ -238,7 +242,11 @@ __device__ __forceinline__ void write_image_group(const float* row, int cols, in
         hi[d] = q.hi[d];
         lo[d] = q.lo[d];
     }
-    reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * q.shi, -136.0f * q.slo);
+    reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * q.shi + -136.0f * q.slo, 0.0f);
+    uint32_t any = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) any |= q.lo[d].x | q.lo[d].y | q.lo[d].z | q.lo[d].w;
+    return any != 0;
 }
 
 // Copy the fragment images of nt tokens (img_of(t): device address of token

@@ -2,24 +2,27 @@
 // tables (the reference prefills with one GEMV per token, decode.rs:469-531;
 // the arithmetic each output restates is q4g64.cu:19-81's).
 //
-// A tile is (routed expert, block of kGemmBM of its tokens, block of weight
-// rows): gate/up tiles take 64 rows of gate and the same 64 rows of up so
-// that SiLU * up is the epilogue; down tiles take 128 rows.  K runs over
-// 32-column sub-groups, one pipeline stage each:
-//   A (activations): the token rows' fragment images (bf16 hi = bf16(x), lo =
-//     bf16(x - hi), MFMA operand order, and the -136 * part sums), gathered
-//     through the dispatch permutation;
-//   B (weights): the q4 nibbles of the stage, turned into bf16 128 + q once
-//     per stage by the loading threads (v_bitop3_b32 per word pair) for all
-//     four waves, plus the rows' f16 scales as f32;
-//   v_mfma_f32_16x16x32_bf16 over one sub-group is then sum_k (hi + lo)_k *
-//     (128 + q_k), seeded with -136 * sum_k (hi + lo)_k so it equals
-//     sum_k x_k (q_k - 8) exactly up to fp32 rounding, and the sub-group's
-//     scale is applied in fp32.  A stage whose lo parts are all zero (bf16
-//     activations) skips the lo MFMAs.
-// Stage g + 1's loads are issued (unconditionally, the last one repeated)
-// before stage g's MFMAs, into registers, and written to the other LDS
-// buffer after them.
+// A tile is (routed expert, block of kGemmBM = 128 of its tokens, block of
+// weight rows): gate/up tiles take 64 rows of gate and the same 64 rows of up
+// so that SiLU * up is the epilogue; down tiles take 128 rows.  Wave w owns
+// the 16-token blocks 2 mt + (w & 1), mt = 0..3, and one half of the rows
+// (w >> 1): 4 x 4 tiles of v_mfma_f32_16x16x32_bf16 (gate/up: two gate tiles
+// and the matching two up tiles).
+//
+// K runs over 32-column sub-groups, one pipeline stage each.  Operands reach
+// LDS by direct-to-LDS loads (no registers, no LDS stores), each stream in
+// whole 64-byte pieces of memory:
+//   A: per stage, the 128 token rows' fragment blocks (bf16 hi = bf16(x), lo
+//      = bf16(x - hi), in MFMA operand order; gate/up gathers the token images
+//      through the dispatch permutation), lo only when a token of the tile has
+//      one; three slots, loads two stages ahead;
+//   B: per kGemmBGroups stages, 64 nibble bytes of each of the tile's 128
+//      weight rows; two slots;
+//   scales: per kGemmSGroups stages, a 16-scale window of each row; two slots.
+// Each wave turns its B words into bf16 128 + q (one v_bitop3_b32 per two
+// values); one MFMA of the A block against bf16(-136) gives -136 sum_k (hi +
+// lo)_k, which seeds the sub-group's MFMAs, so they return sum_k x_k (q_k - 8)
+// exactly up to fp32 rounding; the sub-group's scale is then applied in fp32.
 #include "lp_device.h"
 
 using namespace lp;
@@ -46,183 +49,372 @@ __device__ __forceinline__ ExpertEntry load_entry(uint64_t et, int u) {
     return x;
 }
 
-// One matrix (a q4 region of `rows` x `cols`) read through a raw buffer
-// resource: loads past the region return zero.
-struct Region {
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t data;  // byte offset of the nibbles
-    int ng, gpr;    // 32-column sub-groups per row, scales per row
-};
+__shared__ __align__(16) uint8_t g_lds[kGemmLds];
 
-__device__ __forceinline__ Region region_at(uint64_t base, int rows, int cols, int rs) {
-    Region r;
-    r.ng = cols >> 5;
-    r.gpr = r.ng >> rs;
-    const uint32_t sbytes = (uint32_t)rows * r.gpr * 2;
-    r.data = sbytes;
-    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0,
-                                               (int)(sbytes + (uint32_t)rows * r.ng * 16), kBufferWord3);
-    return r;
+// Chunk kb (16 bytes) of token m's 64-byte block within a 16-token block of
+// LDS sits at slot 4 m + (kb ^ chunk_swz(m)): the MFMA operand read (lane =
+// 16 kb + m) then touches 16 distinct 16-byte bank groups per 16 lanes and 8
+// per 8 lanes, while each direct-load quad still copies one token's 64
+// contiguous bytes.
+__device__ __forceinline__ int chunk_swz(int m) { return ((m >> 1) ^ (m >> 3)) & 3; }
+
+// B slot: row r's kGemmBGroups 16-byte sub-group pieces sit at 64 r + 16 (j ^
+// b_swz(r)) for sub-group j of the load, so that the operand read (16 rows x
+// one 32-bit word) hits distinct banks; each direct-load quad still copies
+// one row's 64 contiguous bytes.
+__device__ __forceinline__ int b_swz(int r) { return (r >> 2) & 3; }
+
+__device__ __forceinline__ void dma16(uint64_t base, uint32_t off, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
-struct StageRegs {
-    uint4 a0, a1;     // this thread's two A units
-    uint4 q;          // waves 0-1: one weight row's 32 nibbles
-    uint32_t sc;      // waves 2-3: one row's f16 scale bits
-    float seed;       // waves 2-3: one (part, token) seed
-};
-
-// Issue stage g's loads.  Thread t: A units t and t + 256 (part = u >> 8,
-// token = (u >> 2) & 63, 16-byte unit u & 3); waves 0-1: weight row t's
-// nibbles; waves 2-3: row (t - 128)'s scale and seed (t - 128).
-template <int MODE, int RS>
-__device__ __forceinline__ void stage_load(StageRegs& R, const uint64_t* rowimg, const Region& r0,
-                                           const Region& r1, int n0, int ngp, int g) {
-    const int t = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the descriptors stay scalar
-    const int u0 = t, u1 = t + 256;
-    R.a0 = gptr<uint4>(rowimg[(u0 >> 2) & 63] + (uint64_t)(u0 >> 8) * ngp * 64 + (uint64_t)g * 64)[u0 & 3];
-    R.a1 = gptr<uint4>(rowimg[(u1 >> 2) & 63] + (uint64_t)(u1 >> 8) * ngp * 64 + (uint64_t)g * 64)[u1 & 3];
-    // gate/up: odd waves take the up matrix (rows 64-127 of the tile are the
-    // same matrix rows as 0-63); down: one matrix, 128 rows
-    const bool up = MODE == 0 && (wave & 1);
-    const __amdgpu_buffer_rsrc_t rsrc = up ? r1.rsrc : r0.rsrc;
-    const int i = t & 127;
-    const int row = n0 + (MODE == 0 ? (i & 63) : i);
-    if (wave < 2) {  // waves 0-1: row i's nibbles
-        R.q = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(r0.data + ((uint32_t)row * r0.ng + g) * 16u), 0, 0));
-    } else {  // waves 2-3: row i's scale, seed i
-        R.sc = __builtin_amdgcn_raw_buffer_load_b16(rsrc, (int)(((uint32_t)row * r0.gpr + (g >> RS)) * 2u), 0, 0);
-        R.seed = gptr<float>(rowimg[i & 63] + (uint64_t)ngp * 128)[2 * g + (i >> 6)];
-    }
+// LDS address of g_lds (the M0 operand of the direct loads is an LDS address).
+__device__ __forceinline__ uint32_t lds_base() {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)g_lds;
 }
 
-// Write stage registers into LDS buffer `buf`; returns whether any lo unit of
-// this thread is non-zero.
-__device__ __forceinline__ bool stage_store(const StageRegs& R, uint8_t* buf) {
-    const int t = threadIdx.x;
-    uint4* A = reinterpret_cast<uint4*>(buf);
-    A[t] = R.a0;
-    A[t + 256] = R.a1;
-    if (t < 128) {
-        uint4* B = reinterpret_cast<uint4*>(buf + kGemmStageA + kGemmStageSeeds) + t * 4;
-        const uint32_t w[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
+// Wait until at most n vector-memory loads of this wave are outstanding and
+// its LDS reads are done; with the loads completing in issue order this is
+// "stage s has landed" when n counts the loads issued after stage s's.
+#define LP_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+// s_barrier as a compiler-level memory fence too: no LDS access or load moves
+// across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+struct GemmTile {
+    ExpertEntry x;
+    int m0, mvalid, n0;   // token block start and size; first matrix row of the tile
+    int K, NR, ng, ngp;   // reduction width, matrix rows, sub-groups, padded sub-groups
+    uint64_t off0, off1;  // byte offsets in the blob: gate/up: gate and up regions; down: down twice
+};
+
+// Matrix row (in 0 .. NR-1) behind row r of the tile's B buffer.
+template <int MODE>
+__device__ __forceinline__ int tile_row(const GemmTile& g, int r) {
+    return min(g.n0 + (MODE == 0 ? (r & 63) : r), g.NR - 1);
+}
+
+template <int MODE, int RS, bool LO>
+__device__ __forceinline__ void gemm_main(const GemmArgs& a, const GemmTile& G) {
+    // Sub-groups per stage: an A slot holds one sub-group's hi and lo parts,
+    // or two sub-groups' hi parts when the tile has no lo.
+    constexpr int GPS = LO ? 1 : 2;
+    constexpr int OPS_A = 4;  // A loads per wave per stage (two 16-token blocks x two parts / sub-groups)
+    const int tid = threadIdx.x, lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA targets stay scalar
+    const int wm = wave & 1, wn = wave >> 1;
+    const int nst = (G.ng + GPS - 1) / GPS;
+    const uint32_t lds0 = lds_base();
+    const uint64_t part_bytes = (uint64_t)G.ngp * 64;
+    const int gpr = G.ng >> RS;
+    const uint32_t sbytes = (uint32_t)G.NR * gpr * 2;
+    const uint64_t* rowimg = reinterpret_cast<const uint64_t*>(g_lds + kGemmLdsRows);
+
+    // --- load sources: a uniform 64-bit base plus per-lane 32-bit offsets ---
+    const uint64_t a_base = a.a_img;
+    // (each half zero-extended: readfirstlane returns a signed int)
+    const uint64_t w_base = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)G.x.blob) |
+                            ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(G.x.blob >> 32)) << 32);
+    // A: block 2 w + j of 16 tokens; lane l copies chunk (l & 3) ^ swz of token l >> 2
+    uint32_t a_off[2];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) B[d] = __builtin_bit_cast(uint4, q4_word_to_bf16x8(w[d]));
-    } else {
-        const int i = t - 128;
-        reinterpret_cast<float*>(buf + kGemmStageA)[i] = R.seed;
-        reinterpret_cast<float*>(buf + kGemmStageA + kGemmStageSeeds + kGemmStageB)[i] = f16_bits_to_f32(R.sc);
+    for (int j = 0; j < 2; ++j) {
+        const int m = lane >> 2;
+        a_off[j] = (uint32_t)(rowimg[16 * (2 * wave + j) + m] - a_base) + (uint32_t)(((lane & 3) ^ chunk_swz(m)) * 16);
     }
-    const uint4 lo = R.a1;  // units t + 256 are all lo parts
-    return (lo.x | lo.y | lo.z | lo.w) != 0u;
+    // B: rows 32 w + 16 i + (l >> 2); lane l copies the row's piece j = l & 3,
+    // i.e. sub-group kGemmBGroups S + (j ^ b_swz(row)) of load S
+    uint32_t b_row[2];
+    const int b_j = (lane & 3) ^ ((lane >> 4) & 3);  // j ^ b_swz(row): row bits 2-3 are lane bits 4-5
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 32 * wave + 16 * i + (lane >> 2);
+        const uint32_t mat = (uint32_t)((MODE == 0 && r >= 64) ? G.off1 : G.off0);
+        b_row[i] = mat + sbytes + (uint32_t)tile_row<MODE>(G, r) * G.ng * 16;
+    }
+    // scales: row 32 w + (l >> 1), 16-byte half l & 1 of the row's window
+    const int s_r = 32 * wave + (lane >> 1);
+    const uint32_t s_mat = (uint32_t)((MODE == 0 && s_r >= 64) ? G.off1 : G.off0) + 16 * (lane & 1);
+    const uint32_t s_idx = (uint32_t)tile_row<MODE>(G, s_r) * gpr;
+
+    // stage st into A slot `slot`: half q of the slot is part q of sub-group
+    // st (LO) or sub-group 2 st + q (no lo; a padding sub-group of the image
+    // past the last one reads as zeros)
+    auto issue_a = [&](int st, int slot) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                dma16(a_base + (LO ? q * part_bytes + (uint64_t)st * 64 : (uint64_t)(GPS * st + q) * 64), a_off[j],
+                      lds0 + slot * kGemmSlotA + q * kGemmBM * 64 + (2 * wave + j) * 1024);
+    };
+    auto issue_b = [&](int S, int slot) {
+        const uint32_t g = (uint32_t)min(kGemmBGroups * S + b_j, G.ng - 1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            dma16(w_base, b_row[i] + g * 16, lds0 + kGemmLdsB + slot * kGemmSlotB + (32 * wave + 16 * i) * 64);
+    };
+    // the window starts at the 8-aligned scale index at or below the row's
+    // first scale of the load: 16 scales cover the 8 >> RS it needs
+    auto issue_s = [&](int S, int slot) {
+        const uint32_t c0 = (s_idx + (uint32_t)((kGemmSGroups * S) >> RS)) & ~7u;
+        dma16(w_base, s_mat + c0 * 2, lds0 + kGemmLdsS + slot * kGemmSlotS + wave * 1024);
+    };
+
+    // --- read side ---
+    // B / scale row of n-tile t: rbase + roff(t)
+    const int rbase = MODE == 0 ? 32 * wn + (lane & 15) : 64 * wn + (lane & 15);
+    auto roff = [](int t) { return MODE == 0 ? (t < 2 ? 16 * t : 64 + 16 * (t - 2)) : 16 * t; };
+    const int am = lane & 15, akb = lane >> 4;
+    // the wave's 16-token blocks are 2 mt + wm (mt = 0..3): both halves of a
+    // partly filled tile get about the same number of valid blocks
+    const uint8_t* a_rd = g_lds + wm * 1024 + (4 * am + (akb ^ chunk_swz(am))) * 16;
+    const uint8_t* b_rd = g_lds + kGemmLdsB + rbase * 64 + akb * 4;
+    const int b_x = b_swz(rbase) << 4;  // roff(t) is a multiple of 16: same swizzle for every t
+    uint32_t s_row[4];                   // the row's scale index at sub-group 0
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s_row[t] = (uint32_t)tile_row<MODE>(G, rbase + roff(t)) * gpr;
+    int s_rd[4];                         // LDS byte offset of the window's first scale of the load
+    const int nmt = max(0, min(4, (((G.mvalid + 15) >> 4) - wm + 1) >> 1));  // valid blocks of the wave
+    const bf16x8_t k136 = __builtin_bit_cast(bf16x8_t, u32x4_t{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // this stage's weight words (as bf16 128 + q) and scales
+    auto stage_b = [&](int g, bf16x8_t (&b)[4], float (&sc)[4], uint32_t (&w)[4]) {
+        const int b_slot = ((g / kGemmBGroups) & 1) * kGemmSlotB + (((g % kGemmBGroups) << 4) ^ b_x);
+        const int s_sub = (g >> RS) - ((kGemmSGroups * (g / kGemmSGroups)) >> RS);  // scale within the load
+        const int s_slot = ((g / kGemmSGroups) & 1) * kGemmSlotS + 2 * s_sub;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            w[t] = *reinterpret_cast<const uint32_t*>(b_rd + b_slot + roff(t) * 64);
+            sc[t] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(g_lds + s_rd[t] + s_slot));
+        }
+        (void)b;
+    };
+    auto mfma = [](const uint4& a, const bf16x8_t& b, const f32x4_t& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), b, c, 0, 0, 0);
+    };
+
+    // Partly filled block set: one block at a time, FMAs right behind.
+    auto compute_part = [&](int g, int a_slot) {
+        if (nmt == 0) return;
+        bf16x8_t b[4];
+        float sc[4];
+        uint32_t w[4];
+        stage_b(g, b, sc, w);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[t] = q4_word_to_bf16x8(w[t]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if (mt < nmt) {
+                const uint4 ahi = *reinterpret_cast<const uint4*>(a_rd + a_slot + mt * 2048);
+                const uint4 alo = LO ? *reinterpret_cast<const uint4*>(a_rd + a_slot + kGemmBM * 64 + mt * 2048) : ahi;
+                f32x4_t c0 = mfma(ahi, k136, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+                if (LO) c0 = mfma(alo, k136, c0);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    f32x4_t c = mfma(ahi, b[t], c0);
+                    if (LO) c = mfma(alo, b[t], c);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(sc[t], c[i], acc[mt][t][i]);
+                }
+            }
+        }
+    };
+
+    // All four blocks valid: a software pipeline in which each MFMA is
+    // followed by the four scale FMAs of an MFMA that finished long before,
+    // so the wave keeps its matrix and vector units busy together.  Block
+    // mt's FMAs run behind block mt + 1's MFMAs; block 3's behind the next
+    // stage's block 0 (cp / scp carry them).  Per stage:
+    //   seed MFMAs of the four blocks, each with a quarter of the nibble
+    //   decode behind it; then per block: per n-tile its MFMA(s), then the
+    //   lagging block's four FMAs of that n-tile.
+    f32x4_t cp[4];
+    float scp[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        cp[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        scp[t] = 0.0f;
+    }
+    auto compute_full = [&](int g, int a_slot) {
+        bf16x8_t b[4];
+        float sc[4];
+        uint32_t w[4];
+        stage_b(g, b, sc, w);
+        uint4 ahi[4], alo[4];
+        f32x4_t c0[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            ahi[mt] = *reinterpret_cast<const uint4*>(a_rd + a_slot + mt * 2048);
+            alo[mt] = LO ? *reinterpret_cast<const uint4*>(a_rd + a_slot + kGemmBM * 64 + mt * 2048) : ahi[mt];
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            c0[mt] = mfma(ahi[mt], k136, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+            if (LO) c0[mt] = mfma(alo[mt], k136, c0[mt]);
+            b[mt] = q4_word_to_bf16x8(w[mt]);
+            __builtin_amdgcn_sched_group_barrier(0x008, LO ? 2 : 1, 0);  // seed MFMA(s)
+            __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);           // a word's decode
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            f32x4_t cc[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                cc[t] = mfma(ahi[mt], b[t], c0[mt]);
+                if (LO) cc[t] = mfma(alo[mt], b[t], cc[t]);
+                // the lagging block: mt - 1 of this sub-group, or block 3 of
+                // the previous one (with its scales; zeros before the first)
+                f32x4_t& dst = acc[mt == 0 ? 3 : mt - 1][t];
+                const float sl = mt == 0 ? scp[t] : sc[t];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[i] = __builtin_fmaf(sl, cp[t][i], dst[i]);
+                __builtin_amdgcn_sched_group_barrier(0x008, LO ? 2 : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cp[t] = cc[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) scp[t] = sc[t];
+    };
+
+    // Stage st (sub-groups g0 = GPS st ..) needs A(st), B(g0 / 4) and
+    // scales(g0 / 8).  Everything issued before A(st + 1) is complete once at
+    // most OPS_A loads are outstanding (loads complete in issue order and
+    // A(st + 1) alone is OPS_A loads), and B / scale loads are issued at
+    // least one stage before the A(st + 1) that follows them; after the last
+    // A, wait for everything.
+    auto stage_begin = [&](int st) {
+        const int g = GPS * st;
+        if (st + 1 < nst) LP_WAIT_VM_LGKM0(OPS_A);
+        else LP_WAIT_VM_LGKM0(0);
+        stage_barrier();
+        if (st + 2 < nst) issue_a(st + 2, (st + 2) % kGemmASlots);
+        if (g % kGemmBGroups == 0 && g + kGemmBGroups < G.ng) issue_b(g / kGemmBGroups + 1, (g / kGemmBGroups + 1) & 1);
+        if (g % kGemmSGroups == 0) {
+            if (g + kGemmSGroups < G.ng) issue_s(g / kGemmSGroups + 1, (g / kGemmSGroups + 1) & 1);
+            const uint32_t first = (uint32_t)(g >> RS);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                s_rd[t] = kGemmLdsS + (rbase + roff(t)) * 32 + 2 * (int)((s_row[t] + first) & 7u);
+        }
+    };
+    issue_a(0, 0);
+    issue_b(0, 0);
+    issue_s(0, 0);
+    if (nst > 1) issue_a(1, 1);
+    if (nmt == 4) {
+        for (int st = 0; st < nst; ++st) {
+            stage_begin(st);
+            const int a_slot = (st % kGemmASlots) * kGemmSlotA;
+            compute_full(GPS * st, a_slot);
+            if (GPS == 2 && GPS * st + 1 < G.ng) compute_full(GPS * st + 1, a_slot + kGemmBM * 64);
+        }
+        // the last stage's block 3
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[3][t][i] = __builtin_fmaf(scp[t], cp[t][i], acc[3][t][i]);
+    } else {
+        for (int st = 0; st < nst; ++st) {
+            stage_begin(st);
+            const int a_slot = (st % kGemmASlots) * kGemmSlotA;
+            compute_part(GPS * st, a_slot);
+            if (GPS == 2 && GPS * st + 1 < G.ng) compute_part(GPS * st + 1, a_slot + kGemmBM * 64);
+        }
+    }
+
+    // epilogue: lane holds C rows 4 akb + i (tokens) of column lane & 15 of each tile
+    float* out = dptr<float>(a.out);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 16 * (2 * mt + wm) + 4 * akb + i;
+            if (m >= G.mvalid) continue;
+            float* orow = out + (size_t)(G.x.p0 + G.m0 + m) * G.NR;
+            if (MODE == 0) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int r = G.n0 + 32 * wn + 16 * t + am;
+                    const float gg = acc[mt][t][i], uu = acc[mt][t + 2][i];
+                    if (r < G.NR) orow[r] = gg / (1.0f + expf(-gg)) * uu;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int r = G.n0 + 64 * wn + 16 * t + am;
+                    if (r < G.NR) orow[r] = acc[mt][t][i];
+                }
+            }
+        }
+    }
 }
 
 template <int MODE, int RS>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
-    extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
-    const int H = L.hidden, I = L.inter, k = L.top_k;
-    const int ti = blockIdx.x / a.nblocks, nb = blockIdx.x - ti * a.nblocks;
+    const int k = L.top_k;
+    // XCD-aware order: workgroup w runs on XCD w % 8, so XCD x takes the
+    // contiguous range [x C, x C + C) of the live (tile, row block) items,
+    // row blocks innermost: the 128 tokens' A tile and the expert's weight
+    // blocks are then fetched into one XCD's L2 and reused there.
     const int count = dptr<const int>(a.W.meta)[2];
-    if (ti >= count) return;
+    const int live = count * a.nblocks;
+    const int C = (live + kXcds - 1) / kXcds;
+    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int item = xcd * C + j;
+    if (j >= C || item >= live) return;
+    const int ti = item / a.nblocks, nb = item - ti * a.nblocks;
     const int tv = dptr<const int>(a.tiles)[ti];
-    const ExpertEntry x = load_entry(a.W.et, tv >> 16);
-    const int m0 = (tv & 0xffff) * kGemmBM;
-    const int mvalid = min(kGemmBM, x.ntok - m0);
-    const int K = MODE == 0 ? H : I;         // reduction width
-    const int NR = MODE == 0 ? I : H;        // rows of each matrix
-    const int n0 = nb * (MODE == 0 ? kGemmRows / 2 : kGemmRows);
-    const int ng = K >> 5, ngp = frag_ngp(K);
-    const uint64_t ib = (uint64_t)image_bytes(K);
-    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    float* out = dptr<float>(a.out);
-    if (x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
+    GemmTile G;
+    G.x = load_entry(a.W.et, tv >> 16);
+    G.m0 = (tv & 0xffff) * kGemmBM;
+    G.mvalid = min(kGemmBM, G.x.ntok - G.m0);
+    G.K = MODE == 0 ? L.hidden : L.inter;
+    G.NR = MODE == 0 ? L.inter : L.hidden;
+    G.ng = G.K >> 5;
+    G.ngp = frag_ngp(G.K);
+    G.n0 = nb * (MODE == 0 ? kGemmBN / 2 : kGemmBN);
+    const int tid = threadIdx.x;
+    if (G.x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
         if (tid == 0 && nb == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
-        const int rows = MODE == 0 ? kGemmRows / 2 : kGemmRows;
-        for (int e = tid; e < mvalid * rows; e += blockDim.x) {
-            const int m = e / rows, r = n0 + e - m * rows;
-            if (r < NR) out[(size_t)(x.p0 + m0 + m) * NR + r] = 0.0f;
+        const int cols = MODE == 0 ? kGemmBN / 2 : kGemmBN;
+        float* out = dptr<float>(a.out);
+        for (int e = tid; e < G.mvalid * cols; e += blockDim.x) {
+            const int m = e / cols, r = G.n0 + e - m * cols;
+            if (r < G.NR) out[(size_t)(G.x.p0 + G.m0 + m) * G.NR + r] = 0.0f;
         }
         return;
     }
-    uint64_t* rowimg = reinterpret_cast<uint64_t*>(lds + 2 * kGemmStage);
+    G.off0 = MODE == 0 ? L.gate_off : L.down_off;
+    G.off1 = MODE == 0 ? L.up_off : L.down_off;
+    const uint64_t ib = (uint64_t)image_bytes(G.K);
+    // the tile rows' image addresses (rows past the block repeat its last
+    // token) and whether any of them carries a lo part
+    int lo = MODE == 1;
     if (tid < kGemmBM) {
-        const int m = min(tid, mvalid - 1);  // rows past the block repeat its last token
-        const int pos = x.p0 + m0 + m;
-        rowimg[tid] = MODE == 0 ? a.a_img + (uint64_t)(dptr<const int>(a.W.perm)[pos] / k) * ib
-                                : a.a_img + (uint64_t)pos * ib;
-    }
-    const Region r0 = region_at(x.blob + (MODE == 0 ? L.gate_off : L.down_off), NR, K, RS);
-    const Region r1 = region_at(x.blob + (MODE == 0 ? L.up_off : L.down_off), NR, K, RS);
-    __syncthreads();
-
-    float acc[8][4];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.0f;
-
-    StageRegs R;
-    stage_load<MODE, RS>(R, rowimg, r0, r1, n0, ngp, 0);
-    bool lo_any = __syncthreads_or(stage_store(R, lds));
-    for (int g = 0; g < ng; ++g) {
-        uint8_t* cur = lds + (g & 1) * kGemmStage;
-        // the next stage's loads go out first (the last stage is loaded twice)
-        stage_load<MODE, RS>(R, rowimg, r0, r1, n0, ngp, min(g + 1, ng - 1));
-        {
-            const uint4* A = reinterpret_cast<const uint4*>(cur);
-            const int am = 16 * wave + (lane & 15), kb = lane >> 4;
-            const uint4 ahi = A[(0 * kGemmBM + am) * 4 + kb];
-            const uint4 alo = A[(1 * kGemmBM + am) * 4 + kb];
-            const float* sd = reinterpret_cast<const float*>(cur + kGemmStageA);
-            const int cm = 16 * wave + 4 * kb;  // the lane's C rows cm .. cm+3
-            const float4 sh = *reinterpret_cast<const float4*>(sd + cm);
-            const float4 sl = *reinterpret_cast<const float4*>(sd + kGemmBM + cm);
-            const uint4* B = reinterpret_cast<const uint4*>(cur + kGemmStageA + kGemmStageSeeds);
-            const float* S = reinterpret_cast<const float*>(cur + kGemmStageA + kGemmStageSeeds + kGemmStageB);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int row = 16 * t + (lane & 15);
-                const bf16x8_t b = __builtin_bit_cast(bf16x8_t, B[row * 4 + kb]);
-                f32x4_t c;
-                c[0] = sh.x + sl.x;
-                c[1] = sh.y + sl.y;
-                c[2] = sh.z + sl.z;
-                c[3] = sh.w + sl.w;
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ahi), b, c, 0, 0, 0);
-                if (lo_any) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, alo), b, c, 0, 0, 0);
-                const float s = S[row];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(s, c[i], acc[t][i]);
-            }
-        }
-        // the other buffer was last read in the previous iteration, which every
-        // wave finished before that iteration's closing barrier
-        lo_any = __syncthreads_or(stage_store(R, lds + ((g + 1) & 1) * kGemmStage));
-    }
-
-    // epilogue: lane holds C rows cm + i (tokens) of column lane & 15 in every row tile
-    const int cm = 16 * wave + 4 * (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = cm + i;
-        if (m >= mvalid) continue;
-        float* orow = out + (size_t)(x.p0 + m0 + m) * NR;
+        const int pos = G.x.p0 + G.m0 + min(tid, G.mvalid - 1);
         if (MODE == 0) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int r = n0 + 16 * t + (lane & 15);
-                const float gg = acc[t][i], uu = acc[t + 4][i];
-                if (r < NR) orow[r] = gg / (1.0f + expf(-gg)) * uu;
-            }
+            const int tok = dptr<const int>(a.W.perm)[pos] / k;
+            reinterpret_cast<uint64_t*>(g_lds + kGemmLdsRows)[tid] = a.a_img + (uint64_t)tok * ib;
+            lo = dptr<const int>(a.W.xlo)[tok] != 0;
         } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int r = n0 + 16 * t + (lane & 15);
-                if (r < NR) orow[r] = acc[t][i];
-            }
+            reinterpret_cast<uint64_t*>(g_lds + kGemmLdsRows)[tid] = a.a_img + (uint64_t)pos * ib;
         }
     }
+    if (__syncthreads_or(lo))
+        gemm_main<MODE, RS, true>(a, G);
+    else
+        gemm_main<MODE, RS, false>(a, G);
 }
 
 #define LP_BY_RS(group, call)          \
@@ -275,16 +467,16 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_actimg(const GemmArgs 
     if (row >= total) return;
     const float* src = dptr<const float>(a.W.act) + (size_t)row * I;
     uint8_t* img = dptr<uint8_t>(a.W.actimg) + (size_t)row * image_bytes(I);
-    for (int g = threadIdx.x & 31; g < frag_ngp(I); g += 32) write_image_group(src, I, g, img);
+    for (int g = threadIdx.x & 31; g < frag_ngp(I); g += 32) (void)write_image_group(src, I, g, img);
 }
 
-extern "C" __global__ void __launch_bounds__(256) lp_gemm_gateup(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) lp_gemm_gateup(const GemmArgs a) {
 #define LP_G(rs) gemm_body<0, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G
 }
 
-extern "C" __global__ void __launch_bounds__(256) lp_gemm_down(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) lp_gemm_down(const GemmArgs a) {
 #define LP_G(rs) gemm_body<1, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G

@@ -44,11 +44,15 @@ __device__ __forceinline__ float div_rn(float a, float b) { return (float)((doub
 // ---------------------------------------------------------------------------
 namespace {
 
+// Token t's image, by the whole workgroup, and its lo flag (W.xlo[t]).
 __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
     const int H = a.L.hidden;
     const float* row = dptr<const float>(a.x) + (size_t)t * H;
     uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-    for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) write_image_group(row, H, g, img);
+    bool lo = false;
+    for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) lo |= write_image_group(row, H, g, img);
+    lo = __syncthreads_or(lo);
+    if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
 }
 
 

@@ -140,6 +140,7 @@ struct Workspace {
     uint64_t sh_y;       // shared MLP: f32 [T, H]
     uint64_t tiles;      // prefill GEMM: i32 tile list
     uint64_t actimg;     // prefill GEMM: [T*k] images of act rows (image_bytes(I) each)
+    uint64_t xlo;        // i32 [T]: 1 when token t's image in xf has a non-zero lo part
 };
 
 struct RouteArgs {
@@ -160,17 +161,26 @@ struct GroupedArgs {
 };
 
 // Prefill grouped GEMM (lp_gemm.hip).
-constexpr int kGemmBM = 64;            // tokens per tile
-constexpr int kGemmRows = 128;         // weight rows per tile (gate/up: 64 gate + the same 64 up)
+constexpr int kGemmBM = 128;           // tokens per tile
+constexpr int kGemmBN = 128;           // weight rows per tile (gate/up: 64 gate + the same 64 up)
 constexpr int kGemmMinPairsPerExpert = 16;  // the experts path switches to the GEMM at this average
+constexpr int kXcds = 8;               // MI355X: workgroup w is dispatched to XCD w % 8
 
-// LDS of one GEMM pipeline stage (one 32-column sub-group of K).
-constexpr int kGemmStageA = 2 * kGemmBM * 64;          // hi / lo bf16 fragments, 64 B per token
-constexpr int kGemmStageSeeds = 2 * kGemmBM * 4;       // -136 * part sums
-constexpr int kGemmStageB = kGemmRows * 64;            // dequantised bf16 weights, 64 B per row
-constexpr int kGemmStageScales = kGemmRows * 4;        // f32 scales
-constexpr int kGemmStage = kGemmStageA + kGemmStageSeeds + kGemmStageB + kGemmStageScales;
-constexpr int kGemmLds = 2 * kGemmStage + kGemmBM * 8; // two stages + the tile rows' image addresses
+// GEMM LDS.  K is consumed one 32-column sub-group per pipeline stage; the
+// activation blocks come per stage (three slots: loads run two stages ahead),
+// the weight nibbles per kGemmBGroups sub-groups (64 bytes of each row) and
+// the scales per kGemmSGroups sub-groups, each in two slots.  Every read is
+// one base register plus an immediate offset below 64 KiB.
+constexpr int kGemmASlots = 3;
+constexpr int kGemmBGroups = 4;
+constexpr int kGemmSGroups = 8;
+constexpr int kGemmSlotA = 2 * kGemmBM * 64;                   // [part][token][64 B]
+constexpr int kGemmSlotB = kGemmBN * kGemmBGroups * 16;        // [row][4 x 16 B]
+constexpr int kGemmSlotS = kGemmBN * 32;                       // [row][16 f16 scales]
+constexpr int kGemmLdsB = kGemmASlots * kGemmSlotA;            // 49,152
+constexpr int kGemmLdsS = kGemmLdsB + 2 * kGemmSlotB;
+constexpr int kGemmLdsRows = kGemmLdsS + 2 * kGemmSlotS;
+constexpr int kGemmLds = kGemmLdsRows + kGemmBM * 8;           // + the tile rows' image addresses
 
 struct GemmArgs {
     LayerView L;

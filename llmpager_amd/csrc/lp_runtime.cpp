@@ -484,6 +484,13 @@ static int gemm_max_tiles(const lp_moe_layer_desc* d, int T) {
     return pairs / kGemmBM + std::min(d->experts, pairs) + 1;
 }
 
+// Workgroups of a GEMM launch: a multiple of kXcds covering every possible
+// (tile, row block) item; the kernel maps them XCD by XCD onto the live ones.
+static unsigned gemm_grid(const GemmArgs& gm) {
+    const long items = (long)gm.max_tiles * gm.nblocks;
+    return (unsigned)((items + kXcds - 1) / kXcds * kXcds);
+}
+
 int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out) {
     if (!d || !out || T <= 0) return fail(LP_E_INVALID, "ws layout: bad arguments");
     const uint64_t E = (uint64_t)d->experts, k = (uint64_t)d->top_k, H = (uint64_t)d->hidden,
@@ -516,6 +523,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     const bool gemm = use_gemm(d, T);
     out->tiles = take(gemm ? (uint64_t)gemm_max_tiles(d, T) * 4 : 0);
     out->actimg = take(gemm ? t * k * (uint64_t)image_bytes((int)I) : 0);
+    out->xlo = take(t * 4);
     out->total = o;
     return LP_OK;
 }
@@ -604,6 +612,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->sh_y = ws + lay.sh_y;
     W->tiles = ws + lay.tiles;
     W->actimg = ws + lay.actimg;
+    W->xlo = ws + lay.xlo;
 }
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
@@ -699,6 +708,11 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     ga.pairs_cap = cap;
     if (use_gemm(d, T)) {
         if ((size_t)kGemmLds > c->max_lds) return fail(LP_E_UNSUPPORTED, "GEMM stages exceed the LDS");
+        // the GEMM loads address images and weights as 32-bit offsets from a base
+        const uint64_t img_span = std::max((uint64_t)T * image_bytes(d->hidden),
+                                           (uint64_t)T * d->top_k * image_bytes(d->inter));
+        if (img_span >= (1ull << 32) || d->slot_span >= (1ull << 32))
+            return fail(LP_E_UNSUPPORTED, "prefill GEMM: activation images or expert slots of 4 GiB or more");
         GemmArgs gm{};
         gm.L = ga.L;
         gm.W = ga.W;
@@ -708,15 +722,15 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         if (int r = launch(c, kGemmTiles, dim3(1), dim3(256), 0, s, gm)) return r;
         gm.a_img = ga.W.xf;
         gm.out = ga.W.act;
-        gm.nblocks = (d->inter + kGemmRows / 2 - 1) / (kGemmRows / 2);
-        if (int r = launch(c, kGemmGateup, dim3((unsigned)(gm.max_tiles * gm.nblocks)), dim3(256), kGemmLds, s, gm))
+        gm.nblocks = (d->inter + kGemmBN / 2 - 1) / (kGemmBN / 2);
+        if (int r = launch(c, kGemmGateup, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
             return r;
         if (int r = launch(c, kGemmActImg, dim3((unsigned)((T * d->top_k + 7) / 8)), dim3(256), 0, s, gm))
             return r;
         gm.a_img = ga.W.actimg;
         gm.out = ga.W.y;
-        gm.nblocks = (d->hidden + kGemmRows - 1) / kGemmRows;
-        if (int r = launch(c, kGemmDown, dim3((unsigned)(gm.max_tiles * gm.nblocks)), dim3(256), kGemmLds, s, gm))
+        gm.nblocks = (d->hidden + kGemmBN - 1) / kGemmBN;
+        if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
             return r;
     } else if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), s)) {
         return r;
