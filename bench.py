@@ -45,7 +45,8 @@ CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-co
 # the rocprofv3 --pmc runs recorded in profiles/lp_moe_gateup_config2_b32.md.
 # Re-measure whenever the kernel changes.
 GATEUP_TRAFFIC_B32 = 180_659_514
-KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_ximage",
+KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_disp_count", "lp_moe_disp_scan",
+           "lp_moe_disp_scatter", "lp_moe_ximage",
            "lp_moe_gateup", "lp_moe_down",
            "lp_moe_down_wide", "lp_moe_combine")
 
@@ -180,7 +181,8 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
 
 
 PREFILL_T = 2048
-PREFILL_KERNELS = ("lp_moe_router", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_ximage", "lp_gemm_tiles",
+DISPATCH_KERNELS = ("lp_moe_topk", "lp_moe_disp_count", "lp_moe_disp_scan", "lp_moe_disp_scatter")
+PREFILL_KERNELS = ("lp_moe_router", "lp_gemm_router", *DISPATCH_KERNELS, "lp_moe_ximage", "lp_gemm_tiles",
                    "lp_gemm_gateup", "lp_gemm_actimg", "lp_gemm_down", "lp_moe_combine")
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
@@ -258,7 +260,7 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
     avg = {k: v[0] / max(v[1], 1) for k, v in prof.items() if v[1]}   # ms per launch
     load = np.diff(gs)
     pairs = int(gs[-1])
-    router_ms = avg.get("lp_moe_router", 0.0)
+    router_ms = avg.get("lp_gemm_router", 0.0) + avg.get("lp_moe_router", 0.0)  # one of them runs
     step_ms = ms + router_ms
     gu_flop = 2.0 * pairs * (2 * I) * H
     dn_flop = 2.0 * pairs * H * I
@@ -277,7 +279,7 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
                   gateup_tflops=tf(gu_flop, gu_ms), down_tflops=tf(dn_flop, dn_ms),
                   tflops=gemm_tf, mfma_util=gemm_tf / MFMA_PEAK_TFLOPS),
         layer_tflops=tf(gu_flop + dn_flop + rt_flop, step_ms),
-        dispatch_us=(avg.get("lp_moe_topk", 0) + avg.get("lp_moe_dispatch", 0)) * 1e3,
+        dispatch_us=sum(avg.get(kn, 0.0) for kn in DISPATCH_KERNELS) * 1e3,
         combine_us=avg.get("lp_moe_combine", 0) * 1e3,
         kernels_avg_us={k: v * 1e3 for k, v in avg.items()},
     )

@@ -171,15 +171,18 @@ typedef struct lp_moe_ws_layout {
     uint64_t tiles;   /* prefill GEMM tile list (size 0 on the decode path) */
     uint64_t actimg;  /* prefill GEMM: images of the act rows (size 0 on the decode path) */
     uint64_t xlo;     /* i32 [T]: 1 when a token's image in xf has a non-zero lo part */
+    uint64_t disp;    /* dispatch scratch of batches above 64 tokens */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;
 
 int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out);
 
 /* Routing for T tokens without the host round trip of decode.rs:305-331:
- * router GEMV (canonical fp32 FMA order), softmax or sigmoid top-k with
- * glibc-exact expf (bit-exact with the reference's host routing given the
- * same logits), and the stable token->expert dispatch.  x: f32 [T, H]. */
+ * router logits (T <= 64: GEMV in the canonical fp32 FMA order; larger T: an
+ * MFMA GEMM over exact products, equal to fp32 rounding), softmax or sigmoid
+ * top-k with glibc-exact expf (bit-exact with the reference's host routing
+ * given the same logits), and the stable token->expert dispatch.
+ * x: f32 [T, H], 16-byte aligned. */
 int lp_moe_route(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t workspace,
                  lp_stream s);
 /* Routing from caller-supplied logits (f32 [T, E], copied into the
@@ -188,7 +191,7 @@ int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits
                         uint64_t workspace, lp_stream s);
 /* Expert half of the layer after lp_moe_route*: fragment images of x,
  * grouped gate/up + SiLU, grouped down, and h[t] += sum_j w[t][j] * y[t][j]
- * in pick order. */
+ * in pick order.  x and h 16-byte aligned. */
 int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
 /* Paged flow (decode.rs:305-331 order: route, then request the picks, then

@@ -426,6 +426,86 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
 }  // namespace
 
+// Router logits of a large batch as an MFMA GEMM: logits[t][e] = sum_h
+// W[e][h] x[t][h] with W bf16 and x split into three bf16 parts (hi = bf16(x),
+// mid = bf16(x - hi), lo = bf16(x - hi - mid): exactly x for normal values),
+// so every product is exact and the sums are fp32 in the matrix core (the
+// GEMV router's lane order is not kept: its results agree to fp32 rounding).
+// The mid and lo MFMAs run only when some lane's x has such a part (never for
+// bf16-valued activations).  Grid (ceil(T / 16), ceil(E / 128)), 256 threads:
+// wave w takes 16 tokens x experts 128 y + 32 w .. + 31; no LDS, no barriers.
+extern "C" __global__ void __launch_bounds__(256) lp_gemm_router(const RouteArgs a) {
+    const int H = a.L.hidden, E = a.L.experts, T = a.T;
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int m = lane & 15, kb = lane >> 4;
+    const int e0 = blockIdx.y * 128 + wave * 32;
+    if (e0 >= E) return;
+    const int t = min((int)blockIdx.x * 16 + m, T - 1);  // rows past the batch repeat its last token
+    const float* xr = dptr<const float>(a.x) + (size_t)t * H + 8 * kb;
+    const uint16_t* w0 = dptr<const uint16_t>(a.L.router_w) + (size_t)min(e0 + m, E - 1) * H + 8 * kb;
+    const uint16_t* w1 = dptr<const uint16_t>(a.L.router_w) + (size_t)min(e0 + 16 + m, E - 1) * H + 8 * kb;
+    f32x4_t c0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0;
+    auto pack = [](const uint32_t (&q)[8]) {
+        return __builtin_bit_cast(bf16x8_t, u32x4_t{q[0] | (q[1] << 16), q[2] | (q[3] << 16),
+                                                    q[4] | (q[5] << 16), q[6] | (q[7] << 16)});
+    };
+    auto step = [&](const float4& xa, const float4& xb, const uint4& wa_, const uint4& wb_) {
+        const bf16x8_t wa = __builtin_bit_cast(bf16x8_t, wa_), wb = __builtin_bit_cast(bf16x8_t, wb_);
+        const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        uint32_t hi[8], r_any = 0;
+        float r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            hi[i] = f32_to_bf16_rne(v[i]);
+            r[i] = v[i] - bf16_to_f32(hi[i]);
+            r_any |= __float_as_uint(r[i]) << 1;  // ignore the sign of zero
+        }
+        const bf16x8_t ah = pack(hi);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wa, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wb, c1, 0, 0, 0);
+        if (__ballot(r_any != 0u)) {
+            uint32_t mid[8], lo[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                mid[i] = f32_to_bf16_rne(r[i]);
+                lo[i] = f32_to_bf16_rne(r[i] - bf16_to_f32(mid[i]));
+            }
+            const bf16x8_t am = pack(mid), al = pack(lo);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, wa, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, wb, c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wa, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wb, c1, 0, 0, 0);
+        }
+    };
+    // four k-steps' loads in flight before their MFMAs (H is a multiple of 32)
+    int h = 0;
+    for (; h + 128 <= H; h += 128) {
+        float4 xa[4], xb[4];
+        uint4 wa[4], wb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xa[q] = *reinterpret_cast<const float4*>(xr + h + 32 * q);
+            xb[q] = *reinterpret_cast<const float4*>(xr + h + 32 * q + 4);
+            wa[q] = *reinterpret_cast<const uint4*>(w0 + h + 32 * q);
+            wb[q] = *reinterpret_cast<const uint4*>(w1 + h + 32 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) step(xa[q], xb[q], wa[q], wb[q]);
+    }
+    for (; h < H; h += 32)
+        step(*reinterpret_cast<const float4*>(xr + h), *reinterpret_cast<const float4*>(xr + h + 4),
+             *reinterpret_cast<const uint4*>(w0 + h), *reinterpret_cast<const uint4*>(w1 + h));
+    // lane holds C rows 4 kb + i (tokens) of column m (experts e0 + m, e0 + 16 + m)
+    float* logits = dptr<float>(a.W.logits);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tt = (int)blockIdx.x * 16 + 4 * kb + i;
+        if (tt >= T) continue;
+        if (e0 + m < E) logits[(size_t)tt * E + e0 + m] = c0[i];
+        if (e0 + 16 + m < E) logits[(size_t)tt * E + e0 + 16 + m] = c1[i];
+    }
+}
+
 // The tile list: for each routed expert u < meta[0], ceil(ntok / kGemmBM)
 // token blocks, as (u << 16) | block; meta[2] = the count.  One workgroup.
 extern "C" __global__ void __launch_bounds__(256) lp_gemm_tiles(const GemmArgs a) {

@@ -109,10 +109,19 @@ __device__ __forceinline__ void router_rows(const RouteArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) { router_rows(a); }
 
-// Fragment images of x alone, for callers that route from their own logits.
-// Grid (T), 256 threads.
+// Fragment images of x alone (callers that route from their own logits, and
+// the large-batch router): one wave per token, lane l converting sub-groups
+// l, l + 64, ...; W.xlo[t] from a wave vote.  Grid (ceil(T / 4)), 256 threads.
 extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs a) {
-    write_image(a, blockIdx.x);
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) return;
+    const int H = a.L.hidden, lane = lane_id();
+    const float* row = dptr<const float>(a.x) + (size_t)t * H;
+    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
+    bool lo = false;
+    for (int g = lane; g < frag_ngp(H); g += 64) lo |= write_image_group(row, H, g, img);
+    lo = __any(lo);
+    if (lane == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -452,10 +461,154 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
-    __shared__ __align__(16) uint8_t sm[kDispatchSmem];
-    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
-                 dptr<const int>(a.L.slot_table));
+// ---------------------------------------------------------------------------
+// Dispatch of a large batch in three launches, with the single-workgroup
+// dispatch_all's result: picks grouped by expert (ascending id), in token
+// order within an expert (the order decode.rs:469-531 visits them).
+//   count:   per block of kDispTok tokens, each expert's picks;
+//   scan:    group starts, each block's first position per expert, the
+//            unique list, the expert table and the expert -> entry map;
+//   scatter: per block, each pick's rank among its expert's picks of the
+//            block (earlier waves' counts plus the set bits below the lane in
+//            the wave's 64-bit mask of that expert), added to the block's
+//            first position.
+// W.disp holds [nb][E] counts, then [nb][E] first positions, then [E] entry
+// indices (nb = ceil(T / kDispTok)).
+// ---------------------------------------------------------------------------
+
+// Grid ceil(T / kDispTok), kDispTok threads.
+extern "C" __global__ void __launch_bounds__(kDispTok) lp_moe_disp_count(const RouteArgs a) {
+    __shared__ int h[kMaxExperts];
+    const int E = a.L.experts, k = a.L.top_k, T = a.T;
+    const int tid = threadIdx.x, b = blockIdx.x;
+    for (int e = tid; e < E; e += kDispTok) h[e] = 0;
+    __syncthreads();
+    const int t = b * kDispTok + tid;
+    if (t < T) {
+        const int c = dptr<const int>(a.W.cnt)[t];
+        const int* ids = dptr<const int>(a.W.ids) + (size_t)t * k;
+        for (int j = 0; j < c; ++j) atomicAdd(&h[ids[j]], 1);
+    }
+    __syncthreads();
+    int* cnt = dptr<int>(a.W.disp) + (size_t)b * E;
+    for (int e = tid; e < E; e += kDispTok) cnt[e] = h[e];
+}
+
+// One workgroup of 1024 threads: thread e takes expert e.
+extern "C" __global__ void __launch_bounds__(1024) lp_moe_disp_scan(const RouteArgs a) {
+    __shared__ int scan_sh[16];
+    const int E = a.L.experts, k = a.L.top_k, T = a.T;
+    const int nb = (T + kDispTok - 1) / kDispTok;
+    const int tid = threadIdx.x;
+    const int* cnt = dptr<const int>(a.W.disp);
+    int* first = dptr<int>(a.W.disp) + (size_t)nb * E;
+    int* uidx = first + (size_t)nb * E;
+    int tot = 0;
+    if (tid < E)
+        for (int b = 0; b < nb; ++b) tot += cnt[(size_t)b * E + tid];
+    int total, nu;
+    const int g0 = block_excl_scan(tot, scan_sh, &total);
+    const int u = block_excl_scan(tot > 0 ? 1 : 0, scan_sh, &nu);
+    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    if (tid < E) {
+        dptr<int>(a.W.gs)[tid] = g0;
+        int o = g0;
+        for (int b = 0; b < nb; ++b) {
+            first[(size_t)b * E + tid] = o;
+            o += cnt[(size_t)b * E + tid];
+        }
+        uidx[tid] = tot > 0 ? u : -1;
+        if (tot > 0) {
+            dptr<int>(a.W.uniq)[u] = tid;
+            const int slot = dptr<const int>(a.L.slot_table)[tid];
+            ExpertEntry x;
+            x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
+            x.p0 = g0;
+            x.ntok = tot;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = -1;  // the scatter fills the first ones
+            et[u] = x;
+        }
+    }
+    if (tid == 0) {
+        dptr<int>(a.W.gs)[E] = total;
+        dptr<int>(a.W.meta)[0] = nu;
+        dptr<int>(a.W.meta)[1] = 0;
+    }
+    // entries past the unique ones are cleared, as dispatch_all does
+    const int maxu = min(T * k, E);
+    for (int v = nu + tid; v < maxu; v += blockDim.x) {
+        ExpertEntry x;
+        x.blob = 0ull;
+        x.p0 = 0;
+        x.ntok = 0;
+#pragma unroll
+        for (int q = 0; q < kEntryToks; ++q) x.tok[q] = -1;
+        et[v] = x;
+    }
+    // the shared MLP (if any) takes every token: one entry, identity token list
+    if (a.L.shared_blob) {
+        for (int t = tid; t < T; t += blockDim.x) dptr<int>(a.W.sh_perm)[t] = t;
+        if (tid == 0) {
+            ExpertEntry x;
+            x.blob = a.L.shared_blob;
+            x.p0 = 0;
+            x.ntok = T;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
+            *dptr<ExpertEntry>(a.W.sh_et) = x;
+        }
+    }
+}
+
+// Grid ceil(T / kDispTok), kDispTok threads (wave w: tokens 64 w .. of the block).
+extern "C" __global__ void __launch_bounds__(kDispTok) lp_moe_disp_scatter(const RouteArgs a) {
+    constexpr int W = kDispTok / 64;
+    __shared__ uint32_t mlo[W][kMaxExperts], mhi[W][kMaxExperts];
+    __shared__ int woff[W][kMaxExperts];
+    const int E = a.L.experts, k = a.L.top_k, T = a.T;
+    const int nb = (T + kDispTok - 1) / kDispTok;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6, b = blockIdx.x;
+    for (int i = tid; i < W * E; i += kDispTok) {
+        mlo[i / E][i % E] = 0u;
+        mhi[i / E][i % E] = 0u;
+    }
+    __syncthreads();
+    const int t = b * kDispTok + tid;
+    const int c = t < T ? dptr<const int>(a.W.cnt)[t] : 0;
+    const int* ids = dptr<const int>(a.W.ids) + (size_t)t * k;
+    for (int j = 0; j < c; ++j) atomicOr(lane < 32 ? &mlo[wave][ids[j]] : &mhi[wave][ids[j]], 1u << (lane & 31));
+    __syncthreads();
+    const int* first = dptr<const int>(a.W.disp) + (size_t)nb * E + (size_t)b * E;
+    for (int e = tid; e < E; e += kDispTok) {
+        int o = first[e];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            woff[w][e] = o;
+            o += __popc(mlo[w][e]) + __popc(mhi[w][e]);
+        }
+    }
+    __syncthreads();
+    if (t >= T) return;
+    int* perm = dptr<int>(a.W.perm);
+    int* inv = dptr<int>(a.W.inv);
+    const int* gs = dptr<const int>(a.W.gs);
+    const int* uidx = first + (size_t)(nb - b) * E;  // [E] after the first positions
+    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int j = 0; j < k; ++j) {
+        if (j < c) {
+            const int e = ids[j];
+            const uint64_t mask = (uint64_t)mlo[wave][e] | ((uint64_t)mhi[wave][e] << 32);
+            const int pos = woff[wave][e] + __popcll(mask & below);
+            perm[pos] = t * k + j;
+            inv[t * k + j] = pos;
+            const int r = pos - gs[e];
+            if (r < kEntryToks) et[uidx[e]].tok[r] = t;
+        } else {
+            inv[t * k + j] = -1;
+        }
+    }
 }
 
 // Re-resolve the expert table's blob addresses through the layer's current
@@ -783,21 +936,54 @@ lp_moe_down_wide(const GroupedArgs a) {
 // ---------------------------------------------------------------------------
 // Combine: h[t][i] += sum_j w[t][j] * y[inv[t*k+j]][i], j in pick order with
 // fused multiply-adds, then one add (q4g64.cu:84-99); with a shared MLP its
-// output is added after that, unweighted (kimi.rs:779).  Grid (ceil(H/256), T).
+// output is added after that, unweighted (kimi.rs:779).  Grid (ceil(H/1024),
+// T): four columns per thread, eight picks' rows loaded before their FMAs;
+// picks past cnt load pick 0's row with weight 0, which leaves the sum as it
+// is.
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedArgs a) {
     const int t = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     const int H = a.L.hidden, k = a.L.top_k;
     if (i >= H) return;
     const int c = dptr<const int>(a.W.cnt)[t];
     const int* inv = dptr<const int>(a.W.inv) + (size_t)t * k;
     const float* w = dptr<const float>(a.W.wts) + (size_t)t * k;
-    const float* y = dptr<const float>(a.W.y);
-    float acc = 0.0f;
-    for (int j = 0; j < c; ++j) acc = __builtin_fmaf(w[j], y[(size_t)inv[j] * H + i], acc);
-    float* h = dptr<float>(a.h) + (size_t)t * H;
-    float v = h[i] + acc;
-    if (a.L.shared_blob) v = v + dptr<const float>(a.W.sh_y)[(size_t)t * H + i];
-    h[i] = v;
+    const float* y = dptr<const float>(a.W.y) + i;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c > 0) {
+        const int row0 = inv[0];
+        for (int j0 = 0; j0 < c; j0 += 8) {
+            float4 yv[8];
+            float wv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int j = j0 + q;
+                const bool live = j < c;
+                wv[q] = live ? w[j] : 0.0f;
+                yv[q] = *reinterpret_cast<const float4*>(y + (size_t)(live ? inv[j] : row0) * H);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                acc.x = __builtin_fmaf(wv[q], yv[q].x, acc.x);
+                acc.y = __builtin_fmaf(wv[q], yv[q].y, acc.y);
+                acc.z = __builtin_fmaf(wv[q], yv[q].z, acc.z);
+                acc.w = __builtin_fmaf(wv[q], yv[q].w, acc.w);
+            }
+        }
+    }
+    float4* h = reinterpret_cast<float4*>(dptr<float>(a.h) + (size_t)t * H + i);
+    float4 v = *h;
+    v.x = v.x + acc.x;
+    v.y = v.y + acc.y;
+    v.z = v.z + acc.z;
+    v.w = v.w + acc.w;
+    if (a.L.shared_blob) {
+        const float4 sy = *reinterpret_cast<const float4*>(dptr<const float>(a.W.sh_y) + (size_t)t * H + i);
+        v.x = v.x + sy.x;
+        v.y = v.y + sy.y;
+        v.z = v.z + sy.z;
+        v.w = v.w + sy.w;
+    }
+    *h = v;
 }

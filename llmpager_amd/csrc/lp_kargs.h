@@ -21,6 +21,7 @@ constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkDispatchMaxT = 64;  // largest T routed by the one-workgroup top-k + dispatch
+constexpr int kDispTok = 256;          // tokens per block of the multi-block dispatch
 constexpr int kMaxPairs = 2;           // token pairs the grouped kernels stage at once
 constexpr int kMaxChunk = 16;          // most MFMA steps (4 sub-groups each) one register chunk holds
 constexpr int kGateupChunk = 16;       // gate/up tiles up to this many steps load in one piece
@@ -141,6 +142,7 @@ struct Workspace {
     uint64_t tiles;      // prefill GEMM: i32 tile list
     uint64_t actimg;     // prefill GEMM: [T*k] images of act rows (image_bytes(I) each)
     uint64_t xlo;        // i32 [T]: 1 when token t's image in xf has a non-zero lo part
+    uint64_t disp;       // multi-block dispatch: i32 [nb][E] counts, [nb][E] first positions, [E] entries
 };
 
 struct RouteArgs {

@@ -57,7 +57,6 @@ enum Fn {
     kAdd,
     kRouter,
     kTopk,
-    kDispatch,
     kGateup,
     kDown,
     kDownWide,
@@ -70,6 +69,10 @@ enum Fn {
     kGemmGateup,
     kGemmActImg,
     kGemmDown,
+    kDispCount,
+    kDispScan,
+    kDispScatter,
+    kGemmRouter,
     kNumFns
 };
 
@@ -83,13 +86,15 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_basic.hsaco", "lp_moe_reduce"},   {"lp_basic.hsaco", "lp_silu_mul"},
     {"lp_basic.hsaco", "lp_bf16_gemv"},    {"lp_basic.hsaco", "lp_add"},
     {"lp_moe.hsaco", "lp_moe_router"},     {"lp_moe.hsaco", "lp_moe_topk"},
-    {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_gateup"},
+    {"lp_moe.hsaco", "lp_moe_gateup"},
     {"lp_moe.hsaco", "lp_moe_down"},       {"lp_moe.hsaco", "lp_moe_down_wide"},
     {"lp_moe.hsaco", "lp_moe_combine"},    {"lp_moe.hsaco", "lp_moe_ximage"},
     {"lp_moe.hsaco", "lp_moe_topk_dispatch"}, {"lp_basic.hsaco", "lp_expf_wave"},
     {"lp_moe.hsaco", "lp_moe_resolve"},
     {"lp_gemm.hsaco", "lp_gemm_tiles"},    {"lp_gemm.hsaco", "lp_gemm_gateup"},
     {"lp_gemm.hsaco", "lp_gemm_actimg"},   {"lp_gemm.hsaco", "lp_gemm_down"},
+    {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
+    {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
@@ -524,6 +529,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->tiles = take(gemm ? (uint64_t)gemm_max_tiles(d, T) * 4 : 0);
     out->actimg = take(gemm ? t * k * (uint64_t)image_bytes((int)I) : 0);
     out->xlo = take(t * 4);
+    out->disp = take(T > kTopkDispatchMaxT ? (2 * ((t + kDispTok - 1) / kDispTok) + 1) * E * 4 : 0);
     out->total = o;
     return LP_OK;
 }
@@ -613,13 +619,17 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->tiles = ws + lay.tiles;
     W->actimg = ws + lay.actimg;
     W->xlo = ws + lay.xlo;
+    W->disp = ws + lay.disp;
 }
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
     if (T <= kTopkDispatchMaxT) return launch(c, kTopkDispatch, dim3(1), dim3(1024), 0, s, ra);
     if (int r = launch(c, kTopk, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
-    return launch(c, kDispatch, dim3(1), dim3(256), 0, s, ra);
+    const unsigned nb = (unsigned)((T + kDispTok - 1) / kDispTok);
+    if (int r = launch(c, kDispCount, dim3(nb), dim3(kDispTok), 0, s, ra)) return r;
+    if (int r = launch(c, kDispScan, dim3(1), dim3(1024), 0, s, ra)) return r;
+    return launch(c, kDispScatter, dim3(nb), dim3(kDispTok), 0, s, ra);
 }
 
 int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws,
@@ -631,6 +641,13 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
     ra.x = x;
     ra.T = T;
     ra.make_xf = 1;
+    if (T > kTopkDispatchMaxT) {
+        // large batch: the MFMA router, then the images of x on their own
+        dim3 g((unsigned)((T + 15) / 16), (unsigned)((d->experts + 127) / 128));
+        if (int r = launch(c, kGemmRouter, g, dim3(256), 0, s, ra)) return r;
+        if (int r = launch(c, kXImage, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
+        return route_tail(c, ra, s);
+    }
     dim3 g((unsigned)((d->experts + 3) / 4), (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
     if (int r = launch(c, kRouter, g, dim3(256), 0, s, ra)) return r;
     return route_tail(c, ra, s);
@@ -681,13 +698,14 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
                         uint64_t ws, lp_stream s, bool have_images) {
     if (int r = check_desc(c, d, T)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
+    if (h % 16) return fail(LP_E_UNSUPPORTED, "h must be 16-byte aligned");
     if (!have_images) {
         RouteArgs ra{};
         fill_views(d, ws, T, &ra.L, &ra.W);
         ra.x = x;
         ra.T = T;
         ra.make_xf = 1;
-        if (int r = launch(c, kXImage, dim3((unsigned)T), dim3(256), 0, s, ra)) return r;
+        if (int r = launch(c, kXImage, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
     }
     GroupedArgs ga{};
     fill_views(d, ws, T, &ga.L, &ga.W);
@@ -751,7 +769,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gs.W.y = ga.W.sh_y;
         if (int r = grouped_ffn(c, gs, 1, s)) return r;
     }
-    return launch(c, kCombine, dim3((unsigned)((d->hidden + 255) / 256), (unsigned)T), dim3(256), 0,
+    return launch(c, kCombine, dim3((unsigned)((d->hidden + 1023) / 1024), (unsigned)T), dim3(256), 0,
                   s, ga);
 }
 
