@@ -45,7 +45,7 @@ CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-co
 # the rocprofv3 --pmc runs recorded in profiles/lp_moe_gateup_config2_b32.md.
 # Re-measure whenever the kernel changes.
 GATEUP_TRAFFIC_B32 = 180_659_514
-KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_disp_count", "lp_moe_disp_scan",
+KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count", "lp_moe_disp_scan",
            "lp_moe_disp_scatter", "lp_moe_ximage",
            "lp_moe_gateup", "lp_moe_down",
            "lp_moe_down_wide", "lp_moe_combine")

@@ -249,14 +249,37 @@ __device__ __forceinline__ bool write_image_group(const float* row, int cols, in
     return any != 0;
 }
 
+// Direct-to-LDS copy from inline assembly: lane l's 16 bytes at base + off
+// land at LDS address lds + 16 l (base and lds uniform over the wave: an SGPR
+// pair and M0).  Given the intrinsic instead, the compiler waits for every
+// outstanding load before the first copy, which here would serialise the
+// image copies behind a tile's weight loads; the callers wait explicitly.
+__device__ __forceinline__ void lds_copy16(uint64_t base, uint32_t off, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// As lds_copy16 for 4 bytes per lane from per-lane 64-bit addresses.
+__device__ __forceinline__ void lds_copy4(uint64_t addr, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    return (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v) |
+           ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32);
+}
+
+__device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p);
+}
+
 // Copy the fragment images of nt tokens (img_of(t): device address of token
 // t's image) into fragment pairs 0 .. ceil(nt/2)-1.  Part blocks go straight
-// from memory into LDS (global_load_lds_dwordx4: 64 lanes fill 1 KB of LDS
-// per instruction, no registers, no LDS store), one instruction per wave in
-// turn; the seeds go through registers.  Ends with every load of the calling
-// thread complete; the caller's barrier then publishes the copy.  The second
-// token of an odd last pair is left as it is: its MFMA output rows are
-// separate and never stored.
+// from memory into LDS (64 lanes fill 1 KB per instruction, no registers, no
+// LDS store), one instruction per wave in turn; the seeds go through
+// registers.  Ends with every load of the calling thread complete; the
+// caller's barrier then publishes the copy.  The second token of an odd last
+// pair is left as it is: its MFMA output rows are separate and never stored.
 template <typename ImgOf>
 __device__ inline void load_images(const Frags& F, int nt, ImgOf img_of) {
     const int lane = lane_id(), wave = threadIdx.x >> 6, W = blockDim.x >> 6;
@@ -266,11 +289,9 @@ __device__ inline void load_images(const Frags& F, int nt, ImgOf img_of) {
         const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + part
         const int t = blk >> 1, part = blk & 1;
         const int q = r * 64 + lane;
-        const uint64_t src = img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)q * 16;
-        uint8_t* dst = frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024;
-        if (q < q4)
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const LP_GLOBAL void*>(src),
-                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)r * 1024);
+        const uint32_t dst = lds_addr_of(frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024);
+        if (q < q4) lds_copy16(base, (uint32_t)lane * 16u, dst);
     }
     for (int f = threadIdx.x; f < nt * F.ngp; f += blockDim.x) {
         const int t = f / F.ngp, g = f - t * F.ngp;
@@ -278,6 +299,36 @@ __device__ inline void load_images(const Frags& F, int nt, ImgOf img_of) {
         *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(off_ptr(F, t >> 1, g)) + (t & 1) * 8) = sd;
     }
     __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct loads have landed
+}
+
+// load_images without registers and without the final wait: the seeds, too,
+// are gathered straight into LDS (one 4-byte copy per lane: dword d of pair
+// p's seed block is seed (d & 1) of token 2p + ((d >> 1) & 1) at sub-group
+// d >> 2; a missing second token repeats the first).  The caller waits for
+// every load of the thread (vmcnt 0) before its barrier, so these may be
+// issued ahead of other loads that the same wait then covers.
+template <typename ImgOf>
+__device__ inline void issue_images(const Frags& F, int nt, ImgOf img_of) {
+    const int lane = lane_id(), wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const int q4 = 4 * F.ngp;          // 16-byte units per part block
+    const int ipb = (q4 + 63) >> 6;    // copies per part block
+    for (int i = wave; i < 2 * nt * ipb; i += W) {
+        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + part
+        const int t = blk >> 1, part = blk & 1;
+        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)r * 1024);
+        const uint32_t dst = lds_addr_of(frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024);
+        if (r * 64 + lane < q4) lds_copy16(base, (uint32_t)lane * 16u, dst);
+    }
+    const int npair = (nt + 1) >> 1;
+    const int spp = (F.ngp * 4 + 63) >> 6;  // seed copies per pair
+    for (int i = wave; i < npair * spp; i += W) {
+        const int p = i / spp, r = i - p * spp;
+        const int d = r * 64 + lane;
+        const int g = d >> 2;
+        const int t = min(2 * p + ((d >> 1) & 1), nt - 1);
+        const uint32_t dst = lds_addr_of(reinterpret_cast<const uint8_t*>(off_ptr(F, p, 0)) + r * 256);
+        if (g < F.ngp) lds_copy4(img_of(t) + (uint64_t)F.ngp * 128 + (uint64_t)g * 8 + (uint64_t)(d & 1) * 4, dst);
+    }
 }
 
 __device__ __forceinline__ int tile_steps(int cols) { return ((cols >> 5) + 3) >> 2; }
@@ -291,6 +342,7 @@ __device__ __forceinline__ int tile_steps(int cols) { return ((cols >> 5) + 3) >
 template <int RS>
 struct WTile {
     __amdgpu_buffer_rsrc_t rsrc;
+    uint64_t base;  // the region's address (the rsrc's base)
     uint32_t dofs;  // lane's nibble byte offset at step 0
     uint32_t sofs;  // lane's scale byte offset at step 0
     bool lastok;    // the lane's sub-group exists at the tile's last step
@@ -306,6 +358,7 @@ __device__ __forceinline__ WTile<RS> wtile(uint64_t region, int rows, int cols, 
     WTile<RS> T;
     T.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(region), (short)0,
                                                (int)(sbytes + (uint32_t)rows * ng * 16), kBufferWord3);
+    T.base = region;
     T.dofs = sbytes + (row * ng + kb) * 16;
     T.sofs = (row * gpr + (kb >> RS)) * 2;
     T.lastok = (ng & 3) == 0 || kb < (int)(ng & 3);
@@ -315,30 +368,61 @@ __device__ __forceinline__ WTile<RS> wtile(uint64_t region, int rows, int cols, 
 // Raw weight registers for steps [c0, c0 + NS) of one tile.  Rows past the
 // matrix read zero nibbles (past the buffer) and garbage scales; their
 // outputs are never stored, so they need no mask.
-template <int NS>
+//
+// Scales: per lane one 16-bit load per step (SL false), or (SL true: group
+// 32, one chunk from step 0, rows' scales 16-byte aligned) the tile's scale
+// lines copied straight into a per-wave LDS window, 2 NS bytes per lane:
+// lane (n, kb') copies bytes [2 NS kb', 2 NS (kb' + 1)) of row n's scales,
+// 16 at a time, the i-th 16 landing at window + 1024 i + 16 lane.  Scale q
+// (= 4 c + kb at step c) of row n then sits at window + 1024 ((q % NS) / 8) +
+// 16 (n + 16 (q / NS)) + 2 (q % 8): a per-lane base plus a constant per step.
+// The per-lane loads touch 16 cache lines per instruction for 128 useful
+// bytes; the window copy reads each line once.
+template <int NS, bool SL = false>
 struct WRegs {
     uint4 w[NS];
-    uint32_t s[NS];  // f16 bits of the lane's sub-group scale
+    // f16 bits of the lane's sub-group scale (SL false), kept 16-bit: a
+    // widening right after the load would make the wave wait for it there
+    uint16_t s[SL ? 1 : NS];
+    uint32_t sbase;  // SL: LDS address of the lane's scale at step 0
     bool lastok;     // the lane's sub-group exists at the tile's last step
 };
+
+// LDS byte offset of step j's scale from WRegs::sbase (SL).
+template <int NS>
+__device__ __forceinline__ constexpr uint32_t scale_step_off(int j) {
+    return 1024u * (uint32_t)(((4 * j) % NS) / 8) + 256u * (uint32_t)((4 * j) / NS) + 8u * (uint32_t)(j & 1);
+}
 
 // Issue the tile's loads for steps c0 .. c0 + NS - 1: one per-lane offset
 // plus an immediate per step (64 B of nibbles, 8 >> RS B of scales).  The
 // loads are unconditional, so the compiler keeps them together ahead of
 // their use.  Steps past the lane's last sub-group read whatever follows in
-// the region (or zeros past its end); wmma gives them a zero scale.
-template <int NS, int RS>
-__device__ __forceinline__ void wload(WRegs<NS>& R, const WTile<RS>& T, int c0) {
+// the region (or zeros past its end); wmma gives them a zero scale.  SL:
+// c0 is 0 and swin is the wave's LDS window for this tile (64 * 2 NS bytes);
+// the copies are waited for by the caller's wait for all loads.
+template <int NS, int RS, bool SL>
+__device__ __forceinline__ void wload(WRegs<NS, SL>& R, const WTile<RS>& T, int c0, uint32_t swin = 0) {
     R.lastok = T.lastok;
     uint32_t d = T.dofs + 64u * (uint32_t)c0;
     uint32_t sc = T.sofs + (8u >> RS) * (uint32_t)c0;
     // opaque per-chunk bases: every step is then base + immediate, and the
     // compiler cannot hoist NS separate step addresses out of a chunk loop
     asm volatile("" : "+v"(d), "+v"(sc));
+    if constexpr (SL) {
+        static_assert(RS == 0 && NS % 8 == 0, "LDS scales: group 32, 16-byte copies");
+        const int lane = lane_id(), kb = lane >> 4;
+        const uint32_t row0 = T.sofs - 2u * (uint32_t)kb;  // the row's first scale
+        const uint64_t base = uniform_u64(T.base);
+#pragma unroll
+        for (int i = 0; i < NS / 8; ++i)
+            lds_copy16(base, row0 + 2u * NS * (uint32_t)kb + 16u * (uint32_t)i, swin + 1024u * (uint32_t)i);
+        R.sbase = swin + 16u * (uint32_t)(lane & 15) + 2u * (uint32_t)kb;
+    }
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         R.w[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(T.rsrc, (int)(d + 64u * j), 0, 0));
-        R.s[j] = __builtin_amdgcn_raw_buffer_load_b16(T.rsrc, (int)(sc + (8u >> RS) * j), 0, 0);
+        if constexpr (!SL) R.s[j] = __builtin_amdgcn_raw_buffer_load_b16(T.rsrc, (int)(sc + (8u >> RS) * j), 0, 0);
     }
 }
 
@@ -347,12 +431,12 @@ __device__ __forceinline__ void wload(WRegs<NS>& R, const WTile<RS>& T, int c0) 
 // it the decoded bf16 weights, invariant across the groups, are hoisted out
 // of the group loop and take four registers per loaded one.  Emits no code;
 // the loads must already be complete (they are, after load_images).
-template <int NS>
-__device__ __forceinline__ void opaque(WRegs<NS>& R) {
+template <int NS, bool SL>
+__device__ __forceinline__ void opaque(WRegs<NS, SL>& R) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         asm volatile("" : "+v"(R.w[j].x), "+v"(R.w[j].y), "+v"(R.w[j].z), "+v"(R.w[j].w));
-        asm volatile("" : "+v"(R.s[j]));
+        if constexpr (!SL) asm volatile("" : "+v"(R.s[j]));
     }
 }
 
@@ -382,8 +466,8 @@ __device__ __forceinline__ ABase abase(const Frags& F, int p, int c0) {
 // and at step rem - 1 lanes without a sub-group (cols % 128 != 0) take a
 // zero scale.  One code path serves every np, so the loaded chunk keeps its
 // registers whatever the token count.
-template <int NS, int P, int M>
-__device__ __forceinline__ void wmma(const WRegs<NS> (&R)[M], const ABase (&B)[P], int rem, int np,
+template <int NS, bool SL, int P, int M>
+__device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&B)[P], int rem, int np,
                                      float (&acc)[M][P][2]) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -391,7 +475,11 @@ __device__ __forceinline__ void wmma(const WRegs<NS> (&R)[M], const ABase (&B)[P
             float s[M];
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                s[m] = f16_bits_to_f32(R[m].s[j]);
+                if constexpr (SL)
+                    s[m] = f16_bits_to_f32(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+                        (uintptr_t)(R[m].sbase + scale_step_off<NS>(j))));
+                else
+                    s[m] = f16_bits_to_f32(R[m].s[j]);
                 if (j == rem - 1 && !R[m].lastok) s[m] = 0.0f;
             }
 #pragma unroll

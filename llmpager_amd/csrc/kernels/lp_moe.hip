@@ -461,6 +461,13 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
 
 }  // namespace
 
+// Dispatch of a medium batch after the multi-workgroup top-k: dispatch_all
+// over the picks in memory, one workgroup of 256.
+extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
+    __shared__ __align__(16) uint8_t sm[kDispatchSmem];
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table));
+}
+
 // ---------------------------------------------------------------------------
 // Dispatch of a large batch in three launches, with the single-workgroup
 // dispatch_all's result: picks grouped by expert (ascending id), in token
@@ -628,17 +635,17 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_resolve(const RouteArgs
 }
 
 // ---------------------------------------------------------------------------
-// Top-k and dispatch in one workgroup of 1024 threads, for decode-sized
-// batches (the host uses it for T <= kTopkDispatchMaxT): wave w ranks tokens
-// w, w + 16, ..., then the whole workgroup builds the dispatch tables.  One
-// launch less than lp_moe_topk + lp_moe_dispatch, and no cross-workgroup
-// synchronisation.
+// Top-k and dispatch in one workgroup of 1024 threads, for the smallest
+// batches (the host uses it for T <= kTopkFusedMaxT, at most one token per
+// wave): wave w ranks token w, then the whole workgroup builds the dispatch
+// tables.  One launch less than lp_moe_topk + lp_moe_dispatch; past one token
+// per wave the top-k on a single CU costs more than the extra launch.
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const RouteArgs a) {
     constexpr int kTopkLds = 16 * kMaxExperts * 4;
     __shared__ __align__(16) uint8_t sm[kDispatchSmem > kTopkLds ? kDispatchSmem : kTopkLds];
-    __shared__ int ids_l[kTopkDispatchMaxT * kMaxTopK];
-    __shared__ int cnt_l[kTopkDispatchMaxT];
+    __shared__ int ids_l[kTopkFusedMaxT * kMaxTopK];
+    __shared__ int cnt_l[kTopkFusedMaxT];
     __shared__ int slots_l[kMaxExperts];
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     // the slot table comes in while the picks are made
@@ -682,6 +689,12 @@ __device__ __forceinline__ ExpertEntry entry_of(const GroupedArgs& a, int u) {
 
 // Token of the expert's i-th (token, pick) pair: from the entry for the first
 // kEntryToks (no dependent load), else through the dispatch permutation.
+// Token i < kEntryToks of the entry, from the entry alone.
+__device__ __forceinline__ int entry_tok(const ExpertEntry& x, int i) {
+    static_assert(kEntryToks == 4, "select chain below");
+    return i == 0 ? x.tok[0] : i == 1 ? x.tok[1] : i == 2 ? x.tok[2] : x.tok[3];
+}
+
 __device__ __forceinline__ int pair_token(const ExpertEntry& x, int i, const int* perm, int k) {
     static_assert(kEntryToks == 4, "select chain below");
     return i == 0 ? x.tok[0] : i == 1 ? x.tok[1] : i == 2 ? x.tok[2] : i == 3 ? x.tok[3] : perm[x.p0 + i] / k;
@@ -702,8 +715,8 @@ __device__ __forceinline__ void missing_expert(const GroupedArgs& a, const Exper
 // after the previous one's MFMAs and, when another token group follows
 // (`reload`), the first chunk again before the epilogue, so that latency
 // overlaps the stores and the next group's image copy.
-template <int P, int NS, bool ONE, int RS>
-__device__ __forceinline__ void gateup_group(const Frags& F, WRegs<NS> (&GU)[2], const WTile<RS>& TG,
+template <int P, int NS, bool ONE, int RS, bool SL>
+__device__ __forceinline__ void gateup_group(const Frags& F, WRegs<NS, SL> (&GU)[2], const WTile<RS>& TG,
                                              const WTile<RS>& TU, int I, int n0, int S, int t0,
                                              int nt, int p0, bool reload, float* act) {
     const int np = (nt + 1) >> 1;
@@ -751,7 +764,11 @@ __device__ __forceinline__ void gateup_group(const Frags& F, WRegs<NS> (&GU)[2],
     }
 }
 
-template <int NS, bool ONE, int RS>
+// Bytes of a wave's LDS scale window for one tile (WRegs SL).
+template <int NS>
+__host__ __device__ constexpr int scale_window_bytes() { return 64 * 2 * NS; }
+
+template <int NS, bool ONE, int RS, bool SL>
 __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -773,29 +790,40 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     const Frags F = frags_at(lds, H);
     const WTile<RS> TG = wtile<RS>(x.blob + L.gate_off, I, H, n0);
     const WTile<RS> TU = wtile<RS>(x.blob + L.up_off, I, H, n0);
-    WRegs<NS> GU[2];
-    wload(GU[0], TG, 0);
-    wload(GU[1], TU, 0);
-    zero_block(F, threadIdx.x, blockDim.x);
     const int* perm = dptr<const int>(a.W.perm);
     const uint64_t xf = a.W.xf;
     const uint64_t ib = (uint64_t)image_bytes(H);
     const int cap = min(kMaxPairs, a.pairs_cap);
+    // The first token group's images (tokens from the entry: no lookup) are
+    // copied first, the weights loaded after them; one wait then covers both
+    // and their latencies overlap.
+    zero_block(F, threadIdx.x, blockDim.x);
+    issue_images(F, min(2 * cap, x.ntok), [&](int t) { return xf + (uint64_t)entry_tok(x, t) * ib; });
+    // the wave's two scale windows follow the fragment area (SL)
+    const uint32_t swin = lds_addr_of(lds) + (uint32_t)frag_lds_bytes(H, a.pairs_cap) +
+                          (uint32_t)(2 * wave * scale_window_bytes<NS>());
+    WRegs<NS, SL> GU[2];
+    wload(GU[0], TG, 0, swin);
+    wload(GU[1], TU, 0, swin + scale_window_bytes<NS>());
     for (int tb = 0; tb < x.ntok; tb += 2 * cap) {
         const int nt = min(2 * cap, x.ntok - tb);
         const bool reload = tb + nt < x.ntok;
-        if (tb > 0) __syncthreads();
-        load_images(F, nt, [&](int t) { return xf + (uint64_t)pair_token(x, tb + t, perm, k) * ib; });
+        if (tb == 0) {
+            __builtin_amdgcn_s_waitcnt(0);  // the copies (and the weights) have landed
+        } else {
+            __syncthreads();
+            load_images(F, nt, [&](int t) { return xf + (uint64_t)pair_token(x, tb + t, perm, k) * ib; });
+        }
         __syncthreads();
-        gateup_group<kMaxPairs, NS, ONE>(F, GU, TG, TU, I, n0, S, tb, nt, x.p0, reload, act);
+        gateup_group<kMaxPairs, NS, ONE, RS, SL>(F, GU, TG, TU, I, n0, S, tb, nt, x.p0, reload, act);
     }
 }
 
 // down MFMAs for one staged token group of P pairs over TW row tiles, into
 // y; D holds the first chunk on entry, and ONE / reload mean what they do
 // for gateup_group.
-template <int P, int TW, int NS, bool ONE, int RS>
-__device__ __forceinline__ void down_group(const Frags& F, WRegs<NS> (&D)[TW],
+template <int P, int TW, int NS, bool ONE, int RS, bool SL>
+__device__ __forceinline__ void down_group(const Frags& F, WRegs<NS, SL> (&D)[TW],
                                            const WTile<RS> (&TD)[TW], int H, const int (&n0)[TW],
                                            int S, int t0, int nt, int p0, bool reload, float* y) {
     const int np = (nt + 1) >> 1;
@@ -841,7 +869,7 @@ __device__ __forceinline__ void down_group(const Frags& F, WRegs<NS> (&D)[TW],
     }
 }
 
-template <int TW, int NS, bool ONE, int RS>
+template <int TW, int NS, bool ONE, int RS, bool SL>
 __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -860,14 +888,17 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
     }
     const int S = tile_steps(I);
     const Frags F = frags_at(lds, I);
-    WRegs<NS> D[TW];
+    WRegs<NS, SL> D[TW];
     WTile<RS> TD[TW];
     int n0[TW];
+    // the wave's scale windows follow the fragment area (SL)
+    const uint32_t swin = lds_addr_of(lds) + (uint32_t)frag_lds_bytes(I, a.pairs_cap) +
+                          (uint32_t)(TW * wave * scale_window_bytes<NS>());
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
         n0[t] = chunk * run + kTileRows * (wave + W * t);
         TD[t] = wtile<RS>(x.blob + L.down_off, H, I, n0[t]);
-        wload(D[t], TD[t], 0);
+        wload(D[t], TD[t], 0, swin + (uint32_t)(t * scale_window_bytes<NS>()));
     }
     zero_block(F, threadIdx.x, blockDim.x);
     const float* act = dptr<const float>(a.W.act);
@@ -879,7 +910,7 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
         stage_rows(F, nt, [&](int t) { return act + (size_t)(x.p0 + tb + t) * I; },
                    threadIdx.x, blockDim.x);
         __syncthreads();
-        down_group<kMaxPairs, TW, NS, ONE>(F, D, TD, H, n0, S, tb, nt, x.p0, reload, y);
+        down_group<kMaxPairs, TW, NS, ONE, RS, SL>(F, D, TD, H, n0, S, tb, nt, x.p0, reload, y);
     }
 }
 
@@ -899,11 +930,15 @@ __device__ __forceinline__ void down_body(const GroupedArgs& a) {
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_gateup(const GroupedArgs a) {
     if (tile_steps(a.L.hidden) <= kGateupChunk) {
-#define LP_GATEUP(rs) gateup_body<kGateupChunk, true, rs>(a)
-        LP_BY_RS(a.L.group, LP_GATEUP)
+        if (scales_in_lds(a.L.group, a.L.hidden)) {
+            gateup_body<kGateupChunk, true, 0, true>(a);
+        } else {
+#define LP_GATEUP(rs) gateup_body<kGateupChunk, true, rs, false>(a)
+            LP_BY_RS(a.L.group, LP_GATEUP)
 #undef LP_GATEUP
+        }
     } else {
-#define LP_GATEUP(rs) gateup_body<kGateupLoopChunk, false, rs>(a)
+#define LP_GATEUP(rs) gateup_body<kGateupLoopChunk, false, rs, false>(a)
         LP_BY_RS(a.L.group, LP_GATEUP)
 #undef LP_GATEUP
     }
@@ -913,9 +948,13 @@ lp_moe_gateup(const GroupedArgs a) {
 // picks this kernel only for those), loaded in one piece.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down(const GroupedArgs a) {
-#define LP_DOWN(rs) down_body<2, kDownChunk, true, rs>(a)
-    LP_BY_RS(a.L.group, LP_DOWN)
+    if (scales_in_lds(a.L.group, a.L.inter)) {
+        down_body<2, kDownChunk, true, 0, true>(a);
+    } else {
+#define LP_DOWN(rs) down_body<2, kDownChunk, true, rs, false>(a)
+        LP_BY_RS(a.L.group, LP_DOWN)
 #undef LP_DOWN
+    }
 }
 
 // Down, one row tile per wave: up to kDownWideChunk steps in one piece,
@@ -923,11 +962,15 @@ lp_moe_down(const GroupedArgs a) {
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down_wide(const GroupedArgs a) {
     if (tile_steps(a.L.inter) <= kDownWideChunk) {
-#define LP_DOWN(rs) down_body<1, kDownWideChunk, true, rs>(a)
-        LP_BY_RS(a.L.group, LP_DOWN)
+        if (scales_in_lds(a.L.group, a.L.inter)) {
+            down_body<1, kDownWideChunk, true, 0, true>(a);
+        } else {
+#define LP_DOWN(rs) down_body<1, kDownWideChunk, true, rs, false>(a)
+            LP_BY_RS(a.L.group, LP_DOWN)
 #undef LP_DOWN
+        }
     } else {
-#define LP_DOWN(rs) down_body<1, kDownLoopChunk, false, rs>(a)
+#define LP_DOWN(rs) down_body<1, kDownLoopChunk, false, rs, false>(a)
         LP_BY_RS(a.L.group, LP_DOWN)
 #undef LP_DOWN
     }

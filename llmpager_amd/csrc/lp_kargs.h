@@ -20,7 +20,8 @@ constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
-constexpr int kTopkDispatchMaxT = 64;  // largest T routed by the one-workgroup top-k + dispatch
+constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
+constexpr int kTopkDispatchMaxT = 64;  // largest T dispatched by one workgroup (after the top-k kernel)
 constexpr int kDispTok = 256;          // tokens per block of the multi-block dispatch
 constexpr int kMaxPairs = 2;           // token pairs the grouped kernels stage at once
 constexpr int kMaxChunk = 16;          // most MFMA steps (4 sub-groups each) one register chunk holds
@@ -48,6 +49,16 @@ LPK_HD constexpr int frag_lds_bytes(int cols, int pairs) {
 // (bf16(x - bf16(x))) as [ngp][64 B] blocks in fragment order, then the
 // accumulator seeds [ngp][2] f32 (-136 * the part's sum over the sub-group).
 LPK_HD constexpr int image_bytes(int cols) { return 136 * frag_ngp(cols); }
+
+// The grouped kernels read a one-chunk tile's scales from a per-wave LDS
+// window (filled by 16-byte copies of whole scale lines) when the group is 32
+// and every row's scales start 16-byte aligned (sub-groups per row a
+// multiple of 8); otherwise each lane loads its own.  The host adds the
+// windows' bytes (scale_window_lds) to the launch's LDS.
+LPK_HD constexpr bool scales_in_lds(int group, int cols) { return group == 32 && (cols >> 5) % 8 == 0; }
+LPK_HD constexpr int scale_window_lds(int waves, int tiles_per_wave, int chunk_steps) {
+    return waves * tiles_per_wave * 64 * 2 * chunk_steps;
+}
 
 // ---- 1:1 launchers (crates/llmpager-cuda/src/kernels.rs) -------------------
 

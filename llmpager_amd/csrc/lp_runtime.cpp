@@ -73,6 +73,7 @@ enum Fn {
     kDispScan,
     kDispScatter,
     kGemmRouter,
+    kDispatch,
     kNumFns
 };
 
@@ -95,6 +96,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_gemm.hsaco", "lp_gemm_actimg"},   {"lp_gemm.hsaco", "lp_gemm_down"},
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
+    {"lp_moe.hsaco", "lp_moe_dispatch"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
@@ -624,8 +626,12 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
 
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
-    if (T <= kTopkDispatchMaxT) return launch(c, kTopkDispatch, dim3(1), dim3(1024), 0, s, ra);
+    // up to kTopkFusedMaxT tokens: one workgroup does both (one token per
+    // wave); more: the top-k spread over workgroups, then one dispatch
+    // workgroup or, past kTopkDispatchMaxT, the three-launch dispatch
+    if (T <= kTopkFusedMaxT) return launch(c, kTopkDispatch, dim3(1), dim3(1024), 0, s, ra);
     if (int r = launch(c, kTopk, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
+    if (T <= kTopkDispatchMaxT) return launch(c, kDispatch, dim3(1), dim3(256), 0, s, ra);
     const unsigned nb = (unsigned)((T + kDispTok - 1) / kDispTok);
     if (int r = launch(c, kDispCount, dim3(nb), dim3(kDispTok), 0, s, ra)) return r;
     if (int r = launch(c, kDispScan, dim3(1), dim3(1024), 0, s, ra)) return r;
@@ -665,6 +671,8 @@ int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, 
     return route_tail(c, ra, s);
 }
 
+static int tile_steps_host(int cols) { return ((cols >> 5) + 3) >> 2; }
+
 // Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
 // (maxu entries): workgroup width chosen so that there are about two work
 // items per CU, down with two tiles per wave when the inner size allows.
@@ -679,17 +687,21 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga, int maxu, lp_stream s) 
     {
         const int w = pick_w(I, 1);
         const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
+        const int win = tile_steps_host(H) <= kGateupChunk && scales_in_lds(ga.L.group, H)
+                            ? scale_window_lds(w, 2, kGateupChunk) : 0;
         if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w),
-                           (size_t)frag_lds_bytes(H, cap), s, ga))
+                           (size_t)(frag_lds_bytes(H, cap) + win), s, ga))
             return r;
     }
-    const int steps = ((I / 32) + 3) / 4;
+    const int steps = tile_steps_host(I);
     const Fn f = steps <= kDownChunk ? kDown : kDownWide;
     const int tw = steps <= kDownChunk ? 2 : 1;
     const int w = pick_w(H, tw);
     const int chunks = (H + kTileRows * w * tw - 1) / (kTileRows * w * tw);
-    return launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), (size_t)frag_lds_bytes(I, cap), s,
-                  ga);
+    const int ns = steps <= kDownChunk ? kDownChunk : kDownWideChunk;
+    const int win = steps <= kDownWideChunk && scales_in_lds(ga.L.group, I) ? scale_window_lds(w, tw, ns) : 0;
+    return launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), (size_t)(frag_lds_bytes(I, cap) + win),
+                  s, ga);
 }
 
 // The grouped expert kernels and the combine; the fragment images of x are
@@ -715,10 +727,12 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     const int H = d->hidden;
     const int Is = d->shared_blob ? d->shared_inter : 0;
     // Token pairs staged at once: enough for T tokens on one expert, bounded
-    // by kMaxPairs and by the LDS the fragments need.
+    // by kMaxPairs and by the LDS the fragments (and at most the largest
+    // scale windows) need.
     int cap = std::min(kMaxPairs, (T + 1) / 2);
     auto lds_for = [&](int p) {
-        return (size_t)std::max({frag_lds_bytes(H, p), frag_lds_bytes(d->inter, p), frag_lds_bytes(std::max(Is, 32), p)});
+        return (size_t)std::max({frag_lds_bytes(H, p), frag_lds_bytes(d->inter, p), frag_lds_bytes(std::max(Is, 32), p)}) +
+               (size_t)scale_window_lds(4, 2, kGateupChunk);
     };
     while (cap > 1 && lds_for(cap) > c->max_lds) --cap;
     if (lds_for(1) > c->max_lds)
