@@ -38,17 +38,18 @@ REGION_BYTES = I * (H // G) * 2 + I * H // 2        # 884,736: one q4 projection
 EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
-DOMINANT = "lp_moe_gateup"
+# The grouped gate/up launch of a layer is the dominant kernel.
+GATEUP_KERNELS = ("lp_moe_gateup",)
+DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide")
 CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
-# HBM bytes per lp_moe_gateup launch at B = 32 (FETCH_SIZE + WRITE_SIZE, each
-# scaled by the factor the same counter reads for the calibration copy), from
-# the rocprofv3 --pmc runs recorded in profiles/lp_moe_gateup_config2_b32.md.
+# HBM bytes per dominant-kernel launch at B = 32 (FETCH_SIZE + WRITE_SIZE,
+# each scaled by the factor the same counter reads for the calibration copy),
+# from the rocprofv3 --pmc runs recorded in profiles/ for that kernel.
 # Re-measure whenever the kernel changes.
-GATEUP_TRAFFIC_B32 = 180_659_514
-KERNELS = ("lp_moe_router", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count", "lp_moe_disp_scan",
-           "lp_moe_disp_scatter", "lp_moe_ximage",
-           "lp_moe_gateup", "lp_moe_down",
-           "lp_moe_down_wide", "lp_moe_combine")
+TRAFFIC_B32 = {}
+KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
+           "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
+           "lp_moe_combine")
 
 
 def log(msg: str) -> None:
@@ -160,15 +161,16 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
     # dominant kernel: grouped gate/up (two of the three projections of every
     # unique expert); its algorithmic bytes are U x 2 x 884,736 per launch
     gu_bytes = float(u.sum()) * 2 * REGION_BYTES
-    dom_ms, dom_n = prof[DOMINANT]
+    dominant = max(GATEUP_KERNELS, key=lambda kn: prof[kn][1])
+    dom_ms, dom_n = prof[dominant]
     dom_gbps = gu_bytes / (dom_ms / 1e3) / 1e9 if dom_ms > 0 else 0.0
-    dn_ms = prof["lp_moe_down"][0] + prof["lp_moe_down_wide"][0]
+    dn_ms = sum(prof[kn][0] for kn in DOWN_KERNELS)
     dn_gbps = float(u.sum()) * REGION_BYTES / (dn_ms / 1e3) / 1e9 if dn_ms > 0 else 0.0
     res = dict(
         batch=B, tok_s=B / sec, ms_per_step=sec * 1e3, unique_experts_per_layer=float(u.mean()),
         bytes_per_step=step_bytes, hbm_gbps=step_bytes / sec / 1e9,
         hbm_frac=step_bytes / sec / 1e9 / PEAK_GBPS,
-        dominant=dict(kernel=DOMINANT, launches=dom_n, avg_us=dom_ms * 1e3 / max(dom_n, 1),
+        dominant=dict(kernel=dominant, launches=dom_n, avg_us=dom_ms * 1e3 / max(dom_n, 1),
                       bytes_per_launch=gu_bytes / max(dom_n, 1), gbps=dom_gbps,
                       frac=dom_gbps / PEAK_GBPS),
         down_gbps=dn_gbps,
@@ -418,13 +420,13 @@ def main() -> int:
         "hbm_frac": round(hl["hbm_frac"], 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": DOMINANT,
+            "kernel": dom["kernel"],
             "bytes_per_launch": round(dom["bytes_per_launch"]),
             "achieved": round(dom["gbps"], 1),
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dom["frac"], 4),
-            "traffic": GATEUP_TRAFFIC_B32 if a.headline == 32 else None,
+            "traffic": TRAFFIC_B32.get(dom["kernel"]) if a.headline == 32 else None,
             "avg_us": round(dom["avg_us"], 3),
         },
         "cpu_baseline": cpu,

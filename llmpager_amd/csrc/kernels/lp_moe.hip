@@ -45,6 +45,53 @@ __device__ __forceinline__ float div_rn(float a, float b) { return (float)((doub
 namespace {
 
 // Token t's image, by the whole workgroup, and its lo flag (W.xlo[t]).
+// Token t's image from its row staged in LDS, by the whole workgroup: thread
+// u takes sub-group u / 4, columns 8 (u % 4) .. 8 (u % 4) + 7, writes their
+// bf16 parts, and the four threads of a sub-group add their part sums by
+// quad permutations ((s0 + s1) + (s2 + s3); the seed's rounding may differ
+// from the sequential sum of write_image_group in the last place).
+__device__ __forceinline__ void write_image_lds(const RouteArgs& a, int t, const float* row) {
+    const int H = a.L.hidden, ng = H >> 5, ngp = frag_ngp(H);
+    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
+    bool lo_any = false;
+    for (int u = threadIdx.x; u < 4 * ngp; u += blockDim.x) {  // whole quads together
+        const int g = u >> 2, d = u & 3;
+        float v[8];
+        if (g < ng) {
+            const float4 f0 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8);
+            const float4 f1 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8 + 4);
+            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+            v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        uint32_t hi[8], lo[8];
+        float shi = 0.0f, slo = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            hi[i] = f32_to_bf16_rne(v[i]);
+            lo[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hi[i]));
+            shi += bf16_to_f32(hi[i]);
+            slo += bf16_to_f32(lo[i]);
+        }
+        shi = shi + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(shi), 0xb1, 0xf, 0xf, false));
+        shi = shi + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(shi), 0x4e, 0xf, 0xf, false));
+        slo = slo + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(slo), 0xb1, 0xf, 0xf, false));
+        slo = slo + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(slo), 0x4e, 0xf, 0xf, false));
+        const uint4 h4 = make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
+                                    hi[3] | (hi[7] << 16));
+        const uint4 l4 = make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
+                                    lo[3] | (lo[7] << 16));
+        reinterpret_cast<uint4*>(img + (size_t)g * 64)[d] = h4;
+        reinterpret_cast<uint4*>(img + (size_t)ngp * 64 + (size_t)g * 64)[d] = l4;
+        if (d == 0) reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * shi + -136.0f * slo, 0.0f);
+        lo_any |= (l4.x | l4.y | l4.z | l4.w) != 0u;
+    }
+    lo_any = __syncthreads_or(lo_any);
+    if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo_any ? 1 : 0;
+}
+
 __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
     const int H = a.L.hidden;
     const float* row = dptr<const float>(a.x) + (size_t)t * H;
@@ -56,16 +103,54 @@ __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
 }
 
 
-__device__ __forceinline__ void router_rows(const RouteArgs& a) {
-    const int wave = threadIdx.x >> 6;
+// v + v[lane ^ o] for o = 32, 16, ..., 1 in turn (the router's butterfly):
+// lane swaps for 32 and 16, a row rotation for 8, a swizzle for 4 and quad
+// permutations for 2 and 1.  Each step adds the same two values as the
+// shuffle form, so the result is bit-identical to it.
+__device__ __forceinline__ float butterfly_sum(float v) {
+    const auto a32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a32[0]) + __uint_as_float(a32[1]);
+    const auto a16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a16[0]) + __uint_as_float(a16[1]);
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+    v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101f));                      // xor 4
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+    return v;
+}
+
+// butterfly_sum over N independent values, step by step for all of them so
+// that the steps' latencies overlap.
+template <int N>
+__device__ __forceinline__ void butterfly_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const auto a32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+        v[i] = __uint_as_float(a32[0]) + __uint_as_float(a32[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const auto a16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+        v[i] = __uint_as_float(a16[0]) + __uint_as_float(a16[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x128, 0xf, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), 0x101f));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x4e, 0xf, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] = v[i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0xb1, 0xf, 0xf, false));
+}
+
+// Logits of expert e for tokens t0 .. t0 + nt - 1 (nt <= kRouterTokBlock) by
+// the calling wave.
+__device__ __forceinline__ void router_dot(const RouteArgs& a, int e, int t0, int nt) {
     const int lane = lane_id();
     const int E = a.L.experts, H = a.L.hidden;
-    const int e = blockIdx.x * 4 + wave;
-    const int t0 = blockIdx.y * kRouterTokBlock;
-    const int nt = min(kRouterTokBlock, a.T - t0);
-    if (a.make_xf)
-        for (int t = t0 + (int)blockIdx.x; t < t0 + nt; t += gridDim.x) write_image(a, t);
-    if (e >= E) return;
     const uint16_t* w = dptr<const uint16_t>(a.L.router_w) + (size_t)e * H;
     const float* x = dptr<const float>(a.x) + (size_t)t0 * H;
     float acc[kRouterTokBlock];
@@ -105,6 +190,128 @@ __device__ __forceinline__ void router_rows(const RouteArgs& a) {
     }
 }
 
+// Logits of experts e0 .. e0 + 8 * kRouteEPW - 1 (kRouteEPW per wave) for
+// tokens t0 .. t0 + nt - 1 by the workgroup of 8 waves, in the same canonical
+// order as router_dot.  The token rows are staged in LDS (xs, kRouteXLds
+// bytes), as many as fit at a time, so that each is read from memory once per
+// workgroup; each lane keeps its weight chunks of its experts in registers.
+
+__device__ __forceinline__ void router_block(const RouteArgs& a, float* xs, int e0, int t0, int nt) {
+    constexpr int CB = 4;  // weight chunks per lane loaded at once
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int E = a.L.experts, H = a.L.hidden;
+    const int chunks = H >> 3;
+    const int tb = min(kRouterTokBlock, kRouteXLds / (H * 4));
+    float* logits = dptr<float>(a.W.logits);
+    int ew[kRouteEPW];
+#pragma unroll
+    for (int j = 0; j < kRouteEPW; ++j) ew[j] = min(e0 + wave * kRouteEPW + j, E - 1);
+    for (int tt = 0; tt < nt; tt += tb) {
+        const int nb = min(tb, nt - tt);
+        float acc[kRouteEPW][kRouterTokBlock];
+#pragma unroll
+        for (int j = 0; j < kRouteEPW; ++j)
+#pragma unroll
+            for (int t = 0; t < kRouterTokBlock; ++t) acc[j][t] = 0.0f;
+        for (int c0 = 0; c0 * 64 < chunks; c0 += CB) {
+            // this batch's weight chunks of the wave's experts: in flight
+            // together (and, for the first batch, with the staged rows)
+            uint4 wv[kRouteEPW][CB];
+#pragma unroll
+            for (int j = 0; j < kRouteEPW; ++j)
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    const int ch = lane + 64 * (c0 + c);
+                    wv[j][c] = ch < chunks ? *reinterpret_cast<const uint4*>(
+                                                 dptr<const uint16_t>(a.L.router_w) + (size_t)ew[j] * H + ch * 8)
+                                           : make_uint4(0, 0, 0, 0);
+                }
+            if (c0 == 0) {
+                __syncthreads();  // the previous sub-block's rows are consumed
+                // every load of the staging in flight at once (up to
+                // kRouteXLds / 16 / 512 per thread), then the LDS stores
+                constexpr int XU = kRouteXLds / 16 / 512;
+                const float4* xg = dptr<const float4>(a.x) + (size_t)(t0 + tt) * (H >> 2);
+                const int n4 = nb * (H >> 2);
+                float4 xr[XU];
+#pragma unroll
+                for (int u = 0; u < XU; ++u) {
+                    const int i = (int)threadIdx.x + 512 * u;
+                    xr[u] = i < n4 ? xg[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int u = 0; u < XU; ++u) {
+                    const int i = (int)threadIdx.x + 512 * u;
+                    if (i < n4) reinterpret_cast<float4*>(xs)[i] = xr[u];
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int ch = lane + 64 * (c0 + c);
+                if (ch >= chunks) break;
+                float wf[kRouteEPW][8];
+#pragma unroll
+                for (int j = 0; j < kRouteEPW; ++j) {
+                    const uint4 w4 = wv[j][c];
+                    wf[j][0] = bf16_to_f32(w4.x & 0xffffu);
+                    wf[j][1] = bf16_to_f32(w4.x >> 16);
+                    wf[j][2] = bf16_to_f32(w4.y & 0xffffu);
+                    wf[j][3] = bf16_to_f32(w4.y >> 16);
+                    wf[j][4] = bf16_to_f32(w4.z & 0xffffu);
+                    wf[j][5] = bf16_to_f32(w4.z >> 16);
+                    wf[j][6] = bf16_to_f32(w4.w & 0xffffu);
+                    wf[j][7] = bf16_to_f32(w4.w >> 16);
+                }
+                // each staged row chunk is read once and serves every expert
+#pragma unroll
+                for (int t = 0; t < kRouterTokBlock; ++t) {
+                    if (t < nb) {
+                        const float4 xa = *reinterpret_cast<const float4*>(xs + (size_t)t * H + ch * 8);
+                        const float4 xb = *reinterpret_cast<const float4*>(xs + (size_t)t * H + ch * 8 + 4);
+#pragma unroll
+                        for (int j = 0; j < kRouteEPW; ++j) {
+                            float v = acc[j][t];
+                            v = __builtin_fmaf(wf[j][0], xa.x, v);
+                            v = __builtin_fmaf(wf[j][1], xa.y, v);
+                            v = __builtin_fmaf(wf[j][2], xa.z, v);
+                            v = __builtin_fmaf(wf[j][3], xa.w, v);
+                            v = __builtin_fmaf(wf[j][4], xb.x, v);
+                            v = __builtin_fmaf(wf[j][5], xb.y, v);
+                            v = __builtin_fmaf(wf[j][6], xb.z, v);
+                            v = __builtin_fmaf(wf[j][7], xb.w, v);
+                            acc[j][t] = v;
+                        }
+                    }
+                }
+            }
+        }
+        float red[kRouteEPW * kRouterTokBlock];
+#pragma unroll
+        for (int j = 0; j < kRouteEPW; ++j)
+#pragma unroll
+            for (int t = 0; t < kRouterTokBlock; ++t) red[j * kRouterTokBlock + t] = acc[j][t];
+        butterfly_sum_n(red);
+#pragma unroll
+        for (int j = 0; j < kRouteEPW; ++j) {
+            const int e = e0 + wave * kRouteEPW + j;
+#pragma unroll
+            for (int t = 0; t < kRouterTokBlock; ++t)
+                if (lane == 0 && e < E && t < nb) logits[(size_t)(t0 + tt + t) * E + e] = red[j * kRouterTokBlock + t];
+        }
+    }
+}
+
+__device__ __forceinline__ void router_rows(const RouteArgs& a) {
+    const int wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 4 + wave;
+    const int t0 = blockIdx.y * kRouterTokBlock;
+    const int nt = min(kRouterTokBlock, a.T - t0);
+    if (a.make_xf)
+        for (int t = t0 + (int)blockIdx.x; t < t0 + nt; t += gridDim.x) write_image(a, t);
+    if (e < a.L.experts) router_dot(a, e, t0, nt);
+}
+
 }  // namespace
 
 extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) { router_rows(a); }
@@ -138,23 +345,29 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs 
 namespace {
 
 // Top-k of token t by the calling wave, PER candidates per lane (expert
-// i = lane + 64 q); sv is the wave's LDS row of kMaxExperts floats (the
-// probabilities, read back for the picks).  The in-order sum runs as a
-// chain of adds over v_readlane values; each pick is two DPP reductions:
-// the largest ordered key, then the lowest id holding it.
+// i = lane + 64 q); sv is the wave's LDS row (kMaxExperts floats; the
+// winners' table uses its first 5 * kMaxTopK words).  The in-order sum of the
+// softmax runs as a chain of adds over v_readlane values.  The k winners
+// come from a radix select on the ordered keys (the largest threshold with
+// at least k keys at or above it; keys equal to it taken lowest id first),
+// each winner's place in the stable descending order is its count of
+// winners ahead of it, and lane j then finishes pick j: no sequential
+// pick loop.
 template <int PER>
 __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv, int* ids_l, int* cnt_l) {
     const int lane = lane_id();
     const int E = a.L.experts, k = a.L.top_k;
     const float* lg = dptr<const float>(a.W.logits) + (size_t)t * E;
     const uint64_t tabv = exp2tab_lane();  // glibc's 2^(i/32) table, one entry per lane
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[PER];
-    float v[PER];
+    float val[PER], v[PER];
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
         const int i = lane + 64 * q;
         v[q] = i < E ? lg[i] : 0.0f;
         key[q] = 0u;
+        val[q] = 0.0f;
     }
     if (a.L.gating == 0) {
         uint32_t mk = 0u;  // max over the ordered keys = the largest logit (f32::MIN start)
@@ -172,21 +385,29 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
         // z = e_0 + e_1 + ... in id order, from -0.0 (the reference's fold):
         // a chain of adds over lane values read with v_readlane
         float z = -0.0f;
+        if (PER <= 4 && (E & 63) == 0) {
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            if (64 * q >= E) break;  // uniform
-            const int n = E - 64 * q;
+            for (int q = 0; q < PER; ++q) {
+                if (64 * q >= E) break;  // uniform
+#pragma unroll
+                for (int l = 0; l < 64; ++l)
+                    z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                if (64 * q >= E) break;  // uniform
+                const int n = E - 64 * q;
 #pragma unroll 8
-            for (int l = 0; l < 64; ++l)
-                if (l < n) z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+                for (int l = 0; l < 64; ++l)
+                    if (l < n) z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+            }
         }
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const int i = lane + 64 * q;
-            if (i < E) {
-                const float p = div_rn(v[q], z);
-                key[q] = ordered_key(p);
-                sv[i] = p;
+            if (lane + 64 * q < E) {
+                val[q] = div_rn(v[q], z);
+                key[q] = ordered_key(val[q]);
             }
         }
     } else {
@@ -197,69 +418,83 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
             const float ex = expf_glibc_wave(-v[q], tabv);  // every lane takes part
             if (i < E) {
                 const float d = 1.0f + ex;
-                const float sg = div_rn(1.0f, d);
-                sv[i] = sg;
-                key[q] = ordered_key((sg + bias[i]) + 0.0f);  // -0 ranks equal to +0
+                val[q] = div_rn(1.0f, d);
+                key[q] = ordered_key((val[q] + bias[i]) + 0.0f);  // -0 ranks equal to +0
             }
         }
     }
-    wave_sync_lds();
-
+    // live keys are >= 1 (ordered_key(-inf) = 0x007fffff); 0 marks no expert
     const int n = k < E ? k : E;
-    int ids[kMaxTopK];
-    float val[kMaxTopK];
+    uint32_t thr = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = thr | (1u << bit);
+        int c = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        ids[j] = -1;
-        val[j] = 0.0f;
-        if (j >= n) continue;
-        uint32_t bk = 0u;  // keys of live candidates are >= 1 (ordered_key(+0) = 0x80000000)
-#pragma unroll
-        for (int q = 0; q < PER; ++q) bk = key[q] > bk ? key[q] : bk;
-        const uint32_t M = wave_max_u32(bk);
-        uint32_t bid = 0xffffffffu;
-#pragma unroll
-        for (int q = 0; q < PER; ++q)
-            if (key[q] == M && key[q] != 0u) bid = min(bid, (uint32_t)(lane + 64 * q));
-        const int id = (int)wave_min_u32(bid);
-#pragma unroll
-        for (int q = 0; q < PER; ++q)
-            if (lane + 64 * q == id) key[q] = 0u;  // picked
-        ids[j] = id;
-        val[j] = sv[id];
+        for (int q = 0; q < PER; ++q) c += __popcll(__ballot(key[q] >= cand));
+        if (c >= n) thr = cand;
     }
-
+    int need = n;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) need -= __popcll(__ballot(key[q] > thr));
+    uint32_t* wk = reinterpret_cast<uint32_t*>(sv);
+    int* wi = reinterpret_cast<int*>(sv) + kMaxTopK;
+    float* wv = sv + 2 * kMaxTopK;
+    int* pid = reinterpret_cast<int*>(sv) + 3 * kMaxTopK;
+    float* pv = sv + 4 * kMaxTopK;
+    int eq_before = 0, slot0 = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const uint64_t eq = __ballot(key[q] == thr);
+        const bool win = key[q] > thr || (key[q] == thr && eq_before + __popcll(eq & below) < need);
+        eq_before += __popcll(eq);
+        const uint64_t wm = __ballot(win);
+        if (win) {
+            const int s = slot0 + __popcll(wm & below);  // winners in id order
+            wk[s] = key[q];
+            wi[s] = lane + 64 * q;
+            wv[s] = val[q];
+        }
+        slot0 += __popcll(wm);
+    }
+    wave_sync_lds();
+    if (lane < n) {
+        const uint32_t kj = wk[lane];
+        const int ij = wi[lane];
+        int rank = 0;
+        for (int s = 0; s < n; ++s) rank += (wk[s] > kj || (wk[s] == kj && wi[s] < ij)) ? 1 : 0;
+        pid[rank] = ij;
+        pv[rank] = wv[lane];
+    }
+    wave_sync_lds();
+    // pick j in lane j; the sum of the picks in pick order, from -0.0
+    const int my_pick = lane < n ? pid[lane] : -1;
+    const float my_val = lane < n ? pv[lane] : 0.0f;
     float s = -0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j)
-        if (j < n) s = s + val[j];
-    // weights in pick order; lane j keeps pick j (min_weight compacts the
-    // survivors: pick j lands in slot kept-so-far)
-    int kept = 0;
-    int my_id = -1;
-    float my_w = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j >= n) continue;
-        float wj;
-        if (a.L.gating == 0) {
-            wj = a.L.renorm ? div_rn(val[j], s) : val[j];
-        } else {
-            wj = val[j];
-            if (a.L.renorm && s > 0.0f) wj = div_rn(wj, s);
-            wj = wj * a.L.routed_scaling;
-            if (a.L.min_weight > 0.0f && !(wj >= a.L.min_weight)) continue;
-        }
-        if (lane == kept) {
-            my_id = ids[j];
-            my_w = wj;
-        }
-        ++kept;
+    for (int j = 0; j < n; ++j) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), j));
+    float wj = my_val;
+    bool keep = lane < n;
+    if (a.L.gating == 0) {
+        if (a.L.renorm) wj = div_rn(my_val, s);
+    } else {
+        if (a.L.renorm && s > 0.0f) wj = div_rn(wj, s);
+        wj = wj * a.L.routed_scaling;
+        if (a.L.min_weight > 0.0f && !(wj >= a.L.min_weight)) keep = false;
     }
+    // survivors keep pick order: pick j lands in slot (survivors before it)
+    wave_sync_lds();
+    const uint64_t km = __ballot(keep);
+    const int kept = __popcll(km);
+    if (keep) {
+        const int slot = __popcll(km & below);
+        pid[slot] = my_pick;
+        pv[slot] = wj;
+    }
+    wave_sync_lds();
     if (lane < k) {
-        dptr<int>(a.W.ids)[(size_t)t * k + lane] = my_id;
-        dptr<float>(a.W.wts)[(size_t)t * k + lane] = my_w;
-        if (ids_l) ids_l[t * k + lane] = my_id;
+        const int id = lane < kept ? pid[lane] : -1;
+        dptr<int>(a.W.ids)[(size_t)t * k + lane] = id;
+        dptr<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? pv[lane] : 0.0f;
+        if (ids_l) ids_l[t * k + lane] = id;
     }
     if (lane == 0) {
         dptr<int>(a.W.cnt)[t] = kept;
@@ -321,12 +556,13 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
 
 // LDS of dispatch_all, carved from one buffer so that the single-workgroup
 // top-k + dispatch kernel can share it with its top-k phase.
-constexpr int kDispatchSmem = 4 * (kMaxExperts * 6 + (kMaxExperts + 4) + kMaxExperts * kEntryToks + 16);
+constexpr int kDispatchSmem = 4 * (kMaxExperts * 6 + (kMaxExperts + 4) + kMaxExperts * kEntryToks + 16 +
+                                   kTopkDispatchMaxT * (kMaxTopK + 1) + kMaxExperts);
 
 // ids / cnt: the picks (global, or LDS copies from the same workgroup);
 // slots: the slot table (global, or an LDS copy).
-__device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids,
-                                             const int* cnt, const int* slots) {
+__device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids_in,
+                                             const int* cnt_in, const int* slots_in) {
     int* cnt_e = reinterpret_cast<int*>(sm);
     int* base = cnt_e + kMaxExperts;
     int* gsl = base + kMaxExperts;                       // kMaxExperts + 1 used
@@ -341,6 +577,14 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     int* perm = dptr<int>(a.W.perm);
     int* inv = dptr<int>(a.W.inv);
     int* meta = dptr<int>(a.W.meta);
+    // the picks and the slot table in LDS first: one round trip to memory
+    // (T <= kTopkDispatchMaxT), every later read from LDS
+    int* ids = scan_sh + 16;
+    int* cnt = ids + kTopkDispatchMaxT * kMaxTopK;
+    int* slots = cnt + kTopkDispatchMaxT;
+    for (int i = tid; i < T * k; i += nth) ids[i] = ids_in[i];
+    for (int i = tid; i < T; i += nth) cnt[i] = cnt_in[i];
+    for (int i = tid; i < E; i += nth) slots[i] = slots_in[i];
 
     for (int e = tid; e < E; e += nth) {
         cnt_e[e] = 0;
@@ -655,6 +899,67 @@ extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const Ro
     for (int t = wave; t < a.T; t += nw) topk_any(a, t, sv, ids_l, cnt_l);
     __syncthreads();
     dispatch_all(a, sm, ids_l, cnt_l, slots_l);
+}
+
+// ---------------------------------------------------------------------------
+// Routing of a decode-sized batch (T <= kTopkDispatchMaxT) in one launch:
+// router logits, top-k and dispatch.  Grid (ceil(E/16), ceil(T/8)), 512
+// threads: workgroup (g, b) computes the logits of experts 16g .. 16g+15 (two
+// per wave, the router GEMV's canonical order) for the tokens of block b
+// (8b .. 8b+7) and, with make_xf, the images of tokens 8b + g, 8b + g +
+// ceil(E/16), ... of the block.  The last
+// workgroup of block b to finish (an arrival counter) ranks the block's
+// tokens, one per wave; the last block to finish ranking builds the dispatch
+// tables.  Release fences before each arrival and acquire fences after it
+// make the other workgroups' logits and picks visible; the last arrival
+// resets its counter, so every launch finds them zero.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Add one arrival at *cnt; true (in every thread) for the n-th, which also
+// resets the counter.  Every thread of the workgroup must call it.
+__device__ __forceinline__ bool last_arrival(int* cnt, int n, int* flag) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last = atomicAdd(cnt, 1) == n - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    const bool last = *flag != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return last;
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const RouteArgs a) {
+    constexpr int kTopkLds = 8 * kMaxExperts * 4;
+    __shared__ __align__(16) uint8_t sm[kDispatchSmem > kTopkLds ? kDispatchSmem : kTopkLds];
+    __shared__ __align__(16) float xs[kRouteXLds / 4];
+    __shared__ int flag;
+    const int wave = threadIdx.x >> 6;
+    const int b = blockIdx.y, t0 = b * kRouterTokBlock;
+    const int nt = min(kRouterTokBlock, a.T - t0);
+    router_block(a, xs, blockIdx.x * 8 * kRouteEPW, t0, nt);
+    // the images are for the expert kernels: after the logits, so that the
+    // ranking waits for no image, and from the rows still staged in LDS when
+    // the whole block fits there
+    if (a.make_xf) {
+        const bool staged = nt * a.L.hidden * 4 <= kRouteXLds;
+        for (int t = blockIdx.x; t < nt; t += gridDim.x) {
+            if (staged)
+                write_image_lds(a, t0 + t, xs + (size_t)t * a.L.hidden);
+            else
+                write_image(a, t0 + t);
+        }
+    }
+    int* cnt = dptr<int>(a.sync);
+    if (!last_arrival(cnt + b, gridDim.x, &flag)) return;
+    if (wave < nt) topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts);
+    if (!last_arrival(cnt + 8, gridDim.y, &flag)) return;
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table));
 }
 
 // ---------------------------------------------------------------------------

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <mutex>
 #include <string>
@@ -74,6 +75,7 @@ enum Fn {
     kDispScatter,
     kGemmRouter,
     kDispatch,
+    kRouteFused,
     kNumFns
 };
 
@@ -96,7 +98,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_gemm.hsaco", "lp_gemm_actimg"},   {"lp_gemm.hsaco", "lp_gemm_down"},
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
-    {"lp_moe.hsaco", "lp_moe_dispatch"},
+    {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
@@ -140,6 +142,11 @@ struct lp_ctx {
     std::vector<hipEvent_t> prof_pool;
     double prof_ms[kNumFns] = {};
     int64_t prof_n[kNumFns] = {};
+    // arrival counters of the fused routing kernel: kSyncSlots slots of
+    // kSyncWords, zero between launches; each launch takes the next slot, so
+    // launches on different streams do not share counters
+    int32_t* sync = nullptr;
+    std::atomic<unsigned> sync_next{0};
 };
 
 namespace {
@@ -244,6 +251,13 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
                                        "): " + hipGetErrorString(e));
         }
     }
+    e = hipMalloc(reinterpret_cast<void**>(&c->sync), (size_t)kSyncSlots * kSyncWords * 4);
+    if (e == hipSuccess) e = hipMemset(c->sync, 0, (size_t)kSyncSlots * kSyncWords * 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        lp_destroy(c);
+        return hip_fail(e, "lp_init: arrival counters");
+    }
     *out = c;
     return LP_OK;
 }
@@ -257,6 +271,10 @@ void lp_destroy(lp_ctx* c) {
     for (hipEvent_t e : c->prof_pool) (void)hipEventDestroy(e);
     for (int m = 0; m < kNumModules; ++m)
         if (c->modules[m]) (void)hipModuleUnload(c->modules[m]);
+    if (c->sync) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->sync);
+    }
     delete c;
 }
 
@@ -654,9 +672,18 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
         if (int r = launch(c, kXImage, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
         return route_tail(c, ra, s);
     }
-    dim3 g((unsigned)((d->experts + 3) / 4), (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
-    if (int r = launch(c, kRouter, g, dim3(256), 0, s, ra)) return r;
-    return route_tail(c, ra, s);
+    if (d->hidden * 4 > kRouteXLds) {
+        // token rows too wide for the fused kernel's staging: router, then top-k + dispatch
+        dim3 g((unsigned)((d->experts + 3) / 4), (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
+        if (int r = launch(c, kRouter, g, dim3(256), 0, s, ra)) return r;
+        return route_tail(c, ra, s);
+    }
+    // decode-sized batch: logits, top-k and dispatch in one launch
+    ra.sync = reinterpret_cast<uint64_t>(c->sync) +
+              (uint64_t)(c->sync_next.fetch_add(1) % kSyncSlots) * kSyncWords * 4;
+    dim3 g((unsigned)((d->experts + 8 * kRouteEPW - 1) / (8 * kRouteEPW)),
+           (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
+    return launch(c, kRouteFused, g, dim3(512), 0, s, ra);
 }
 
 int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, int T,

@@ -133,6 +133,29 @@ def test_layer_missing_expert_flags(cuda):
     L.free()
 
 
+def test_layer_heavy_experts(cuda):
+    # Decode-sized batch on few experts: experts hold more (token, pick) pairs
+    # than one staged token group, so the grouped kernels run several groups
+    # per expert.
+    L = DeviceLayer(cuda, H=2048, I=768, E=16, k=2, group=32, seed=12, router_std=0.3)
+    T = 48
+    x, h, g = _run_layer(cuda, L, T, seed=5)
+    assert np.bincount(g["ids"][:, :2].ravel(), minlength=16).max() > 8
+    _check_layer(L, x, h, g, T)
+    L.free()
+
+
+def test_layer_missing_expert_full_shape(cuda):
+    # The missing-expert path at the config-1 shape: flag raised, finite out.
+    slots = np.arange(128, dtype=np.int32)
+    slots[::3] = -1
+    L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=2, slots=slots)
+    x, h, g = _run_layer(cuda, L, 4, seed=2)
+    assert g["status"][1] == 1
+    assert np.isfinite(g["h"]).all()
+    L.free()
+
+
 def _route_logits(cuda, L: DeviceLayer, logits: np.ndarray):
     T = logits.shape[0]
     lay = lp.ws_layout(L.desc, T)
