@@ -292,6 +292,115 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
     return res
 
 
+# BASELINE config 4: Qwen3-235B-A22B shape with expert paging.
+P_H, P_I, P_E, P_K, P_G = 4096, 1536, 128, 8, 32
+P_LAYERS, P_SLOTS, P_TOKENS, P_ZIPF = 94, 64, 512, 1.1
+
+
+def zipf_trace(layers: int, tokens: int, E: int, k: int, s: float = P_ZIPF, seed: int = 0) -> np.ndarray:
+    """[tokens, layers, k] expert ids: per (token, layer) k distinct experts
+    drawn without replacement with probability proportional to rank^-s over
+    a per-layer seeded ranking of the experts, in draw order (Gumbel top-k,
+    which has the sequential draws' distribution)."""
+    rng = np.random.default_rng(seed)
+    logw = -s * np.log(np.arange(1, E + 1, dtype=np.float64))
+    out = np.empty((tokens, layers, k), np.int32)
+    for l in range(layers):
+        expert_of_rank = rng.permutation(E)
+        keys = logw[None, :] + rng.gumbel(size=(tokens, E))
+        ranks = np.argsort(-keys, axis=1, kind="stable")[:, :k]
+        out[:, l, :] = expert_of_rank[ranks]
+    return out
+
+
+def run_paged(cuda, s, layers: int, tokens: int, slots: int) -> dict:
+    """H4096 / I1536 / E128 / top-8 / g32, `layers` layers,
+    `slots` VRAM expert slots per layer; every expert blob sits in one pinned
+    host pack (layers x 128 x 10.6 MB).  A `tokens`-token routing trace (8
+    distinct experts per token and layer, Zipf(1.1) over a per-layer ranking)
+    drives batch-1 decode through the reference's order per layer: route (from
+    logits that rank the trace's picks first), request the picks from the
+    pager (misses copied host -> VRAM on its copy streams, the compute stream
+    waiting on them), re-resolve the expert table, run the experts, release
+    after the stream passes.  Reports tok/s, hit rate and H2D GB/s over the
+    whole trace (cold start included)."""
+    import llmpager_amd as lp
+    blob = lp.blob_bytes(P_H, P_I, P_G)
+    span = align(blob)
+    t0 = time.time()
+    while True:
+        n = layers * P_E * span
+        try:
+            pin = cuda.alloc_pinned(n)
+            break
+        except Exception as e:  # the host cannot pin the whole pack: fewer layers, said in the line
+            if layers <= 8:
+                raise
+            log(f"paged: pinning {n / 1e9:.1f} GB failed ({e}); trying {layers // 2} layers")
+            layers //= 2
+    view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(pin))
+    threads = min(16, os.cpu_count() or 1)
+    for l in range(layers):
+        lp.synth_blobs(P_E, span, P_H, P_I, P_G, 0, l, threads=threads, out=view[l * P_E * span:(l + 1) * P_E * span])
+    log(f"paged: host pack {n / 1e9:.1f} GB of {layers} x {P_E} experts in {time.time() - t0:.0f} s")
+    cfg = lp.PagerConfig(layers=layers, experts_per_layer=P_E, slots_per_layer=slots, decay_interval=256,
+                         blob_bytes=blob, span=0, host_blobs=pin, host_stride=span, copy_streams=4,
+                         global_pool=0)
+    pg = lp.Pager(cuda, cfg)
+    go, uo, do = lp.blob_offsets(P_H, P_I, P_G)
+    d_rw = cuda.upload(lp.synth_bf16(P_E * P_H, 0.02, 0, 1000), s)   # unused by route_logits
+    descs = [lp.LayerDesc(hidden=P_H, inter=P_I, experts=P_E, top_k=P_K, group=P_G, gating=lp.GATING_SOFTMAX,
+                          renorm=1, routed_scaling=1.0, min_weight=0.0, router_w=d_rw, router_bias=0,
+                          slot_table=pg.slot_table(l), arena_base=pg.arena, slot_span=pg.span,
+                          gate_off=go, up_off=uo, down_off=do) for l in range(layers)]
+    moe = [lp.MoeLayer(cuda, d) for d in descs]
+    trace = zipf_trace(layers, tokens, P_E, P_K)
+    # logits that make the trace's picks the top-k, in draw order
+    lg = np.zeros((tokens, layers, P_E), np.float32)
+    np.put_along_axis(lg, trace.astype(np.int64), (16.0 - np.arange(P_K, dtype=np.float32))[None, None, :], axis=2)
+    dlg = cuda.upload(lg, s)
+    lay = lp.ws_layout(descs[0], 1)
+    ws = cuda.alloc_device(lay.total)
+    dx = cuda.upload(lp.synth_f32_bf16(P_H, 1.0, 0, 3), s)
+    dh = cuda.upload(lp.synth_f32_bf16(P_H, 1.0, 0, 4), s)
+    cuda.sync()
+    picks = [[sorted(set(int(e) for e in trace[t, l])) for l in range(layers)] for t in range(tokens)]
+    t0 = time.time()
+    for t in range(tokens):
+        for l in range(layers):
+            moe[l].route_logits(dlg + ((t * layers + l) * P_E) * 4, 1, ws, s)
+            got = pg.request(l, picks[t][l], s)
+            moe[l].resolve(1, ws, s)
+            moe[l].experts(dx, dh, 1, ws, s)
+            pg.release_after(got, s)
+        pg.tick()
+        if t % 128 == 127:
+            log(f"paged: {t + 1}/{tokens} tokens")
+    cuda.sync()
+    pg.sync()
+    sec = time.time() - t0
+    m = pg.metrics()
+    uniq, err = moe[-1].status(ws, 1, s)
+    pg.close()
+    for p in (dlg, ws, dx, dh, d_rw):
+        cuda.free_device(p)
+    cuda.free_pinned(pin)
+    assert err == 0, f"paged decode reported error flags {err}"
+    lookups = m["hits"] + m["misses"]
+    # the experts' weights and scales (the trace replaces the router GEMV)
+    compute_bytes = tokens * layers * P_K * (blob - 32)
+    res = dict(
+        layers=layers, tokens=tokens, slots_per_layer=slots, expert_bytes=blob,
+        tok_s=tokens / sec, seconds=sec, hits=m["hits"], misses=m["misses"],
+        hit_rate=m["hits"] / max(lookups, 1), bytes_fetched=m["bytes_fetched"],
+        h2d_gbps=m["bytes_fetched"] / sec / 1e9, stalls=m["stalls"],
+        hbm_gbps=compute_bytes / sec / 1e9,
+    )
+    log(f"paged ({layers} layers, {slots} slots, {tokens} tokens): {res['tok_s']:.1f} tok/s, hit rate "
+        f"{res['hit_rate']:.4f}, {res['misses']} misses, H2D {res['h2d_gbps']:.1f} GB/s")
+    return res
+
+
 def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
     """The oracle (oracle/, the CPU restatement of the reference path) on the
     host cores: the first layers kept in host memory, B tokens, repeated until
@@ -363,6 +472,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill leg")
     ap.add_argument("--prefill-only", action="store_true")
+    ap.add_argument("--no-paged", action="store_true", help="skip the config-4 paging leg")
+    ap.add_argument("--paged-only", action="store_true")
+    ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
+    ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: this build's MoE path runs on a single MI355X "
@@ -387,6 +500,11 @@ def main() -> int:
     prefill = None if a.no_prefill else run_prefill(cuda, s, a.steps, a.warmup)
     if a.prefill_only:
         print(json.dumps({"prefill": prefill}), flush=True)
+        cuda.close()
+        return 0
+    paged = None if a.no_paged else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
+    if a.paged_only:
+        print(json.dumps({"paged": paged}), flush=True)
         cuda.close()
         return 0
     log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
@@ -431,6 +549,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "prefill": None if prefill is None else _rounded(prefill),
+        "paged": None if paged is None else _rounded(paged),
         "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
                              for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
                     | {"gateup_gbps": round(r["dominant"]["gbps"], 1),
