@@ -401,6 +401,73 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int) -> dict:
     return res
 
 
+# the MoE half of a DeepSeek-V2-Lite-style layer (the MLA
+# attention that precedes it in the model is outside this path).
+D_H, D_I, D_E, D_K, D_G, D_SH, D_LAYERS = 2048, 1408, 64, 6, 32, 2816, 26
+
+
+def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
+    """BASELINE config 5's MoE layer: 64 routed experts top-6 (softmax, no
+    renormalisation, as DeepSeek-V2-Lite) of width 1408 plus the always-on
+    shared MLP of width 2816 (2 shared experts), g32, stacked over 26 layers
+    (8.4 GB of distinct weights, so the 256 MB MALL cannot serve repeats) in
+    lockstep decode; tok/s and algorithmic GB/s at each batch."""
+    import llmpager_amd as lp
+    span = align(lp.blob_bytes(D_H, D_I, D_G))
+    go, uo, do = lp.blob_offsets(D_H, D_I, D_G)
+    sgo, suo, sdo = lp.blob_offsets(D_H, D_SH, D_G)
+    threads = min(16, os.cpu_count() or 1)
+    allocs, layers = [], []
+    d_slots = cuda.upload(np.arange(D_E, dtype=np.int32), s)
+    for l in range(D_LAYERS):
+        arena = cuda.upload(lp.synth_blobs(D_E, span, D_H, D_I, D_G, 5, l, threads=threads), s)
+        shared = cuda.upload(lp.synth_blob(D_H, D_SH, D_G, 5, 100 + l, 1 << 20), s)
+        d_rw = cuda.upload(lp.synth_bf16(D_E * D_H, 0.02, 5, 1000 + l), s)
+        cuda.sync_stream(s)
+        allocs += [arena, shared, d_rw]
+        desc = lp.LayerDesc(hidden=D_H, inter=D_I, experts=D_E, top_k=D_K, group=D_G, gating=lp.GATING_SOFTMAX,
+                            renorm=0, routed_scaling=1.0, min_weight=0.0, router_w=d_rw, router_bias=0,
+                            slot_table=d_slots, arena_base=arena, slot_span=span, gate_off=go, up_off=uo,
+                            down_off=do)
+        desc.shared_blob, desc.shared_inter, desc.shared_group = shared, D_SH, D_G
+        desc.sh_gate_off, desc.sh_up_off, desc.sh_down_off = sgo, suo, sdo
+        layers.append(lp.MoeLayer(cuda, desc))
+    expert_bytes = 3 * D_I * (D_H // D_G) * 2 + 3 * D_I * D_H // 2
+    shared_bytes = 3 * D_SH * (D_H // D_G) * 2 + 3 * D_SH * D_H // 2
+    out = {}
+    for B in batches:
+        ws = cuda.alloc_device(lp.ws_layout(layers[0].desc, B).total)
+        h0 = cuda.upload(lp.synth_f32_bf16((steps + warmup) * B * D_H, 1.0, 5, 2), s)
+        for i in range(warmup):
+            for L in layers:
+                L.forward(h0 + (steps + i) * B * D_H * 4, h0 + (steps + i) * B * D_H * 4, B, ws, s)
+        e0, e1 = cuda.event(), cuda.event()
+        cuda.sync()
+        cuda.record_event(e0, s)
+        for i in range(steps):
+            for L in layers:
+                L.forward(h0 + i * B * D_H * 4, h0 + i * B * D_H * 4, B, ws, s)
+        cuda.record_event(e1, s)
+        cuda.sync()
+        sec = cuda.elapsed_ms(e0, e1) / 1e3 / steps
+        L0 = layers[0]
+        L0.forward(h0, h0, B, ws, s)
+        u, err = L0.status(ws, B, s)
+        assert err == 0, f"config-5 step reported error flags {err}"
+        step_bytes = D_LAYERS * (D_E * D_H * 2 + u * expert_bytes + shared_bytes + B * D_H * 12)
+        out[str(B)] = dict(batch=B, tok_s=B / sec, us_per_layer=sec / D_LAYERS * 1e6, unique_experts=u,
+                           hbm_gbps=step_bytes / sec / 1e9, hbm_frac=step_bytes / sec / 1e9 / PEAK_GBPS)
+        log(f"config 5 B={B}: {B / sec:.1f} tok/s over {D_LAYERS} MoE layers, {sec / D_LAYERS * 1e6:.1f} us "
+            f"per layer, {step_bytes / sec / 1e9:.0f} GB/s (unique routed experts {u})")
+        for p in (ws, h0):
+            cuda.free_device(p)
+        for e in (e0, e1):
+            cuda.destroy_event(e)
+    for p in allocs + [d_slots]:
+        cuda.free_device(p)
+    return out
+
+
 def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
     """The oracle (oracle/, the CPU restatement of the reference path) on the
     host cores: the first layers kept in host memory, B tokens, repeated until
@@ -473,6 +540,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill leg")
     ap.add_argument("--prefill-only", action="store_true")
     ap.add_argument("--no-paged", action="store_true", help="skip the config-4 paging leg")
+    ap.add_argument("--no-shared", action="store_true", help="skip the config-5 shared-expert leg")
     ap.add_argument("--paged-only", action="store_true")
     ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
     ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
@@ -503,6 +571,7 @@ def main() -> int:
         cuda.close()
         return 0
     paged = None if a.no_paged else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
+    shared = None if a.no_shared or a.paged_only else run_shared(cuda, s, (1, 16), a.steps, a.warmup)
     if a.paged_only:
         print(json.dumps({"paged": paged}), flush=True)
         cuda.close()
@@ -550,6 +619,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill": None if prefill is None else _rounded(prefill),
         "paged": None if paged is None else _rounded(paged),
+        "shared": None if shared is None else _rounded(shared),
         "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
                              for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
                     | {"gateup_gbps": round(r["dominant"]["gbps"], 1),
