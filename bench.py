@@ -39,7 +39,7 @@ EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 # The grouped gate/up launch of a layer is the dominant kernel.
-GATEUP_KERNELS = ("lp_moe_gateup",)
+GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal")
 DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide")
 CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
 # HBM bytes per dominant-kernel launch at B = 32 (FETCH_SIZE + WRITE_SIZE,

@@ -376,8 +376,14 @@ __device__ __forceinline__ WTile<RS> wtile(uint64_t region, int rows, int cols, 
 // 16 at a time, the i-th 16 landing at window + 1024 i + 16 lane.  Scale q
 // (= 4 c + kb at step c) of row n then sits at window + 1024 ((q % NS) / 8) +
 // 16 (n + 16 (q / NS)) + 2 (q % 8): a per-lane base plus a constant per step.
+// Here NS is the window's width, window_steps<NS>(): the chunk's steps
+// rounded up to a multiple of 8, so that a chunk of 6 or 12 steps loads only
+// its own nibbles and still copies whole 16-byte scale lines.
 // The per-lane loads touch 16 cache lines per instruction for 128 useful
 // bytes; the window copy reads each line once.
+template <int NS>
+__host__ __device__ constexpr int window_steps() { return (NS + 7) / 8 * 8; }
+
 template <int NS, bool SL = false>
 struct WRegs {
     uint4 w[NS];
@@ -388,10 +394,11 @@ struct WRegs {
     bool lastok;     // the lane's sub-group exists at the tile's last step
 };
 
-// LDS byte offset of step j's scale from WRegs::sbase (SL).
-template <int NS>
+// LDS byte offset of step j's scale from WRegs::sbase (SL) in a window NW
+// steps wide.
+template <int NW>
 __device__ __forceinline__ constexpr uint32_t scale_step_off(int j) {
-    return 1024u * (uint32_t)(((4 * j) % NS) / 8) + 256u * (uint32_t)((4 * j) / NS) + 8u * (uint32_t)(j & 1);
+    return 1024u * (uint32_t)(((4 * j) % NW) / 8) + 256u * (uint32_t)((4 * j) / NW) + 8u * (uint32_t)(j & 1);
 }
 
 // Issue the tile's loads for steps c0 .. c0 + NS - 1: one per-lane offset
@@ -410,13 +417,14 @@ __device__ __forceinline__ void wload(WRegs<NS, SL>& R, const WTile<RS>& T, int 
     // compiler cannot hoist NS separate step addresses out of a chunk loop
     asm volatile("" : "+v"(d), "+v"(sc));
     if constexpr (SL) {
-        static_assert(RS == 0 && NS % 8 == 0, "LDS scales: group 32, 16-byte copies");
+        static_assert(RS == 0, "LDS scales: group 32");
+        constexpr int NW = window_steps<NS>();
         const int lane = lane_id(), kb = lane >> 4;
         const uint32_t row0 = T.sofs - 2u * (uint32_t)kb;  // the row's first scale
         const uint64_t base = uniform_u64(T.base);
 #pragma unroll
-        for (int i = 0; i < NS / 8; ++i)
-            lds_copy16(base, row0 + 2u * NS * (uint32_t)kb + 16u * (uint32_t)i, swin + 1024u * (uint32_t)i);
+        for (int i = 0; i < NW / 8; ++i)
+            lds_copy16(base, row0 + 2u * NW * (uint32_t)kb + 16u * (uint32_t)i, swin + 1024u * (uint32_t)i);
         R.sbase = swin + 16u * (uint32_t)(lane & 15) + 2u * (uint32_t)kb;
     }
 #pragma unroll
@@ -477,7 +485,7 @@ __device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&
             for (int m = 0; m < M; ++m) {
                 if constexpr (SL)
                     s[m] = f16_bits_to_f32(*reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
-                        (uintptr_t)(R[m].sbase + scale_step_off<NS>(j))));
+                        (uintptr_t)(R[m].sbase + scale_step_off<window_steps<NS>()>(j))));
                 else
                     s[m] = f16_bits_to_f32(R[m].s[j]);
                 if (j == rem - 1 && !R[m].lastok) s[m] = 0.0f;

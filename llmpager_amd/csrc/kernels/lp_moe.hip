@@ -1071,7 +1071,7 @@ __device__ __forceinline__ void gateup_group(const Frags& F, WRegs<NS, SL> (&GU)
 
 // Bytes of a wave's LDS scale window for one tile (WRegs SL).
 template <int NS>
-__host__ __device__ constexpr int scale_window_bytes() { return 64 * 2 * NS; }
+__host__ __device__ constexpr int scale_window_bytes() { return 64 * 2 * window_steps<NS>(); }
 
 template <int NS, bool ONE, int RS, bool SL>
 __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
@@ -1122,6 +1122,209 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
         __syncthreads();
         gateup_group<kMaxPairs, NS, ONE, RS, SL>(F, GU, TG, TU, I, n0, S, tb, nt, x.p0, reload, act);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Balanced gate/up for decode batches (lp_moe_gateup_bal).  One workgroup of
+// kBalMinWaves waves per CU.  Work is cut into units of 8 rows of gate plus the
+// same 8 rows of up over the whole of K (one MFMA tile: lanes n < 8 carry gate
+// row r0 + n, lanes n >= 8 up row r0 + n - 8), for each "virtual expert" =
+// (routed expert, group of up to 4 of its tokens).  Virtual experts are
+// numbered by a prefix sum over the expert table and every workgroup takes
+// an equal contiguous range of the V * R units (R = ceil(I / 8)); with V no
+// larger than the grid a range touches at most two virtual experts, whose
+// token images are staged once, into pair slots 0-1 and 2-3.  Each wave then
+// walks its units (every W-th of the range, W waves) with the next unit's
+// weights in flight while the current one is multiplied: two register
+// buffers, loads unconditional (a past-the-end unit reads a zero-size
+// buffer) and every store issued (a dropped one past the end of act), so
+// that the compiler's wait before each unit counts only the other buffer's
+// loads.  No barrier after the start.
+// ---------------------------------------------------------------------------
+
+// The merged gate/up tile of rows [r0, r0 + 8) of an expert blob; `valid`
+// false gives a tile whose nibble loads read zeros and whose scale-window
+// copies (SL) read the first bytes at `dummy`.
+template <int RS>
+__device__ __forceinline__ WTile<RS> wtile_gu(uint64_t blob, bool valid, uint64_t dummy, uint32_t goff,
+                                              uint32_t uoff, int rows, int cols, int r0) {
+    const int lane = lane_id();
+    const int n = lane & 15, kb = lane >> 4;
+    const uint32_t ng = (uint32_t)cols >> 5, gpr = ng >> RS;
+    const uint32_t sbytes = (uint32_t)rows * gpr * 2;
+    const uint32_t rbytes = sbytes + (uint32_t)rows * ng * 16;
+    const uint32_t row = (uint32_t)min(r0 + (n & 7), rows - 1);
+    const uint32_t off = n < 8 ? goff : uoff;
+    // blob, valid and the record count are uniform over the wave; saying so
+    // keeps the resource in SGPRs (no per-lane loop around each load)
+    const uint64_t base = uniform_u64(valid ? blob : dummy);
+    const int nrec = __builtin_amdgcn_readfirstlane(valid ? (int)(max(goff, uoff) + rbytes) : 0);
+    WTile<RS> T;
+    T.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, nrec, kBufferWord3);
+    T.base = base;
+    T.dofs = off + sbytes + (row * ng + kb) * 16;
+    T.sofs = valid ? off + (row * gpr + (kb >> RS)) * 2 : 2u * (uint32_t)(kb >> RS);
+    T.lastok = (ng & 3) == 0 || kb < (int)(ng & 3);
+    return T;
+}
+
+template <int NS, int RS, bool SL>
+__device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LayerView& L = a.L;
+    const int H = L.hidden, I = L.inter, k = L.top_k;
+    const int tid = (int)threadIdx.x, lane = lane_id(), wave = tid >> 6, W = (int)(blockDim.x >> 6);
+    const int maxu = a.maxu;
+    const int R = (I + 7) >> 3;
+    const Frags F = frags_at(lds, H);
+    int* tot = reinterpret_cast<int*>(lds + bal_meta_off(H));  // [kBalMaxWaves] wave totals
+    int* sl = tot + kBalMaxWaves;                                // [2][2]: expert, token group
+    ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(H) + 128);
+    zero_block(F, tid, blockDim.x);
+    if (tid < 4) sl[tid] = 0;
+    // virtual experts: ceil(ntok / 4) per entry, numbered by a prefix sum
+    int ng = 0;
+    if (tid < maxu) {
+        const ExpertEntry x = entry_of(a, tid);
+        ent[tid] = x;
+        ng = (x.ntok + 3) >> 2;
+    }
+    int inc = ng;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) tot[wave] = inc;
+    __syncthreads();
+    int before = 0, V = 0;
+    for (int w = 0; w < W; ++w) {
+        const int t = tot[w];
+        before += w < wave ? t : 0;
+        V += t;
+    }
+    const int pre = before + inc - ng;  // this entry's first virtual expert
+    const long N = (long)V * R;
+    const int lo = (int)(N * blockIdx.x / gridDim.x), hi = (int)(N * (blockIdx.x + 1) / gridDim.x);
+    if (lo >= hi) return;  // whole workgroup
+    const int v0 = lo / R, v1 = (hi - 1) / R;  // v1 <= v0 + 1
+    if (tid < maxu) {
+        if (pre <= v0 && v0 < pre + ng) {
+            sl[0] = tid;
+            sl[1] = v0 - pre;
+        }
+        if (v1 != v0 && pre <= v1 && v1 < pre + ng) {
+            sl[2] = tid;
+            sl[3] = v1 - pre;
+        }
+    }
+    __syncthreads();
+    // the two slots' blob, first dispatch position and token count (slot 1
+    // repeats slot 0 when the range has one virtual expert)
+    uint64_t sblob[2];
+    int sp0[2], snt[2];
+    const LP_GLOBAL int* perm = gptr<int>(a.W.perm);
+    const uint64_t xf = a.W.xf, ib = (uint64_t)image_bytes(H);
+    const int nslot = v1 != v0 ? 2 : 1;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int q = s < nslot ? s : 0;
+        const ExpertEntry x = ent[sl[2 * q]];
+        const int tg = sl[2 * q + 1];
+        sblob[s] = x.blob;
+        sp0[s] = x.p0 + 4 * tg;
+        snt[s] = min(4, x.ntok - 4 * tg);
+        if (s < nslot) {
+            Frags Fs = F;
+            Fs.lds = F.lds + 2 * s * frag_pair_bytes(F.ngp);
+            issue_images(Fs, snt[s], [&](int t) {
+                const int i = 4 * tg + t;
+                const int tok = i < kEntryToks ? entry_tok(x, i) : perm[x.p0 + i] / k;
+                return xf + (uint64_t)tok * ib;
+            });
+        }
+    }
+    // this wave's units: lo + wave + W * j < hi
+    const int J = hi - lo > wave ? (hi - lo - wave + W - 1) / W : 0;
+    const int Sx = tile_steps(H);
+    const uint64_t dummy = L.router_w;
+    const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(H) +
+                          (uint32_t)(2 * wave * scale_window_bytes<NS>());
+    LP_GLOBAL float* act = gptr_w<float>(a.W.act);
+    auto unit_of = [&](int j, int& s, int& r0) {
+        const int un = lo + wave + W * j;
+        const int v = un / R;
+        s = v - v0;
+        r0 = 8 * (un - v * R);
+    };
+    auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
+        int s, r0;
+        unit_of(j, s, r0);
+        const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
+        const bool valid = j < J && blob != 0;
+        const WTile<RS> T = wtile_gu<RS>(blob, valid, dummy, (uint32_t)L.gate_off, (uint32_t)L.up_off, I, H, r0);
+        wload(B, T, 0, win);
+    };
+    // act through a raw buffer: a lane with nothing to store writes at its end,
+    // which the hardware drops, so every unit issues the same memory operations
+    // (branch-free stores keep the compiler's count of outstanding loads exact:
+    // it then waits for one buffer's loads only, not for the other's)
+    const uint32_t act_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)I * 4u;
+    const __amdgpu_buffer_rsrc_t act_rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.act), (short)0, (int)act_bytes, kBufferWord3);
+    bool missing = false;
+    auto compute = [&](const WRegs<NS, SL>& B, int j) {
+        int s, r0;
+        unit_of(j, s, r0);
+        const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
+        const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
+        const int np = (qnt + 1) >> 1;
+        const int row = r0 + (lane & 15);
+        const bool out = lane < 32 && (lane & 15) < 8 && row < I;
+        missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
+        WRegs<NS, SL> Rm[1] = {B};
+        if constexpr (SL) {
+            // read the scale window only once B's first nibble load has landed,
+            // and with it the window copies issued before that load
+            uint32_t z;
+            asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B.w[0].x));
+            Rm[0].sbase += z;
+        }
+        float acc[1][kMaxPairs][2];
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
+        ABase Bs[kMaxPairs];
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) Bs[p] = abase(F, 2 * s + p, 0);
+        wmma(Rm, Bs, Sx, np, acc);
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) {
+            const float g0 = tile_reduce(acc[0][p][0]), g1 = tile_reduce(acc[0][p][1]);
+            // up of row n sits in lane n + 8 of the same 16
+            const float u0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(g0), 0x128, 0xf, 0xf, false));
+            const float u1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(g1), 0x128, 0xf, 0xf, false));
+            const int t = 2 * p + (lane >> 4);
+            const float g = lane < 16 ? g0 : g1;
+            const float u = lane < 16 ? u0 : u1;
+            const float v = qblob == 0 ? 0.0f : g / (1.0f + expf(-g)) * u;
+            const bool st = out && p < np && t < qnt;
+            const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)I + (uint32_t)row) * 4u : act_bytes;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), act_rs, (int)off, 0, 0);
+        }
+    };
+    WRegs<NS, SL> RA, RB;
+    load(RA, 0, swin);
+    __builtin_amdgcn_s_waitcnt(0);  // images, seeds and the first unit have landed
+    __syncthreads();
+    for (int j = 0; j < J; j += 2) {
+        load(RB, j + 1, swin + scale_window_bytes<NS>());
+        compute(RA, j);
+        if (j + 1 >= J) break;
+        load(RA, j + 2, swin);
+        compute(RB, j + 1);
+    }
+    if (missing && lane == 0) atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);
+    __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) unit's loads
 }
 
 // down MFMAs for one staged token group of P pairs over TW row tiles, into
@@ -1249,12 +1452,40 @@ lp_moe_gateup(const GroupedArgs a) {
     }
 }
 
+// Balanced gate/up (decode batches, the host checks the bounds it assumes:
+// tile_steps(hidden) <= 16, at most kBalMaxU entries, no more virtual
+// experts than workgroups, kBalMinWaves .. kBalMaxWaves waves).
+extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup_bal(const GroupedArgs a) {
+    if (tile_steps(a.L.hidden) > 8) {
+        if (scales_in_lds(a.L.group, a.L.hidden)) {
+            gateup_bal_body<16, 0, true>(a);
+        } else {
+#define LP_GATEUP(rs) gateup_bal_body<16, rs, false>(a)
+            LP_BY_RS(a.L.group, LP_GATEUP)
+#undef LP_GATEUP
+        }
+    } else {
+        if (scales_in_lds(a.L.group, a.L.hidden)) {
+            gateup_bal_body<8, 0, true>(a);
+        } else {
+#define LP_GATEUP(rs) gateup_bal_body<8, rs, false>(a)
+            LP_BY_RS(a.L.group, LP_GATEUP)
+#undef LP_GATEUP
+        }
+    }
+}
+
 // Down, two row tiles per wave: tiles of at most kDownChunk steps (the host
 // picks this kernel only for those), loaded in one piece.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down(const GroupedArgs a) {
     if (scales_in_lds(a.L.group, a.L.inter)) {
-        down_body<2, kDownChunk, true, 0, true>(a);
+        // a 6-step tile (inter 768) loads only its own 6 steps
+        if (tile_steps(a.L.inter) == 6)
+            down_body<2, 6, true, 0, true>(a);
+        else
+            down_body<2, kDownChunk, true, 0, true>(a);
     } else {
 #define LP_DOWN(rs) down_body<2, kDownChunk, true, rs, false>(a)
         LP_BY_RS(a.L.group, LP_DOWN)
@@ -1266,9 +1497,18 @@ lp_moe_down(const GroupedArgs a) {
 // longer tiles streamed kDownLoopChunk steps at a time.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down_wide(const GroupedArgs a) {
-    if (tile_steps(a.L.inter) <= kDownWideChunk) {
+    const int S = tile_steps(a.L.inter);
+    if (S <= kDownWideChunk) {
+        // tiles of 9..12 steps (inter 1152..1536) load 12 steps, not 16
         if (scales_in_lds(a.L.group, a.L.inter)) {
-            down_body<1, kDownWideChunk, true, 0, true>(a);
+            if (S <= 12)
+                down_body<1, 12, true, 0, true>(a);
+            else
+                down_body<1, kDownWideChunk, true, 0, true>(a);
+        } else if (S <= 12) {
+#define LP_DOWN(rs) down_body<1, 12, true, rs, false>(a)
+            LP_BY_RS(a.L.group, LP_DOWN)
+#undef LP_DOWN
         } else {
 #define LP_DOWN(rs) down_body<1, kDownWideChunk, true, rs, false>(a)
             LP_BY_RS(a.L.group, LP_DOWN)

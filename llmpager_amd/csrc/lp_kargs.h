@@ -176,7 +176,22 @@ struct GroupedArgs {
     uint64_t h;          // f32 [T, H] residual (combine)
     int32_t T;
     int32_t pairs_cap;   // token pairs the dynamic LDS holds at once
+    int32_t maxu;        // expert-table entries (balanced kernels)
+    int32_t pad0;
 };
+
+// Balanced decode gate/up (lp_moe_gateup_bal): one workgroup per CU of
+// kBalMinWaves .. kBalMaxWaves waves.  LDS: the zero block and two slots of
+// two token pairs (frag_lds_bytes(H, 4)), 128 bytes of counters, the expert
+// table (kBalMaxU entries), then two scale windows per wave.
+constexpr int kBalMinWaves = 8;
+constexpr int kBalMaxWaves = 16;
+constexpr int kBalMaxU = 64 * kBalMinWaves;
+LPK_HD constexpr int bal_meta_off(int hidden) { return (frag_lds_bytes(hidden, 4) + 15) & ~15; }
+LPK_HD constexpr int bal_win_off(int hidden) { return bal_meta_off(hidden) + 128 + kBalMaxU * 32; }
+LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
+    return bal_win_off(hidden) + waves * 2 * 64 * 2 * window_steps;
+}
 
 // Prefill grouped GEMM (lp_gemm.hip).
 constexpr int kGemmBM = 128;           // tokens per tile

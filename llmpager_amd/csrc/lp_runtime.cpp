@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -76,6 +77,7 @@ enum Fn {
     kGemmRouter,
     kDispatch,
     kRouteFused,
+    kGateupBal,
     kNumFns
 };
 
@@ -99,6 +101,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
+    {"lp_moe.hsaco", "lp_moe_gateup_bal"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
@@ -147,6 +150,10 @@ struct lp_ctx {
     // launches on different streams do not share counters
     int32_t* sync = nullptr;
     std::atomic<unsigned> sync_next{0};
+    // decode gate/up through lp_moe_gateup_bal (LLMPAGER_HIP_GATEUP_BAL=0 at
+    // lp_init turns it off, for comparison)
+    bool gateup_bal = true;
+    int bal_waves = kBalMinWaves;  // its workgroup size (LLMPAGER_HIP_BAL_WAVES)
 };
 
 namespace {
@@ -232,6 +239,9 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     }
     c->cus = prop.multiProcessorCount;
     c->max_lds = prop.sharedMemPerBlock;
+    if (const char* e = std::getenv("LLMPAGER_HIP_GATEUP_BAL")) c->gateup_bal = std::atoi(e) != 0;
+    if (const char* e = std::getenv("LLMPAGER_HIP_BAL_WAVES"))
+        c->bal_waves = std::min(kBalMaxWaves, std::max(kBalMinWaves, std::atoi(e)));
     const std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
     for (int m = 0; m < kNumModules; ++m) {
         const std::string path = dir + "/" + kModules[m];
@@ -250,6 +260,16 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
             return fail(LP_E_LOAD, std::string("hipModuleGetFunction(") + kSpecs[f].name +
                                        "): " + hipGetErrorString(e));
         }
+    }
+    {
+        // a workgroup size the loaded code object accepts (its launch bound)
+        int mt = 0;
+        if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[kGateupBal]) ==
+                hipSuccess &&
+            mt >= 64 * kBalMinWaves)
+            c->bal_waves = std::min(c->bal_waves, mt / 64);
+        else
+            c->bal_waves = kBalMinWaves;
     }
     e = hipMalloc(reinterpret_cast<void**>(&c->sync), (size_t)kSyncSlots * kSyncWords * 4);
     if (e == hipSuccess) e = hipMemset(c->sync, 0, (size_t)kSyncSlots * kSyncWords * 4);
@@ -700,10 +720,24 @@ int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, 
 
 static int tile_steps_host(int cols) { return ((cols >> 5) + 3) >> 2; }
 
+// Whether lp_moe_gateup_bal takes the gate/up of ga's routed experts: one
+// chunk of K, an expert table it can hold, no more virtual experts (groups
+// of up to 4 tokens of one expert) than CUs, and its LDS.
+static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
+    const int H = ga.L.hidden, pairs = ga.T * ga.L.top_k;
+    const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
+    const int nw = tile_steps_host(H) > 8 ? 16 : 8;
+    return tile_steps_host(H) <= kGateupChunk && maxu <= kBalMaxU && maxv <= c->cus &&
+           (size_t)bal_lds_bytes(H, nw, c->bal_waves) <= c->max_lds && ga.L.slot_span < (1ull << 31);
+}
+
 // Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
 // (maxu entries): workgroup width chosen so that there are about two work
 // items per CU, down with two tiles per wave when the inner size allows.
-static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga, int maxu, lp_stream s) {
+// `routed`: the routed experts (the balanced gate/up may take them).
+static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s) {
+    GroupedArgs ga = ga0;
+    ga.maxu = maxu;
     const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
     auto pick_w = [&](int rows, int tw) {
         for (int w = 4; w > 1; w >>= 1)
@@ -711,7 +745,12 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga, int maxu, lp_stream s) 
                 return w;
         return 1;
     };
-    {
+    if (routed && c->gateup_bal && gateup_balanced(c, ga, maxu)) {
+        const int nw = tile_steps_host(H) > 8 ? 16 : 8;
+        if (int r = launch(c, kGateupBal, dim3((unsigned)c->cus), dim3(64 * c->bal_waves),
+                           (size_t)bal_lds_bytes(H, nw, c->bal_waves), s, ga))
+            return r;
+    } else {
         const int w = pick_w(I, 1);
         const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
         const int win = tile_steps_host(H) <= kGateupChunk && scales_in_lds(ga.L.group, H)
@@ -791,7 +830,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gm.nblocks = (d->hidden + kGemmBN - 1) / kGemmBN;
         if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
             return r;
-    } else if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), s)) {
+    } else if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s)) {
         return r;
     }
     if (d->shared_blob) {
@@ -808,7 +847,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gs.W.perm = ga.W.sh_perm;
         gs.W.act = ga.W.sh_act;
         gs.W.y = ga.W.sh_y;
-        if (int r = grouped_ffn(c, gs, 1, s)) return r;
+        if (int r = grouped_ffn(c, gs, 1, false, s)) return r;
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 1023) / 1024), (unsigned)T), dim3(256), 0,
                   s, ga);
