@@ -40,7 +40,7 @@ ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 # The grouped gate/up launch of a layer is the dominant kernel.
 GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal")
-DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide")
+DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide", "lp_moe_down_bal", "lp_moe_down_bal6")
 CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
 # HBM bytes per dominant-kernel launch at B = 32 (FETCH_SIZE + WRITE_SIZE,
 # each scaled by the factor the same counter reads for the calibration copy),

@@ -1168,21 +1168,26 @@ __device__ __forceinline__ WTile<RS> wtile_gu(uint64_t blob, bool valid, uint64_
     return T;
 }
 
-template <int NS, int RS, bool SL>
-__device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const LayerView& L = a.L;
-    const int H = L.hidden, I = L.inter, k = L.top_k;
+// The workgroup's share of a balanced launch: the entries' virtual experts
+// (ceil(ntok / 4) each) numbered by a prefix sum over the expert table,
+// then the workgroup's contiguous range [lo, hi) of the V * R units and the
+// (at most two) virtual experts it touches.  Returns false for an empty
+// range (the whole workgroup).  The LDS meta area follows the fragments of
+// `cols`-wide rows (bal_meta_off).
+struct BalPlan {
+    int lo, hi, v0, nslot;
+    ExpertEntry x[2];  // slot 1 repeats slot 0 when the range has one virtual expert
+    int tg[2];         // token group of the slot's expert (tokens 4 tg .. 4 tg + 3)
+    int nt[2];         // tokens in the slot (1..4)
+};
+
+__device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, BalPlan& P) {
     const int tid = (int)threadIdx.x, lane = lane_id(), wave = tid >> 6, W = (int)(blockDim.x >> 6);
     const int maxu = a.maxu;
-    const int R = (I + 7) >> 3;
-    const Frags F = frags_at(lds, H);
-    int* tot = reinterpret_cast<int*>(lds + bal_meta_off(H));  // [kBalMaxWaves] wave totals
-    int* sl = tot + kBalMaxWaves;                                // [2][2]: expert, token group
-    ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(H) + 128);
-    zero_block(F, tid, blockDim.x);
+    int* tot = reinterpret_cast<int*>(lds + bal_meta_off(cols));  // [kBalMaxWaves] wave totals
+    int* sl = tot + kBalMaxWaves;                                   // [2][2]: expert, token group
+    ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(cols) + 128);
     if (tid < 4) sl[tid] = 0;
-    // virtual experts: ceil(ntok / 4) per entry, numbered by a prefix sum
     int ng = 0;
     if (tid < maxu) {
         const ExpertEntry x = entry_of(a, tid);
@@ -1205,9 +1210,10 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     }
     const int pre = before + inc - ng;  // this entry's first virtual expert
     const long N = (long)V * R;
-    const int lo = (int)(N * blockIdx.x / gridDim.x), hi = (int)(N * (blockIdx.x + 1) / gridDim.x);
-    if (lo >= hi) return;  // whole workgroup
-    const int v0 = lo / R, v1 = (hi - 1) / R;  // v1 <= v0 + 1
+    P.lo = (int)(N * blockIdx.x / gridDim.x);
+    P.hi = (int)(N * (blockIdx.x + 1) / gridDim.x);
+    if (P.lo >= P.hi) return false;
+    const int v0 = P.lo / R, v1 = (P.hi - 1) / R;  // v1 <= v0 + 1
     if (tid < maxu) {
         if (pre <= v0 && v0 < pre + ng) {
             sl[0] = tid;
@@ -1219,22 +1225,43 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         }
     }
     __syncthreads();
-    // the two slots' blob, first dispatch position and token count (slot 1
-    // repeats slot 0 when the range has one virtual expert)
+    P.v0 = v0;
+    P.nslot = v1 != v0 ? 2 : 1;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int q = s < P.nslot ? s : 0;
+        P.x[s] = ent[sl[2 * q]];
+        P.tg[s] = sl[2 * q + 1];
+        P.nt[s] = min(4, P.x[s].ntok - 4 * P.tg[s]);
+    }
+    return true;
+}
+
+template <int NS, int RS, bool SL>
+__device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LayerView& L = a.L;
+    const int H = L.hidden, I = L.inter, k = L.top_k;
+    const int lane = lane_id(), wave = (int)threadIdx.x >> 6, W = (int)(blockDim.x >> 6);
+    const int R = (I + 7) >> 3;
+    const Frags F = frags_at(lds, H);
+    zero_block(F, threadIdx.x, blockDim.x);
+    BalPlan P;
+    if (!bal_plan(a, lds, H, R, P)) return;
+    const int lo = P.lo, hi = P.hi, v0 = P.v0;
+    // the two slots' blob, first dispatch position and token count
     uint64_t sblob[2];
     int sp0[2], snt[2];
     const LP_GLOBAL int* perm = gptr<int>(a.W.perm);
     const uint64_t xf = a.W.xf, ib = (uint64_t)image_bytes(H);
-    const int nslot = v1 != v0 ? 2 : 1;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-        const int q = s < nslot ? s : 0;
-        const ExpertEntry x = ent[sl[2 * q]];
-        const int tg = sl[2 * q + 1];
+        const ExpertEntry x = P.x[s];
+        const int tg = P.tg[s];
         sblob[s] = x.blob;
         sp0[s] = x.p0 + 4 * tg;
-        snt[s] = min(4, x.ntok - 4 * tg);
-        if (s < nslot) {
+        snt[s] = P.nt[s];
+        if (s < P.nslot) {
             Frags Fs = F;
             Fs.lds = F.lds + 2 * s * frag_pair_bytes(F.ngp);
             issue_images(Fs, snt[s], [&](int t) {
@@ -1316,6 +1343,131 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     load(RA, 0, swin);
     __builtin_amdgcn_s_waitcnt(0);  // images, seeds and the first unit have landed
     __syncthreads();
+    for (int j = 0; j < J; j += 2) {
+        load(RB, j + 1, swin + scale_window_bytes<NS>());
+        compute(RA, j);
+        if (j + 1 >= J) break;
+        load(RA, j + 2, swin);
+        compute(RB, j + 1);
+    }
+    if (missing && lane == 0) atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);
+    __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) unit's loads
+}
+
+// Balanced down for decode batches (lp_moe_down_bal): the plan of the
+// balanced gate/up over units of 16 rows of down (all of K = inter), the
+// slots' act rows staged as fragments, two register buffers in turn and
+// branch-free stores into y (a dropped one past its end).
+template <int RS>
+__device__ __forceinline__ WTile<RS> wtile_dn(uint64_t blob, bool valid, uint64_t dummy, uint32_t off, int rows,
+                                              int cols, int r0) {
+    const int lane = lane_id();
+    const int n = lane & 15, kb = lane >> 4;
+    const uint32_t ng = (uint32_t)cols >> 5, gpr = ng >> RS;
+    const uint32_t sbytes = (uint32_t)rows * gpr * 2;
+    const uint32_t rbytes = sbytes + (uint32_t)rows * ng * 16;
+    const uint32_t row = (uint32_t)min(r0 + n, rows - 1);
+    // blob, valid and the record count are uniform over the wave
+    const uint64_t base = uniform_u64(valid ? blob + off : dummy);
+    const int nrec = __builtin_amdgcn_readfirstlane(valid ? (int)rbytes : 0);
+    WTile<RS> T;
+    T.rsrc = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(base), (short)0, nrec, kBufferWord3);
+    T.base = base;
+    T.dofs = sbytes + (row * ng + kb) * 16;
+    T.sofs = valid ? (row * gpr + (kb >> RS)) * 2 : 2u * (uint32_t)(kb >> RS);
+    T.lastok = (ng & 3) == 0 || kb < (int)(ng & 3);
+    return T;
+}
+
+template <int NS, int RS, bool SL>
+__device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LayerView& L = a.L;
+    const int H = L.hidden, I = L.inter, k = L.top_k;
+    const int lane = lane_id(), wave = (int)threadIdx.x >> 6, W = (int)(blockDim.x >> 6);
+    const int R = (H + 15) >> 4;
+    const Frags F = frags_at(lds, I);
+    zero_block(F, threadIdx.x, blockDim.x);
+    BalPlan P;
+    if (!bal_plan(a, lds, I, R, P)) return;
+    const int lo = P.lo, hi = P.hi, v0 = P.v0;
+    uint64_t sblob[2];
+    int sp0[2], snt[2];
+    const float* actp = dptr<const float>(a.W.act);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        sblob[s] = P.x[s].blob;
+        sp0[s] = P.x[s].p0 + 4 * P.tg[s];
+        snt[s] = P.nt[s];
+        if (s < P.nslot) {
+            Frags Fs = F;
+            Fs.lds = F.lds + 2 * s * frag_pair_bytes(F.ngp);
+            const int p0 = sp0[s];
+            stage_rows(Fs, snt[s], [&](int t) { return actp + (size_t)(p0 + t) * I; }, threadIdx.x, blockDim.x);
+        }
+    }
+    // this wave's units: lo + wave + W * j < hi
+    const int J = hi - lo > wave ? (hi - lo - wave + W - 1) / W : 0;
+    const int Sx = tile_steps(I);
+    const uint64_t dummy = L.router_w;
+    const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(I) +
+                          (uint32_t)(2 * wave * scale_window_bytes<NS>());
+    auto unit_of = [&](int j, int& s, int& r0) {
+        const int un = lo + wave + W * j;
+        const int v = un / R;
+        s = v - v0;
+        r0 = 16 * (un - v * R);
+    };
+    auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
+        int s, r0;
+        unit_of(j, s, r0);
+        const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
+        const bool valid = j < J && blob != 0;
+        const WTile<RS> T = wtile_dn<RS>(blob, valid, dummy, (uint32_t)L.down_off, H, I, r0);
+        wload(B, T, 0, win);
+    };
+    const uint32_t y_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)H * 4u;
+    const __amdgpu_buffer_rsrc_t y_rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.y), (short)0, (int)y_bytes, kBufferWord3);
+    bool missing = false;
+    auto compute = [&](const WRegs<NS, SL>& B, int j) {
+        int s, r0;
+        unit_of(j, s, r0);
+        const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
+        const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
+        const int np = (qnt + 1) >> 1;
+        const int row = r0 + (lane & 15);
+        const bool out = lane < 32 && row < H;
+        missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
+        WRegs<NS, SL> Rm[1] = {B};
+        if constexpr (SL) {
+            // read the scale window only once B's first nibble load has landed,
+            // and with it the window copies issued before that load
+            uint32_t z;
+            asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B.w[0].x));
+            Rm[0].sbase += z;
+        }
+        float acc[1][kMaxPairs][2];
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
+        ABase Bs[kMaxPairs];
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) Bs[p] = abase(F, 2 * s + p, 0);
+        wmma(Rm, Bs, Sx, np, acc);
+#pragma unroll
+        for (int p = 0; p < kMaxPairs; ++p) {
+            const float y0 = tile_reduce(acc[0][p][0]), y1 = tile_reduce(acc[0][p][1]);
+            const int t = 2 * p + (lane >> 4);
+            const float v = qblob == 0 ? 0.0f : lane < 16 ? y0 : y1;
+            const bool st = out && p < np && t < qnt;
+            const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)H + (uint32_t)row) * 4u : y_bytes;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, (int)off, 0, 0);
+        }
+    };
+    WRegs<NS, SL> RA, RB;
+    load(RA, 0, swin);
+    __builtin_amdgcn_s_waitcnt(0);  // the first unit has landed
+    __syncthreads();                // and the staged act rows are in place
     for (int j = 0; j < J; j += 2) {
         load(RB, j + 1, swin + scale_window_bytes<NS>());
         compute(RA, j);
@@ -1474,6 +1626,19 @@ lp_moe_gateup_bal(const GroupedArgs a) {
 #undef LP_GATEUP
         }
     }
+}
+
+// Balanced down (decode batches; the host checks what lp_moe_gateup_bal
+// needs, with inter for hidden): units of 16 rows over all of K, tiles of 6
+// steps (inter 768) or of up to 8.
+extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_down_bal(const GroupedArgs a) {
+    down_bal_body<8, 0, true>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_down_bal6(const GroupedArgs a) {
+    down_bal_body<6, 0, true>(a);
 }
 
 // Down, two row tiles per wave: tiles of at most kDownChunk steps (the host

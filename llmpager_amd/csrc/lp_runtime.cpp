@@ -78,6 +78,8 @@ enum Fn {
     kDispatch,
     kRouteFused,
     kGateupBal,
+    kDownBal,
+    kDownBal6,
     kNumFns
 };
 
@@ -102,6 +104,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
     {"lp_moe.hsaco", "lp_moe_gateup_bal"},
+    {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
@@ -728,7 +731,21 @@ static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
     const int nw = tile_steps_host(H) > 8 ? 16 : 8;
     return tile_steps_host(H) <= kGateupChunk && maxu <= kBalMaxU && maxv <= c->cus &&
-           (size_t)bal_lds_bytes(H, nw, c->bal_waves) <= c->max_lds && ga.L.slot_span < (1ull << 31);
+           (size_t)bal_lds_bytes(H, nw, c->bal_waves) <= c->max_lds && ga.L.slot_span < (1ull << 31) &&
+           (uint64_t)pairs * ga.L.inter * 4 < (1ull << 31);
+}
+
+// Whether lp_moe_down_bal(6) takes the down projection of ga's routed
+// experts: at most 8 steps of K with scales in LDS windows, and what
+// gateup_balanced asks of the table and the grid.  Below 32 (token, pick)
+// pairs the one-shot kernel is faster: too few units to share.
+static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
+    const int I = ga.L.inter, pairs = ga.T * ga.L.top_k;
+    const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
+    return pairs >= 32 && tile_steps_host(I) <= 8 && scales_in_lds(ga.L.group, I) && maxu <= kBalMaxU &&
+           maxv <= c->cus &&
+           (size_t)bal_lds_bytes(I, 8, kBalMinWaves) <= c->max_lds &&
+           (uint64_t)pairs * ga.L.hidden * 4 < (1ull << 31);
 }
 
 // Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
@@ -760,6 +777,10 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
             return r;
     }
     const int steps = tile_steps_host(I);
+    if (routed && c->gateup_bal && down_balanced(c, ga, maxu)) {
+        return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalMinWaves),
+                      (size_t)bal_lds_bytes(I, 8, kBalMinWaves), s, ga);
+    }
     const Fn f = steps <= kDownChunk ? kDown : kDownWide;
     const int tw = steps <= kDownChunk ? 2 : 1;
     const int w = pick_w(H, tw);

@@ -156,6 +156,37 @@ def test_layer_missing_expert_full_shape(cuda):
     L.free()
 
 
+def _zero_expert_blob(L: DeviceLayer, blob: np.ndarray) -> np.ndarray:
+    # every nibble 8 (q - 8 = 0): the expert's output is exactly zero, which
+    # is what the layer gives for an expert without a slot
+    z = blob.copy()
+    go, uo, do = lp.blob_offsets(L.H, L.I, L.group)
+    for off, rows, cols in ((go, L.I, L.H), (uo, L.I, L.H), (do, L.H, L.I)):
+        sb = rows * (cols // L.group) * 2
+        z[off + sb: off + sb + rows * cols // 2] = 0x88
+    return z
+
+
+@pytest.mark.parametrize("T", [4, 32])
+def test_layer_missing_expert_matches_zero_expert(cuda, T):
+    # Experts without a slot contribute zero (flag raised); the rest of the
+    # layer, at decode batch sizes through both the one-shot and the balanced
+    # grouped kernels, matches the oracle with those experts zeroed.
+    slots = np.arange(128, dtype=np.int32)
+    slots[::3] = -1
+    L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=2, slots=slots)
+    x, h, g = _run_layer(cuda, L, T, seed=2)
+    assert g["status"][1] == 1
+    present = next(b for b in L.oracle_blobs() if b is not None)
+    zero = _zero_expert_blob(L, present)
+    blobs = [b if b is not None else zero for b in L.oracle_blobs()]
+    want_h, _, want_ids, _, want_cnt = O.moe_layer(L.oracle_desc(), blobs, x, h, threads=8)
+    assert np.array_equal(g["cnt"], want_cnt)
+    assert any(slots[e] < 0 for e in want_ids[0, :want_cnt[0]]) or T > 4
+    assert rel_l2(g["h"] - h, want_h - h) <= 1e-3
+    L.free()
+
+
 def _route_logits(cuda, L: DeviceLayer, logits: np.ndarray):
     T = logits.shape[0]
     lay = lp.ws_layout(L.desc, T)
