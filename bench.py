@@ -46,7 +46,7 @@ CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-co
 # each scaled by the factor the same counter reads for the calibration copy),
 # from the rocprofv3 --pmc runs recorded in profiles/ for that kernel.
 # Re-measure whenever the kernel changes.
-TRAFFIC_B32 = {"lp_moe_gateup": 181_856_889}
+TRAFFIC_B32 = {"lp_moe_gateup": 181_856_889, "lp_moe_gateup_bal": 209_553_912}
 KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
            "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
            "lp_moe_combine")
