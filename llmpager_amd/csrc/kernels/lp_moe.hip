@@ -703,6 +703,102 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     }
 }
 
+// dispatch_all's tables for at most kDispatchWaveMaxPicks picks (at most
+// 64), by one wave and no barrier:
+// lane p holds pick p = t k + j (valid when j < cnt[t]); its position in the
+// expert-major order is the number of valid picks with a smaller expert id
+// plus those with the same id and a smaller pick index (stable by token, as
+// dispatch_all), found by one pass over the picks with lane reads.  The
+// expert table, gs, uniq, inv and perm are then written from registers.
+__device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids_in, const int* cnt_in,
+                                              const int* slots_in) {
+    const int lane = lane_id();
+    const int E = a.L.experts, k = a.L.top_k, T = a.T;
+    const int P = T * k;  // <= 64
+    const int t = lane / k, j = lane - t * k;
+    const bool inb = lane < P;
+    const int c = inb ? cnt_in[t] : 0;
+    const bool valid = inb && j < c;
+    const int e = valid ? ids_in[lane] : 0x7fffffff;
+    int less = 0, before = 0, same = 0;  // valid picks: smaller id; same id and earlier; same id
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        less += eq < e;
+        before += eq == e && q < lane;
+        same += eq == e;
+    }
+    const bool first = valid && before == 0;  // the expert's first pick
+    const uint64_t firsts = __ballot(first);
+    const int U = __popcll(firsts);
+    // the expert's index in the unique list, and (first lanes) its first
+    // four tokens from the picks of rank 0..3
+    int uidx = 0;
+    int tok[kEntryToks] = {-1, -1, -1, -1};
+    for (int q = 0; q < P; ++q) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        const bool fq = (firsts >> q) & 1ull;
+        uidx += fq && eq < e;
+        if (eq == e) {
+            const int rq = __builtin_amdgcn_readlane(before, q);
+            const int tq = q / k;
+#pragma unroll
+            for (int r = 0; r < kEntryToks; ++r)
+                if (rq == r) tok[r] = tq;
+        }
+    }
+    int* perm = dptr<int>(a.W.perm);
+    int* inv = dptr<int>(a.W.inv);
+    if (inb) inv[lane] = valid ? less + before : -1;
+    if (valid) perm[less + before] = lane;
+    // gs[x] = valid picks with an expert id below x, for x = 0 .. E
+    int* gs = dptr<int>(a.W.gs);
+    for (int x0 = 0; x0 <= E; x0 += 64) {
+        const int x = x0 + lane;
+        int below = 0;
+        for (int q = 0; q < P; ++q) below += __builtin_amdgcn_readlane(e, q) < x;
+        if (x <= E) gs[x] = below;
+    }
+    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    if (first) {
+        dptr<int>(a.W.uniq)[uidx] = e;
+        const int slot = slots_in[e];
+        ExpertEntry x;
+        x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
+        x.p0 = less;
+        x.ntok = same;
+#pragma unroll
+        for (int r = 0; r < kEntryToks; ++r) x.tok[r] = tok[r];
+        et[uidx] = x;
+    }
+    const int maxu = min(P, E);
+    if (lane >= U && lane < maxu) {
+        ExpertEntry x;
+        x.blob = 0ull;
+        x.p0 = 0;
+        x.ntok = 0;
+#pragma unroll
+        for (int r = 0; r < kEntryToks; ++r) x.tok[r] = -1;
+        et[lane] = x;
+    }
+    if (lane == 0) {
+        dptr<int>(a.W.meta)[0] = U;
+        dptr<int>(a.W.meta)[1] = 0;
+    }
+    // the shared MLP (if any) takes every token: one entry, identity token list
+    if (a.L.shared_blob) {
+        if (lane < T) dptr<int>(a.W.sh_perm)[lane] = lane;
+        if (lane == 0) {
+            ExpertEntry x;
+            x.blob = a.L.shared_blob;
+            x.p0 = 0;
+            x.ntok = T;
+#pragma unroll
+            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
+            *dptr<ExpertEntry>(a.W.sh_et) = x;
+        }
+    }
+}
+
 }  // namespace
 
 // Dispatch of a medium batch after the multi-workgroup top-k: dispatch_all
@@ -958,6 +1054,20 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     int* cnt = dptr<int>(a.sync);
     if (!last_arrival(cnt + b, gridDim.x, &flag)) return;
     if (wave < nt) topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts);
+    if (gridDim.y == 1) {
+        // one token block, ranked by this workgroup: no second arrival; up
+        // to 16 picks one wave builds the tables, more take the workgroup
+        __syncthreads();
+        if (a.T * a.L.top_k <= kDispatchWaveMaxPicks) {
+            if (wave == 0)
+                dispatch_wave(a, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
+                              dptr<const int>(a.L.slot_table));
+        } else {
+            dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
+                         dptr<const int>(a.L.slot_table));
+        }
+        return;
+    }
     if (!last_arrival(cnt + 8, gridDim.y, &flag)) return;
     dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table));
 }
