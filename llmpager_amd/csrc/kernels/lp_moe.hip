@@ -1014,18 +1014,22 @@ namespace {
 
 // Add one arrival at *cnt; true (in every thread) for the n-th, which also
 // resets the counter.  Every thread of the workgroup must call it.
-__device__ __forceinline__ bool last_arrival(int* cnt, int n, int* flag) {
+__device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0) {
-        const bool last = atomicAdd(cnt, 1) == n - 1;
-        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last ? 1 : 0;
+        const int o = atomicAdd(cnt, 1);
+        if (o == n - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = o;
     }
     __syncthreads();
-    const bool last = *flag != 0;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return last;
+    const int o = *flag;
+    if (o == n - 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return o;
+}
+
+__device__ __forceinline__ bool last_arrival(int* cnt, int n, int* flag) {
+    return arrival_order(cnt, n, flag) == n - 1;
 }
 
 }  // namespace
@@ -1039,20 +1043,29 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     const int b = blockIdx.y, t0 = b * kRouterTokBlock;
     const int nt = min(kRouterTokBlock, a.T - t0);
     router_block(a, xs, blockIdx.x * 8 * kRouteEPW, t0, nt);
-    // the images are for the expert kernels: after the logits, so that the
-    // ranking waits for no image, and from the rows still staged in LDS when
-    // the whole block fits there
-    if (a.make_xf) {
+    // The images are for the expert kernels only.  The workgroups that are
+    // not the last of their block to arrive write them, shared by arrival
+    // order, after arriving: the last one, which goes on to rank the block,
+    // writes none (unless it is alone), so no image store or release waits
+    // on the ranking's path.  From the rows still staged in LDS when the
+    // whole block fits there.
+    auto images = [&](int first, int step) {
+        if (!a.make_xf) return;
         const bool staged = nt * a.L.hidden * 4 <= kRouteXLds;
-        for (int t = blockIdx.x; t < nt; t += gridDim.x) {
+        for (int t = first; t < nt; t += step) {
             if (staged)
                 write_image_lds(a, t0 + t, xs + (size_t)t * a.L.hidden);
             else
                 write_image(a, t0 + t);
         }
-    }
+    };
     int* cnt = dptr<int>(a.sync);
-    if (!last_arrival(cnt + b, gridDim.x, &flag)) return;
+    const int order = arrival_order(cnt + b, gridDim.x, &flag);
+    if (order != (int)gridDim.x - 1) {
+        images(order, gridDim.x - 1);
+        return;
+    }
+    if (gridDim.x == 1) images(0, 1);
     if (wave < nt) topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts);
     if (gridDim.y == 1) {
         // one token block, ranked by this workgroup: no second arrival; up
