@@ -561,6 +561,27 @@ constexpr int kDispatchSmem = 4 * (kMaxExperts * 6 + (kMaxExperts + 4) + kMaxExp
 
 // ids / cnt: the picks (global, or LDS copies from the same workgroup);
 // slots: the slot table (global, or an LDS copy).
+// The shared MLP's table (if the layer has one): every token, identity
+// dispatch order, as shared_entries(T) entries of consecutive tokens (groups
+// of 4 for decode batches, so the grouped kernels take it without token
+// loops; one entry for larger batches).  Threads tid, tid + nth, ... of the
+// caller write it.
+__device__ __forceinline__ void write_shared_table(const RouteArgs& a, int tid, int nth) {
+    if (!a.L.shared_blob) return;
+    const int T = a.T, nv = shared_entries(T);
+    const int per = nv == 1 ? T : kEntryToks;
+    for (int t = tid; t < T; t += nth) dptr<int>(a.W.sh_perm)[t] = t;
+    for (int v = tid; v < nv; v += nth) {
+        ExpertEntry x;
+        x.blob = a.L.shared_blob;
+        x.p0 = v * per;
+        x.ntok = min(per, T - v * per);
+#pragma unroll
+        for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < x.ntok ? x.p0 + q : -1;
+        dptr<ExpertEntry>(a.W.sh_et)[v] = x;
+    }
+}
+
 __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids_in,
                                              const int* cnt_in, const int* slots_in) {
     int* cnt_e = reinterpret_cast<int*>(sm);
@@ -666,19 +687,7 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
         for (int e = tid; e < E; e += nth) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
         __syncthreads();
     }
-    // the shared MLP (if any) takes every token: one entry, identity token list
-    if (a.L.shared_blob) {
-        for (int t = tid; t < T; t += nth) dptr<int>(a.W.sh_perm)[t] = t;
-        if (tid == 0) {
-            ExpertEntry x;
-            x.blob = a.L.shared_blob;
-            x.p0 = 0;
-            x.ntok = T;
-#pragma unroll
-            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
-            *dptr<ExpertEntry>(a.W.sh_et) = x;
-        }
-    }
+    write_shared_table(a, tid, nth);
     // the expert table for the grouped kernels
     ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
     const int maxu = min(T * k, E);
@@ -784,19 +793,7 @@ __device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids
         dptr<int>(a.W.meta)[0] = U;
         dptr<int>(a.W.meta)[1] = 0;
     }
-    // the shared MLP (if any) takes every token: one entry, identity token list
-    if (a.L.shared_blob) {
-        if (lane < T) dptr<int>(a.W.sh_perm)[lane] = lane;
-        if (lane == 0) {
-            ExpertEntry x;
-            x.blob = a.L.shared_blob;
-            x.p0 = 0;
-            x.ntok = T;
-#pragma unroll
-            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
-            *dptr<ExpertEntry>(a.W.sh_et) = x;
-        }
-    }
+    write_shared_table(a, lane, 64);
 }
 
 }  // namespace
@@ -893,19 +890,7 @@ extern "C" __global__ void __launch_bounds__(1024) lp_moe_disp_scan(const RouteA
         for (int q = 0; q < kEntryToks; ++q) x.tok[q] = -1;
         et[v] = x;
     }
-    // the shared MLP (if any) takes every token: one entry, identity token list
-    if (a.L.shared_blob) {
-        for (int t = tid; t < T; t += blockDim.x) dptr<int>(a.W.sh_perm)[t] = t;
-        if (tid == 0) {
-            ExpertEntry x;
-            x.blob = a.L.shared_blob;
-            x.p0 = 0;
-            x.ntok = T;
-#pragma unroll
-            for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < T ? q : -1;
-            *dptr<ExpertEntry>(a.W.sh_et) = x;
-        }
-    }
+    write_shared_table(a, tid, blockDim.x);
 }
 
 // Grid ceil(T / kDispTok), kDispTok threads (wave w: tokens 64 w .. of the block).

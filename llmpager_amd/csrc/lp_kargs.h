@@ -151,7 +151,7 @@ struct Workspace {
     uint64_t act;        // f32 [T * k, I] expert-major activations
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
     uint64_t xf;         // [T] fragment images of the layer input (image_bytes(H) each)
-    uint64_t sh_et;      // shared MLP: one ExpertEntry (all T tokens)
+    uint64_t sh_et;      // shared MLP: shared_entries(T) ExpertEntry (consecutive tokens)
     uint64_t sh_perm;    // shared MLP: i32 [T], t
     uint64_t sh_act;     // shared MLP: f32 [T, shared_inter]
     uint64_t sh_y;       // shared MLP: f32 [T, H]
@@ -160,6 +160,11 @@ struct Workspace {
     uint64_t xlo;        // i32 [T]: 1 when token t's image in xf has a non-zero lo part
     uint64_t disp;       // multi-block dispatch: i32 [nb][E] counts, [nb][E] first positions, [E] entries
 };
+
+// Entries of the shared MLP's expert table: groups of kEntryToks consecutive
+// tokens for decode batches (the grouped kernels then need no token loop),
+// one entry of all T tokens above 64.
+LPK_HD constexpr int shared_entries(int T) { return T <= 64 ? (T + kEntryToks - 1) / kEntryToks : 1; }
 
 struct RouteArgs {
     LayerView L;

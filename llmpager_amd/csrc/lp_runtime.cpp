@@ -564,7 +564,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->xf = take(t * (uint64_t)image_bytes((int)H));
     const bool sh = d->shared_blob != 0;
     const uint64_t Is = sh ? (uint64_t)d->shared_inter : 0;
-    out->sh_et = take(sh ? sizeof(ExpertEntry) : 0);
+    out->sh_et = take(sh ? (uint64_t)shared_entries(T) * sizeof(ExpertEntry) : 0);
     out->sh_perm = take(sh ? t * 4 : 0);
     out->sh_act = take(t * Is * 4);
     out->sh_y = take(sh ? t * H * 4 : 0);
@@ -751,7 +751,9 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
 // Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
 // (maxu entries): workgroup width chosen so that there are about two work
 // items per CU, down with two tiles per wave when the inner size allows.
-// `routed`: the routed experts (the balanced gate/up may take them).
+// `routed`: the routed experts (the balanced down may take them; the
+// balanced gate/up takes the shared MLP too, as ceil(T / 4) virtual experts
+// whose weight rows neighbouring workgroups of one XCD read together).
 static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s) {
     GroupedArgs ga = ga0;
     ga.maxu = maxu;
@@ -762,7 +764,7 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
                 return w;
         return 1;
     };
-    if (routed && c->gateup_bal && gateup_balanced(c, ga, maxu)) {
+    if (c->gateup_bal && gateup_balanced(c, ga, maxu)) {
         const int nw = tile_steps_host(H) > 8 ? 16 : 8;
         if (int r = launch(c, kGateupBal, dim3((unsigned)c->cus), dim3(64 * c->bal_waves),
                            (size_t)bal_lds_bytes(H, nw, c->bal_waves), s, ga))
@@ -856,7 +858,8 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     }
     if (d->shared_blob) {
         // the shared MLP through the same kernels: its own width, group and
-        // regions, one expert entry covering every token (written by dispatch)
+        // regions, an expert table of consecutive token groups (written by
+        // dispatch)
         GroupedArgs gs = ga;
         gs.L.inter = Is;
         gs.L.group = d->shared_group;
@@ -868,7 +871,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gs.W.perm = ga.W.sh_perm;
         gs.W.act = ga.W.sh_act;
         gs.W.y = ga.W.sh_y;
-        if (int r = grouped_ffn(c, gs, 1, false, s)) return r;
+        if (int r = grouped_ffn(c, gs, shared_entries(T), false, s)) return r;
     }
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 1023) / 1024), (unsigned)T), dim3(256), 0,
                   s, ga);
