@@ -77,9 +77,11 @@ def test_layer_small(cuda, group, T):
     L.free()
 
 
-@pytest.mark.parametrize("T", [1, 8, 32])
+@pytest.mark.parametrize("T", [1, 2, 8, 9, 32, 64])
 def test_layer_config1(cuda, T):
-    # Qwen3-30B-A3B shape: H2048, E128, top-8, I768, q4 g32, softmax + renorm
+    # Qwen3-30B-A3B shape: H2048, E128, top-8, I768, q4 g32, softmax + renorm.
+    # T = 2: the one-wave dispatch at its 16-pick limit; 9: two token blocks;
+    # 64: the largest fused-routing batch, balanced kernels at their bound.
     L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=0)
     x, h, g = _run_layer(cuda, L, T, seed=T)
     _check_layer(L, x, h, g, T)
