@@ -529,8 +529,8 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_topk(const RouteArgs a)
 // ascending), meta[0] = unique count (meta[1], the error flags, cleared), and
 // the expert table et[u] for u < min(T*k, E) that the grouped kernels read
 // (blob address through the slot table, positions, first kEntryToks tokens).
-// Stability comes from ranking each pick by the tokens before it inside a
-// 64-token block (one bit per lane) plus a running per-expert base.
+// Stability comes from ranking each pick by the tokens before it with the
+// same expert (a 64-bit token mask per expert; every caller has T <= 64).
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -555,9 +555,13 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
 }
 
 // LDS of dispatch_all, carved from one buffer so that the single-workgroup
-// top-k + dispatch kernel can share it with its top-k phase.
-constexpr int kDispatchSmem = 4 * (kMaxExperts * 6 + (kMaxExperts + 4) + kMaxExperts * kEntryToks + 16 +
-                                   kTopkDispatchMaxT * (kMaxTopK + 1) + kMaxExperts);
+// top-k + dispatch kernel can share it with its top-k phase: token masks
+// (2 x E), group starts (E + 4), unique list (E), first tokens (E x
+// kEntryToks), picks (kTopkDispatchMaxT x kMaxTopK), pick counts
+// (kTopkDispatchMaxT), slot table (E) and 4 words.
+constexpr int kDispatchSmem = 4 * (kMaxExperts * 2 + (kMaxExperts + 4) + kMaxExperts + kMaxExperts * kEntryToks +
+                                   kTopkDispatchMaxT * (kMaxTopK + 1) + kMaxExperts + 4);
+static_assert(kTopkDispatchMaxT <= 64, "dispatch_all ranks the tokens of one 64-bit mask");
 
 // ids / cnt: the picks (global, or LDS copies from the same workgroup);
 // slots: the slot table (global, or an LDS copy).
@@ -584,113 +588,96 @@ __device__ __forceinline__ void write_shared_table(const RouteArgs& a, int tid, 
 
 __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids_in,
                                              const int* cnt_in, const int* slots_in) {
-    int* cnt_e = reinterpret_cast<int*>(sm);
-    int* base = cnt_e + kMaxExperts;
-    int* gsl = base + kMaxExperts;                       // kMaxExperts + 1 used
+    // T <= kTopkDispatchMaxT <= 64: expert e's picks are the set bits of
+    // its token mask (a token picks an expert at most once), its count is
+    // the mask's popcount and a pick's rank among them the bits below its
+    // token; one thread per pick, four barriers.
+    uint32_t* mlo = reinterpret_cast<uint32_t*>(sm);  // tokens 0..31
+    uint32_t* mhi = mlo + kMaxExperts;                 // tokens 32..63
+    int* gsl = reinterpret_cast<int*>(mhi + kMaxExperts);  // kMaxExperts + 1 used
     int* uniq_l = gsl + kMaxExperts + 4;
     int (*tokf)[kEntryToks] = reinterpret_cast<int (*)[kEntryToks]>(uniq_l + kMaxExperts);
-    uint32_t* mlo = reinterpret_cast<uint32_t*>(uniq_l + kMaxExperts + kMaxExperts * kEntryToks);
-    uint32_t* mhi = mlo + kMaxExperts;
-    int* scan_sh = reinterpret_cast<int*>(mhi + kMaxExperts);
+    int* ids = uniq_l + kMaxExperts + kMaxExperts * kEntryToks;
+    int* cnt = ids + kTopkDispatchMaxT * kMaxTopK;
+    int* slots = cnt + kTopkDispatchMaxT;
+    int* nu_l = slots + kMaxExperts;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-    const int nth = blockDim.x;  // 256 .. 1024; 4 * nth >= kMaxExperts
-    const int E = a.L.experts, k = a.L.top_k, T = a.T;
+    const int nth = blockDim.x;
+    const int E = a.L.experts, k = a.L.top_k, T = a.T, P = T * k;
     int* perm = dptr<int>(a.W.perm);
     int* inv = dptr<int>(a.W.inv);
     int* meta = dptr<int>(a.W.meta);
-    // the picks and the slot table in LDS first: one round trip to memory
-    // (T <= kTopkDispatchMaxT), every later read from LDS
-    int* ids = scan_sh + 16;
-    int* cnt = ids + kTopkDispatchMaxT * kMaxTopK;
-    int* slots = cnt + kTopkDispatchMaxT;
-    for (int i = tid; i < T * k; i += nth) ids[i] = ids_in[i];
+    // the picks and the slot table in LDS (one round trip when they are in
+    // memory), the masks and first tokens cleared
+    for (int i = tid; i < P; i += nth) ids[i] = ids_in[i];
     for (int i = tid; i < T; i += nth) cnt[i] = cnt_in[i];
-    for (int i = tid; i < E; i += nth) slots[i] = slots_in[i];
-
     for (int e = tid; e < E; e += nth) {
-        cnt_e[e] = 0;
-        base[e] = 0;
+        slots[e] = slots_in[e];
+        mlo[e] = 0u;
+        mhi[e] = 0u;
 #pragma unroll
         for (int q = 0; q < kEntryToks; ++q) tokf[e][q] = -1;
     }
     __syncthreads();
-    for (int p = tid; p < T * k; p += nth) {
+    for (int p = tid; p < P; p += nth) {
         const int t = p / k, j = p - t * k;
-        if (j < cnt[t]) atomicAdd(&cnt_e[ids[p]], 1);
+        if (j < cnt[t]) atomicOr(t < 32 ? &mlo[ids[p]] : &mhi[ids[p]], 1u << (t & 31));
     }
     __syncthreads();
-    // group starts and the unique list: thread i covers experts 4i .. 4i+3
-    {
-        int c[4], f[4], sc = 0, sf = 0;
-        for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            c[q] = e < E ? cnt_e[e] : 0;
-            f[q] = c[q] > 0;
-            sc += c[q];
-            sf += f[q];
-        }
-        int tot_c, tot_f;
-        int oc = block_excl_scan(sc, scan_sh, &tot_c);
-        int of = block_excl_scan(sf, scan_sh, &tot_f);
-        for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            if (e < E) {
-                gsl[e] = oc;
-                if (f[q]) uniq_l[of++] = e;
+    // one wave: counts, their exclusive scan (group starts) and the unique
+    // list, 64 experts a pass
+    if (wave == 0) {
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        int run = 0, urun = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const int c = e < E ? __popc(mlo[e]) + __popc(mhi[e]) : 0;
+            int x = c;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
             }
-            oc += c[q];
+            const uint64_t f = __ballot(c > 0);
+            if (e < E) gsl[e] = run + x - c;
+            if (c > 0) uniq_l[urun + __popcll(f & below)] = e;
+            run += __shfl(x, 63, 64);
+            urun += __popcll(f);
         }
-        if (tid == 0) {
-            gsl[E] = tot_c;
-            meta[0] = tot_f;
+        if (lane == 0) {
+            gsl[E] = run;
+            *nu_l = urun;
+            meta[0] = urun;
             meta[1] = 0;
         }
     }
     __syncthreads();
+    // each pick's position: its expert's start plus the tokens before it
+    // with the same expert
+    for (int p = tid; p < P; p += nth) {
+        const int t = p / k, j = p - t * k;
+        if (j < cnt[t]) {
+            const int e = ids[p];
+            const uint64_t m = (uint64_t)mlo[e] | ((uint64_t)mhi[e] << 32);
+            const int rank = __popcll(m & ((1ull << t) - 1ull));
+            const int pos = gsl[e] + rank;
+            perm[pos] = p;
+            inv[p] = pos;
+            if (rank < kEntryToks) tokf[e][rank] = t;
+        } else {
+            inv[p] = -1;
+        }
+    }
+    const int nu = *nu_l;
     int* gs = dptr<int>(a.W.gs);
     for (int e = tid; e <= E; e += nth) gs[e] = gsl[e];
-    int nu = 0;
-    for (int e = 0; e < E; e += 64) nu += __popcll(__ballot(e + lane < E && cnt_e[e + lane] > 0));
     int* uniq = dptr<int>(a.W.uniq);
     for (int u = tid; u < nu; u += nth) uniq[u] = uniq_l[u];
-
-    for (int tb = 0; tb < T; tb += 64) {
-        for (int e = tid; e < E; e += nth) {
-            mlo[e] = 0u;
-            mhi[e] = 0u;
-        }
-        __syncthreads();
-        const int t = tb + lane;
-        const int c = (wave == 0 && t < T) ? cnt[t] : 0;
-        for (int j = 0; j < c; ++j) {
-            const int e = ids[t * k + j];
-            atomicOr(lane < 32 ? &mlo[e] : &mhi[e], 1u << (lane & 31));
-        }
-        __syncthreads();
-        if (wave == 0 && t < T) {
-            for (int j = 0; j < k; ++j) {
-                if (j < c) {
-                    const int e = ids[t * k + j];
-                    const uint64_t mask = (uint64_t)mlo[e] | ((uint64_t)mhi[e] << 32);
-                    const uint64_t below = lane == 0 ? 0ull : (mask & ((1ull << lane) - 1ull));
-                    const int rank = base[e] + __popcll(below);
-                    const int pos = gsl[e] + rank;
-                    perm[pos] = t * k + j;
-                    inv[t * k + j] = pos;
-                    if (rank < kEntryToks) tokf[e][rank] = t;
-                } else {
-                    inv[t * k + j] = -1;
-                }
-            }
-        }
-        __syncthreads();
-        for (int e = tid; e < E; e += nth) base[e] += __popc(mlo[e]) + __popc(mhi[e]);
-        __syncthreads();
-    }
     write_shared_table(a, tid, nth);
+    __syncthreads();
     // the expert table for the grouped kernels
     ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
-    const int maxu = min(T * k, E);
+    const int maxu = min(P, E);
     for (int u = tid; u < maxu; u += nth) {
         ExpertEntry x;
         if (u < nu) {
@@ -698,7 +685,7 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
             const int slot = slots[e];
             x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
             x.p0 = gsl[e];
-            x.ntok = cnt_e[e];
+            x.ntok = gsl[e + 1] - gsl[e];
 #pragma unroll
             for (int q = 0; q < kEntryToks; ++q) x.tok[q] = tokf[e][q];
         } else {
@@ -984,16 +971,16 @@ extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const Ro
 
 // ---------------------------------------------------------------------------
 // Routing of a decode-sized batch (T <= kTopkDispatchMaxT) in one launch:
-// router logits, top-k and dispatch.  Grid (ceil(E/16), ceil(T/8)), 512
-// threads: workgroup (g, b) computes the logits of experts 16g .. 16g+15 (two
-// per wave, the router GEMV's canonical order) for the tokens of block b
-// (8b .. 8b+7) and, with make_xf, the images of tokens 8b + g, 8b + g +
-// ceil(E/16), ... of the block.  The last
-// workgroup of block b to finish (an arrival counter) ranks the block's
-// tokens, one per wave; the last block to finish ranking builds the dispatch
-// tables.  Release fences before each arrival and acquire fences after it
-// make the other workgroups' logits and picks visible; the last arrival
-// resets its counter, so every launch finds them zero.
+// router logits, top-k and dispatch.  Grid (ceil(E/(8 kRouteEPW)), ceil(T/8)),
+// 512 threads: workgroup (g, b) computes the logits of experts
+// 8 kRouteEPW g .. (kRouteEPW per wave, the router GEMV's canonical order)
+// for the tokens of block b (8b .. 8b+7).  The last workgroup of block b to
+// finish (an arrival counter) ranks the block's tokens, one per wave, while
+// the others write the block's fragment images (make_xf); the last block to
+// finish ranking builds the dispatch tables.  Release fences before each
+// arrival and acquire fences after it make the other workgroups' logits and
+// picks visible; the last arrival resets its counter, so every launch finds
+// them zero.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -1030,11 +1017,23 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     constexpr int kTopkLds = 8 * kMaxExperts * 4;
     __shared__ __align__(16) uint8_t sm[kDispatchSmem > kTopkLds ? kDispatchSmem : kTopkLds];
     __shared__ __align__(16) float xs[kRouteXLds / 4];
+    __shared__ int slots_l[kMaxExperts];
+    __shared__ int ids_l[kRouterTokBlock * kMaxTopK];  // one token block's picks
+    __shared__ int cnt_l[kRouterTokBlock];
     __shared__ int flag;
-    const int wave = threadIdx.x >> 6;
+    static_assert(kMaxExperts <= 2 * 512, "two slot-table entries per thread");
+    const int wave = threadIdx.x >> 6, tid = threadIdx.x;
     const int b = blockIdx.y, t0 = b * kRouterTokBlock;
     const int nt = min(kRouterTokBlock, a.T - t0);
+    // the slot table comes in with the router weights (every workgroup:
+    // which one dispatches is known only at the end)
+    const int E = a.L.experts;
+    const int* st = dptr<const int>(a.L.slot_table);
+    const int sl0 = tid < E ? st[tid] : 0;
+    const int sl1 = tid + 512 < E ? st[tid + 512] : 0;
     router_block(a, xs, blockIdx.x * 8 * kRouteEPW, t0, nt);
+    if (tid < E) slots_l[tid] = sl0;
+    if (tid + 512 < E) slots_l[tid + 512] = sl1;
     // The images are for the expert kernels only.  The workgroups that are
     // not the last of their block to arrive write them, shared by arrival
     // order, after arriving: the last one, which goes on to rank the block,
@@ -1058,23 +1057,25 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
         return;
     }
     if (gridDim.x == 1) images(0, 1);
-    if (wave < nt) topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts);
-    if (gridDim.y == 1) {
-        // one token block, ranked by this workgroup: no second arrival; up
-        // to 16 picks one wave builds the tables, more take the workgroup
+    // one token block: the picks also go to LDS (token t = wave)
+    const bool one = gridDim.y == 1;
+    if (wave < nt)
+        topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts, one ? ids_l : nullptr,
+                 one ? cnt_l : nullptr);
+    if (one) {
+        // ranked by this workgroup: no second arrival, and the tables come
+        // from LDS alone; up to 16 picks one wave builds them, more take the
+        // workgroup
         __syncthreads();
         if (a.T * a.L.top_k <= kDispatchWaveMaxPicks) {
-            if (wave == 0)
-                dispatch_wave(a, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
-                              dptr<const int>(a.L.slot_table));
+            if (wave == 0) dispatch_wave(a, ids_l, cnt_l, slots_l);
         } else {
-            dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt),
-                         dptr<const int>(a.L.slot_table));
+            dispatch_all(a, sm, ids_l, cnt_l, slots_l);
         }
         return;
     }
     if (!last_arrival(cnt + 8, gridDim.y, &flag)) return;
-    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table));
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l);
 }
 
 // ---------------------------------------------------------------------------

@@ -330,6 +330,19 @@ def test_route_sequence(cuda):
     L.free()
 
 
+@pytest.mark.parametrize("E,k,T", [(8, 2, 64), (4, 2, 1), (64, 6, 17), (128, 8, 32), (300, 16, 5),
+                                   (300, 16, 64), (1024, 16, 64), (1024, 16, 7)])
+def test_route_one_launch_tables(cuda, E, k, T):
+    # The one-launch routing's tables at its sizes (T <= 64): one token block
+    # (picks from LDS) and several (picks from memory), up to 1024 picks and
+    # the largest expert count; 8 experts x 64 tokens put 16 picks on each.
+    # A permuted slot table, so each entry's blob shows which slot it read.
+    slots = np.random.default_rng(E + k).permutation(E).astype(np.int32)
+    L = DeviceLayer(cuda, H=256, I=64, E=E, k=k, group=32, seed=6, router_std=0.05, slots=slots)
+    _check_route(cuda, L, T, seed=400 + T)
+    L.free()
+
+
 @pytest.mark.parametrize("E,k,T", [(128, 8, 300), (8, 2, 1100), (300, 16, 513)])
 def test_route_multiblock(cuda, E, k, T):
     # Batches above the one-workgroup limit dispatch in blocks of 256 tokens:
