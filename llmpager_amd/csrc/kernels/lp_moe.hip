@@ -439,8 +439,6 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
     uint32_t* wk = reinterpret_cast<uint32_t*>(sv);
     int* wi = reinterpret_cast<int*>(sv) + kMaxTopK;
     float* wv = sv + 2 * kMaxTopK;
-    int* pid = reinterpret_cast<int*>(sv) + 3 * kMaxTopK;
-    float* pv = sv + 4 * kMaxTopK;
     int eq_before = 0, slot0 = 0;
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -457,22 +455,34 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
         slot0 += __popcll(wm);
     }
     wave_sync_lds();
-    if (lane < n) {
-        const uint32_t kj = wk[lane];
-        const int ij = wi[lane];
-        int rank = 0;
-        for (int s = 0; s < n; ++s) rank += (wk[s] > kj || (wk[s] == kj && wi[s] < ij)) ? 1 : 0;
-        pid[rank] = ij;
-        pv[rank] = wv[lane];
+    // winner j (id order) in lane j; its place in the stable descending
+    // order from the other winners read across lanes, then every lane
+    // pushed to its place (lanes n.. keep theirs: a permutation)
+    const bool inn = lane < n;
+    const uint32_t kj = inn ? wk[lane] : 0u;
+    const int ij = inn ? wi[lane] : 0;
+    const float vj = inn ? wv[lane] : 0.0f;
+    int rank = lane;
+    if (inn) {
+        rank = 0;
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; ++s) {
+            if (s < n) {  // uniform
+                const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)kj, s);
+                const int is = __builtin_amdgcn_readlane(ij, s);
+                rank += (ks > kj || (ks == kj && is < ij)) ? 1 : 0;
+            }
+        }
     }
-    wave_sync_lds();
     // pick j in lane j; the sum of the picks in pick order, from -0.0
-    const int my_pick = lane < n ? pid[lane] : -1;
-    const float my_val = lane < n ? pv[lane] : 0.0f;
+    const int pk = __builtin_amdgcn_ds_permute(rank * 4, ij);
+    const int pv = __builtin_amdgcn_ds_permute(rank * 4, __float_as_int(vj));
+    const int my_pick = inn ? pk : -1;
+    const float my_val = inn ? __int_as_float(pv) : 0.0f;
     float s = -0.0f;
     for (int j = 0; j < n; ++j) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), j));
     float wj = my_val;
-    bool keep = lane < n;
+    bool keep = inn;
     if (a.L.gating == 0) {
         if (a.L.renorm) wj = div_rn(my_val, s);
     } else {
@@ -480,20 +490,22 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
         wj = wj * a.L.routed_scaling;
         if (a.L.min_weight > 0.0f && !(wj >= a.L.min_weight)) keep = false;
     }
-    // survivors keep pick order: pick j lands in slot (survivors before it)
-    wave_sync_lds();
+    // survivors keep pick order: pick j moves to slot (survivors before it),
+    // the dropped ones after them, lanes n.. stay (a permutation again)
     const uint64_t km = __ballot(keep);
     const int kept = __popcll(km);
-    if (keep) {
-        const int slot = __popcll(km & below);
-        pid[slot] = my_pick;
-        pv[slot] = wj;
+    int out_pick = my_pick;
+    float out_w = wj;
+    if (kept != n) {  // uniform
+        const uint64_t nm = n >= 64 ? ~0ull : ((1ull << n) - 1ull);
+        const int dst = keep ? __popcll(km & below) : (inn ? kept + __popcll(~km & nm & below) : lane);
+        out_pick = __builtin_amdgcn_ds_permute(dst * 4, my_pick);
+        out_w = __int_as_float(__builtin_amdgcn_ds_permute(dst * 4, __float_as_int(wj)));
     }
-    wave_sync_lds();
     if (lane < k) {
-        const int id = lane < kept ? pid[lane] : -1;
+        const int id = lane < kept ? out_pick : -1;
         dptr<int>(a.W.ids)[(size_t)t * k + lane] = id;
-        dptr<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? pv[lane] : 0.0f;
+        dptr<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? out_w : 0.0f;
         if (ids_l) ids_l[t * k + lane] = id;
     }
     if (lane == 0) {
