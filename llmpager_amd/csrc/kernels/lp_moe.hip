@@ -202,7 +202,7 @@ __device__ __forceinline__ void router_block(const RouteArgs& a, float* xs, int 
     const int E = a.L.experts, H = a.L.hidden;
     const int chunks = H >> 3;
     const int tb = min(kRouterTokBlock, kRouteXLds / (H * 4));
-    float* logits = dptr<float>(a.W.logits);
+    LP_GLOBAL float* logits = gptr_w<float>(a.W.logits);
     int ew[kRouteEPW];
 #pragma unroll
     for (int j = 0; j < kRouteEPW; ++j) ew[j] = min(e0 + wave * kRouteEPW + j, E - 1);
@@ -222,22 +222,24 @@ __device__ __forceinline__ void router_block(const RouteArgs& a, float* xs, int 
 #pragma unroll
                 for (int c = 0; c < CB; ++c) {
                     const int ch = lane + 64 * (c0 + c);
-                    wv[j][c] = ch < chunks ? *reinterpret_cast<const uint4*>(
-                                                 dptr<const uint16_t>(a.L.router_w) + (size_t)ew[j] * H + ch * 8)
-                                           : make_uint4(0, 0, 0, 0);
+                    wv[j][c] = make_uint4(0, 0, 0, 0);
+                    if (ch < chunks)
+                        wv[j][c] = *reinterpret_cast<const LP_GLOBAL uint4*>(gptr<uint16_t>(a.L.router_w) +
+                                                                            (size_t)ew[j] * H + ch * 8);
                 }
             if (c0 == 0) {
                 __syncthreads();  // the previous sub-block's rows are consumed
                 // every load of the staging in flight at once (up to
                 // kRouteXLds / 16 / 512 per thread), then the LDS stores
                 constexpr int XU = kRouteXLds / 16 / 512;
-                const float4* xg = dptr<const float4>(a.x) + (size_t)(t0 + tt) * (H >> 2);
+                const LP_GLOBAL float4* xg = gptr<float4>(a.x) + (size_t)(t0 + tt) * (H >> 2);
                 const int n4 = nb * (H >> 2);
                 float4 xr[XU];
 #pragma unroll
                 for (int u = 0; u < XU; ++u) {
                     const int i = (int)threadIdx.x + 512 * u;
-                    xr[u] = i < n4 ? xg[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    xr[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (i < n4) xr[u] = xg[i];
                 }
 #pragma unroll
                 for (int u = 0; u < XU; ++u) {
@@ -357,7 +359,7 @@ template <int PER>
 __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv, int* ids_l, int* cnt_l) {
     const int lane = lane_id();
     const int E = a.L.experts, k = a.L.top_k;
-    const float* lg = dptr<const float>(a.W.logits) + (size_t)t * E;
+    const LP_GLOBAL float* lg = gptr<float>(a.W.logits) + (size_t)t * E;
     const uint64_t tabv = exp2tab_lane();  // glibc's 2^(i/32) table, one entry per lane
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     uint32_t key[PER];
@@ -411,7 +413,7 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
             }
         }
     } else {
-        const float* bias = dptr<const float>(a.L.router_bias);
+        const LP_GLOBAL float* bias = gptr<float>(a.L.router_bias);
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int i = lane + 64 * q;
@@ -504,12 +506,12 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
     }
     if (lane < k) {
         const int id = lane < kept ? out_pick : -1;
-        dptr<int>(a.W.ids)[(size_t)t * k + lane] = id;
-        dptr<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? out_w : 0.0f;
+        gptr_w<int>(a.W.ids)[(size_t)t * k + lane] = id;
+        gptr_w<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? out_w : 0.0f;
         if (ids_l) ids_l[t * k + lane] = id;
     }
     if (lane == 0) {
-        dptr<int>(a.W.cnt)[t] = kept;
+        gptr_w<int>(a.W.cnt)[t] = kept;
         if (cnt_l) cnt_l[t] = kept;
     }
 }
@@ -586,7 +588,7 @@ __device__ __forceinline__ void write_shared_table(const RouteArgs& a, int tid, 
     if (!a.L.shared_blob) return;
     const int T = a.T, nv = shared_entries(T);
     const int per = nv == 1 ? T : kEntryToks;
-    for (int t = tid; t < T; t += nth) dptr<int>(a.W.sh_perm)[t] = t;
+    for (int t = tid; t < T; t += nth) gptr_w<int>(a.W.sh_perm)[t] = t;
     for (int v = tid; v < nv; v += nth) {
         ExpertEntry x;
         x.blob = a.L.shared_blob;
@@ -594,7 +596,7 @@ __device__ __forceinline__ void write_shared_table(const RouteArgs& a, int tid, 
         x.ntok = min(per, T - v * per);
 #pragma unroll
         for (int q = 0; q < kEntryToks; ++q) x.tok[q] = q < x.ntok ? x.p0 + q : -1;
-        dptr<ExpertEntry>(a.W.sh_et)[v] = x;
+        gptr_w<ExpertEntry>(a.W.sh_et)[v] = x;
     }
 }
 
@@ -616,9 +618,9 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int nth = blockDim.x;
     const int E = a.L.experts, k = a.L.top_k, T = a.T, P = T * k;
-    int* perm = dptr<int>(a.W.perm);
-    int* inv = dptr<int>(a.W.inv);
-    int* meta = dptr<int>(a.W.meta);
+    LP_GLOBAL int* perm = gptr_w<int>(a.W.perm);
+    LP_GLOBAL int* inv = gptr_w<int>(a.W.inv);
+    LP_GLOBAL int* meta = gptr_w<int>(a.W.meta);
     // the picks and the slot table in LDS (one round trip when they are in
     // memory), the masks and first tokens cleared
     for (int i = tid; i < P; i += nth) ids[i] = ids_in[i];
@@ -681,14 +683,14 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
         }
     }
     const int nu = *nu_l;
-    int* gs = dptr<int>(a.W.gs);
+    LP_GLOBAL int* gs = gptr_w<int>(a.W.gs);
     for (int e = tid; e <= E; e += nth) gs[e] = gsl[e];
-    int* uniq = dptr<int>(a.W.uniq);
+    LP_GLOBAL int* uniq = gptr_w<int>(a.W.uniq);
     for (int u = tid; u < nu; u += nth) uniq[u] = uniq_l[u];
     write_shared_table(a, tid, nth);
     __syncthreads();
     // the expert table for the grouped kernels
-    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    LP_GLOBAL ExpertEntry* et = gptr_w<ExpertEntry>(a.W.et);
     const int maxu = min(P, E);
     for (int u = tid; u < maxu; u += nth) {
         ExpertEntry x;
@@ -754,21 +756,21 @@ __device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids
                 if (rq == r) tok[r] = tq;
         }
     }
-    int* perm = dptr<int>(a.W.perm);
-    int* inv = dptr<int>(a.W.inv);
+    LP_GLOBAL int* perm = gptr_w<int>(a.W.perm);
+    LP_GLOBAL int* inv = gptr_w<int>(a.W.inv);
     if (inb) inv[lane] = valid ? less + before : -1;
     if (valid) perm[less + before] = lane;
     // gs[x] = valid picks with an expert id below x, for x = 0 .. E
-    int* gs = dptr<int>(a.W.gs);
+    LP_GLOBAL int* gs = gptr_w<int>(a.W.gs);
     for (int x0 = 0; x0 <= E; x0 += 64) {
         const int x = x0 + lane;
         int below = 0;
         for (int q = 0; q < P; ++q) below += __builtin_amdgcn_readlane(e, q) < x;
         if (x <= E) gs[x] = below;
     }
-    ExpertEntry* et = dptr<ExpertEntry>(a.W.et);
+    LP_GLOBAL ExpertEntry* et = gptr_w<ExpertEntry>(a.W.et);
     if (first) {
-        dptr<int>(a.W.uniq)[uidx] = e;
+        gptr_w<int>(a.W.uniq)[uidx] = e;
         const int slot = slots_in[e];
         ExpertEntry x;
         x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
@@ -789,8 +791,8 @@ __device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids
         et[lane] = x;
     }
     if (lane == 0) {
-        dptr<int>(a.W.meta)[0] = U;
-        dptr<int>(a.W.meta)[1] = 0;
+        gptr_w<int>(a.W.meta)[0] = U;
+        gptr_w<int>(a.W.meta)[1] = 0;
     }
     write_shared_table(a, lane, 64);
 }
@@ -1040,7 +1042,7 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     // the slot table comes in with the router weights (every workgroup:
     // which one dispatches is known only at the end)
     const int E = a.L.experts;
-    const int* st = dptr<const int>(a.L.slot_table);
+    const LP_GLOBAL int* st = gptr<int>(a.L.slot_table);
     const int sl0 = tid < E ? st[tid] : 0;
     const int sl1 = tid + 512 < E ? st[tid + 512] : 0;
     router_block(a, xs, blockIdx.x * 8 * kRouteEPW, t0, nt);
