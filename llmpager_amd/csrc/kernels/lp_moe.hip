@@ -1822,47 +1822,67 @@ lp_moe_down_wide(const GroupedArgs a) {
 // output is added after that, unweighted (kimi.rs:779).  Grid (ceil(H/1024),
 // T): four columns per thread, eight picks' rows loaded before their FMAs;
 // picks past cnt load pick 0's row with weight 0, which leaves the sum as it
-// is.
+// is.  The pick count, the first eight picks' rows and weights (in bounds
+// whatever the count), the residual and the shared output are loaded
+// together, so the picked rows are the only dependent round trip.
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedArgs a) {
     const int t = blockIdx.y;
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     const int H = a.L.hidden, k = a.L.top_k;
     if (i >= H) return;
-    const int c = dptr<const int>(a.W.cnt)[t];
-    const int* inv = dptr<const int>(a.W.inv) + (size_t)t * k;
-    const float* w = dptr<const float>(a.W.wts) + (size_t)t * k;
-    const float* y = dptr<const float>(a.W.y) + i;
+    const LP_GLOBAL int* inv = gptr<int>(a.W.inv) + (size_t)t * k;
+    const LP_GLOBAL float* w = gptr<float>(a.W.wts) + (size_t)t * k;
+    const LP_GLOBAL float* y = gptr<float>(a.W.y) + i;
+    LP_GLOBAL float4* h = reinterpret_cast<LP_GLOBAL float4*>(gptr_w<float>(a.h) + (size_t)t * H + i);
+    const int c = gptr<int>(a.W.cnt)[t];
+    int iv[8];
+    float wv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        iv[q] = 0;
+        wv[q] = 0.0f;
+        if (q < k) {
+            iv[q] = inv[q];
+            wv[q] = w[q];
+        }
+    }
+    float4 v = *h;
+    float4 sy = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (a.L.shared_blob)
+        sy = *reinterpret_cast<const LP_GLOBAL float4*>(gptr<float>(a.W.sh_y) + (size_t)t * H + i);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c > 0) {
-        const int row0 = inv[0];
+        const int row0 = iv[0];
         for (int j0 = 0; j0 < c; j0 += 8) {
             float4 yv[8];
-            float wv[8];
+            float wl[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 const int j = j0 + q;
                 const bool live = j < c;
-                wv[q] = live ? w[j] : 0.0f;
-                yv[q] = *reinterpret_cast<const float4*>(y + (size_t)(live ? inv[j] : row0) * H);
+                int r = row0;
+                wl[q] = 0.0f;
+                if (live) {
+                    r = j0 == 0 ? iv[q] : inv[j];
+                    wl[q] = j0 == 0 ? wv[q] : w[j];
+                }
+                yv[q] = *reinterpret_cast<const LP_GLOBAL float4*>(y + (size_t)r * H);
             }
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                acc.x = __builtin_fmaf(wv[q], yv[q].x, acc.x);
-                acc.y = __builtin_fmaf(wv[q], yv[q].y, acc.y);
-                acc.z = __builtin_fmaf(wv[q], yv[q].z, acc.z);
-                acc.w = __builtin_fmaf(wv[q], yv[q].w, acc.w);
+                acc.x = __builtin_fmaf(wl[q], yv[q].x, acc.x);
+                acc.y = __builtin_fmaf(wl[q], yv[q].y, acc.y);
+                acc.z = __builtin_fmaf(wl[q], yv[q].z, acc.z);
+                acc.w = __builtin_fmaf(wl[q], yv[q].w, acc.w);
             }
         }
     }
-    float4* h = reinterpret_cast<float4*>(dptr<float>(a.h) + (size_t)t * H + i);
-    float4 v = *h;
     v.x = v.x + acc.x;
     v.y = v.y + acc.y;
     v.z = v.z + acc.z;
     v.w = v.w + acc.w;
     if (a.L.shared_blob) {
-        const float4 sy = *reinterpret_cast<const float4*>(dptr<const float>(a.W.sh_y) + (size_t)t * H + i);
         v.x = v.x + sy.x;
         v.y = v.y + sy.y;
         v.z = v.z + sy.z;
