@@ -77,6 +77,30 @@ def test_layer_small(cuda, group, T):
     L.free()
 
 
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_layer_top16(cuda, T):
+    # top-16 of 64 experts: the combine sums each token's picks in two
+    # blocks of 8; T = 1 puts 16 picks in the one-wave dispatch.
+    L = DeviceLayer(cuda, H=256, I=64, E=64, k=16, group=32, seed=9, router_std=0.2)
+    x, h, g = _run_layer(cuda, L, T, seed=50 + T)
+    _check_layer(L, x, h, g, T)
+    L.free()
+
+
+def test_layer_sigmoid_dropped_picks(cuda):
+    # sigmoid gating with a min_weight that drops some of each token's
+    # picks (count < k), top-12: the combine's pick count cuts its second
+    # block of 8 short.
+    E, k = 32, 12
+    L = DeviceLayer(cuda, H=256, I=64, E=E, k=k, group=32, seed=10, router_std=0.2,
+                    gating=lp.GATING_SIGMOID, renorm=False, routed_scaling=1.0, min_weight=0.7,
+                    bias=np.zeros(E, np.float32))
+    x, h, g = _run_layer(cuda, L, 24, seed=77)
+    assert g["cnt"].min() < k
+    _check_layer(L, x, h, g, 24)
+    L.free()
+
+
 @pytest.mark.parametrize("T", [1, 2, 8, 9, 32, 64])
 def test_layer_config1(cuda, T):
     # Qwen3-30B-A3B shape: H2048, E128, top-8, I768, q4 g32, softmax + renorm.
