@@ -1000,20 +1000,24 @@ namespace {
 
 // Add one arrival at *cnt; returns (in every thread) the workgroup's arrival
 // order, n - 1 for the last, which also resets the counter.  Every thread of
-// the workgroup must call it.  The barrier makes every wave's stores visible
-// to thread 0 (workgroup scope) and thread 0 alone carries them to agent
-// scope: an agent-scope release writes back this XCD's L2, and one per
-// workgroup instead of one per wave took 8 us off a 64-workgroup launch.
-// Thread 0 of the last arrival likewise acquires for the workgroup before
-// the second barrier.
+// the workgroup must call it.  Each wave first waits until its own stores
+// have completed (reached this XCD's L2: the barrier alone does not wait for
+// global stores), then thread 0 alone carries them to agent scope: an
+// agent-scope release writes back the whole L2, and one per workgroup
+// instead of one per wave took 8 us off a 64-workgroup launch.  Thread 0 of
+// the last arrival likewise acquires for the workgroup before the second
+// barrier.
 __device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt, expcnt and lgkmcnt all zero
     __syncthreads();
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __builtin_amdgcn_s_waitcnt(0);  // the L2 write-back done before the arrival counts
         const int o = atomicAdd(cnt, 1);
         if (o == n - 1) {
             __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __builtin_amdgcn_s_waitcnt(0);  // the invalidate done before any wave loads
         }
         *flag = o;
     }
