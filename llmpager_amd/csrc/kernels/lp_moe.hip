@@ -1260,7 +1260,7 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
 
 // ---------------------------------------------------------------------------
 // Balanced gate/up for decode batches (lp_moe_gateup_bal).  One workgroup of
-// kBalMinWaves waves per CU.  Work is cut into units of 8 rows of gate plus the
+// kBalWaves waves per CU.  Work is cut into units of 8 rows of gate plus the
 // same 8 rows of up over the whole of K (one MFMA tile: lanes n < 8 carry gate
 // row r0 + n, lanes n >= 8 up row r0 + n - 8), for each "virtual expert" =
 // (routed expert, group of up to 4 of its tokens).  Virtual experts are
@@ -1318,8 +1318,8 @@ struct BalPlan {
 __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, BalPlan& P) {
     const int tid = (int)threadIdx.x, lane = lane_id(), wave = tid >> 6, W = (int)(blockDim.x >> 6);
     const int maxu = a.maxu;
-    int* tot = reinterpret_cast<int*>(lds + bal_meta_off(cols));  // [kBalMaxWaves] wave totals
-    int* sl = tot + kBalMaxWaves;                                   // [2][2]: expert, token group
+    int* tot = reinterpret_cast<int*>(lds + bal_meta_off(cols));  // [kBalWaves] wave totals
+    int* sl = tot + kBalWaves;                                      // [2][2]: expert, token group
     ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(cols) + 128);
     if (tid < 4) sl[tid] = 0;
     int ng = 0;
@@ -1740,8 +1740,8 @@ lp_moe_gateup(const GroupedArgs a) {
 
 // Balanced gate/up (decode batches, the host checks the bounds it assumes:
 // tile_steps(hidden) <= 16, at most kBalMaxU entries, no more virtual
-// experts than workgroups, kBalMinWaves .. kBalMaxWaves waves).
-extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+// experts than workgroups, kBalWaves waves).
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_gateup_bal(const GroupedArgs a) {
     if (tile_steps(a.L.hidden) > 8) {
         if (scales_in_lds(a.L.group, a.L.hidden)) {
@@ -1765,12 +1765,12 @@ lp_moe_gateup_bal(const GroupedArgs a) {
 // Balanced down (decode batches; the host checks what lp_moe_gateup_bal
 // needs, with inter for hidden): units of 16 rows over all of K, tiles of 6
 // steps (inter 768) or of up to 8.
-extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down_bal(const GroupedArgs a) {
     down_bal_body<8, 0, true>(a);
 }
 
-extern "C" __global__ void __launch_bounds__(64 * kBalMinWaves) __attribute__((amdgpu_waves_per_eu(2)))
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_down_bal6(const GroupedArgs a) {
     down_bal_body<6, 0, true>(a);
 }

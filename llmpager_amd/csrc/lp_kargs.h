@@ -186,13 +186,15 @@ struct GroupedArgs {
     int32_t pad0;
 };
 
-// Balanced decode gate/up (lp_moe_gateup_bal): one workgroup per CU of
-// kBalMinWaves .. kBalMaxWaves waves.  LDS: the zero block and two slots of
-// two token pairs (frag_lds_bytes(H, 4)), 128 bytes of counters, the expert
-// table (kBalMaxU entries), then two scale windows per wave.
-constexpr int kBalMinWaves = 8;
-constexpr int kBalMaxWaves = 16;
-constexpr int kBalMaxU = 64 * kBalMinWaves;
+// Balanced decode gate/up (lp_moe_gateup_bal): one workgroup of kBalWaves
+// waves per CU (the kernels' launch bound; the only size they are built and
+// tested for).  LDS: the zero block and two slots of two token pairs
+// (frag_lds_bytes(H, 4)), 128 bytes of counters (kBalWaves wave totals, then
+// four slot words), the expert table (kBalMaxU entries), then two scale
+// windows per wave.
+constexpr int kBalWaves = 8;
+constexpr int kBalMaxU = 64 * kBalWaves;
+static_assert(4 * kBalWaves + 16 <= 128, "bal_plan's counters fit their 128 bytes");
 LPK_HD constexpr int bal_meta_off(int hidden) { return (frag_lds_bytes(hidden, 4) + 15) & ~15; }
 LPK_HD constexpr int bal_win_off(int hidden) { return bal_meta_off(hidden) + 128 + kBalMaxU * 32; }
 LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {

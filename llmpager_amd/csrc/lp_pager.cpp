@@ -236,9 +236,18 @@ int lp_pager_request(lp_pager* p, uint16_t layer, const uint16_t* experts, int n
     if (int r = drain(p, p->deferred, false)) return r;
     if (int r = drain(p, p->prefetched, false)) return r;
     const uint32_t E = p->cfg.experts_per_layer;
-    hipStream_t cs = (hipStream_t)compute;
-    for (int i = 0; i < n; ++i) {
+    for (int i = 0; i < n; ++i)
         if (experts[i] >= E) return fail(LP_E_INVALID, "lp_pager_request: expert id out of range");
+    hipStream_t cs = (hipStream_t)compute;
+    // the pins this call has taken: handed back if it fails part-way, so a
+    // failed request leaves no slot pinned
+    std::vector<uint32_t> pinned;
+    pinned.reserve((size_t)n);
+    auto unwind = [&](int code) {
+        for (uint32_t s : pinned) lp_cache_release(p->cache, s);
+        return code;
+    };
+    for (int i = 0; i < n; ++i) {
         const uint32_t id = lp_cache_fold(layer, experts[i], E);
         uint32_t slot = 0;
         int64_t evicted = -1;
@@ -250,39 +259,44 @@ int lp_pager_request(lp_pager* p, uint16_t layer, const uint16_t* experts, int n
             // prefetches; with neither, nothing can free a slot (pager.rs:430-451)
             p->stalls += 1;
             if (!p->deferred.empty()) {
-                if (int q = drain(p, p->deferred, true)) return q;
+                if (int q = drain(p, p->deferred, true)) return unwind(q);
             } else if (!p->prefetched.empty()) {
-                if (int q = drain(p, p->prefetched, true)) return q;
+                if (int q = drain(p, p->prefetched, true)) return unwind(q);
             } else {
-                return fail(LP_E_INVALID, "expert cache deadlock: every slot of the pool is pinned "
-                                          "with no release pending (handles held across a pass)");
+                return unwind(fail(LP_E_INVALID, "expert cache deadlock: every slot of the pool is pinned "
+                                                 "with no release pending (handles held across a pass)"));
             }
         }
-        if (r < 0) return r;
+        if (r < 0) return unwind(r);
+        pinned.push_back(slot);
         if (r == LP_LOOKUP_MISS) {
             table_update(p, layer, experts[i], slot, evicted);
-            if (int q = fill_slot(p, layer, experts[i], slot)) return q;
+            if (int q = fill_slot(p, layer, experts[i], slot)) return unwind(q);
         }
         if (p->fill[slot] == Fill::InFlight) {
             hipError_t e = hipEventQuery(p->fill_ev[slot]);
             if (e == hipSuccess) {
                 p->fill[slot] = Fill::Ready;
             } else if (e == hipErrorNotReady) {
-                PCHK(hipStreamWaitEvent(cs, p->fill_ev[slot], 0));  // pager.rs:499-503
+                e = hipStreamWaitEvent(cs, p->fill_ev[slot], 0);  // pager.rs:499-503
+                if (e != hipSuccess) return unwind(hip_fail(e, "hipStreamWaitEvent"));
             } else {
-                return hip_fail(e, "fill event");
+                return unwind(hip_fail(e, "fill event"));
             }
         }
         if (slots_out) slots_out[i] = slot;
     }
     // the layer's slot table, refreshed in stream order on the compute stream
     const size_t r = p->stage_next++ % kRing;
-    PCHK(hipEventSynchronize(p->stage_ev[r]));  // its previous copy has been consumed
+    hipError_t e = hipEventSynchronize(p->stage_ev[r]);  // its previous copy has been consumed
+    if (e != hipSuccess) return unwind(hip_fail(e, "slot-table staging event"));
     int32_t* st = p->stage + r * E;
     memcpy(st, p->host_tables + (size_t)layer * E, (size_t)E * 4);
-    PCHK(hipMemcpyAsync(reinterpret_cast<void*>(lp_pager_slot_table(p, layer)), st, (size_t)E * 4,
-                        hipMemcpyHostToDevice, cs));
-    PCHK(hipEventRecord(p->stage_ev[r], cs));
+    e = hipMemcpyAsync(reinterpret_cast<void*>(lp_pager_slot_table(p, layer)), st, (size_t)E * 4,
+                       hipMemcpyHostToDevice, cs);
+    if (e != hipSuccess) return unwind(hip_fail(e, "slot-table copy"));
+    e = hipEventRecord(p->stage_ev[r], cs);
+    if (e != hipSuccess) return unwind(hip_fail(e, "slot-table event"));
     return LP_OK;
 }
 

@@ -149,14 +149,17 @@ struct lp_ctx {
     double prof_ms[kNumFns] = {};
     int64_t prof_n[kNumFns] = {};
     // arrival counters of the fused routing kernel: kSyncSlots slots of
-    // kSyncWords, zero between launches; each launch takes the next slot, so
-    // launches on different streams do not share counters
+    // kSyncWords, zero between launches.  A slot belongs to one stream (the
+    // first kSyncSlots streams that route through the context get one each):
+    // launches on one stream run one after another, so they may share it,
+    // and launches on different streams never do.
     int32_t* sync = nullptr;
-    std::atomic<unsigned> sync_next{0};
+    std::mutex sync_mu;
+    hipStream_t sync_owner[kSyncSlots] = {};  // slot i belongs to sync_owner[i] when sync_used[i]
+    bool sync_used[kSyncSlots] = {};
     // decode gate/up through lp_moe_gateup_bal (LLMPAGER_HIP_GATEUP_BAL=0 at
     // lp_init turns it off, for comparison)
     bool gateup_bal = true;
-    int bal_waves = kBalMinWaves;  // its workgroup size (LLMPAGER_HIP_BAL_WAVES)
 };
 
 namespace {
@@ -243,8 +246,16 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     c->cus = prop.multiProcessorCount;
     c->max_lds = prop.sharedMemPerBlock;
     if (const char* e = std::getenv("LLMPAGER_HIP_GATEUP_BAL")) c->gateup_bal = std::atoi(e) != 0;
-    if (const char* e = std::getenv("LLMPAGER_HIP_BAL_WAVES"))
-        c->bal_waves = std::min(kBalMaxWaves, std::max(kBalMinWaves, std::atoi(e)));
+    if (const char* e = std::getenv("LLMPAGER_HIP_BAL_WAVES")) {
+        // The balanced kernels run at kBalWaves waves only: a 16-wave build
+        // of lp_moe_gateup_bal faulted and was never fixed, so no other
+        // workgroup size is offered.
+        if (std::atoi(e) != kBalWaves) {
+            delete c;
+            return fail(LP_E_UNSUPPORTED, "LLMPAGER_HIP_BAL_WAVES: the balanced kernels run at " +
+                                              std::to_string(kBalWaves) + " waves only");
+        }
+    }
     const std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
     for (int m = 0; m < kNumModules; ++m) {
         const std::string path = dir + "/" + kModules[m];
@@ -265,14 +276,17 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
         }
     }
     {
-        // a workgroup size the loaded code object accepts (its launch bound)
-        int mt = 0;
-        if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[kGateupBal]) ==
-                hipSuccess &&
-            mt >= 64 * kBalMinWaves)
-            c->bal_waves = std::min(c->bal_waves, mt / 64);
-        else
-            c->bal_waves = kBalMinWaves;
+        // the loaded code objects must take the balanced kernels' fixed
+        // workgroup size (their launch bound)
+        for (Fn f : {kGateupBal, kDownBal, kDownBal6}) {
+            int mt = 0;
+            if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[f]) != hipSuccess ||
+                mt < 64 * kBalWaves) {
+                lp_destroy(c);
+                return fail(LP_E_LOAD, std::string(kSpecs[f].name) + ": code object does not take " +
+                                           std::to_string(64 * kBalWaves) + "-thread workgroups");
+            }
+        }
     }
     e = hipMalloc(reinterpret_cast<void**>(&c->sync), (size_t)kSyncSlots * kSyncWords * 4);
     if (e == hipSuccess) e = hipMemset(c->sync, 0, (size_t)kSyncSlots * kSyncWords * 4);
@@ -354,6 +368,18 @@ int lp_stream_create(lp_ctx* c, lp_stream* out) {
 
 int lp_stream_destroy(lp_ctx* c, lp_stream s) {
     if (int r = check_ctx(c)) return r;
+    {
+        // a stream that owns arrival counters gives them up once its work is
+        // done, so a stream created later may take them
+        std::lock_guard<std::mutex> g(c->sync_mu);
+        for (int i = 0; i < kSyncSlots; ++i) {
+            if (c->sync_used[i] && c->sync_owner[i] == (hipStream_t)s) {
+                HIPCHK(hipStreamSynchronize((hipStream_t)s));
+                c->sync_used[i] = false;
+                break;
+            }
+        }
+    }
     HIPCHK(hipStreamDestroy((hipStream_t)s));
     return LP_OK;
 }
@@ -665,6 +691,23 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->disp = ws + lay.disp;
 }
 
+// The stream's slot of arrival counters (taken on its first use), or -1
+// when every slot belongs to another stream.
+static int sync_slot(lp_ctx* c, lp_stream s) {
+    std::lock_guard<std::mutex> g(c->sync_mu);
+    const hipStream_t hs = (hipStream_t)s;
+    int free_slot = -1;
+    for (int i = 0; i < kSyncSlots; ++i) {
+        if (c->sync_used[i] && c->sync_owner[i] == hs) return i;
+        if (!c->sync_used[i] && free_slot < 0) free_slot = i;
+    }
+    if (free_slot >= 0) {
+        c->sync_used[free_slot] = true;
+        c->sync_owner[free_slot] = hs;
+    }
+    return free_slot;
+}
+
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
     // up to kTopkFusedMaxT tokens: one workgroup does both (one token per
@@ -702,8 +745,11 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
         return route_tail(c, ra, s);
     }
     // decode-sized batch: logits, top-k and dispatch in one launch
-    ra.sync = reinterpret_cast<uint64_t>(c->sync) +
-              (uint64_t)(c->sync_next.fetch_add(1) % kSyncSlots) * kSyncWords * 4;
+    const int slot = sync_slot(c, s);
+    if (slot < 0)
+        return fail(LP_E_UNSUPPORTED, "lp_moe_route: more than " + std::to_string(kSyncSlots) +
+                                          " streams have routed through this context");
+    ra.sync = reinterpret_cast<uint64_t>(c->sync) + (uint64_t)slot * kSyncWords * 4;
     dim3 g((unsigned)((d->experts + 8 * kRouteEPW - 1) / (8 * kRouteEPW)),
            (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
     return launch(c, kRouteFused, g, dim3(512), 0, s, ra);
@@ -731,7 +777,7 @@ static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
     const int nw = tile_steps_host(H) > 8 ? 16 : 8;
     return tile_steps_host(H) <= kGateupChunk && maxu <= kBalMaxU && maxv <= c->cus &&
-           (size_t)bal_lds_bytes(H, nw, c->bal_waves) <= c->max_lds && ga.L.slot_span < (1ull << 31) &&
+           (size_t)bal_lds_bytes(H, nw, kBalWaves) <= c->max_lds && ga.L.slot_span < (1ull << 31) &&
            (uint64_t)pairs * ga.L.inter * 4 < (1ull << 31);
 }
 
@@ -744,7 +790,7 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
     return pairs >= 32 && tile_steps_host(I) <= 8 && scales_in_lds(ga.L.group, I) && maxu <= kBalMaxU &&
            maxv <= c->cus &&
-           (size_t)bal_lds_bytes(I, 8, kBalMinWaves) <= c->max_lds &&
+           (size_t)bal_lds_bytes(I, 8, kBalWaves) <= c->max_lds &&
            (uint64_t)pairs * ga.L.hidden * 4 < (1ull << 31);
 }
 
@@ -766,8 +812,8 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
     };
     if (c->gateup_bal && gateup_balanced(c, ga, maxu)) {
         const int nw = tile_steps_host(H) > 8 ? 16 : 8;
-        if (int r = launch(c, kGateupBal, dim3((unsigned)c->cus), dim3(64 * c->bal_waves),
-                           (size_t)bal_lds_bytes(H, nw, c->bal_waves), s, ga))
+        if (int r = launch(c, kGateupBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
+                           (size_t)bal_lds_bytes(H, nw, kBalWaves), s, ga))
             return r;
     } else {
         const int w = pick_w(I, 1);
@@ -780,8 +826,8 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
     }
     const int steps = tile_steps_host(I);
     if (routed && c->gateup_bal && down_balanced(c, ga, maxu)) {
-        return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalMinWaves),
-                      (size_t)bal_lds_bytes(I, 8, kBalMinWaves), s, ga);
+        return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
+                      (size_t)bal_lds_bytes(I, 8, kBalWaves), s, ga);
     }
     const Fn f = steps <= kDownChunk ? kDown : kDownWide;
     const int tw = steps <= kDownChunk ? 2 : 1;

@@ -38,28 +38,6 @@ uint16_t lpo_f32_to_f16_ref(float x) {
     return (uint16_t)(sign | (uint16_t)((uint32_t)e << 10) | (uint16_t)((frac + 0x1000u) >> 13));
 }
 
-uint16_t lpo_f32_to_f16_rne(float x) {
-    uint32_t b = f2u(x);
-    uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
-    uint32_t a = b & 0x7FFFFFFFu;
-    if (a >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (a > 0x7F800000u ? 0x200u : 0u));
-    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to >= 65520 */
-    if (a < 0x38800000u) {                                   /* f16 subnormal range */
-        if (a < 0x33000000u) return sign;                    /* < 2^-25: rounds to 0 */
-        uint32_t e = a >> 23;
-        uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
-        uint32_t shift = 126 - e; /* value = m * 2^(e-150); f16 sub ulp = 2^-24 */
-        uint32_t q = m >> shift;
-        uint32_t rem = m & ((1u << shift) - 1u);
-        uint32_t half = 1u << (shift - 1);
-        if (rem > half || (rem == half && (q & 1u))) q++;
-        return (uint16_t)(sign | q);
-    }
-    uint32_t r = a + 0xFFFu + ((a >> 13) & 1u);
-    r -= 0x38000000u; /* rebias 127 -> 15 */
-    return (uint16_t)(sign | (r >> 13));
-}
-
 /* quant.rs:173-189 */
 float lpo_f16_to_f32(uint16_t h) {
     uint32_t sign = ((uint32_t)(h & 0x8000u)) << 16;
@@ -77,15 +55,6 @@ float lpo_f16_to_f32(uint16_t h) {
         bits = sign | ((exp + 127 - 15) << 23) | (frac << 13);
     }
     return u2f(bits);
-}
-
-/* kernels_bench.rs:16-18 */
-uint16_t lpo_bf16_halfup(float x) { return (uint16_t)((f2u(x) + 0x8000u) >> 16); }
-
-uint16_t lpo_bf16_rne(float x) {
-    uint32_t b = f2u(x);
-    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x40u);
-    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
 /* kernels_bench.rs:20-22, decode.cu:8-11 */

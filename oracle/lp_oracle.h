@@ -27,13 +27,8 @@ extern "C" {
  * including its rounding quirk: the rounding carry is OR-ed (not added) into
  * the exponent, and ties round half-up. */
 uint16_t lpo_f32_to_f16_ref(float x);
-/* IEEE round-to-nearest-even f32 -> f16 (used for synthetic scales). */
-uint16_t lpo_f32_to_f16_rne(float x);
 /* f16 bits -> f32, quant.rs:173-189 (exact). */
 float lpo_f16_to_f32(uint16_t h);
-/* bf16 half-up rounding, crates/llmpager-bench/src/kernels_bench.rs:16-18. */
-uint16_t lpo_bf16_halfup(float x);
-uint16_t lpo_bf16_rne(float x);
 float lpo_bf16_to_f32(uint16_t h);
 
 /* libm expf: what Rust's f32::exp lowers to on the reference host (glibc). */

@@ -38,10 +38,7 @@ def lib():
         vp, i32, f32, u64, sz = C.c_void_p, C.c_int, C.c_float, C.c_uint64, C.c_size_t
         sigs = {
             "lpo_f32_to_f16_ref": (C.c_uint16, [f32]),
-            "lpo_f32_to_f16_rne": (C.c_uint16, [f32]),
             "lpo_f16_to_f32": (f32, [C.c_uint16]),
-            "lpo_bf16_halfup": (C.c_uint16, [f32]),
-            "lpo_bf16_rne": (C.c_uint16, [f32]),
             "lpo_bf16_to_f32": (f32, [C.c_uint16]),
             "lpo_expf": (f32, [f32]),
             "lpo_expf_sweep": (None, [C.c_uint32, C.c_uint32, sz, vp]),

@@ -309,3 +309,54 @@ def test_layer_composition_small():
         assert np.array_equal(want, hout[t])
     h1 = O.moe_layer(desc, blobs, x, h, wave=1)[0]
     assert np.allclose(h1, hout, rtol=1e-6, atol=1e-6)
+
+
+def test_layer_composition_sigmoid_shared():
+    """The sigmoid + bias branch with renormalisation, scaling and min_weight,
+    plus the always-on shared MLP (kimi.rs:739-779): lpo_moe_layer equals the
+    composition of the pinned pieces -- routed picks summed in pick order and
+    added once, then the shared MLP's output added unweighted -- at any
+    thread count."""
+    import llmpager_amd as lp
+    H, I, E, k, g = 128, 64, 16, 4, 32
+    SI, SG = 128, 64
+    span = 16384
+    host = lp.synth_blobs(E, span, H, I, g, 6, 0)
+    bb = lp.blob_bytes(H, I, g)
+    blobs = [host[e * span: e * span + bb] for e in range(E)]
+    go, uo, do = lp.blob_offsets(H, I, g)
+    sgo, suo, sdo = lp.blob_offsets(H, SI, SG)
+    shared = lp.synth_blob(H, SI, SG, 6, 0, 1 << 20)
+    rw = lp.synth_bf16(E * H, 0.2, 6, 1)
+    bias = (np.random.default_rng(6).standard_normal(E) * 0.3).astype(np.float32)
+    scaling, min_w = 2.5, 0.6
+    desc = dict(hidden=H, inter=I, experts=E, top_k=k, group=g, gating=O.GATING_SIGMOID, renorm=True,
+                routed_scaling=scaling, min_weight=min_w, router_w=rw, router_bias=bias,
+                offsets=(go, uo, do))
+    sh = dict(blob=shared, inter=SI, group=SG, offsets=(sgo, suo, sdo))
+    T = 6
+    x = lp.synth_f32_bf16(T * H, 1.0, 6, 1).reshape(T, H)
+    h = lp.synth_f32_bf16(T * H, 1.0, 6, 2).reshape(T, H)
+    hout, logits, ids, w, cnt = O.moe_layer(desc, blobs, x, h, shared_blob=sh)
+    assert (cnt < k).any() and (cnt > 0).all()  # min_weight dropped some picks, not all
+    for t in range(T):
+        lg = O.router_logits(rw, x[t], E, H)
+        assert np.array_equal(lg, logits[t])
+        wi, ww = O.sigmoid_topk(lg, bias, k, True, scaling, min_w)
+        assert np.array_equal(wi, ids[t, :cnt[t]])
+        assert np.array_equal(ww.view(np.uint32), w[t, :cnt[t]].view(np.uint32))
+        ys = []
+        for e in wi:
+            b = blobs[e]
+            gg = O.q4_gemv(b[go:], x[t], I, H, g)
+            uu = O.q4_gemv(b[uo:], x[t], I, H, g)
+            ys.append(O.q4_gemv(b[do:], O.silu_mul(gg, uu), H, I, g))
+        want = O.moe_reduce(np.stack(ys), ww, h[t])
+        sg = O.q4_gemv(shared[sgo:], x[t], SI, H, SG)
+        su = O.q4_gemv(shared[suo:], x[t], SI, H, SG)
+        want = O.add(want, O.q4_gemv(shared[sdo:], O.silu_mul(sg, su), H, SI, SG))
+        assert np.array_equal(want, hout[t])
+    # the shared output is the exact difference a no-shared layer leaves
+    h_routed = O.moe_layer(desc, blobs, x, h)[0]
+    assert not np.array_equal(h_routed, hout)
+    assert np.array_equal(O.moe_layer(desc, blobs, x, h, shared_blob=sh, threads=4)[0], hout)
