@@ -185,6 +185,7 @@ def test_paged_stack_config4_shape(cuda):
     for t in range(steps):
         ht = dh + t * P_H * 4
         for l in range(layers):
+            cuda.sync_stream(s)    # the previous layer's update of ht is done
             x_in = cuda.download(ht, (1, P_H), np.float32)
             moe[l].route(ht, 1, ws, s)
             cuda.sync_stream(s)
@@ -194,6 +195,7 @@ def test_paged_stack_config4_shape(cuda):
             moe[l].resolve(1, ws, s)
             moe[l].experts(ht, ht, 1, ws, s)
             pg.release_after(got, s)
+            cuda.sync_stream(s)
             out = cuda.download(ht, (1, P_H), np.float32)
             assert moe[l].status(ws, 1, s)[1] == 0
             desc = dict(hidden=P_H, inter=P_I, experts=P_E, top_k=P_K, group=P_G, gating=0, renorm=True,
