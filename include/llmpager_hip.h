@@ -204,6 +204,20 @@ int lp_moe_resolve(lp_ctx* ctx, const lp_moe_layer_desc* d, int T, uint64_t work
  * written by the router kernel.  h: f32 [T, H], updated in place. */
 int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
+/* lp_moe_forward without a workspace argument and without any allocation:
+ * no counterpart in the reference.  For callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The workspace is a file-scope device array of
+ * LP_NOALLOC_SCRATCH_BYTES per device, held until the process ends; a layer
+ * whose lp_moe_ws_layout total exceeds it gets LP_E_UNSUPPORTED.  Every call
+ * on a device shares that device's array: calls that overlap on one device
+ * (different streams or unordered threads) race, so callers serialise them.
+ * The routing tables a call leaves in the array are those of the last call. */
+#define LP_NOALLOC_SCRATCH_BYTES (16ull << 20)
+int lp_moe_forward_noalloc(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
+                           lp_stream s);
+/* LP_NOALLOC_SCRATCH_BYTES, as built into the library. */
+uint64_t lp_noalloc_scratch_bytes(void);
 /* Synchronising readback of meta[0..1] (unique count, error flags). */
 int lp_moe_status_sync(lp_ctx* ctx, uint64_t workspace, const lp_moe_layer_desc* d, int T,
                        lp_stream s, int32_t* unique_count, int32_t* error_flags);

@@ -101,6 +101,8 @@ def _sig(lib):
         "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
         "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, vp]),
         "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
+        "lp_moe_forward_noalloc": (i32, [vp, P(LayerDesc), u64, u64, i32, vp]),
+        "lp_noalloc_scratch_bytes": (u64, []),
         "lp_moe_status_sync": (i32, [vp, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
         "lp_q4_bytes": (u64, [i32, i32, i32]),
         "lp_blob_bytes": (u64, [i32, i32, i32]),
@@ -474,6 +476,11 @@ class MoeLayer:
 
     def forward(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
         _check(lib().lp_moe_forward(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))
+
+    def forward_noalloc(self, x: int, h: int, T: int, stream=None) -> None:
+        """lp_moe_forward_noalloc: the layer with the library's built-in
+        per-device scratch as its workspace (no allocation)."""
+        _check(lib().lp_moe_forward_noalloc(self.cuda.ctx, C.byref(self.desc), x, h, T, stream))
 
     def status(self, ws: int, T: int, stream=None) -> tuple[int, int]:
         u, e = C.c_int32(), C.c_int32()

@@ -25,6 +25,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip", "lp_gemm.hip"]
 HOST_SOURCES = ["lp_runtime.cpp", "lp_synth.cpp", "lp_cache.cpp", "lp_pager.cpp"]
+HOST_HIP_SOURCES = ["lp_noalloc.hip"]
 
 # Packed-FP32 instructions stay off (the code is written for scalar fp32).
 HIPCC_FLAGS = [
@@ -63,14 +64,26 @@ def build_host() -> str:
     os.makedirs(OUT, exist_ok=True)
     dst = os.path.join(OUT, "libllmpager_hip.so")
     srcs = [os.path.join(CSRC, s) for s in HOST_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    # host-library sources that carry device code (a file-scope device array):
+    # compiled by hipcc into relocatable objects with an embedded gfx950 code
+    # object, then linked into the library with the rest
+    objs = []
+    for src in HOST_HIP_SOURCES:
+        obj = os.path.join(OUT, src.replace(".hip", ".o"))
+        _run([_hipcc(), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-c",
+              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+              "-Wno-unused-command-line-argument", "-I", CSRC, os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     cmd = [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off",
         "-Wall", "-Wno-unused-function",
         "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", CSRC,
-        *srcs, "-o", dst,
+        *srcs, *objs, "-o", dst,
         "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
     ]
     _run(cmd)
+    for obj in objs:
+        os.remove(obj)
     return dst
 
 

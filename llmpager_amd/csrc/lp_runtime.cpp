@@ -162,6 +162,8 @@ struct lp_ctx {
     bool gateup_bal = true;
 };
 
+int lpi::ctx_device(const lp_ctx* c) { return c ? c->device : -1; }
+
 namespace {
 
 hipEvent_t prof_event(lp_ctx* c) {
@@ -287,6 +289,10 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
                                            std::to_string(64 * kBalWaves) + "-thread workgroups");
             }
         }
+    }
+    if (int r = lpi::noalloc_setup(device)) {
+        lp_destroy(c);
+        return r;
     }
     e = hipMalloc(reinterpret_cast<void**>(&c->sync), (size_t)kSyncSlots * kSyncWords * 4);
     if (e == hipSuccess) e = hipMemset(c->sync, 0, (size_t)kSyncSlots * kSyncWords * 4);
