@@ -95,10 +95,11 @@ class Stack:
                 log(f"resident layers {l + 1}/{layers}")
         cuda.free_pinned(pin)
         self.layers = [lp.MoeLayer(cuda, d) for d in self.descs]
+        self.stack = lp.MoeStack(cuda, self.descs)
 
     def step(self, h: int, T: int, ws: int) -> None:
-        for L in self.layers:
-            L.forward(h, h, T, ws, self.s)
+        """One eager pass: the library's layer-stack driver (no host sync)."""
+        self.stack.forward(h, T, ws, self.s)
 
     def unique_counts(self, h: int, T: int, ws: int) -> list[int]:
         out = []
@@ -109,36 +110,57 @@ class Stack:
 
 
 def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
-    """Each step decodes a fresh batch of B tokens: step i works in place on
-    its own resident residual buffer (inputs already in HBM), restored from a
-    saved copy before every pass so the three passes see identical inputs."""
+    """Each step decodes a fresh batch of B tokens (resident in HBM): it
+    copies the step's B token rows into the stack's residual buffer and
+    replays the 48-layer stack captured once as a HIP graph
+    (lp_moe_stack_capture).  The same steps are then run eagerly through
+    lp_moe_stack_forward (its time is reported too), once more with every
+    kernel bracketed by events (per-kernel times), and once with a status
+    readback per layer (the measured unique-expert counts)."""
     import llmpager_amd as lp
     s = stack.s
-    ws = cuda.alloc_device(lp.ws_layout(stack.descs[0], B).total)
+    ws = cuda.alloc_device(stack.stack.ws_bytes(B))
     n = steps + warmup
     h0 = lp.synth_f32_bf16(n * B * H, 1.0, 0, 2)
     tok_bytes = B * H * 4
     saved = cuda.upload(h0, s)
     hbuf = cuda.alloc_device(h0.nbytes)
+    hcur = cuda.alloc_device(tok_bytes)
+    graph = stack.stack.capture(hcur, B, ws, s)
 
     def restore():
         cuda.dtod_async(hbuf, saved, h0.nbytes, s)
         cuda.sync()
 
+    def run_graph(i):
+        cuda.dtod_async(hcur, saved + i * tok_bytes, tok_bytes, s)
+        graph.launch(s)
+
     def run(i):
         stack.step(hbuf + i * tok_bytes, B, ws)
 
+    e0, e1 = cuda.event(), cuda.event()
+    for i in range(warmup):
+        run_graph(steps + i)
+    cuda.sync()
+    cuda.record_event(e0, s)
+    for i in range(steps):
+        run_graph(i)
+    cuda.record_event(e1, s)
+    cuda.sync()
+    ms = cuda.elapsed_ms(e0, e1)
+    # the same steps eagerly (host launches through lp_moe_stack_forward)
     restore()
     for i in range(warmup):
         run(steps + i)
-    e0, e1 = cuda.event(), cuda.event()
     cuda.sync()
     cuda.record_event(e0, s)
     for i in range(steps):
         run(i)
     cuda.record_event(e1, s)
     cuda.sync()
-    ms = cuda.elapsed_ms(e0, e1)
+    ms_eager = cuda.elapsed_ms(e0, e1)
+    graph.close()
     # the same steps again, each kernel bracketed by events on its stream
     restore()
     cuda.profile_reset()
@@ -151,7 +173,7 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
     # and once more with a status readback per layer: the measured unique counts
     restore()
     uniq = [stack.unique_counts(hbuf + i * tok_bytes, B, ws) for i in range(steps)]
-    for p in (ws, hbuf, saved):
+    for p in (ws, hbuf, saved, hcur):
         cuda.free_device(p)
     for e in (e0, e1):
         cuda.destroy_event(e)
@@ -167,7 +189,8 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
     dn_ms = sum(prof[kn][0] for kn in DOWN_KERNELS)
     dn_gbps = float(u.sum()) * REGION_BYTES / (dn_ms / 1e3) / 1e9 if dn_ms > 0 else 0.0
     res = dict(
-        batch=B, tok_s=B / sec, ms_per_step=sec * 1e3, unique_experts_per_layer=float(u.mean()),
+        batch=B, tok_s=B / sec, ms_per_step=sec * 1e3, ms_per_step_eager=ms_eager / steps,
+        tok_s_eager=B / (ms_eager / 1e3 / steps), unique_experts_per_layer=float(u.mean()),
         bytes_per_step=step_bytes, hbm_gbps=step_bytes / sec / 1e9,
         hbm_frac=step_bytes / sec / 1e9 / PEAK_GBPS,
         dominant=dict(kernel=dominant, launches=dom_n, avg_us=dom_ms * 1e3 / max(dom_n, 1),
@@ -176,7 +199,7 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
         down_gbps=dn_gbps,
         kernels_avg_us={k: v[0] * 1e3 / max(v[1], 1) for k, v in prof.items() if v[1]},
     )
-    log(f"B={B}: {res['tok_s']:.1f} tok/s, {res['ms_per_step']:.3f} ms/step, "
+    log(f"B={B}: {res['tok_s']:.1f} tok/s (graph; eager {res['tok_s_eager']:.1f}), {res['ms_per_step']:.3f} ms/step, "
         f"{res['hbm_gbps']:.0f} GB/s step, gate/up {dom_gbps:.0f} GB/s, down {dn_gbps:.0f} GB/s, "
         f"U={res['unique_experts_per_layer']:.1f}")
     return res
@@ -468,10 +491,40 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
     return out
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
-    """The oracle (oracle/, the CPU restatement of the reference path) on the
-    host cores: the first layers kept in host memory, B tokens, repeated until
-    about budget_s seconds of work; scaled to the 48-layer stack."""
+    """The reference CPU path on the host cores, in the same run: the oracle
+    (oracle/, the C restatement of the reference's arithmetic, decode.rs
+    routing with glibc expf, q4 dequant-then-dot GEMVs, pick-order combine)
+    over the first layers kept in host memory, scaled to the 48-layer stack.
+
+    Two variants, as the reference's own CPU path is timed:
+      ref-scalar  one thread, the reference's operation order;
+      ref-omp     the same arithmetic with OpenMP over each GEMV's rows, on
+                  every core this process may use (the GPU box gives each
+                  GPU a share of the host: OMP_NUM_THREADS, else the
+                  affinity mask).
+    Each at config 1 (one layer, one token) and at config 2's headline
+    batch B, until its share of about budget_s seconds is spent."""
     import llmpager_amd as lp
     path = os.path.join(ROOT, "oracle", "liblp_oracle.so")
     lib = C.CDLL(path)
@@ -490,7 +543,11 @@ def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
     lib.lpo_moe_layer.argtypes = [C.POINTER(Layer), vp, vp, C.c_int, vp, vp, vp, vp, vp, C.c_int,
                                   C.c_int]
     lib.lpo_moe_layer.restype = C.c_int
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    try:
+        share = len(os.sched_getaffinity(0))
+    except AttributeError:
+        share = os.cpu_count() or 1
+    all_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or share
     layers = []
     go, uo, do = stack.offsets
     for hb, rw in zip(stack.host, stack.router_host):
@@ -498,26 +555,41 @@ def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
         layers.append((Layer(hidden=H, inter=I, experts=E, top_k=K, group=G, gating=0, renorm=1,
                              routed_scaling=1.0, min_weight=0.0, router_w=rw.ctypes.data,
                              blobs=C.cast(ptrs, vp), gate_off=go, up_off=uo, down_off=do), ptrs))
-    h = lp.synth_f32_bf16(B * H, 1.0, 0, 2).reshape(B, H)
-    x = np.empty_like(h)
-    t0 = time.perf_counter()
-    n_layer_passes = 0
-    while True:
-        for L, _ in layers:
-            x[:] = h
-            rc = lib.lpo_moe_layer(C.byref(L), x.ctypes.data, h.ctypes.data, B, None, None, None,
-                                   None, None, 0, threads)
-            assert rc == 0
-            n_layer_passes += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
-    per_step = dt / n_layer_passes * LAYERS
-    log(f"cpu baseline: {n_layer_passes} layer passes of B={B} in {dt:.1f}s on {threads} threads")
-    return dict(value=B / per_step, unit="tok/s", cores=threads, kind="port",
-                sample=f"oracle lpo_moe_layer (reference semantics, OpenMP over rows) on "
-                       f"{n_layer_passes} layer passes of batch {B} over the first "
-                       f"{len(layers)} layers, scaled to the 48-layer stack")
+
+    def leg(batch: int, threads: int, seconds: float) -> dict:
+        h = lp.synth_f32_bf16(batch * H, 1.0, 0, 2).reshape(batch, H)
+        x = np.empty_like(h)
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for L, _ in layers:
+                x[:] = h
+                rc = lib.lpo_moe_layer(C.byref(L), x.ctypes.data, h.ctypes.data, batch, None, None, None,
+                                       None, None, 0, threads)
+                assert rc == 0
+                passes += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+        per_layer = dt / passes
+        per_step = per_layer * LAYERS
+        log(f"cpu baseline: batch {batch} on {threads} thread(s): {passes} layer passes in {dt:.1f} s, "
+            f"{per_layer * 1e3:.2f} ms per layer")
+        return dict(batch=batch, threads=threads, layer_passes=passes, seconds=round(dt, 3),
+                    ms_per_layer=per_layer * 1e3, tok_s=batch / per_step)
+
+    legs = {
+        "config1_scalar": leg(1, 1, budget_s * 0.1),
+        "config1_omp": leg(1, all_threads, budget_s * 0.1),
+        f"config2_b{B}_scalar": leg(B, 1, budget_s * 0.4),
+        f"config2_b{B}_omp": leg(B, all_threads, budget_s * 0.4),
+    }
+    head = legs[f"config2_b{B}_omp"]
+    return dict(value=head["tok_s"], unit="tok/s", cores=all_threads, kind="port",
+                sample=f"oracle lpo_moe_layer (the reference's CPU semantics in C, OpenMP over GEMV rows) "
+                       f"on {head['layer_passes']} layer passes of batch {B} over the first {len(layers)} "
+                       f"of the 48 layers, scaled to 48 layers; config-1 and single-thread legs in 'legs'",
+                cpu_model=cpu_model(), nproc=os.cpu_count(), affinity_cpus=share,
+                legs={k: _rounded(v) for k, v in legs.items()})
 
 
 def _rounded(d):
@@ -535,7 +607,7 @@ def main() -> int:
     ap.add_argument("--batches", default="1,8,32")
     ap.add_argument("--headline", type=int, default=32)
     ap.add_argument("--layers", type=int, default=LAYERS)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=24.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill leg")
     ap.add_argument("--prefill-only", action="store_true")

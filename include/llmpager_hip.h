@@ -204,6 +204,28 @@ int lp_moe_resolve(lp_ctx* ctx, const lp_moe_layer_desc* d, int T, uint64_t work
  * written by the router kernel.  h: f32 [T, H], updated in place. */
 int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, lp_stream s);
+/* The layer-stack driver (decode.rs:277-343 restricted to the MoE block;
+ * the batched layer loop decode.rs:431-532): lp_moe_forward over
+ * layers[0 .. n_layers), in order, the layer input being the residual itself
+ * (x = h; the router and expert GEMVs read h, the combine updates it in
+ * place).  One workspace serves every layer: size it for the largest
+ * lp_moe_ws_layout of the stack.  Every descriptor is checked before the
+ * first launch.  No host synchronisation between layers (the reference reads
+ * the router logits back and syncs once per layer, decode.rs:306-307). */
+int lp_moe_stack_forward(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
+                         uint64_t workspace, lp_stream s);
+/* The same stack captured once into a HIP graph (no counterpart in the
+ * reference, whose launches are issued one by one from the host): every
+ * kernel node keeps the arguments given here (h, T, workspace, the
+ * descriptors' tables), so a replay reruns exactly this stack.  s must be a
+ * created stream (the null stream cannot be captured); the routing kernels'
+ * arrival counters are those of s, so replays must not overlap one another
+ * or routing launches on s.  The graph holds no memset nodes. */
+typedef struct lp_graph lp_graph;
+int lp_moe_stack_capture(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
+                         uint64_t workspace, lp_stream s, lp_graph** out);
+int lp_graph_launch(lp_ctx* ctx, lp_graph* g, lp_stream s);
+void lp_graph_destroy(lp_graph* g);
 /* lp_moe_forward without a workspace argument and without any allocation:
  * no counterpart in the reference.  For callers that cannot call hipMalloc
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

@@ -102,6 +102,10 @@ def _sig(lib):
         "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, vp]),
         "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
         "lp_moe_forward_noalloc": (i32, [vp, P(LayerDesc), u64, u64, i32, vp]),
+        "lp_moe_stack_forward": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, vp]),
+        "lp_moe_stack_capture": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, vp, P(vp)]),
+        "lp_graph_launch": (i32, [vp, vp, vp]),
+        "lp_graph_destroy": (None, [vp]),
         "lp_noalloc_scratch_bytes": (u64, []),
         "lp_moe_status_sync": (i32, [vp, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
         "lp_q4_bytes": (u64, [i32, i32, i32]),
@@ -487,3 +491,40 @@ class MoeLayer:
         _check(lib().lp_moe_status_sync(self.cuda.ctx, ws, C.byref(self.desc), T, stream,
                                         C.byref(u), C.byref(e)))
         return u.value, e.value
+
+
+class MoeStack:
+    """The layer-stack driver (lp_moe_stack_forward): MoE layers in order over
+    one residual buffer, the layer input being the residual itself; `capture`
+    records the same launches into a replayable HIP graph."""
+
+    def __init__(self, cuda: Cuda, descs):
+        self.cuda = cuda
+        self.descs = (LayerDesc * len(descs))(*descs)
+        self.n = len(descs)
+
+    def ws_bytes(self, T: int) -> int:
+        return max(ws_layout(d, T).total for d in self.descs)
+
+    def forward(self, h: int, T: int, ws: int, stream=None) -> None:
+        _check(lib().lp_moe_stack_forward(self.cuda.ctx, self.descs, self.n, h, T, ws, stream))
+
+    def capture(self, h: int, T: int, ws: int, stream) -> "Graph":
+        g = C.c_void_p()
+        _check(lib().lp_moe_stack_capture(self.cuda.ctx, self.descs, self.n, h, T, ws, stream, C.byref(g)))
+        return Graph(self.cuda, g.value)
+
+
+class Graph:
+    """An instantiated HIP graph (lp_graph)."""
+
+    def __init__(self, cuda: Cuda, g: int):
+        self.cuda, self.g = cuda, g
+
+    def launch(self, stream) -> None:
+        _check(lib().lp_graph_launch(self.cuda.ctx, self.g, stream))
+
+    def close(self) -> None:
+        if self.g:
+            lib().lp_graph_destroy(self.g)
+            self.g = None

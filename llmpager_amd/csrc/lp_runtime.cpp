@@ -948,6 +948,70 @@ int lp_moe_forward(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h
     return experts_impl(c, d, x, h, T, ws, s, true);
 }
 
+int lp_moe_stack_forward(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
+                         uint64_t ws, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (!layers || n_layers <= 0) return fail(LP_E_INVALID, "lp_moe_stack_forward: no layers");
+    // every layer's shape is checked before the first launch, so a bad
+    // descriptor part-way down the stack leaves h untouched
+    for (int l = 0; l < n_layers; ++l)
+        if (int r = check_desc(c, &layers[l], T))
+            return fail(r, "lp_moe_stack_forward: layer " + std::to_string(l) + ": " + g_err);
+    for (int l = 0; l < n_layers; ++l)
+        if (int r = lp_moe_forward(c, &layers[l], h, h, T, ws, s)) return r;
+    return LP_OK;
+}
+
+struct lp_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int lp_moe_stack_capture(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
+                         uint64_t ws, lp_stream s, lp_graph** out) {
+    if (int r = check_ctx(c)) return r;
+    if (!out) return fail(LP_E_INVALID, "lp_moe_stack_capture: null out");
+    *out = nullptr;
+    if (!s) return fail(LP_E_INVALID, "lp_moe_stack_capture: the null stream cannot be captured");
+    // no profiling events inside the graph
+    const bool prof = c->prof;
+    c->prof = false;
+    HIPCHK(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal));
+    const int r = lp_moe_stack_forward(c, layers, n_layers, h, T, ws, s);
+    const std::string err = g_err;
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture((hipStream_t)s, &g);
+    c->prof = prof;
+    if (r != LP_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(r, err);
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    lp_graph* G = new lp_graph();
+    G->graph = g;
+    const hipError_t ie = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        lp_graph_destroy(G);
+        return hip_fail(ie, "hipGraphInstantiate");
+    }
+    *out = G;
+    return LP_OK;
+}
+
+int lp_graph_launch(lp_ctx* c, lp_graph* g, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (!g || !g->exec) return fail(LP_E_INVALID, "lp_graph_launch: null graph");
+    HIPCHK(hipGraphLaunch(g->exec, (hipStream_t)s));
+    return LP_OK;
+}
+
+void lp_graph_destroy(lp_graph* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T, lp_stream s,
                        int32_t* unique_count, int32_t* error_flags) {
     if (int r = check_ctx(c)) return r;
