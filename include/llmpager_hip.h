@@ -111,6 +111,64 @@ int lp_bf16_gemv(lp_ctx* ctx, uint64_t w, uint64_t x, uint64_t y, int rows, int 
 /* add (kernels.rs:239-250; decode.cu:131-140): a += b. */
 int lp_add(lp_ctx* ctx, uint64_t a, uint64_t b, int n, lp_stream s);
 
+/* ---- the rest of the decode step: kernels::Kernels (kernels.rs; decode.cu) -- */
+
+/* rmsnorm (kernels.rs:145-158; decode.cu:17-41): per row r < rows,
+ * y[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w; y may be x. */
+int lp_rmsnorm(lp_ctx* ctx, uint64_t x, uint64_t w, uint64_t y, int rows, int n, float eps, lp_stream s);
+/* scale_add (kernels.rs:161-173; decode.cu:44-53): a += s * b. */
+int lp_scale_add(lp_ctx* ctx, uint64_t a, uint64_t b, float s_, int n, lp_stream s);
+/* kv_append (kernels.rs:176-196; decode.cu:57-77, 242-261): k, v
+ * [kv_heads, head_dim] into caches [kv_heads, max_seq, head_dim] at pos;
+ * f16 != 0: IEEE half caches (round to nearest even). */
+int lp_kv_append(lp_ctx* ctx, uint64_t k, uint64_t v, uint64_t kcache, uint64_t vcache, int kv_heads,
+                 int head_dim, int pos, int max_seq, int f16, lp_stream s);
+/* rope (kernels.rs:252-266; decode.cu:145-167): NeoX rotate-half RoPE in
+ * place over [heads, head_dim], theta_i = pos * base^(-2i/head_dim). */
+int lp_rope(lp_ctx* ctx, uint64_t x, int heads, int head_dim, int pos, float base, lp_stream s);
+/* attn_decode (kernels.rs:269-292; decode.cu:172-325): one query per head
+ * [heads, head_dim] against caches [kv_heads, max_seq, head_dim] (f32, or
+ * half when f16 != 0), GQA head -> kv head h / (heads / kv_heads),
+ * positions < seq_len; scratch [heads, max_seq] f32 (split records). */
+int lp_attn_decode(lp_ctx* ctx, uint64_t q, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch,
+                   int heads, int kv_heads, int head_dim, int seq_len, int max_seq, float scale, int f16,
+                   lp_stream s);
+/* bf16_row (kernels.rs:294-306; decode.cu:328-339): out[:n] = f32(table[row, :n]). */
+int lp_bf16_row(lp_ctx* ctx, uint64_t table, int row, int n, uint64_t out, lp_stream s);
+
+/* ---- MLA absorbed decode: kernels::Kernels (kernels.rs; mla.cu) ----------- */
+
+/* mla_rope (kernels.rs:311-330; mla.cu:22-45): pairs (2i, 2i+1) of the
+ * slice at `offset` of n_vecs vectors (stride apart) rotate by
+ * pos * inv_freq[i] (device f32 [half]), both factors times mscale. */
+int lp_mla_rope(lp_ctx* ctx, uint64_t x, int n_vecs, int stride, int offset, int half, int pos,
+                uint64_t inv_freq, float mscale, lp_stream s);
+/* mla_attn_decode (kernels.rs:333-354; mla.cu:51-111): MQA decode over one
+ * f32 latent cache [max_seq, qk_dim] shared by all heads; scores use all
+ * qk_dim of q [heads, qk_dim], ctx [heads, c_dim] the first c_dim columns;
+ * scratch [heads, max_seq] f32. */
+int lp_mla_attn_decode(lp_ctx* ctx, uint64_t q, uint64_t cache, uint64_t ctx_out, uint64_t scratch, int heads,
+                       int qk_dim, int c_dim, int seq_len, int max_seq, float scale, lp_stream s);
+/* bf16_gemv_batch (kernels.rs:357-381; mla.cu:120-148): y_b = W_b x_b with
+ * W_b = w + b*w_stride bf16 [rows, cols], x_b = x + b*x_stride,
+ * y_b = y + b*y_stride (strides in elements). */
+int lp_bf16_gemv_batch(lp_ctx* ctx, uint64_t w, uint64_t w_stride, uint64_t x, int x_stride, uint64_t y,
+                       int y_stride, int rows, int cols, int batch, lp_stream s);
+/* strided_copy (kernels.rs:386-404; mla.cu:153-166). */
+int lp_strided_copy(lp_ctx* ctx, uint64_t src, int src_stride, int src_off, uint64_t dst, int dst_stride,
+                    int dst_off, int n_vecs, int n, lp_stream s);
+/* Batched MLA decode over bf16 latent caches (no reference counterpart: the
+ * reference calls mla_attn_decode once per sequence, kimi.rs:892-939):
+ * q f32 [batch][heads][qk_dim]; sequence b's cache rows (bf16 [seq, qk_dim])
+ * at cache + b * cache_stride bytes; seq_lens device i32 [batch], each in
+ * 1..max_seq; ctx_out f32 [batch][heads][c_dim].  heads <= 16, qk_dim =
+ * 32 x {3,4,6,8,12,16,18,20}, c_dim a multiple of 64 up to 512.  The
+ * workspace holds lp_mla_batch_ws_bytes(ctx, batch, c_dim, max_seq) bytes. */
+uint64_t lp_mla_batch_ws_bytes(lp_ctx* ctx, int batch, int c_dim, int max_seq);
+int lp_mla_attn_decode_batch(lp_ctx* ctx, uint64_t q, uint64_t cache, uint64_t cache_stride, uint64_t seq_lens,
+                             uint64_t ctx_out, uint64_t workspace, int batch, int heads, int qk_dim, int c_dim,
+                             int max_seq, float scale, lp_stream s);
+
 /* ---- fused MoE layer ------------------------------------------------------ */
 
 enum { LP_GATING_SOFTMAX = 0, LP_GATING_SIGMOID = 1 };

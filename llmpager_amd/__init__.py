@@ -95,6 +95,18 @@ def _sig(lib):
         "lp_silu_mul": (i32, [vp, u64, u64, u64, i32, vp]),
         "lp_bf16_gemv": (i32, [vp, u64, u64, u64, i32, i32, vp]),
         "lp_add": (i32, [vp, u64, u64, i32, vp]),
+        "lp_rmsnorm": (i32, [vp, u64, u64, u64, i32, i32, f32, vp]),
+        "lp_scale_add": (i32, [vp, u64, u64, f32, i32, vp]),
+        "lp_kv_append": (i32, [vp, u64, u64, u64, u64, i32, i32, i32, i32, i32, vp]),
+        "lp_rope": (i32, [vp, u64, i32, i32, i32, f32, vp]),
+        "lp_attn_decode": (i32, [vp, u64, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, i32, vp]),
+        "lp_bf16_row": (i32, [vp, u64, i32, i32, u64, vp]),
+        "lp_mla_rope": (i32, [vp, u64, i32, i32, i32, i32, i32, u64, f32, vp]),
+        "lp_mla_attn_decode": (i32, [vp, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
+        "lp_bf16_gemv_batch": (i32, [vp, u64, u64, u64, i32, u64, i32, i32, i32, i32, vp]),
+        "lp_strided_copy": (i32, [vp, u64, i32, i32, u64, i32, i32, i32, i32, vp]),
+        "lp_mla_batch_ws_bytes": (u64, [vp, i32, i32, i32]),
+        "lp_mla_attn_decode_batch": (i32, [vp, u64, u64, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
         "lp_moe_ws_layout_get": (i32, [P(LayerDesc), i32, P(WsLayout)]),
         "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
         "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
@@ -381,6 +393,58 @@ class Kernels:
 
     def add(self, a: int, b: int, n: int, stream=None) -> None:
         _check(lib().lp_add(self.cuda.ctx, a, b, n, stream))
+
+    # the rest of the decode step (kernels.rs, decode.cu)
+    def rmsnorm(self, x: int, w: int, y: int, rows: int, n: int, eps: float, stream=None) -> None:
+        _check(lib().lp_rmsnorm(self.cuda.ctx, x, w, y, rows, n, eps, stream))
+
+    def scale_add(self, a: int, b: int, s: float, n: int, stream=None) -> None:
+        _check(lib().lp_scale_add(self.cuda.ctx, a, b, s, n, stream))
+
+    def kv_append(self, k: int, v: int, kcache: int, vcache: int, kv_heads: int, head_dim: int, pos: int,
+                  max_seq: int, f16: bool, stream=None) -> None:
+        _check(lib().lp_kv_append(self.cuda.ctx, k, v, kcache, vcache, kv_heads, head_dim, pos, max_seq,
+                                  int(f16), stream))
+
+    def rope(self, x: int, heads: int, head_dim: int, pos: int, base: float, stream=None) -> None:
+        _check(lib().lp_rope(self.cuda.ctx, x, heads, head_dim, pos, base, stream))
+
+    def attn_decode(self, q: int, kcache: int, vcache: int, out: int, scratch: int, heads: int, kv_heads: int,
+                    head_dim: int, seq_len: int, max_seq: int, scale: float, f16: bool, stream=None) -> None:
+        _check(lib().lp_attn_decode(self.cuda.ctx, q, kcache, vcache, out, scratch, heads, kv_heads, head_dim,
+                                    seq_len, max_seq, scale, int(f16), stream))
+
+    def bf16_row(self, table: int, row: int, n: int, out: int, stream=None) -> None:
+        _check(lib().lp_bf16_row(self.cuda.ctx, table, row, n, out, stream))
+
+    # MLA absorbed decode (kernels.rs, mla.cu)
+    def mla_rope(self, x: int, n_vecs: int, stride: int, offset: int, half: int, pos: int, inv_freq: int,
+                 mscale: float, stream=None) -> None:
+        _check(lib().lp_mla_rope(self.cuda.ctx, x, n_vecs, stride, offset, half, pos, inv_freq, mscale, stream))
+
+    def mla_attn_decode(self, q: int, cache: int, ctx: int, scratch: int, heads: int, qk_dim: int, c_dim: int,
+                        seq_len: int, max_seq: int, scale: float, stream=None) -> None:
+        _check(lib().lp_mla_attn_decode(self.cuda.ctx, q, cache, ctx, scratch, heads, qk_dim, c_dim, seq_len,
+                                        max_seq, scale, stream))
+
+    def bf16_gemv_batch(self, w: int, w_stride: int, x: int, x_stride: int, y: int, y_stride: int, rows: int,
+                        cols: int, batch: int, stream=None) -> None:
+        _check(lib().lp_bf16_gemv_batch(self.cuda.ctx, w, w_stride, x, x_stride, y, y_stride, rows, cols, batch,
+                                        stream))
+
+    def strided_copy(self, src: int, src_stride: int, src_off: int, dst: int, dst_stride: int, dst_off: int,
+                     n_vecs: int, n: int, stream=None) -> None:
+        _check(lib().lp_strided_copy(self.cuda.ctx, src, src_stride, src_off, dst, dst_stride, dst_off, n_vecs, n,
+                                     stream))
+
+    def mla_batch_ws_bytes(self, batch: int, c_dim: int, max_seq: int) -> int:
+        return int(lib().lp_mla_batch_ws_bytes(self.cuda.ctx, batch, c_dim, max_seq))
+
+    def mla_attn_decode_batch(self, q: int, cache: int, cache_stride: int, seq_lens: int, ctx: int, ws: int,
+                              batch: int, heads: int, qk_dim: int, c_dim: int, max_seq: int, scale: float,
+                              stream=None) -> None:
+        _check(lib().lp_mla_attn_decode_batch(self.cuda.ctx, q, cache, cache_stride, seq_lens, ctx, ws, batch,
+                                              heads, qk_dim, c_dim, max_seq, scale, stream))
 
 
 # ---- fused MoE layer ----------------------------------------------------------------

@@ -104,6 +104,101 @@ struct ExpfSweepArgs {              // device expf check (no reference counterpa
     uint32_t first, stride;
 };
 
+// ---- the rest of the decode step (decode.cu) and MLA (mla.cu) ----------------
+
+struct RmsNormArgs {                // kernels.rs:145-158 (rmsnorm_f32); rows = grid
+    uint64_t x, w, y;
+    int32_t n;
+    float eps;
+};
+
+struct ScaleAddArgs {               // kernels.rs:161-173 (scale_add_f32)
+    uint64_t a, b;
+    float s;
+    int32_t n;
+};
+
+struct KvAppendArgs {               // kernels.rs:176-196 (kv_append_f32 / _f16)
+    uint64_t k, v, kcache, vcache;
+    int32_t kv_heads, head_dim, pos, max_seq;
+};
+
+struct RopeArgs {                   // kernels.rs:252-266 (rope_f32, NeoX rotate-half)
+    uint64_t x;
+    int32_t heads, head_dim, pos;
+    float base;
+};
+
+struct RowArgs {                    // kernels.rs:294-306 (bf16_row_to_f32)
+    uint64_t table, out;
+    int32_t row, n;
+};
+
+struct MlaRopeArgs {                // kernels.rs:311-330 (mla_rope_f32, interleaved pairs)
+    uint64_t x, inv_freq;
+    int32_t n_vecs, stride, offset, half, pos;
+    float mscale;
+};
+
+struct Bf16GemvBatchArgs {          // kernels.rs:357-381 (bf16_gemv_batch)
+    uint64_t w, w_stride, x, y;     // w_stride in elements
+    int32_t x_stride, y_stride, rows, cols, batch, pad0;
+};
+
+struct StridedCopyArgs {            // kernels.rs:386-404 (strided_copy_f32)
+    uint64_t src, dst;
+    int32_t src_stride, src_off, dst_stride, dst_off, n_vecs, n;
+};
+
+// Decode attention over one query per head (attn_decode_f32 / _f16kv,
+// kernels.rs:269-292; mla_attn_decode_f32, kernels.rs:333-354), split over
+// positions: split s of head h covers positions [s span, (s + 1) span) and
+// either writes the head's output (one split) or a partial record
+// {max, sum, acc[out_dim]} at scratch + h * scratch_stride + s * (out_dim + 2)
+// that lp_attn_combine merges.  Keys of head h: k + (h / group) * kv_stride,
+// row p at p * row_stride elements, `dot_dim` wide; values likewise from v,
+// `out_dim` wide.  GQA decode has k != v; MLA reads both from its one cache.
+constexpr int kAttnSpanMax = 1024;  // positions per split (LDS scores)
+struct AttnArgs {
+    uint64_t q, k, v, out, scratch;
+    uint64_t kv_stride;             // elements between kv heads' caches
+    int32_t heads, group;           // query heads, query heads per kv head
+    int32_t dot_dim, out_dim, row_stride, seq_len;
+    int32_t splits, span, scratch_stride;
+    float scale;
+    int32_t f16;                    // caches hold IEEE half (else f32)
+    int32_t pad0;
+};
+
+// The batched MLA decode of config 5 (no reference counterpart: the
+// reference runs mla_attn_decode_f32 once per sequence over an f32 cache):
+// bf16 latent caches, MFMA scores and context, splits of `span` positions
+// (a multiple of kMlaRows) per workgroup, partial records merged by
+// lp_mla_combine.  Heads <= 16, qk_dim a multiple of 32 (<= kMlaMaxQk),
+// c_dim a multiple of 64 (<= kMlaMaxC).
+constexpr int kMlaRows = 64;        // cache rows per chunk (4 waves x 16)
+constexpr int kMlaMaxQk = 640;
+constexpr int kMlaMaxC = 512;
+constexpr int kMlaColStride = 144;  // bytes per column of the transposed chunk: 64 rows + pad, 16-byte aligned
+// LDS: the query images (hi and lo bf16 in MFMA A order, 2 x qk/32 x 1 KB),
+// the transposed chunk (c_dim x kMlaColStride) and the scores (16 x 64 f32).
+LPK_HD constexpr int mla_lds_bytes(int qk_dim, int c_dim) {
+    return 2 * (qk_dim / 32) * 1024 + c_dim * kMlaColStride + 16 * kMlaRows * 4;
+}
+// Floats of one partial record: max[16], sum[16], acc[16][c_dim].
+LPK_HD constexpr int mla_part_floats(int c_dim) { return 32 + 16 * c_dim; }
+struct MlaBatchArgs {
+    uint64_t q;                     // f32 [batch][heads][qk_dim]
+    uint64_t cache;                 // bf16; sequence b's rows at cache + b * cache_stride bytes
+    uint64_t cache_stride;          // bytes
+    uint64_t seq_lens;              // i32 [batch]
+    uint64_t ctx;                   // f32 [batch][heads][c_dim]
+    uint64_t part;                  // f32 [batch][splits] partial records
+    int32_t batch, heads, qk_dim, c_dim, splits, span;
+    float scale;
+    int32_t pad0;
+};
+
 // ---- fused MoE layer ---------------------------------------------------------
 
 // Device-side view of one MoE layer's routing and expert tables.

@@ -80,6 +80,20 @@ enum Fn {
     kGateupBal,
     kDownBal,
     kDownBal6,
+    kRmsNorm,
+    kScaleAdd,
+    kKvAppendF32,
+    kKvAppendF16,
+    kRope,
+    kBf16Row,
+    kMlaRope,
+    kBf16GemvBatch,
+    kStridedCopy,
+    kAttnSplitF32,
+    kAttnSplitF16,
+    kAttnCombine,
+    kMlaSplit,
+    kMlaCombine,
     kNumFns
 };
 
@@ -105,10 +119,17 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
     {"lp_moe.hsaco", "lp_moe_gateup_bal"},
     {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
+    {"lp_attn.hsaco", "lp_rmsnorm"},       {"lp_attn.hsaco", "lp_scale_add"},
+    {"lp_attn.hsaco", "lp_kv_append_f32"}, {"lp_attn.hsaco", "lp_kv_append_f16"},
+    {"lp_attn.hsaco", "lp_rope"},          {"lp_attn.hsaco", "lp_bf16_row_to_f32"},
+    {"lp_attn.hsaco", "lp_mla_rope"},      {"lp_attn.hsaco", "lp_bf16_gemv_batch"},
+    {"lp_attn.hsaco", "lp_strided_copy"},  {"lp_attn.hsaco", "lp_attn_split_f32"},
+    {"lp_attn.hsaco", "lp_attn_split_f16"}, {"lp_attn.hsaco", "lp_attn_combine"},
+    {"lp_attn.hsaco", "lp_mla_split"},     {"lp_attn.hsaco", "lp_mla_combine"},
 };
 
-const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco"};
-constexpr int kNumModules = 3;
+const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco", "lp_attn.hsaco"};
+constexpr int kNumModules = 4;
 
 std::string library_dir() {
     Dl_info info;
@@ -548,6 +569,189 @@ int lp_add(lp_ctx* c, uint64_t pa, uint64_t pb, int n, lp_stream s) {
     if (n < 0) return fail(LP_E_INVALID, "add: negative size");
     AddArgs a{pa, pb, n, 0};
     return launch(c, kAdd, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+// ---- the rest of the decode step (decode.cu) and MLA (mla.cu) ----------------------
+
+int lp_rmsnorm(lp_ctx* c, uint64_t x, uint64_t w, uint64_t y, int rows, int n, float eps, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (rows < 0 || n <= 0) return fail(LP_E_INVALID, "rmsnorm: bad shape");
+    if (rows == 0) return LP_OK;
+    RmsNormArgs a{x, w, y, n, eps};
+    return launch(c, kRmsNorm, dim3((unsigned)rows), dim3(256), 0, s, a);
+}
+
+int lp_scale_add(lp_ctx* c, uint64_t pa, uint64_t pb, float sc, int n, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n < 0) return fail(LP_E_INVALID, "scale_add: negative size");
+    ScaleAddArgs a{pa, pb, sc, n};
+    return launch(c, kScaleAdd, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+int lp_kv_append(lp_ctx* c, uint64_t k, uint64_t v, uint64_t kcache, uint64_t vcache, int kv_heads,
+                 int head_dim, int pos, int max_seq, int f16, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (kv_heads <= 0 || head_dim <= 0 || pos < 0 || pos >= max_seq)
+        return fail(LP_E_INVALID, "kv_append: need 0 <= pos < max_seq and a non-empty head");
+    KvAppendArgs a{k, v, kcache, vcache, kv_heads, head_dim, pos, max_seq};
+    return launch(c, f16 ? kKvAppendF16 : kKvAppendF32, dim3(grid_1d(kv_heads * head_dim)), dim3(256), 0, s, a);
+}
+
+int lp_rope(lp_ctx* c, uint64_t x, int heads, int head_dim, int pos, float base, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (heads <= 0 || head_dim <= 0 || head_dim % 2) return fail(LP_E_INVALID, "rope: head_dim must be even");
+    RopeArgs a{x, heads, head_dim, pos, base};
+    return launch(c, kRope, dim3(grid_1d(heads * head_dim / 2)), dim3(256), 0, s, a);
+}
+
+int lp_bf16_row(lp_ctx* c, uint64_t table, int row, int n, uint64_t out, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (row < 0 || n < 0) return fail(LP_E_INVALID, "bf16_row: bad row or size");
+    RowArgs a{table, out, row, n};
+    return launch(c, kBf16Row, dim3(grid_1d(n)), dim3(256), 0, s, a);
+}
+
+int lp_mla_rope(lp_ctx* c, uint64_t x, int n_vecs, int stride, int offset, int half, int pos,
+                uint64_t inv_freq, float mscale, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n_vecs < 0 || half < 0 || offset < 0 || offset + 2 * half > stride)
+        return fail(LP_E_INVALID, "mla_rope: the rope slice must lie inside each vector");
+    MlaRopeArgs a{x, inv_freq, n_vecs, stride, offset, half, pos, mscale};
+    return launch(c, kMlaRope, dim3(grid_1d(n_vecs * half)), dim3(256), 0, s, a);
+}
+
+int lp_bf16_gemv_batch(lp_ctx* c, uint64_t w, uint64_t w_stride, uint64_t x, int x_stride, uint64_t y,
+                       int y_stride, int rows, int cols, int batch, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (rows <= 0 || cols <= 0 || batch <= 0 || x_stride < 0 || y_stride < 0)
+        return fail(LP_E_INVALID, "bf16_gemv_batch: bad shape");
+    Bf16GemvBatchArgs a{w, w_stride, x, y, x_stride, y_stride, rows, cols, batch, 0};
+    return launch(c, kBf16GemvBatch, dim3((unsigned)((rows + 3) / 4), (unsigned)batch), dim3(256), 0, s, a);
+}
+
+int lp_strided_copy(lp_ctx* c, uint64_t src, int src_stride, int src_off, uint64_t dst, int dst_stride,
+                    int dst_off, int n_vecs, int n, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (n_vecs < 0 || n < 0) return fail(LP_E_INVALID, "strided_copy: negative size");
+    StridedCopyArgs a{src, dst, src_stride, src_off, dst_stride, dst_off, n_vecs, n};
+    return launch(c, kStridedCopy, dim3(grid_1d(n_vecs * n)), dim3(256), 0, s, a);
+}
+
+// Split decode attention: splits so that the grid fills the chip, each split
+// at most kAttnSpanMax positions (and at least 32), the partial records in
+// the caller's scratch [heads, max_seq] (splits * (out_dim + 2) floats per
+// head); one split writes the output directly.
+static int attn_launch(lp_ctx* c, AttnArgs a, int max_seq, lp_stream s) {
+    if (a.seq_len < 1 || a.seq_len > max_seq) return fail(LP_E_INVALID, "attention: need 1 <= seq_len <= max_seq");
+    if (a.dot_dim < 1 || a.dot_dim > 1024 || a.out_dim < 1 || a.out_dim > a.row_stride || a.dot_dim > a.row_stride)
+        return fail(LP_E_UNSUPPORTED, "attention: dims must be 1..1024 and fit a cache row");
+    const int by_span = (a.seq_len + kAttnSpanMax - 1) / kAttnSpanMax;
+    const int by_scratch = max_seq / (a.out_dim + 2);
+    int splits = std::max(1, (2 * c->cus + a.heads - 1) / a.heads);
+    splits = std::min(splits, std::max(1, (a.seq_len + 31) / 32));
+    splits = std::min(splits, std::max(1, by_scratch));
+    splits = std::max(splits, by_span);
+    if (splits > 1 && splits > by_scratch)
+        return fail(LP_E_UNSUPPORTED, "attention: the scratch cannot hold the split records");
+    a.span = (a.seq_len + splits - 1) / splits;
+    a.splits = (a.seq_len + a.span - 1) / a.span;
+    a.scratch_stride = max_seq;
+    if (int r = launch(c, a.f16 ? kAttnSplitF16 : kAttnSplitF32, dim3((unsigned)a.heads, (unsigned)a.splits),
+                       dim3(256), 0, s, a))
+        return r;
+    if (a.splits == 1) return LP_OK;
+    return launch(c, kAttnCombine, dim3((unsigned)a.heads), dim3(256), 0, s, a);
+}
+
+int lp_attn_decode(lp_ctx* c, uint64_t q, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch,
+                   int heads, int kv_heads, int head_dim, int seq_len, int max_seq, float scale, int f16,
+                   lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+        return fail(LP_E_INVALID, "attn_decode: heads must be a multiple of kv_heads");
+    AttnArgs a{};
+    a.q = q;
+    a.k = kcache;
+    a.v = vcache;
+    a.out = out;
+    a.scratch = scratch;
+    a.kv_stride = (uint64_t)max_seq * head_dim;
+    a.heads = heads;
+    a.group = heads / kv_heads;
+    a.dot_dim = a.out_dim = a.row_stride = head_dim;
+    a.seq_len = seq_len;
+    a.scale = scale;
+    a.f16 = f16 != 0;
+    return attn_launch(c, a, max_seq, s);
+}
+
+int lp_mla_attn_decode(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t ctx, uint64_t scratch, int heads,
+                       int qk_dim, int c_dim, int seq_len, int max_seq, float scale, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (heads <= 0 || c_dim > qk_dim) return fail(LP_E_INVALID, "mla_attn_decode: need heads >= 1, c_dim <= qk_dim");
+    AttnArgs a{};
+    a.q = q;
+    a.k = a.v = cache;
+    a.out = ctx;
+    a.scratch = scratch;
+    a.kv_stride = 0;  // one cache shared by every head (MQA)
+    a.heads = heads;
+    a.group = heads;
+    a.dot_dim = qk_dim;
+    a.out_dim = c_dim;
+    a.row_stride = qk_dim;
+    a.seq_len = seq_len;
+    a.scale = scale;
+    return attn_launch(c, a, max_seq, s);
+}
+
+// The batched MLA decode's split plan: about one workgroup per CU over the
+// batch, each split a whole number of 64-row chunks.
+static void mla_plan(const lp_ctx* c, int batch, int max_seq, int* splits, int* span) {
+    const int chunks = std::max(1, (max_seq + kMlaRows - 1) / kMlaRows);
+    int sp = std::max(1, std::min(chunks, (c->cus + batch - 1) / batch));
+    const int per = (chunks + sp - 1) / sp;
+    *span = per * kMlaRows;
+    *splits = (max_seq + *span - 1) / *span;
+}
+
+uint64_t lp_mla_batch_ws_bytes(lp_ctx* c, int batch, int c_dim, int max_seq) {
+    if (!c || batch <= 0 || c_dim <= 0 || max_seq <= 0) return 0;
+    int splits, span;
+    mla_plan(c, batch, max_seq, &splits, &span);
+    return (uint64_t)batch * splits * mla_part_floats(c_dim) * 4;
+}
+
+int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cache_stride, uint64_t seq_lens,
+                             uint64_t ctx_out, uint64_t workspace, int batch, int heads, int qk_dim, int c_dim,
+                             int max_seq, float scale, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    const int steps = qk_dim / 32;
+    const bool steps_ok = qk_dim % 32 == 0 && (steps == 3 || steps == 4 || steps == 6 || steps == 8 || steps == 12 ||
+                                               steps == 16 || steps == 18 || steps == 20);
+    if (batch <= 0 || heads <= 0 || heads > 16 || !steps_ok || c_dim <= 0 || c_dim % 64 || c_dim > kMlaMaxC ||
+        c_dim > qk_dim || max_seq <= 0)
+        return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: heads <= 16, qk_dim = 32 x {3,4,6,8,12,16,18,20}, "
+                                      "c_dim a multiple of 64 up to 512 and <= qk_dim");
+    if ((uint64_t)max_seq * qk_dim * 2 >= (1ull << 31) || cache % 16 || cache_stride % 16)
+        return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: caches must be 16-byte aligned and under 2 GiB each");
+    const size_t lds = (size_t)mla_lds_bytes(qk_dim, c_dim);
+    if (lds > c->max_lds) return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: LDS");
+    MlaBatchArgs a{};
+    a.q = q;
+    a.cache = cache;
+    a.cache_stride = cache_stride;
+    a.seq_lens = seq_lens;
+    a.ctx = ctx_out;
+    a.part = workspace;
+    a.batch = batch;
+    a.heads = heads;
+    a.qk_dim = qk_dim;
+    a.c_dim = c_dim;
+    a.scale = scale;
+    mla_plan(c, batch, max_seq, &a.splits, &a.span);
+    if (int r = launch(c, kMlaSplit, dim3((unsigned)a.splits, (unsigned)batch), dim3(256), lds, s, a)) return r;
+    return launch(c, kMlaCombine, dim3((unsigned)batch), dim3(256), 0, s, a);
 }
 
 // ---- fused MoE layer --------------------------------------------------------------

@@ -457,3 +457,187 @@ int lpo_moe_layer(const lpo_layer* L, const float* x, float* h, int T,
     free(in_wave); free(used); free(uni);
     return rc;
 }
+
+/* ---- the rest of the decode step: CPU forms of the checks at
+ * crates/llmpager-bench/src/kernels_bench.rs:60-256 (decode.cu semantics) ---- */
+
+/* IEEE binary16, round to nearest even (what __float2half does in
+ * kv_append_f16, decode.cu:242-261). */
+uint16_t lpo_f32_to_f16_rne(float x) {
+    uint32_t b = f2u(x);
+    uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    uint32_t a = b & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (a > 0x7F800000u ? 0x200u : 0u));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* rounds to >= 65520: inf */
+    if (a < 0x38800000u) {                                   /* below the f16 normal range */
+        if (a < 0x33000000u) return sign;                    /* <= 2^-25: rounds to 0 */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126 - e; /* value = m * 2^(e-150); f16 subnormal unit = 2^-24 */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = a + 0xFFFu + ((a >> 13) & 1u);
+    r -= 0x38000000u; /* rebias 127 -> 15 */
+    return (uint16_t)(sign | (r >> 13));
+}
+
+/* kernels_bench.rs:64-101 (decode.cu:17-41): ms = sum(v*v)/n, inv =
+ * 1/sqrt(ms + eps), y = x*inv*w, per row. */
+void lpo_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * n;
+        float ms = -0.0f;
+        for (int i = 0; i < n; ++i) ms += xr[i] * xr[i];
+        ms /= (float)n;
+        const float inv = 1.0f / sqrtf(ms + eps);
+        for (int i = 0; i < n; ++i) y[(size_t)r * n + i] = xr[i] * inv * w[i];
+    }
+}
+
+/* kernels_bench.rs:104-113 (decode.cu:44-53) */
+void lpo_scale_add(float* a, const float* b, float s, int n) {
+    for (int i = 0; i < n; ++i) a[i] = a[i] + s * b[i];
+}
+
+/* kernels_bench.rs:116-135 (decode.cu:57-77, 242-261) */
+void lpo_kv_append(const float* k, const float* v, void* kcache, void* vcache, int kv_heads, int head_dim,
+                   int pos, int max_seq, int f16) {
+    for (int h = 0; h < kv_heads; ++h)
+        for (int d = 0; d < head_dim; ++d) {
+            const size_t dst = ((size_t)h * max_seq + pos) * head_dim + d;
+            const size_t src = (size_t)h * head_dim + d;
+            if (f16) {
+                ((uint16_t*)kcache)[dst] = lpo_f32_to_f16_rne(k[src]);
+                ((uint16_t*)vcache)[dst] = lpo_f32_to_f16_rne(v[src]);
+            } else {
+                ((float*)kcache)[dst] = k[src];
+                ((float*)vcache)[dst] = v[src];
+            }
+        }
+}
+
+/* kernels_bench.rs:171-192 (decode.cu:145-167, NeoX rotate-half): freq =
+ * base^(-2i/hd), (s, c) = sin_cos(pos * freq). */
+void lpo_rope(float* x, int heads, int head_dim, int pos, float base) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < heads; ++h)
+        for (int i = 0; i < half; ++i) {
+            const float freq = powf(base, -2.0f * (float)i / (float)head_dim);
+            const float ang = (float)pos * freq;
+            const float s = sinf(ang), c = cosf(ang);
+            float* p = x + (size_t)h * head_dim;
+            const float x1 = p[i], x2 = p[i + half];
+            p[i] = x1 * c - x2 * s;
+            p[i + half] = x1 * s + x2 * c;
+        }
+}
+
+static float cache_val(const void* c, size_t i, int f16) {
+    return f16 ? lpo_f16_to_f32(((const uint16_t*)c)[i]) : ((const float*)c)[i];
+}
+
+/* One query against rows [0, seq) of a cache (row stride `stride`): scores
+ * sum_d q[d]*k[d] (sequential) times scale; m = fold(f32::MIN, max); e =
+ * exp(s - m); z = sum e; out[d] = sum_p e_p / z * v[p][d]
+ * (kernels_bench.rs:205-220, 284-298). */
+static void attend(const float* q, const void* k, const void* v, size_t kv_off, int stride, int dot_dim,
+                   int out_dim, int seq, float scale, int f16, float* out, float* e) {
+    float m = -3.40282347e+38f;
+    for (int p = 0; p < seq; ++p) {
+        float dot = -0.0f;
+        for (int d = 0; d < dot_dim; ++d) dot += q[d] * cache_val(k, kv_off + (size_t)p * stride + d, f16);
+        e[p] = dot * scale;
+        m = e[p] > m ? e[p] : m;
+    }
+    float z = -0.0f;
+    for (int p = 0; p < seq; ++p) {
+        e[p] = expf(e[p] - m);
+        z += e[p];
+    }
+    for (int d = 0; d < out_dim; ++d) {
+        float acc = -0.0f;
+        for (int p = 0; p < seq; ++p) acc += e[p] / z * cache_val(v, kv_off + (size_t)p * stride + d, f16);
+        out[d] = acc;
+    }
+}
+
+/* kernels_bench.rs:195-249 (decode.cu:172-325): GQA decode attention over
+ * caches [kv_heads, max_seq, head_dim], f32 or IEEE half. */
+void lpo_attn_decode(const float* q, const void* kcache, const void* vcache, float* out, int heads, int kv_heads,
+                     int head_dim, int seq_len, int max_seq, float scale, int f16) {
+    float* e = (float*)malloc(sizeof(float) * (size_t)(seq_len > 0 ? seq_len : 1));
+    for (int h = 0; h < heads; ++h) {
+        const int kv = h / (heads / kv_heads);
+        attend(q + (size_t)h * head_dim, kcache, vcache, (size_t)kv * max_seq * head_dim, head_dim, head_dim,
+               head_dim, seq_len, scale, f16, out + (size_t)h * head_dim, e);
+    }
+    free(e);
+}
+
+/* kernels_bench.rs:250-256 (decode.cu:328-339) */
+void lpo_bf16_row(const uint16_t* table, int row, int n, float* out) {
+    for (int i = 0; i < n; ++i) out[i] = lpo_bf16_to_f32(table[(size_t)row * n + i]);
+}
+
+/* ---- MLA: CPU forms of kernels_bench.rs:258-351 (mla.cu semantics) ---- */
+
+/* kernels_bench.rs:258-282 (mla.cu:22-45) */
+void lpo_mla_rope(float* x, int n_vecs, int stride, int offset, int half, int pos, const float* inv_freq,
+                  float mscale) {
+    for (int v = 0; v < n_vecs; ++v)
+        for (int i = 0; i < half; ++i) {
+            const float ang = (float)pos * inv_freq[i];
+            const float s = sinf(ang) * mscale, c = cosf(ang) * mscale;
+            float* p = x + (size_t)v * stride + offset + 2 * i;
+            const float x1 = p[0], x2 = p[1];
+            p[0] = x1 * c - x2 * s;
+            p[1] = x1 * s + x2 * c;
+        }
+}
+
+/* kernels_bench.rs:284-310 (mla.cu:51-111): MQA over one latent cache
+ * [seq, qk_dim] (f32, or bf16 when cache_bf16), ctx [heads, c_dim].  Heads
+ * in parallel over `threads`. */
+void lpo_mla_attn_decode(const float* q, const void* cache, int cache_bf16, float* ctx, int heads, int qk_dim,
+                         int c_dim, int seq_len, float scale, int threads) {
+    if (cache_bf16) {
+        /* widen once: the bf16 values are exact in f32 */
+        float* wide = (float*)malloc(sizeof(float) * (size_t)seq_len * qk_dim);
+        for (size_t i = 0; i < (size_t)seq_len * qk_dim; ++i) wide[i] = lpo_bf16_to_f32(((const uint16_t*)cache)[i]);
+        lpo_mla_attn_decode(q, wide, 0, ctx, heads, qk_dim, c_dim, seq_len, scale, threads);
+        free(wide);
+        return;
+    }
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int h = 0; h < heads; ++h) {
+        float* e = (float*)malloc(sizeof(float) * (size_t)(seq_len > 0 ? seq_len : 1));
+        attend(q + (size_t)h * qk_dim, cache, cache, 0, qk_dim, qk_dim, c_dim, seq_len, scale, 0,
+               ctx + (size_t)h * c_dim, e);
+        free(e);
+    }
+}
+
+/* kernels_bench.rs:313-330 (mla.cu:120-148) */
+void lpo_bf16_gemv_batch(const uint16_t* w, uint64_t w_stride, const float* x, int x_stride, float* y,
+                         int y_stride, int rows, int cols, int batch) {
+    for (int b = 0; b < batch; ++b)
+        for (int r = 0; r < rows; ++r) {
+            const uint16_t* wr = w + (size_t)b * w_stride + (size_t)r * cols;
+            const float* xb = x + (size_t)b * x_stride;
+            float acc = -0.0f;
+            for (int c = 0; c < cols; ++c) acc += lpo_bf16_to_f32(wr[c]) * xb[c];
+            y[(size_t)b * y_stride + r] = acc;
+        }
+}
+
+/* kernels_bench.rs:332-344 (mla.cu:153-166) */
+void lpo_strided_copy(const float* src, int src_stride, int src_off, float* dst, int dst_stride, int dst_off,
+                      int n_vecs, int n) {
+    for (int v = 0; v < n_vecs; ++v)
+        for (int i = 0; i < n; ++i)
+            dst[(size_t)v * dst_stride + dst_off + i] = src[(size_t)v * src_stride + src_off + i];
+}

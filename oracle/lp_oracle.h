@@ -144,6 +144,30 @@ int lpo_moe_layer(const lpo_layer* L, const float* x, float* h, int T,
                   int32_t* ids_out, float* w_out, int32_t* cnt_out, int wave,
                   int threads);
 
+/* ---- the rest of the decode step (kernels_bench.rs:60-256; decode.cu) --- */
+
+/* IEEE round-to-nearest-even f32 -> f16 bits (__float2half). */
+uint16_t lpo_f32_to_f16_rne(float x);
+void lpo_rmsnorm(const float* x, const float* w, float* y, int rows, int n, float eps);
+void lpo_scale_add(float* a, const float* b, float s, int n);
+void lpo_kv_append(const float* k, const float* v, void* kcache, void* vcache, int kv_heads, int head_dim,
+                   int pos, int max_seq, int f16);
+void lpo_rope(float* x, int heads, int head_dim, int pos, float base);
+void lpo_attn_decode(const float* q, const void* kcache, const void* vcache, float* out, int heads, int kv_heads,
+                     int head_dim, int seq_len, int max_seq, float scale, int f16);
+void lpo_bf16_row(const uint16_t* table, int row, int n, float* out);
+
+/* ---- MLA absorbed decode (kernels_bench.rs:258-351; mla.cu) -------------- */
+
+void lpo_mla_rope(float* x, int n_vecs, int stride, int offset, int half, int pos, const float* inv_freq,
+                  float mscale);
+void lpo_mla_attn_decode(const float* q, const void* cache, int cache_bf16, float* ctx, int heads, int qk_dim,
+                         int c_dim, int seq_len, float scale, int threads);
+void lpo_bf16_gemv_batch(const uint16_t* w, uint64_t w_stride, const float* x, int x_stride, float* y,
+                         int y_stride, int rows, int cols, int batch);
+void lpo_strided_copy(const float* src, int src_stride, int src_off, float* dst, int dst_stride, int dst_off,
+                      int n_vecs, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,17 @@ def lib():
             "lpo_router_logits": (None, [vp, vp, vp, i32, i32]),
             "lpo_moe_dispatch": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp]),
             "lpo_moe_layer": (i32, [C.POINTER(Layer), vp, vp, i32, vp, vp, vp, vp, vp, i32, i32]),
+            "lpo_f32_to_f16_rne": (C.c_uint16, [f32]),
+            "lpo_rmsnorm": (None, [vp, vp, vp, i32, i32, f32]),
+            "lpo_scale_add": (None, [vp, vp, f32, i32]),
+            "lpo_kv_append": (None, [vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+            "lpo_rope": (None, [vp, i32, i32, i32, f32]),
+            "lpo_attn_decode": (None, [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32]),
+            "lpo_bf16_row": (None, [vp, i32, i32, vp]),
+            "lpo_mla_rope": (None, [vp, i32, i32, i32, i32, i32, vp, f32]),
+            "lpo_mla_attn_decode": (None, [vp, vp, i32, vp, i32, i32, i32, i32, f32, i32]),
+            "lpo_bf16_gemv_batch": (None, [vp, u64, vp, i32, vp, i32, i32, i32, i32]),
+            "lpo_strided_copy": (None, [vp, i32, i32, vp, i32, i32, i32, i32]),
         }
         for n, (r, a) in sigs.items():
             fn = getattr(L, n)
@@ -219,3 +230,78 @@ def moe_layer(desc: dict, blobs: list, x: np.ndarray, h: np.ndarray, logits_in=N
     if rc != 0:
         raise RuntimeError("oracle: routed expert without a blob")
     return hout, logits, ids, w, cnt
+
+
+# ---- the rest of the decode step and MLA (kernels_bench.rs CPU forms) --------
+
+def f32_to_f16_rne(x: float) -> int:
+    return lib().lpo_f32_to_f16_rne(x)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def rmsnorm(x, w, rows, n, eps):
+    x, w = _f32(x), _f32(w)
+    y = np.zeros(rows * n, np.float32)
+    lib().lpo_rmsnorm(_p(x), _p(w), _p(y), rows, n, eps)
+    return y
+
+
+def scale_add(a, b, s):
+    a = np.array(a, np.float32, copy=True)
+    lib().lpo_scale_add(_p(a), _p(_f32(b)), s, a.size)
+    return a
+
+
+def kv_append(k, v, kcache, vcache, kv_heads, head_dim, pos, max_seq, f16):
+    kc, vc = np.array(kcache, copy=True), np.array(vcache, copy=True)
+    lib().lpo_kv_append(_p(_f32(k)), _p(_f32(v)), _p(kc), _p(vc), kv_heads, head_dim, pos, max_seq, int(f16))
+    return kc, vc
+
+
+def rope(x, heads, head_dim, pos, base):
+    x = np.array(x, np.float32, copy=True)
+    lib().lpo_rope(_p(x), heads, head_dim, pos, base)
+    return x
+
+
+def attn_decode(q, kcache, vcache, heads, kv_heads, head_dim, seq_len, max_seq, scale, f16):
+    out = np.zeros(heads * head_dim, np.float32)
+    lib().lpo_attn_decode(_p(_f32(q)), _p(np.ascontiguousarray(kcache)), _p(np.ascontiguousarray(vcache)), _p(out),
+                          heads, kv_heads, head_dim, seq_len, max_seq, scale, int(f16))
+    return out
+
+
+def bf16_row(table, row, n):
+    out = np.zeros(n, np.float32)
+    lib().lpo_bf16_row(_p(np.ascontiguousarray(table, np.uint16)), row, n, _p(out))
+    return out
+
+
+def mla_rope(x, n_vecs, stride, offset, half, pos, inv_freq, mscale):
+    x = np.array(x, np.float32, copy=True)
+    lib().lpo_mla_rope(_p(x), n_vecs, stride, offset, half, pos, _p(_f32(inv_freq)), mscale)
+    return x
+
+
+def mla_attn_decode(q, cache, heads, qk_dim, c_dim, seq_len, scale, bf16=False, threads=8):
+    ctx = np.zeros(heads * c_dim, np.float32)
+    c = np.ascontiguousarray(cache, np.uint16 if bf16 else np.float32)
+    lib().lpo_mla_attn_decode(_p(_f32(q)), _p(c), int(bf16), _p(ctx), heads, qk_dim, c_dim, seq_len, scale,
+                              threads)
+    return ctx
+
+
+def bf16_gemv_batch(w, w_stride, x, x_stride, y_stride, rows, cols, batch):
+    y = np.zeros(max(1, (batch - 1) * y_stride + rows), np.float32)
+    lib().lpo_bf16_gemv_batch(_p(np.ascontiguousarray(w, np.uint16)), w_stride, _p(_f32(x)), x_stride, _p(y),
+                              y_stride, rows, cols, batch)
+    return y
+
+
+def strided_copy(src, src_stride, src_off, dst, dst_stride, dst_off, n_vecs, n):
+    dst = np.array(dst, np.float32, copy=True)
+    lib().lpo_strided_copy(_p(_f32(src)), src_stride, src_off, _p(dst), dst_stride, dst_off, n_vecs, n)
+    return dst
