@@ -491,6 +491,77 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
     return out
 
 
+# BASELINE config 5's attention half: MLA absorbed decode over bf16 latent KV.
+M_HEADS, M_QK, M_C, M_CTX = 16, 576, 512, 4096
+
+
+def run_mla(cuda, s, batches, steps: int) -> dict:
+    """Config 5's MLA decode: 16 heads, latent rows [kv_lora 512 | rope 64]
+    in bf16 N(0, 1), context 4096, batch 1 and 16, through
+    lp_mla_attn_decode_batch (scores and context on MFMA, split over
+    positions, partial records merged).  Each call reads every sequence's
+    latent cache once: batch x 4096 x 576 x 2 bytes, the algorithmic bytes;
+    calls rotate over enough distinct caches (>= 512 MB) that the 256 MB
+    MALL cannot serve repeats.  Timed with events over `steps` x rotations
+    calls; the kernels' own times come from the profile events."""
+    import llmpager_amd as lp
+    K = lp.Kernels(cuda)
+    out = {}
+    row_bytes = M_QK * 2
+    for B in batches:
+        seq_bytes = M_CTX * row_bytes
+        sets = max(2, (512 << 20) // (B * seq_bytes) + 1)
+        rng = np.random.default_rng(B)
+        caches = []
+        for _ in range(sets):
+            c = rng.standard_normal(B * M_CTX * M_QK).astype(np.float32)
+            caches.append(cuda.upload(((c.view(np.uint32) + 0x8000) >> 16).astype(np.uint16), s))
+        q = cuda.upload((rng.standard_normal(B * M_HEADS * M_QK) * 0.05).astype(np.float32), s)
+        sl = cuda.upload(np.full(B, M_CTX, np.int32), s)
+        ctx = cuda.alloc_device(B * M_HEADS * M_C * 4)
+        ws = cuda.alloc_device(K.mla_batch_ws_bytes(B, M_C, M_CTX))
+        scale = 1.0 / np.sqrt(192.0)
+
+        def call(i):
+            K.mla_attn_decode_batch(q, caches[i % sets], seq_bytes, sl, ctx, ws, B, M_HEADS, M_QK, M_C, M_CTX,
+                                    scale, s)
+
+        for i in range(sets):
+            call(i)
+        n = steps * sets
+        e0, e1 = cuda.event(), cuda.event()
+        cuda.sync()
+        cuda.record_event(e0, s)
+        for i in range(n):
+            call(i)
+        cuda.record_event(e1, s)
+        cuda.sync()
+        us = cuda.elapsed_ms(e0, e1) * 1e3 / n
+        cuda.profile_reset()
+        cuda.profile(True)
+        for i in range(n):
+            call(i)
+        cuda.sync()
+        split_ms, split_n = cuda.profile_read("lp_mla_split")
+        comb_ms, comb_n = cuda.profile_read("lp_mla_combine")
+        cuda.profile(False)
+        kv_bytes = B * M_CTX * row_bytes
+        split_us = split_ms * 1e3 / max(split_n, 1)
+        out[str(B)] = dict(batch=B, context=M_CTX, us_per_call=us, latent_kv_bytes=kv_bytes,
+                           hbm_gbps=kv_bytes / (us * 1e-6) / 1e9, hbm_frac=kv_bytes / (us * 1e-6) / 1e9 / PEAK_GBPS,
+                           split_us=split_us, combine_us=comb_ms * 1e3 / max(comb_n, 1),
+                           split_gbps=kv_bytes / (split_us * 1e-6) / 1e9 if split_us > 0 else 0.0,
+                           split_frac=kv_bytes / (split_us * 1e-6) / 1e9 / PEAK_GBPS if split_us > 0 else 0.0)
+        log(f"MLA decode B={B}, context {M_CTX}: {us:.1f} us per call, {out[str(B)]['hbm_gbps']:.0f} GB/s of latent "
+            f"KV ({100 * out[str(B)]['hbm_frac']:.1f}% of 8 TB/s); split kernel {split_us:.1f} us, combine "
+            f"{out[str(B)]['combine_us']:.1f} us")
+        for p in caches + [q, sl, ctx, ws]:
+            cuda.free_device(p)
+        for e in (e0, e1):
+            cuda.destroy_event(e)
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
     import subprocess
@@ -614,6 +685,8 @@ def main() -> int:
     ap.add_argument("--no-paged", action="store_true", help="skip the config-4 paging leg")
     ap.add_argument("--no-shared", action="store_true", help="skip the config-5 shared-expert leg")
     ap.add_argument("--paged-only", action="store_true")
+    ap.add_argument("--no-mla", action="store_true", help="skip the config-5 MLA attention leg")
+    ap.add_argument("--mla-only", action="store_true")
     ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
     ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
     a = ap.parse_args()
@@ -637,7 +710,12 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
-    prefill = None if a.no_prefill else run_prefill(cuda, s, a.steps, a.warmup)
+    mla = None if a.no_mla else run_mla(cuda, s, (1, 16), a.steps)
+    if a.mla_only:
+        print(json.dumps({"mla": _rounded(mla)}), flush=True)
+        cuda.close()
+        return 0
+    prefill = None if a.no_prefill or a.paged_only else run_prefill(cuda, s, a.steps, a.warmup)
     if a.prefill_only:
         print(json.dumps({"prefill": prefill}), flush=True)
         cuda.close()
@@ -692,6 +770,7 @@ def main() -> int:
         "prefill": None if prefill is None else _rounded(prefill),
         "paged": None if paged is None else _rounded(paged),
         "shared": None if shared is None else _rounded(shared),
+        "mla": None if mla is None else _rounded(mla),
         "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
                              for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
                     | {"gateup_gbps": round(r["dominant"]["gbps"], 1),

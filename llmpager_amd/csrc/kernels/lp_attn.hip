@@ -321,7 +321,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_attn_combine(const AttnArgs
 //           hi + lo, two MFMAs per step, so the query keeps 16 significant
 //           bits) and 16 cache rows per wave as B, loaded as 16-byte row
 //           pieces straight into registers (the next chunk's loads are in
-//           flight while this chunk is finished);
+//           flight while this chunk's softmax and context are computed);
 //   softmax per head over the chunk, the running max and sum rescaled;
 //   context ctx[h][d] += sum_r p[h][r] row_r[d]: the same MFMA with the
 //           probabilities (hi + lo) as A and the chunk, stored transposed
@@ -370,14 +370,6 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
     const int nchunks = p1 > p0 ? (p1 - p0 + kMlaRows - 1) / kMlaRows : 0;
     // the query's hi / lo images in A order: step j, lane (m, kb) holds
     // q[m][32 j + 8 kb .. + 7]; heads past H are zero
-    const float* q = dptr<const float>(a.q) + (size_t)b * H * QK;
-    for (int u = tid; u < STEPS * 64; u += 256) {
-        const int j = u >> 6, l = u & 63, m = l & 15, k8 = l >> 4;
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = m < H ? q[(size_t)m * QK + 32 * j + 8 * k8 + i] : 0.0f;
-        split8(v, qhi[u], qlo[u]);
-    }
     // the sequence's valid rows through a raw buffer: rows past p1 read zero
     const uint64_t cb = a.cache + (uint64_t)b * a.cache_stride;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -394,8 +386,9 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
     f32x4_t acc[kMlaMaxC / 64];
 #pragma unroll
     for (int c = 0; c < kMlaMaxC / 64; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    __syncthreads();  // the query images
-    auto chunk = [&](uint4 (&Bc)[STEPS], uint4 (&Bn)[STEPS], int c) {
+    // one register buffer: a chunk's rows are dead once its scores are made,
+    // so the next chunk's loads go into the same registers at that point
+    auto chunk = [&](uint4 (&Bc)[STEPS], int c) {
         // scores of rows 16 wave + n; the chunk's first c_dim columns stored
         // transposed (column-major, 64 rows per column) for the context pass
         f32x4_t s4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -415,7 +408,7 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
                 }
             }
         }
-        if (c + 1 < nchunks) load_chunk(Bn, c + 1);
+        if (c + 1 < nchunks) load_chunk(Bc, c + 1);
         const bool rvalid = p0 + c * kMlaRows + rl < p1;
 #pragma unroll
         for (int v = 0; v < 4; ++v) sl[(4 * kb + v) * kMlaRows + rl] = rvalid ? s4[v] * a.scale : -INFINITY;
@@ -473,13 +466,35 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
         }
         __syncthreads();  // the chunk's LDS is free for the next one
     };
-    uint4 B0[STEPS], B1[STEPS];
+    // the first chunk's rows are in flight while the query images are made
+    uint4 B0[STEPS];
     if (nchunks > 0) load_chunk(B0, 0);
-    for (int c = 0; c < nchunks; c += 2) {
-        chunk(B0, B1, c);
-        if (c + 1 >= nchunks) break;
-        chunk(B1, B0, c + 1);
+    {
+        constexpr int kUnits = (STEPS * 64 + 255) / 256;  // query pieces per thread
+        const float* q = dptr<const float>(a.q) + (size_t)b * H * QK;
+        float4 v4[kUnits][2];
+#pragma unroll
+        for (int r = 0; r < kUnits; ++r) {
+            const int u = tid + 256 * r, j = u >> 6, l = u & 63, m = l & 15, k8 = l >> 4;
+            v4[r][0] = v4[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (u < STEPS * 64 && m < H) {
+                const float4* src = reinterpret_cast<const float4*>(q + (size_t)m * QK + 32 * j + 8 * k8);
+                v4[r][0] = src[0];
+                v4[r][1] = src[1];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kUnits; ++r) {
+            const int u = tid + 256 * r;
+            if (u < STEPS * 64) {
+                const float v[8] = {v4[r][0].x, v4[r][0].y, v4[r][0].z, v4[r][0].w,
+                                    v4[r][1].x, v4[r][1].y, v4[r][1].z, v4[r][1].w};
+                split8(v, qhi[u], qlo[u]);
+            }
+        }
     }
+    __syncthreads();  // the query images
+    for (int c = 0; c < nchunks; ++c) chunk(B0, c);
     // the partial record
     float* part = dptr<float>(a.part) + ((size_t)b * a.splits + sp) * mla_part_floats(CD);
     if (wave == 0 && lane < 16) {
@@ -512,23 +527,41 @@ extern "C" __global__ void __launch_bounds__(256) lp_mla_split(const MlaBatchArg
     }
 }
 
-// ctx[b][h][d] from the splits' records.  Grid batch, 256 threads.
+// ctx[b][h][d] from the splits' records.  Grid (heads, batch, c_dim / 64),
+// 256 threads: the weights e^(m_s - M) / sum_s e^(m_s - M) l_s go to LDS once
+// per workgroup, then thread (column d, group g) sums the splits s = g, g + 4,
+// ... of its column (four loads in flight per step) and the four groups'
+// sums meet in LDS.
 extern "C" __global__ void __launch_bounds__(256) lp_mla_combine(const MlaBatchArgs a) {
-    const int b = blockIdx.x;
+    __shared__ float wsh[kMlaMaxSplits];
+    __shared__ float red[4];
+    __shared__ float part_sum[4][64];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int CD = a.c_dim, PF = mla_part_floats(CD);
     const float* base = dptr<const float>(a.part) + (size_t)b * a.splits * PF;
-    for (int idx = threadIdx.x; idx < a.heads * CD; idx += 256) {
-        const int h = idx / CD, d = idx - h * CD;
-        float M = -INFINITY;
-        for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[(size_t)s * PF + h]);
-        float num = 0.0f, den = 0.0f;
-        for (int s = 0; s < a.splits; ++s) {
-            const float ms = base[(size_t)s * PF + h];
-            if (ms == -INFINITY) continue;
-            const float w = expf(ms - M);
-            num = __builtin_fmaf(w, base[(size_t)s * PF + 32 + (size_t)h * CD + d], num);
-            den = __builtin_fmaf(w, base[(size_t)s * PF + 16 + h], den);
-        }
-        dptr<float>(a.ctx)[((size_t)b * a.heads + h) * CD + d] = num / den;
+    const float ms = tid < a.splits ? base[(size_t)tid * PF + h] : -INFINITY;
+    const float ls = tid < a.splits ? base[(size_t)tid * PF + 16 + h] : 0.0f;
+    const float M = block_max(ms, red);
+    const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
+    const float den = block_sum(w * ls, red);
+    if (tid < a.splits) wsh[tid] = w / den;
+    __syncthreads();
+    const int d = blockIdx.z * 64 + (tid & 63), g = tid >> 6;
+    const float* col = base + 32 + (size_t)h * CD + d;
+    float num = 0.0f;
+    int s = g;
+    for (; s + 12 < a.splits; s += 16) {
+        const float v0 = col[(size_t)s * PF], v1 = col[(size_t)(s + 4) * PF];
+        const float v2 = col[(size_t)(s + 8) * PF], v3 = col[(size_t)(s + 12) * PF];
+        num = __builtin_fmaf(wsh[s], v0, num);
+        num = __builtin_fmaf(wsh[s + 4], v1, num);
+        num = __builtin_fmaf(wsh[s + 8], v2, num);
+        num = __builtin_fmaf(wsh[s + 12], v3, num);
     }
+    for (; s < a.splits; s += 4) num = __builtin_fmaf(wsh[s], col[(size_t)s * PF], num);
+    part_sum[g][tid & 63] = num;
+    __syncthreads();
+    if (g == 0)
+        dptr<float>(a.ctx)[((size_t)b * a.heads + h) * CD + d] =
+            (part_sum[0][tid] + part_sum[1][tid]) + (part_sum[2][tid] + part_sum[3][tid]);
 }

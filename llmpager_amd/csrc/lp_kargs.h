@@ -179,6 +179,7 @@ struct AttnArgs {
 constexpr int kMlaRows = 64;        // cache rows per chunk (4 waves x 16)
 constexpr int kMlaMaxQk = 640;
 constexpr int kMlaMaxC = 512;
+constexpr int kMlaMaxSplits = 256;  // splits per sequence (the merge keeps one weight per split in LDS)
 constexpr int kMlaColStride = 144;  // bytes per column of the transposed chunk: 64 rows + pad, 16-byte aligned
 // LDS: the query images (hi and lo bf16 in MFMA A order, 2 x qk/32 x 1 KB),
 // the transposed chunk (c_dim x kMlaColStride) and the scores (16 x 64 f32).

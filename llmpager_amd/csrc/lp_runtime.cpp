@@ -709,7 +709,7 @@ int lp_mla_attn_decode(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t ctx, uint
 // batch, each split a whole number of 64-row chunks.
 static void mla_plan(const lp_ctx* c, int batch, int max_seq, int* splits, int* span) {
     const int chunks = std::max(1, (max_seq + kMlaRows - 1) / kMlaRows);
-    int sp = std::max(1, std::min(chunks, (c->cus + batch - 1) / batch));
+    int sp = std::max(1, std::min({chunks, (c->cus + batch - 1) / batch, kMlaMaxSplits}));
     const int per = (chunks + sp - 1) / sp;
     *span = per * kMlaRows;
     *splits = (max_seq + *span - 1) / *span;
@@ -733,8 +733,9 @@ int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cac
         c_dim > qk_dim || max_seq <= 0)
         return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: heads <= 16, qk_dim = 32 x {3,4,6,8,12,16,18,20}, "
                                       "c_dim a multiple of 64 up to 512 and <= qk_dim");
-    if ((uint64_t)max_seq * qk_dim * 2 >= (1ull << 31) || cache % 16 || cache_stride % 16)
-        return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: caches must be 16-byte aligned and under 2 GiB each");
+    if ((uint64_t)max_seq * qk_dim * 2 >= (1ull << 31) || cache % 16 || cache_stride % 16 || q % 16)
+        return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: q and the caches must be 16-byte aligned, "
+                                      "each cache under 2 GiB");
     const size_t lds = (size_t)mla_lds_bytes(qk_dim, c_dim);
     if (lds > c->max_lds) return fail(LP_E_UNSUPPORTED, "mla_attn_decode_batch: LDS");
     MlaBatchArgs a{};
@@ -751,7 +752,8 @@ int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cac
     a.scale = scale;
     mla_plan(c, batch, max_seq, &a.splits, &a.span);
     if (int r = launch(c, kMlaSplit, dim3((unsigned)a.splits, (unsigned)batch), dim3(256), lds, s, a)) return r;
-    return launch(c, kMlaCombine, dim3((unsigned)batch), dim3(256), 0, s, a);
+    return launch(c, kMlaCombine, dim3((unsigned)heads, (unsigned)batch, (unsigned)(c_dim / 64)), dim3(256), 0, s,
+                  a);
 }
 
 // ---- fused MoE layer --------------------------------------------------------------
