@@ -336,39 +336,34 @@ def zipf_trace(layers: int, tokens: int, E: int, k: int, s: float = P_ZIPF, seed
     return out
 
 
-def run_paged(cuda, s, layers: int, tokens: int, slots: int) -> dict:
+def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4, stage_threads: int = 4) -> dict:
     """H4096 / I1536 / E128 / top-8 / g32, `layers` layers,
-    `slots` VRAM expert slots per layer; every expert blob sits in one pinned
-    host pack (layers x 128 x 10.6 MB).  A `tokens`-token routing trace (8
-    distinct experts per token and layer, Zipf(1.1) over a per-layer ranking)
-    drives batch-1 decode through the reference's order per layer: route (from
-    logits that rank the trace's picks first), request the picks from the
-    pager (misses copied host -> VRAM on its copy streams, the compute stream
-    waiting on them), re-resolve the expert table, run the experts, release
-    after the stream passes.  Reports tok/s, hit rate and H2D GB/s over the
-    whole trace (cold start included)."""
+    `slots` VRAM expert slots per layer; every expert blob sits in pageable
+    host memory (the RAM tier: layers x 128 x 10.6 MB), and misses reach VRAM
+    through the pager's pinned staging ring: `io_threads` I/O workers each copy
+    a blob (split over `stage_threads` threads) into one of their two
+    span-sized pinned buffers and DMA it to the slot on their own stream
+    (pager.rs:650-718).  A `tokens`-token routing
+    trace (8 distinct experts per token and layer, Zipf(1.1) over a per-layer
+    ranking) drives batch-1 decode through the reference's order per layer:
+    route (from logits that rank the trace's picks first), request the picks
+    from the pager (the compute stream waits on their fills), re-resolve the
+    expert table, run the experts, release after the stream passes.  Reports
+    tok/s, hit rate and H2D GB/s over the whole trace (cold start included)."""
     import llmpager_amd as lp
     blob = lp.blob_bytes(P_H, P_I, P_G)
     span = align(blob)
     t0 = time.time()
-    while True:
-        n = layers * P_E * span
-        try:
-            pin = cuda.alloc_pinned(n)
-            break
-        except Exception as e:  # the host cannot pin the whole pack: fewer layers, said in the line
-            if layers <= 8:
-                raise
-            log(f"paged: pinning {n / 1e9:.1f} GB failed ({e}); trying {layers // 2} layers")
-            layers //= 2
-    view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(pin))
+    n = layers * P_E * span
+    host = np.empty(n, np.uint8)          # pageable: no pinned copy of the pack
     threads = min(16, os.cpu_count() or 1)
     for l in range(layers):
-        lp.synth_blobs(P_E, span, P_H, P_I, P_G, 0, l, threads=threads, out=view[l * P_E * span:(l + 1) * P_E * span])
-    log(f"paged: host pack {n / 1e9:.1f} GB of {layers} x {P_E} experts in {time.time() - t0:.0f} s")
+        lp.synth_blobs(P_E, span, P_H, P_I, P_G, 0, l, threads=threads, out=host[l * P_E * span:(l + 1) * P_E * span])
+    log(f"paged: host pack {n / 1e9:.1f} GB of {layers} x {P_E} experts (pageable) in {time.time() - t0:.0f} s")
     cfg = lp.PagerConfig(layers=layers, experts_per_layer=P_E, slots_per_layer=slots, decay_interval=256,
-                         blob_bytes=blob, span=0, host_blobs=pin, host_stride=span, copy_streams=4,
-                         global_pool=0)
+                         blob_bytes=blob, span=0, host_blobs=host.ctypes.data, host_stride=span, copy_streams=1,
+                         global_pool=0, source=lp.PAGER_SRC_HOST, io_threads=io_threads, ring_slots=2,
+                         stage_threads=stage_threads)
     pg = lp.Pager(cuda, cfg)
     go, uo, do = lp.blob_offsets(P_H, P_I, P_G)
     d_rw = cuda.upload(lp.synth_bf16(P_E * P_H, 0.02, 0, 1000), s)   # unused by route_logits
@@ -407,13 +402,15 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int) -> dict:
     pg.close()
     for p in (dlg, ws, dx, dh, d_rw):
         cuda.free_device(p)
-    cuda.free_pinned(pin)
+    del host
     assert err == 0, f"paged decode reported error flags {err}"
     lookups = m["hits"] + m["misses"]
     # the experts' weights and scales (the trace replaces the router GEMV)
     compute_bytes = tokens * layers * P_K * (blob - 32)
     res = dict(
-        layers=layers, tokens=tokens, slots_per_layer=slots, expert_bytes=blob,
+        layers=layers, tokens=tokens, slots_per_layer=slots, expert_bytes=blob, source="pageable host memory",
+        io_threads=io_threads, stage_threads=stage_threads, ring_buffers_per_thread=2,
+        staging_bytes=io_threads * 2 * span,
         tok_s=tokens / sec, seconds=sec, hits=m["hits"], misses=m["misses"],
         hit_rate=m["hits"] / max(lookups, 1), bytes_fetched=m["bytes_fetched"],
         h2d_gbps=m["bytes_fetched"] / sec / 1e9, stalls=m["stalls"],
@@ -710,7 +707,7 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
-    mla = None if a.no_mla else run_mla(cuda, s, (1, 16), a.steps)
+    mla = None if a.no_mla or a.paged_only else run_mla(cuda, s, (1, 16), a.steps)
     if a.mla_only:
         print(json.dumps({"mla": _rounded(mla)}), flush=True)
         cuda.close()

@@ -342,6 +342,15 @@ int64_t lp_cache_slot_id(const lp_cache* c, uint32_t slot);
 
 typedef struct lp_pager lp_pager;
 
+/* Where missed experts are copied from (pager.rs:650-718 reads a pack into a
+ * pinned staging buffer on I/O worker threads, then copies it to the slot). */
+enum {
+    LP_PAGER_SRC_PINNED = 0, /* host_blobs is pinned: copies go straight from it */
+    LP_PAGER_SRC_HOST = 1,   /* host_blobs is pageable (a RAM tier, a mapped file): workers stage
+                                each blob through a pinned ring, then copy it */
+    LP_PAGER_SRC_PACK = 2    /* a .llmpk pack (lp_pager_open): workers pread into the ring */
+};
+
 typedef struct lp_pager_config {
     uint32_t layers;            /* pack layers (pager.rs:263-264) */
     uint32_t experts_per_layer; /* ids fold (layer, expert) on this (pager.rs:224-226) */
@@ -349,21 +358,42 @@ typedef struct lp_pager_config {
     uint32_t decay_interval;    /* per-layer pools: halve counters every this many inserts (:37) */
     uint64_t blob_bytes;        /* bytes copied per miss */
     uint64_t span;              /* VRAM bytes per slot; 0 = blob_bytes rounded up to 4096 (:263) */
-    const void* host_blobs;     /* pinned host memory: blob (l, e) at host_blobs + (l*E + e)*host_stride */
+    const void* host_blobs;     /* PINNED / HOST sources: blob (l, e) at host_blobs + (l*E + e)*host_stride */
     uint64_t host_stride;
-    int32_t copy_streams;       /* 1..8 copy streams (the io_threads' role, :35) */
+    int32_t copy_streams;       /* PINNED source: 1..8 copy streams */
     int32_t global_pool;        /* one pool for every layer (LLMPAGER_GLOBAL_POOL, :296-318) */
     uint32_t pool_decay_tokens; /* global pool: decay every this many ticks; 0 = 4 (:361-365) */
-    uint32_t reserved0;
+    int32_t source;             /* LP_PAGER_SRC_* */
+    int32_t direct;             /* pack reads with O_DIRECT (PagerConfig::direct, :38-41) */
+    uint32_t io_threads;        /* HOST / PACK: I/O workers, each with its own copy stream
+                                   (PagerConfig::io_threads, :35); 0 = 4 */
+    uint32_t ring_slots;        /* pinned staging buffers of one span per worker; 0 = 2 */
+    uint32_t stage_threads;     /* threads sharing one blob's staging copy or read; 0 = 4 */
+    uint64_t ram_bytes;         /* PACK: host-RAM expert tier in bytes, 0 = none (PagerConfig::ram_bytes, :42-45) */
 } lp_pager_config;
 
 typedef struct lp_pager_metrics {
     uint64_t hits, misses, bytes_fetched, fetches, stalls; /* pager.rs:568-589 (Metrics) */
+    uint64_t ram_hits;                                     /* fills served by the RAM tier */
 } lp_pager_metrics;
 
-/* Pager::new (pager.rs:260-388): one arena of layers x slots_per_layer slots,
- * per-layer device slot tables (expert -> global slot, -1 absent), copy streams. */
+/* ExpertHandle (pager.rs:169-178): a pinned, resident or in-flight expert. */
+typedef struct lp_expert_handle {
+    uint16_t layer, expert;
+    uint32_t slot;
+    uint64_t dev;  /* device address of the expert's blob */
+    uint64_t len;  /* valid bytes */
+} lp_expert_handle;
+
+/* Pager::new (pager.rs:260-388) over host memory (PINNED or HOST source): one
+ * arena of layers x slots_per_layer slots, per-layer device slot tables
+ * (expert -> global slot, -1 absent), copy streams or I/O workers. */
 int lp_pager_new(lp_ctx* ctx, const lp_pager_config* cfg, lp_pager** out);
+/* Pager::new(cuda, &Path, cfg) (pager.rs:260-388) over a .llmpk pack: layers,
+ * experts and the span come from the pack (cfg's must be 0 or equal); reads
+ * by cfg->io_threads workers into pinned staging rings, O_DIRECT when
+ * cfg->direct, through a RAM tier of cfg->ram_bytes. */
+int lp_pager_open(lp_ctx* ctx, const char* pack_path, const lp_pager_config* cfg, lp_pager** out);
 /* Drop (pager.rs:606-620): waits for copies in flight, frees the arena. */
 void lp_pager_free(lp_pager* p);
 /* The arena base (the layer desc's arena_base), the slot span (its
@@ -380,6 +410,18 @@ uint32_t lp_pager_slots_per_layer(const lp_pager* p);
  * deadlock) when none is.  slots_out: n global slot numbers (may be NULL). */
 int lp_pager_request(lp_pager* p, uint16_t layer, const uint16_t* experts, int n, lp_stream compute,
                      uint32_t* slots_out);
+/* Pager::request (pager.rs:402-460): pin n experts of `layer` and schedule the
+ * misses; returns at once with one handle per expert.  Before a kernel reads
+ * handle i: lp_pager_wait_stream (or lp_pager_wait), and for the fused layer
+ * kernels lp_pager_refresh_table. */
+int lp_pager_request_handles(lp_pager* p, uint16_t layer, const uint16_t* experts, int n,
+                             lp_expert_handle* out);
+/* Pager::wait_stream (pager.rs:497-503): `s` waits for the handle's fill (the
+ * host waits only until the copy is enqueued). */
+int lp_pager_wait_stream(lp_pager* p, const lp_expert_handle* h, lp_stream s);
+/* The layer's device slot table refreshed in stream order on `s` (no
+ * counterpart in the reference, whose kernels take per-pick blob pointers). */
+int lp_pager_refresh_table(lp_pager* p, uint16_t layer, lp_stream s);
 /* Pager::release (pager.rs:505-510): unpin now (the GPU is done with them). */
 int lp_pager_release(lp_pager* p, const uint32_t* slots, int n);
 /* The deferred release of decode.rs:621-649: unpin once `compute` has passed
@@ -396,6 +438,30 @@ int lp_pager_tick(lp_pager* p);
 int lp_pager_sync(lp_pager* p);
 /* Pager::metrics (pager.rs:568-589). */
 int lp_pager_get_metrics(lp_pager* p, lp_pager_metrics* out);
+
+/* ---- the .llmpk pack (crates/llmpager-core/src/pack.rs) ------------------ */
+
+typedef struct lp_pack lp_pack;
+typedef struct lp_pack_writer lp_pack_writer;
+/* PackWriter::create / add_blob / finish (pack.rs:67-150): blobs appended in
+ * row-major (layer, expert) order, header and index written at finish. */
+int lp_pack_create(const char* path, const char* model, const char* dtype, uint32_t layers, uint32_t experts,
+                   lp_pack_writer** out);
+int lp_pack_add_blob(lp_pack_writer* w, const void* blob, uint64_t nbytes);
+int lp_pack_finish(lp_pack_writer* w);
+/* PackReader::open / open_direct (pack.rs:152-205); compressed packs are
+ * refused (LP_E_INVALID). */
+int lp_pack_open(const char* path, int direct, lp_pack** out);
+void lp_pack_close(lp_pack* p);
+int lp_pack_info(const lp_pack* p, uint32_t* layers, uint32_t* experts, uint64_t* max_blob_bytes);
+/* PackReader::entry (pack.rs:211-213) */
+int lp_pack_entry(const lp_pack* p, uint32_t layer, uint32_t expert, uint64_t* offset, uint64_t* nbytes);
+/* PackReader::read_blob_into (pack.rs:230-246): reads the blob's 4096-aligned
+ * span (buf_len >= it; buf 4096-aligned under O_DIRECT); returns the blob's
+ * length or a negative error. */
+int64_t lp_pack_read_blob(lp_pack* p, uint32_t layer, uint32_t expert, void* buf, uint64_t buf_len);
+/* pread of bytes [offset, offset + n) of the pack (4096-aligned under O_DIRECT). */
+int lp_pack_read_range(lp_pack* p, uint64_t offset, void* buf, uint64_t n);
 
 /* ---- measurement ------------------------------------------------------------ */
 

@@ -134,6 +134,18 @@ def _sig(lib):
         "lp_route_expf_sweep": (None, [C.c_uint32, C.c_uint32, u64, vp]),
         "lp_route_expf_device": (i32, [vp, C.c_uint32, C.c_uint32, u64, u64, vp]),
         "lp_pager_new": (i32, [vp, vp, P(vp)]),
+        "lp_pager_open": (i32, [vp, C.c_char_p, vp, P(vp)]),
+        "lp_pager_request_handles": (i32, [vp, C.c_uint16, vp, i32, vp]),
+        "lp_pager_wait_stream": (i32, [vp, vp, vp]),
+        "lp_pager_refresh_table": (i32, [vp, C.c_uint16, vp]),
+        "lp_pack_create": (i32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_uint32, C.c_uint32, P(vp)]),
+        "lp_pack_add_blob": (i32, [vp, vp, u64]),
+        "lp_pack_finish": (i32, [vp]),
+        "lp_pack_open": (i32, [C.c_char_p, i32, P(vp)]),
+        "lp_pack_close": (None, [vp]),
+        "lp_pack_info": (i32, [vp, P(C.c_uint32), P(C.c_uint32), P(u64)]),
+        "lp_pack_entry": (i32, [vp, C.c_uint32, C.c_uint32, P(u64), P(u64)]),
+        "lp_pack_read_blob": (C.c_int64, [vp, C.c_uint32, C.c_uint32, vp, u64]),
         "lp_pager_free": (None, [vp]),
         "lp_pager_arena": (u64, [vp]),
         "lp_pager_span": (u64, [vp]),
@@ -456,23 +468,101 @@ class PagerConfig(C.Structure):
         ("layers", C.c_uint32), ("experts_per_layer", C.c_uint32), ("slots_per_layer", C.c_uint32),
         ("decay_interval", C.c_uint32), ("blob_bytes", C.c_uint64), ("span", C.c_uint64),
         ("host_blobs", C.c_void_p), ("host_stride", C.c_uint64), ("copy_streams", C.c_int32),
-        ("global_pool", C.c_int32), ("pool_decay_tokens", C.c_uint32), ("reserved0", C.c_uint32),
+        ("global_pool", C.c_int32), ("pool_decay_tokens", C.c_uint32), ("source", C.c_int32),
+        ("direct", C.c_int32), ("io_threads", C.c_uint32), ("ring_slots", C.c_uint32),
+        ("stage_threads", C.c_uint32), ("ram_bytes", C.c_uint64),
     ]
 
 
+PAGER_SRC_PINNED, PAGER_SRC_HOST, PAGER_SRC_PACK = 0, 1, 2
+
+
 class PagerMetrics(C.Structure):
-    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "bytes_fetched", "fetches", "stalls")]
+    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "bytes_fetched", "fetches", "stalls", "ram_hits")]
+
+
+class ExpertHandle(C.Structure):
+    """lp_expert_handle: pager.rs ExpertHandle {layer, expert, slot, dev, len}."""
+
+    _fields_ = [("layer", C.c_uint16), ("expert", C.c_uint16), ("slot", C.c_uint32), ("dev", C.c_uint64),
+                ("len", C.c_uint64)]
+
+
+class PackWriter:
+    """PackWriter (pack.rs:67-150) over lp_pack_create / add_blob / finish."""
+
+    def __init__(self, path: str, layers: int, experts: int, model: str = "synthetic", dtype: str = "q4g32-gud"):
+        w = C.c_void_p()
+        _check(lib().lp_pack_create(path.encode(), model.encode(), dtype.encode(), layers, experts, C.byref(w)))
+        self.w = w.value
+
+    def add_blob(self, blob: np.ndarray) -> None:
+        b = np.ascontiguousarray(blob, np.uint8)
+        _check(lib().lp_pack_add_blob(self.w, _ptr(b), b.size))
+
+    def finish(self) -> None:
+        w, self.w = self.w, None
+        _check(lib().lp_pack_finish(w))
+
+
+class Pack:
+    """PackReader (pack.rs:152-260) over lp_pack_open / read_blob."""
+
+    def __init__(self, path: str, direct: bool = False):
+        p = C.c_void_p()
+        _check(lib().lp_pack_open(path.encode(), int(direct), C.byref(p)))
+        self.p = p.value
+        L, E, m = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        _check(lib().lp_pack_info(self.p, C.byref(L), C.byref(E), C.byref(m)))
+        self.layers, self.experts, self.max_blob = L.value, E.value, m.value
+
+    def entry(self, layer: int, expert: int) -> tuple[int, int]:
+        o, n = C.c_uint64(), C.c_uint64()
+        _check(lib().lp_pack_entry(self.p, layer, expert, C.byref(o), C.byref(n)))
+        return o.value, n.value
+
+    def read_blob(self, layer: int, expert: int) -> np.ndarray:
+        _, n = self.entry(layer, expert)
+        span = (n + 4095) // 4096 * 4096
+        raw = np.zeros(span + 4096, np.uint8)
+        off = (-raw.ctypes.data) % 4096          # a 4096-aligned view, as O_DIRECT needs
+        buf = raw[off:off + span]
+        got = lib().lp_pack_read_blob(self.p, layer, expert, _ptr(buf), span)
+        if got < 0:
+            _check(int(got))
+        return buf[:got].copy()
+
+    def close(self) -> None:
+        if self.p:
+            lib().lp_pack_close(self.p)
+            self.p = None
 
 
 class Pager:
     """pager::Pager (pager.rs) over the C ABI: VRAM expert slots, misses filled
     from pinned host blobs on copy streams."""
 
-    def __init__(self, cuda: "Cuda", cfg: PagerConfig):
+    def __init__(self, cuda: "Cuda", cfg: PagerConfig, pack_path: str | None = None):
         self.cuda, self.cfg = cuda, cfg
         p = C.c_void_p()
-        _check(lib().lp_pager_new(cuda.ctx, C.byref(cfg), C.byref(p)))
+        if pack_path is None:
+            _check(lib().lp_pager_new(cuda.ctx, C.byref(cfg), C.byref(p)))
+        else:
+            _check(lib().lp_pager_open(cuda.ctx, pack_path.encode(), C.byref(cfg), C.byref(p)))
         self.p = p.value
+
+    def request_handles(self, layer: int, experts) -> list:
+        """Pager::request: pins and schedules, returns ExpertHandles at once."""
+        ex = np.ascontiguousarray(experts, np.uint16)
+        out = (ExpertHandle * max(len(ex), 1))()
+        _check(lib().lp_pager_request_handles(self.p, layer, _ptr(ex), len(ex), out))
+        return [out[i] for i in range(len(ex))]
+
+    def wait_stream(self, h: ExpertHandle, stream=None) -> None:
+        _check(lib().lp_pager_wait_stream(self.p, C.byref(h), stream))
+
+    def refresh_table(self, layer: int, stream=None) -> None:
+        _check(lib().lp_pager_refresh_table(self.p, layer, stream))
 
     @property
     def arena(self) -> int:

@@ -24,7 +24,7 @@ ROOT = os.path.dirname(HERE)
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip", "lp_gemm.hip", "lp_attn.hip"]
-HOST_SOURCES = ["lp_runtime.cpp", "lp_synth.cpp", "lp_cache.cpp", "lp_pager.cpp"]
+HOST_SOURCES = ["lp_runtime.cpp", "lp_synth.cpp", "lp_cache.cpp", "lp_pager.cpp", "lp_pack.cpp"]
 HOST_HIP_SOURCES = ["lp_noalloc.hip"]
 
 # Packed-FP32 instructions stay off (the code is written for scalar fp32).

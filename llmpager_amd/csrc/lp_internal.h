@@ -4,6 +4,7 @@
 #include <string>
 
 struct lp_ctx;
+struct lp_pack;
 
 namespace lpi {
 

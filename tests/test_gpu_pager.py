@@ -16,30 +16,52 @@ H, I, E, K, G = 128, 64, 8, 2, 32
 
 
 class HostPack:
-    """Every (layer, expert) blob in pinned host memory, span-strided."""
+    """Every (layer, expert) blob, span-strided, as the pager's fill source:
+    pinned host memory ("pinned"), pageable host memory staged through the
+    pager's pinned ring ("host"), or a .llmpk pack file read by its I/O
+    workers ("pack")."""
 
-    def __init__(self, cuda, layers: int, seed: int):
-        self.cuda, self.layers = cuda, layers
+    def __init__(self, cuda, layers: int, seed: int, source: str = "pinned", tmp=None):
+        self.cuda, self.layers, self.source = cuda, layers, source
         self.blob = lp.blob_bytes(H, I, G)
         self.span = align(self.blob)
         n = layers * E * self.span
-        self.pin = cuda.alloc_pinned(n)
-        self.view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(self.pin))
+        self.pin = cuda.alloc_pinned(n) if source == "pinned" else None
+        self.view = (np.ctypeslib.as_array((C.c_uint8 * n).from_address(self.pin)) if self.pin
+                     else np.zeros(n, np.uint8))
         for l in range(layers):
             lp.synth_blobs(E, self.span, H, I, G, seed, l, out=self.view[l * E * self.span:(l + 1) * E * self.span])
+        self.path = None
+        if source == "pack":
+            self.path = str(tmp / f"pack{seed}.llmpk")
+            w = lp.PackWriter(self.path, layers, E)
+            for l in range(layers):
+                for e in range(E):
+                    w.add_blob(self.blob_of(l, e))
+            w.finish()
 
     def blob_of(self, l: int, e: int) -> np.ndarray:
         o = (l * E + e) * self.span
         return self.view[o:o + self.blob]
 
-    def pager(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256) -> lp.Pager:
+    def pager(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256, ram_bytes: int = 0) -> lp.Pager:
+        src = {"pinned": lp.PAGER_SRC_PINNED, "host": lp.PAGER_SRC_HOST, "pack": lp.PAGER_SRC_PACK}[self.source]
         cfg = lp.PagerConfig(layers=self.layers, experts_per_layer=E, slots_per_layer=slots,
-                             decay_interval=decay, blob_bytes=self.blob, span=0, host_blobs=self.pin,
-                             host_stride=self.span, copy_streams=streams, global_pool=glob)
+                             decay_interval=decay, blob_bytes=self.blob, span=0,
+                             host_blobs=self.pin or self.view.ctypes.data, host_stride=self.span,
+                             copy_streams=streams, global_pool=glob, source=src, io_threads=3, ring_slots=2,
+                             ram_bytes=ram_bytes)
+        if self.source == "pack":
+            cfg.host_blobs, cfg.blob_bytes, cfg.host_stride = None, 0, 0
+            return lp.Pager(self.cuda, cfg, pack_path=self.path)
         return lp.Pager(self.cuda, cfg)
 
     def free(self):
-        self.cuda.free_pinned(self.pin)
+        if self.pin:
+            self.cuda.free_pinned(self.pin)
+
+
+SOURCES = ["pinned", "host", "pack"]
 
 
 def _cache_model(layers: int, slots: int, glob: bool):
@@ -53,8 +75,9 @@ def _cache_model(layers: int, slots: int, glob: bool):
     return L.lp_cache_partitioned(layers, E, slots, 256)
 
 
-def test_pager_fills_are_byte_exact(cuda):
-    pk = HostPack(cuda, 2, seed=3)
+@pytest.mark.parametrize("source", SOURCES)
+def test_pager_fills_are_byte_exact(cuda, source, tmp_path):
+    pk = HostPack(cuda, 2, seed=3, source=source, tmp=tmp_path)
     pg = pk.pager(slots=3)
     s = cuda.stream()
     slots = pg.request(1, [3, 5, 1], s)
@@ -73,8 +96,9 @@ def test_pager_fills_are_byte_exact(cuda):
     pk.free()
 
 
-def test_pager_prefetch_then_hit(cuda):
-    pk = HostPack(cuda, 1, seed=4)
+@pytest.mark.parametrize("source", SOURCES)
+def test_pager_prefetch_then_hit(cuda, source, tmp_path):
+    pk = HostPack(cuda, 1, seed=4, source=source, tmp=tmp_path)
     pg = pk.pager(slots=4)
     pg.prefetch(0, [6, 2])
     s = cuda.stream()
@@ -92,10 +116,11 @@ def test_pager_prefetch_then_hit(cuda):
     pk.free()
 
 
-def test_pager_deadlock_is_an_error(cuda):
+@pytest.mark.parametrize("source", SOURCES)
+def test_pager_deadlock_is_an_error(cuda, source, tmp_path):
     # every slot pinned and nothing pending: the reference bails out rather than
     # hang (pager.rs:430-451); so does the C ABI
-    pk = HostPack(cuda, 1, seed=5)
+    pk = HostPack(cuda, 1, seed=5, source=source, tmp=tmp_path)
     pg = pk.pager(slots=2)
     s = cuda.stream()
     pg.request(0, [0, 1], s)
@@ -109,8 +134,9 @@ def test_pager_deadlock_is_an_error(cuda):
     pk.free()
 
 
+@pytest.mark.parametrize("source", SOURCES)
 @pytest.mark.parametrize("glob", [0, 1])
-def test_paged_stack_matches_the_oracle(cuda, glob):
+def test_paged_stack_matches_the_oracle(cuda, glob, source, tmp_path):
     # Two layers, 4 of 8 expert slots per layer (8 in one pool when glob): each
     # decode step routes on the device, reads the picks back, asks the pager for
     # them (misses copied on the copy streams), re-resolves the expert table and
@@ -118,7 +144,7 @@ def test_paged_stack_matches_the_oracle(cuda, glob):
     # routing on the GPU.  Hits and misses must be those of the ExpertCache fed
     # the same requests, and h must match the oracle with every expert resident.
     layers, slots, steps = 2, 4, 10
-    pk = HostPack(cuda, layers, seed=6)
+    pk = HostPack(cuda, layers, seed=6, source=source, tmp=tmp_path)
     pg = pk.pager(slots=slots, glob=glob)
     model = _cache_model(layers, slots, bool(glob))
     Lc = lp.lib()
@@ -187,3 +213,32 @@ def test_paged_stack_matches_the_oracle(cuda, glob):
         cuda.free_device(p)
     cuda.destroy_stream(s)
     pk.free()
+
+
+def test_pager_handles_and_ram_tier(cuda, tmp_path):
+    # Pager::request -> ExpertHandle, wait_stream, then the layer's slot table
+    # refreshed for the fused kernels (pager.rs:402-503), over a pack with a
+    # RAM tier: a second round of the same experts after they were evicted
+    # from VRAM is served from host RAM, byte-exact.
+    pk = HostPack(cuda, 1, seed=9, source="pack", tmp=tmp_path)
+    pg = pk.pager(slots=3, ram_bytes=8 * pk.span)
+    s = cuda.stream()
+    for rnd in range(2):
+        for group in ([0, 1, 2], [3, 4, 5]):
+            hs = pg.request_handles(0, group)
+            assert [h.expert for h in hs] == group and all(h.len == pk.blob for h in hs)
+            assert all(h.dev == pg.arena + h.slot * pg.span for h in hs)
+            for h in hs:
+                pg.wait_stream(h, s)
+            pg.refresh_table(0, s)
+            cuda.sync_stream(s)
+            table = cuda.download(pg.slot_table(0), (E,), np.int32)
+            for h in hs:
+                assert table[h.expert] == h.slot
+                assert np.array_equal(cuda.download(h.dev, (pk.blob,), np.uint8), pk.blob_of(0, h.expert))
+            pg.release([h.slot for h in hs])
+    m = pg.metrics()
+    assert m["misses"] == 12 and m["ram_hits"] == 6   # the second round came from the RAM tier
+    pg.sync()
+    pg.close()
+    cuda.destroy_stream(s)
