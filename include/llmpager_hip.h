@@ -436,6 +436,13 @@ int lp_pager_wait(lp_pager* p, uint32_t slot);
 int lp_pager_tick(lp_pager* p);
 /* Wait for every copy in flight and hand back every deferred release. */
 int lp_pager_sync(lp_pager* p);
+/* Pager::expert_stats (pager.rs:532-538): fills per (layer, expert), row-major;
+ * copies min(n, layers * E) counts and returns layers * E. */
+int lp_pager_expert_stats(lp_pager* p, uint64_t* counts, uint64_t n);
+/* Pager::prewarm (pager.rs:540-567): the most-fetched experts of `counts`
+ * that fit the RAM tier read into it, in pack order; returns how many (0
+ * without a RAM tier). */
+int lp_pager_prewarm(lp_pager* p, const uint64_t* counts, uint64_t n);
 /* Pager::metrics (pager.rs:568-589). */
 int lp_pager_get_metrics(lp_pager* p, lp_pager_metrics* out);
 

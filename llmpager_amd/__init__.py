@@ -138,6 +138,8 @@ def _sig(lib):
         "lp_pager_request_handles": (i32, [vp, C.c_uint16, vp, i32, vp]),
         "lp_pager_wait_stream": (i32, [vp, vp, vp]),
         "lp_pager_refresh_table": (i32, [vp, C.c_uint16, vp]),
+        "lp_pager_expert_stats": (i32, [vp, vp, u64]),
+        "lp_pager_prewarm": (i32, [vp, vp, u64]),
         "lp_pack_create": (i32, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_uint32, C.c_uint32, P(vp)]),
         "lp_pack_add_blob": (i32, [vp, vp, u64]),
         "lp_pack_finish": (i32, [vp]),
@@ -563,6 +565,23 @@ class Pager:
 
     def refresh_table(self, layer: int, stream=None) -> None:
         _check(lib().lp_pager_refresh_table(self.p, layer, stream))
+
+    def expert_stats(self) -> np.ndarray:
+        n = lib().lp_pager_expert_stats(self.p, None, 0)
+        if n < 0:
+            _check(n)
+        out = np.zeros(n, np.uint64)
+        r = lib().lp_pager_expert_stats(self.p, _ptr(out), n)
+        if r < 0:
+            _check(r)
+        return out
+
+    def prewarm(self, counts) -> int:
+        c = np.ascontiguousarray(counts, np.uint64)
+        r = lib().lp_pager_prewarm(self.p, _ptr(c), c.size)
+        if r < 0:
+            _check(r)
+        return r
 
     @property
     def arena(self) -> int:

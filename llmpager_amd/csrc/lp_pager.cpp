@@ -106,6 +106,7 @@ struct lp_pager {
     std::string worker_msg;
     int pending_prefetch = 0;              // prefetch jobs not yet enqueued
     RamTier* ram = nullptr;
+    std::vector<uint64_t> fetch_counts;    // per (layer, expert): fills, the profile prewarm uses
 };
 
 namespace {
@@ -172,6 +173,7 @@ int fill_slot_pinned(lp_pager* p, uint16_t layer, uint16_t expert, uint32_t slot
     lp_cache_publish(p->cache, slot);
     p->bytes_fetched += p->cfg.blob_bytes;
     p->fetches += 1;
+    p->fetch_counts[(size_t)layer * p->cfg.experts_per_layer + expert] += 1;
     return LP_OK;
 }
 
@@ -335,6 +337,7 @@ void worker_main(lp_pager* p, int wid) {
                 p->fill[job.slot] = Fill::InFlight;
                 p->bytes_fetched += p->cfg.blob_bytes;
                 p->fetches += 1;
+                p->fetch_counts[(size_t)job.layer * p->cfg.experts_per_layer + job.expert] += 1;
                 if (done) p->prefetched.push_back(Deferred{done, {job.slot}});
             } else {
                 if (p->worker_err == LP_OK) {
@@ -469,6 +472,7 @@ int pager_init(lp_ctx* ctx, const lp_pager_config* cfg, lp_pack* pack, lp_pager*
     if (e == hipSuccess) e = hipHostMalloc((void**)&p->host_tables, (size_t)L * E * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipHostMalloc((void**)&p->stage, kRing * E * 4, hipHostMallocDefault);
     if (e == hipSuccess) {
+        p->fetch_counts.assign((size_t)L * E, 0);
         memset(p->host_tables, 0xff, (size_t)L * E * 4);
         p->fill.assign(total, Fill::Empty);
         p->fill_ev.assign(total, nullptr);
@@ -767,6 +771,44 @@ int lp_pager_sync(lp_pager* p) {
     if (int r = drain(p, p->prefetched, true)) return r;
     if (p->worker_err != LP_OK) return fail(p->worker_err, p->worker_msg);
     return LP_OK;
+}
+
+int lp_pager_expert_stats(lp_pager* p, uint64_t* counts, uint64_t n) {
+    if (!p || (!counts && n)) return fail(LP_E_INVALID, "lp_pager_expert_stats: bad arguments");
+    std::lock_guard<std::mutex> g(p->mu);
+    const uint64_t m = std::min<uint64_t>(n, p->fetch_counts.size());
+    for (uint64_t i = 0; i < m; ++i) counts[i] = p->fetch_counts[i];
+    return (int)std::min<uint64_t>(p->fetch_counts.size(), 0x7fffffff);
+}
+
+int lp_pager_prewarm(lp_pager* p, const uint64_t* counts, uint64_t n) {
+    if (!p || (!counts && n)) return fail(LP_E_INVALID, "lp_pager_prewarm: bad arguments");
+    if (!p->ram || !p->pack) return 0;  // pager.rs:540-543: no RAM tier, nothing to warm
+    const uint64_t total = std::min<uint64_t>(n, (uint64_t)p->cfg.layers * p->cfg.experts_per_layer);
+    const uint64_t capacity = p->ram->bytes / p->ram->span;
+    // the most-fetched experts that fit, read in pack order (pager.rs:544-567)
+    std::vector<std::pair<uint64_t, uint64_t>> ranked;
+    for (uint64_t i = 0; i < total; ++i)
+        if (counts[i] > 0) ranked.emplace_back(counts[i], i);
+    std::stable_sort(ranked.begin(), ranked.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
+    if (ranked.size() > capacity) ranked.resize(capacity);
+    std::vector<uint64_t> idx;
+    for (const auto& r : ranked) idx.push_back(r.second);
+    std::sort(idx.begin(), idx.end());
+    void* buf = nullptr;
+    if (posix_memalign(&buf, kAlign, p->span) != 0) return fail(LP_E_INVALID, "lp_pager_prewarm: out of memory");
+    int loaded = 0;
+    for (uint64_t i : idx) {
+        const uint16_t layer = (uint16_t)(i / p->cfg.experts_per_layer), expert = (uint16_t)(i % p->cfg.experts_per_layer);
+        if (lp_pack_read_blob(p->pack, layer, expert, buf, p->span) < 0) {
+            free(buf);
+            return fail(LP_E_INVALID, "lp_pager_prewarm: pack read failed");
+        }
+        ram_put(p->ram, layer, expert, buf);
+        ++loaded;
+    }
+    free(buf);
+    return loaded;
 }
 
 int lp_pager_get_metrics(lp_pager* p, lp_pager_metrics* out) {

@@ -242,3 +242,28 @@ def test_pager_handles_and_ram_tier(cuda, tmp_path):
     pg.sync()
     pg.close()
     cuda.destroy_stream(s)
+
+
+def test_pager_expert_stats_and_prewarm(cuda, tmp_path):
+    # Pager::expert_stats / prewarm (pager.rs:532-567): the fill profile of one
+    # pager warms the RAM tier of a fresh one, whose misses then come from RAM
+    pk = HostPack(cuda, 1, seed=10, source="pack", tmp=tmp_path)
+    pg = pk.pager(slots=2)
+    s = cuda.stream()
+    for group in ([0, 1], [2, 3], [0, 1]):
+        pg.release(pg.request(0, group, s))
+    stats = pg.expert_stats()
+    assert stats.tolist() == [2, 2, 1, 1, 0, 0, 0, 0]
+    pg.sync()
+    pg.close()
+    pg2 = pk.pager(slots=2, ram_bytes=3 * pk.span)
+    assert pg2.prewarm(stats) == 3                     # the three most fetched that fit
+    got = pg2.request(0, [0, 1], s)
+    cuda.sync_stream(s)
+    assert pg2.metrics()["ram_hits"] == 2
+    for e, sl in zip((0, 1), got):
+        assert np.array_equal(cuda.download(pg2.arena + int(sl) * pg2.span, (pk.blob,), np.uint8), pk.blob_of(0, e))
+    pg2.release(got)
+    pg2.sync()
+    pg2.close()
+    cuda.destroy_stream(s)
