@@ -213,7 +213,7 @@ MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
 
 def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
-    """a 2048-token chunk through one Qwen3-30B-A3B-shape
+    """Workload config 3: a 2048-token chunk through one Qwen3-30B-A3B-shape
     layer whose router logits carry a Zipf(1.1) per-expert offset
     (v_e += -1.1 ln rank_e, rank a seeded permutation of 1..128), so expert
     loads are skewed (the top expert takes ~23% of the picks).
@@ -315,7 +315,7 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
     return res
 
 
-# Qwen3-235B-A22B shape with expert paging.
+# Workload config 4: Qwen3-235B-A22B shape with expert paging.
 P_H, P_I, P_E, P_K, P_G = 4096, 1536, 128, 8, 32
 P_LAYERS, P_SLOTS, P_TOKENS, P_ZIPF = 94, 64, 512, 1.1
 
@@ -337,7 +337,7 @@ def zipf_trace(layers: int, tokens: int, E: int, k: int, s: float = P_ZIPF, seed
 
 
 def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4, stage_threads: int = 4) -> dict:
-    """H4096 / I1536 / E128 / top-8 / g32, `layers` layers,
+    """Workload config 4: H4096 / I1536 / E128 / top-8 / g32, `layers` layers,
     `slots` VRAM expert slots per layer; every expert blob sits in pageable
     host memory (the RAM tier: layers x 128 x 10.6 MB), and misses reach VRAM
     through the pager's pinned staging ring: `io_threads` I/O workers each copy
@@ -414,6 +414,7 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4
         tok_s=tokens / sec, seconds=sec, hits=m["hits"], misses=m["misses"],
         hit_rate=m["hits"] / max(lookups, 1), bytes_fetched=m["bytes_fetched"],
         h2d_gbps=m["bytes_fetched"] / sec / 1e9, stalls=m["stalls"],
+        fetch_latency_ms_buckets=dict(zip(("<1", "<2", "<5", "<10", "<20", "<50", ">=50"), m["latency_ms_buckets"])),
         hbm_gbps=compute_bytes / sec / 1e9,
     )
     log(f"paged ({layers} layers, {slots} slots, {tokens} tokens): {res['tok_s']:.1f} tok/s, hit rate "
@@ -421,13 +422,13 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4
     return res
 
 
-# the MoE half of a DeepSeek-V2-Lite-style layer (the MLA
+# Workload config 5: the MoE half of a DeepSeek-V2-Lite-style layer (the MLA
 # attention that precedes it in the model is outside this path).
 D_H, D_I, D_E, D_K, D_G, D_SH, D_LAYERS = 2048, 1408, 64, 6, 32, 2816, 26
 
 
 def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
-    """BASELINE config 5's MoE layer: 64 routed experts top-6 (softmax, no
+    """Workload config 5's MoE layer: 64 routed experts top-6 (softmax, no
     renormalisation, as DeepSeek-V2-Lite) of width 1408 plus the always-on
     shared MLP of width 2816 (2 shared experts), g32, stacked over 26 layers
     (8.4 GB of distinct weights, so the 256 MB MALL cannot serve repeats) in
@@ -488,7 +489,7 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
     return out
 
 
-# BASELINE config 5's attention half: MLA absorbed decode over bf16 latent KV.
+# Workload config 5's attention half: MLA absorbed decode over bf16 latent KV.
 M_HEADS, M_QK, M_C, M_CTX = 16, 576, 512, 4096
 
 

@@ -375,6 +375,8 @@ typedef struct lp_pager_config {
 typedef struct lp_pager_metrics {
     uint64_t hits, misses, bytes_fetched, fetches, stalls; /* pager.rs:568-589 (Metrics) */
     uint64_t ram_hits;                                     /* fills served by the RAM tier */
+    uint64_t latency_ms_buckets[7]; /* worker fetches' read-and-enqueue time: <1, <2, <5, <10, <20, <50,
+                                       >=50 ms (pager.rs:677-686; zero for the pinned source) */
 } lp_pager_metrics;
 
 /* ExpertHandle (pager.rs:169-178): a pinned, resident or in-flight expert. */

@@ -480,7 +480,8 @@ PAGER_SRC_PINNED, PAGER_SRC_HOST, PAGER_SRC_PACK = 0, 1, 2
 
 
 class PagerMetrics(C.Structure):
-    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "bytes_fetched", "fetches", "stalls", "ram_hits")]
+    _fields_ = [(n, C.c_uint64) for n in ("hits", "misses", "bytes_fetched", "fetches", "stalls", "ram_hits")] + [
+        ("latency_ms_buckets", C.c_uint64 * 7)]
 
 
 class ExpertHandle(C.Structure):
@@ -624,7 +625,9 @@ class Pager:
     def metrics(self) -> dict:
         m = PagerMetrics()
         _check(lib().lp_pager_get_metrics(self.p, C.byref(m)))
-        return {n: getattr(m, n) for n, _ in PagerMetrics._fields_}
+        out = {n: getattr(m, n) for n, _ in PagerMetrics._fields_}
+        out["latency_ms_buckets"] = list(m.latency_ms_buckets)
+        return out
 
     def close(self) -> None:
         if self.p:

@@ -32,6 +32,7 @@
 #include <sys/mman.h>
 
 #include <algorithm>
+#include <chrono>
 #include <condition_variable>
 #include <deque>
 #include <mutex>
@@ -107,6 +108,7 @@ struct lp_pager {
     int pending_prefetch = 0;              // prefetch jobs not yet enqueued
     RamTier* ram = nullptr;
     std::vector<uint64_t> fetch_counts;    // per (layer, expert): fills, the profile prewarm uses
+    uint64_t lat_buckets[7] = {};          // worker fetch time: <1, <2, <5, <10, <20, <50, >=50 ms
 };
 
 namespace {
@@ -309,6 +311,7 @@ void worker_main(lp_pager* p, int wid) {
             job = p->jobs.front();
             p->jobs.pop_front();
         }
+        const auto t0 = std::chrono::steady_clock::now();
         const size_t r = next++ % nring;
         bool ok = hipEventSynchronize(ring_ev[r]) == hipSuccess;  // its previous copy has landed
         if (ok) {
@@ -339,6 +342,13 @@ void worker_main(lp_pager* p, int wid) {
                 p->fetches += 1;
                 p->fetch_counts[(size_t)job.layer * p->cfg.experts_per_layer + job.expert] += 1;
                 if (done) p->prefetched.push_back(Deferred{done, {job.slot}});
+                // pager.rs:677-686: the read-and-enqueue time of the fetch
+                const double ms =
+                    std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+                const double edges[6] = {1, 2, 5, 10, 20, 50};
+                int bk = 0;
+                while (bk < 6 && ms >= edges[bk]) ++bk;
+                p->lat_buckets[bk] += 1;
             } else {
                 if (p->worker_err == LP_OK) {
                     p->worker_err = LP_E_DEVICE;
@@ -822,6 +832,7 @@ int lp_pager_get_metrics(lp_pager* p, lp_pager_metrics* out) {
     out->fetches = p->fetches;
     out->stalls = p->stalls;
     out->ram_hits = 0;
+    for (int i = 0; i < 7; ++i) out->latency_ms_buckets[i] = p->lat_buckets[i];
     if (p->ram) {
         std::lock_guard<std::mutex> rg(p->ram->mu);
         out->ram_hits = p->ram->hits;

@@ -239,6 +239,8 @@ def test_pager_handles_and_ram_tier(cuda, tmp_path):
             pg.release([h.slot for h in hs])
     m = pg.metrics()
     assert m["misses"] == 12 and m["ram_hits"] == 6   # the second round came from the RAM tier
+    # the fetch latency histogram (pager.rs:677-686) counts every worker fetch once
+    assert len(m["latency_ms_buckets"]) == 7 and sum(m["latency_ms_buckets"]) == m["fetches"] == 12
     pg.sync()
     pg.close()
     cuda.destroy_stream(s)
