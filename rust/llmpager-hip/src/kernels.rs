@@ -1,0 +1,287 @@
+//! Hot-path launchers: the surface of `kernels::Kernels`
+//! (`crates/llmpager-cuda/src/kernels.rs`), one method per reference
+//! method with the same argument order and meaning, each a call into the
+//! library's gfx950 launcher (`include/llmpager_hip.h` cites the reference
+//! line each replaces).  The fused MoE layer entries (`moe_*`, `stack_*`)
+//! have no reference method: they replace the per-expert sequence the
+//! reference's decode loop issues (`decode.rs:734-790`).
+use anyhow::Result;
+
+use crate::driver::{CUdeviceptr, CUstream, Cuda};
+use crate::ffi::{self, check, lp_moe_layer_desc, lp_moe_ws_layout};
+
+/// The code objects are loaded by [`Cuda::init`]; `Kernels` keeps the
+/// reference's shape (`load`, then `&self` methods taking `&Cuda`).
+pub struct Kernels {
+    _priv: (),
+}
+
+/// A captured HIP graph of a layer stack (`lp_moe_stack_capture`).
+pub struct Graph {
+    g: *mut ffi::lp_graph,
+}
+
+impl Drop for Graph {
+    fn drop(&mut self) {
+        unsafe { ffi::lp_graph_destroy(self.g) };
+    }
+}
+
+unsafe impl Send for Graph {}
+
+impl Kernels {
+    /// `kernels.rs:44-68`.
+    pub fn load(_cuda: &Cuda) -> Result<Self> {
+        Ok(Self { _priv: () })
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn q4g64_gemv(
+        &self, cuda: &Cuda, blob: CUdeviceptr, x: CUdeviceptr, y: CUdeviceptr, rows: i32, cols: i32, group: i32,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_q4_gemv(cuda.ctx, blob, x, y, rows, cols, group, stream) }, "q4g64_gemv")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn q4g64_gemv_batch(
+        &self, cuda: &Cuda, blobs: CUdeviceptr, region_off: u64, x: CUdeviceptr, x_stride: i32, y: CUdeviceptr,
+        rows: i32, cols: i32, group: i32, experts: i32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_q4_gemv_batch(cuda.ctx, blobs, region_off, x, x_stride, y, rows, cols, group, experts, stream)
+        };
+        check(rc, "q4g64_gemv_batch")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_reduce(
+        &self, cuda: &Cuda, eouts: CUdeviceptr, wts: CUdeviceptr, out: CUdeviceptr, experts: i32, n: i32,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_reduce(cuda.ctx, eouts, wts, out, experts, n, stream) }, "moe_reduce")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn rmsnorm(
+        &self, cuda: &Cuda, x: CUdeviceptr, w: CUdeviceptr, y: CUdeviceptr, rows: i32, n: i32, eps: f32,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_rmsnorm(cuda.ctx, x, w, y, rows, n, eps, stream) }, "rmsnorm")
+    }
+
+    pub fn scale_add(&self, cuda: &Cuda, a: CUdeviceptr, b: CUdeviceptr, s: f32, n: i32, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_scale_add(cuda.ctx, a, b, s, n, stream) }, "scale_add")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn kv_append(
+        &self, cuda: &Cuda, k: CUdeviceptr, v: CUdeviceptr, kcache: CUdeviceptr, vcache: CUdeviceptr, kv_heads: i32,
+        head_dim: i32, pos: i32, max_seq: i32, f16: bool, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_kv_append(cuda.ctx, k, v, kcache, vcache, kv_heads, head_dim, pos, max_seq, f16 as i32, stream)
+        };
+        check(rc, "kv_append")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn bf16_gemv(
+        &self, cuda: &Cuda, w: CUdeviceptr, x: CUdeviceptr, y: CUdeviceptr, rows: i32, cols: i32, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_bf16_gemv(cuda.ctx, w, x, y, rows, cols, stream) }, "bf16_gemv")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn silu_mul(
+        &self, cuda: &Cuda, gate: CUdeviceptr, up: CUdeviceptr, out: CUdeviceptr, n: i32, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_silu_mul(cuda.ctx, gate, up, out, n, stream) }, "silu_mul")
+    }
+
+    /// `a += b` (`kernels.rs:239-251`).
+    pub fn add(&self, cuda: &Cuda, a: CUdeviceptr, b: CUdeviceptr, n: i32, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_add(cuda.ctx, a, b, n, stream) }, "add")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn rope(
+        &self, cuda: &Cuda, x: CUdeviceptr, heads: i32, head_dim: i32, pos: i32, base: f32, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_rope(cuda.ctx, x, heads, head_dim, pos, base, stream) }, "rope")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn attn_decode(
+        &self, cuda: &Cuda, q: CUdeviceptr, kcache: CUdeviceptr, vcache: CUdeviceptr, out: CUdeviceptr,
+        scratch: CUdeviceptr, heads: i32, kv_heads: i32, head_dim: i32, seq_len: i32, max_seq: i32, scale: f32,
+        f16: bool, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_attn_decode(
+                cuda.ctx, q, kcache, vcache, out, scratch, heads, kv_heads, head_dim, seq_len, max_seq, scale,
+                f16 as i32, stream,
+            )
+        };
+        check(rc, "attn_decode")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn bf16_row(
+        &self, cuda: &Cuda, table: CUdeviceptr, row: i32, n: i32, out: CUdeviceptr, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_bf16_row(cuda.ctx, table, row, n, out, stream) }, "bf16_row")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn mla_rope(
+        &self, cuda: &Cuda, x: CUdeviceptr, n_vecs: i32, stride: i32, offset: i32, half: i32, pos: i32,
+        inv_freq: CUdeviceptr, mscale: f32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe { ffi::lp_mla_rope(cuda.ctx, x, n_vecs, stride, offset, half, pos, inv_freq, mscale, stream) };
+        check(rc, "mla_rope")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn mla_attn_decode(
+        &self, cuda: &Cuda, q: CUdeviceptr, cache: CUdeviceptr, ctx: CUdeviceptr, scratch: CUdeviceptr, heads: i32,
+        qk_dim: i32, c_dim: i32, seq_len: i32, max_seq: i32, scale: f32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_mla_attn_decode(cuda.ctx, q, cache, ctx, scratch, heads, qk_dim, c_dim, seq_len, max_seq, scale, stream)
+        };
+        check(rc, "mla_attn_decode")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn bf16_gemv_batch(
+        &self, cuda: &Cuda, w: CUdeviceptr, w_stride: u64, x: CUdeviceptr, x_stride: i32, y: CUdeviceptr,
+        y_stride: i32, rows: i32, cols: i32, batch: i32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_bf16_gemv_batch(cuda.ctx, w, w_stride, x, x_stride, y, y_stride, rows, cols, batch, stream)
+        };
+        check(rc, "bf16_gemv_batch")
+    }
+
+    #[allow(clippy::too_many_arguments)]
+    pub fn strided_copy(
+        &self, cuda: &Cuda, src: CUdeviceptr, src_stride: i32, src_off: i32, dst: CUdeviceptr, dst_stride: i32,
+        dst_off: i32, n_vecs: i32, n: i32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_strided_copy(cuda.ctx, src, src_stride, src_off, dst, dst_stride, dst_off, n_vecs, n, stream)
+        };
+        check(rc, "strided_copy")
+    }
+
+    // ---- beyond the reference's launchers ----
+
+    /// Workspace bytes for [`Self::mla_attn_decode_batch`].
+    pub fn mla_batch_ws_bytes(&self, cuda: &Cuda, batch: i32, c_dim: i32, max_seq: i32) -> u64 {
+        unsafe { ffi::lp_mla_batch_ws_bytes(cuda.ctx, batch, c_dim, max_seq) }
+    }
+
+    /// MLA absorbed decode for `batch` sequences over bf16 latent caches
+    /// (`seq_lens`: device i32 [batch]) on the matrix cores.
+    #[allow(clippy::too_many_arguments)]
+    pub fn mla_attn_decode_batch(
+        &self, cuda: &Cuda, q: CUdeviceptr, cache: CUdeviceptr, cache_stride: u64, seq_lens: CUdeviceptr,
+        ctx: CUdeviceptr, workspace: CUdeviceptr, batch: i32, heads: i32, qk_dim: i32, c_dim: i32, max_seq: i32,
+        scale: f32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_mla_attn_decode_batch(
+                cuda.ctx, q, cache, cache_stride, seq_lens, ctx, workspace, batch, heads, qk_dim, c_dim, max_seq,
+                scale, stream,
+            )
+        };
+        check(rc, "mla_attn_decode_batch")
+    }
+
+    /// Workspace layout (and `total` bytes) of one MoE layer over `t` tokens.
+    pub fn moe_ws_layout(&self, d: &lp_moe_layer_desc, t: i32) -> Result<lp_moe_ws_layout> {
+        let mut out = lp_moe_ws_layout::default();
+        check(unsafe { ffi::lp_moe_ws_layout_get(d, t, &mut out) }, "moe_ws_layout")?;
+        Ok(out)
+    }
+
+    /// Routing alone: router GEMV, top-k, dispatch groups into `ws`.
+    pub fn moe_route(&self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_moe_route(cuda.ctx, d, x, t, ws, stream) }, "moe_route")
+    }
+
+    /// Routing from caller-supplied router logits (f32 [t, experts]).
+    pub fn moe_route_logits(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, logits: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_route_logits(cuda.ctx, d, logits, t, ws, stream) }, "moe_route_logits")
+    }
+
+    /// Paged flow: after routing and the pager's requests for the picks,
+    /// re-resolve the expert entries through the now-current slot table.
+    pub fn moe_resolve(&self, cuda: &Cuda, d: &lp_moe_layer_desc, t: i32, ws: CUdeviceptr, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_moe_resolve(cuda.ctx, d, t, ws, stream) }, "moe_resolve")
+    }
+
+    /// The expert half of a routed layer: `h += sum_k w * expert_k(x)`.
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_experts(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, ws: CUdeviceptr,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_experts(cuda.ctx, d, x, h, t, ws, stream) }, "moe_experts")
+    }
+
+    /// One whole MoE layer: route, gate/up, SiLU, down, weighted combine
+    /// into `h` (`x` = the normalised input, f32 [t, hidden]).
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_forward(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, ws: CUdeviceptr,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_forward(cuda.ctx, d, x, h, t, ws, stream) }, "moe_forward")
+    }
+
+    /// [`Self::moe_forward`] with its workspace in the library's own
+    /// device scratch: no allocation, for callers that cannot allocate.
+    pub fn moe_forward_noalloc(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_forward_noalloc(cuda.ctx, d, x, h, t, stream) }, "moe_forward_noalloc")
+    }
+
+    /// A stack of MoE layers over the residual `h` (f32 [t, hidden]).
+    pub fn stack_forward(
+        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe { ffi::lp_moe_stack_forward(cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, stream) };
+        check(rc, "stack_forward")
+    }
+
+    /// [`Self::stack_forward`] captured once into a HIP graph.
+    pub fn stack_capture(
+        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+    ) -> Result<Graph> {
+        let mut g = std::ptr::null_mut();
+        let rc = unsafe {
+            ffi::lp_moe_stack_capture(cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, stream, &mut g)
+        };
+        check(rc, "stack_capture")?;
+        Ok(Graph { g })
+    }
+
+    pub fn graph_launch(&self, cuda: &Cuda, g: &Graph, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_graph_launch(cuda.ctx, g.g, stream) }, "graph_launch")
+    }
+
+    /// Synchronise `stream` and read the layer's (unique experts, error
+    /// flags); a non-zero flag word is an error.
+    pub fn moe_status(&self, cuda: &Cuda, ws: CUdeviceptr, d: &lp_moe_layer_desc, t: i32, stream: CUstream) -> Result<i32> {
+        let (mut uniq, mut flags) = (0i32, 0i32);
+        let rc = unsafe { ffi::lp_moe_status_sync(cuda.ctx, ws, d, t, stream, &mut uniq, &mut flags) };
+        check(rc, "moe_status")?;
+        anyhow::ensure!(flags == 0, "MoE layer reported error flags {flags:#x}");
+        Ok(uniq)
+    }
+}

@@ -62,7 +62,7 @@ def test_blob_format_matches_converter():
     b = lp.synth_blob(H, I, g, 1, 2, 3)
     hdr = b[:32].view(np.uint32)
     assert list(hdr) == [64, 128, 64, 128, 128, 64, 64, 0]  # lib.rs:276-281
-    # config-1 shape: 2,654,240 B per blob
+    # config-1 shape (Qwen3-30B-A3B, H 2048, I 768, group 32): 2,654,240 B per blob
     assert lp.blob_bytes(2048, 768, 32) == 2654240
     assert lp.blob_offsets(2048, 768, 32) == (32, 884768, 1769504)
 
@@ -146,3 +146,30 @@ def test_ws_layout_alignment_and_size():
         assert all(o % 256 == 0 for o in offs)
         assert offs == sorted(offs)
         assert lay.total >= lay.y + T * 8 * 2048 * 4
+
+
+def _c_struct_fields(text, name):
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = decl.split(None, 1)[1] if not decl.startswith("const ") else decl.split(None, 2)[2]
+        fields += [re.sub(r"[\s*]|\[.*\]", "", n) for n in names.split(",")]
+    return fields
+
+
+def test_rust_bindings_follow_the_header():
+    """rust/llmpager-hip/src/ffi.rs declares only functions the header
+    declares, and its repr(C) structs list the header's fields in order."""
+    rs = open(os.path.join(ROOT, "rust", "llmpager-hip", "src", "ffi.rs")).read()
+    hdr = open(HEADER).read()
+    fns = set(re.findall(r"pub fn (lp_[a-z0-9_]+)\(", rs))
+    assert len(fns) > 80
+    assert not fns - set(declared_functions())
+    for st in ("lp_moe_layer_desc", "lp_moe_ws_layout", "lp_pager_config", "lp_pager_metrics", "lp_expert_handle"):
+        body = re.search(r"pub struct %s \{(.*?)\n\}" % st, rs, flags=re.S).group(1)
+        rs_fields = re.findall(r"pub ([a-z0-9_]+):", body)
+        assert rs_fields == _c_struct_fields(hdr, st), st
