@@ -221,7 +221,9 @@ typedef struct lp_moe_ws_layout {
     uint64_t et;      /* 32-byte expert entries [E] for the grouped kernels */
     uint64_t act;     /* f32 [T*k, I] */
     uint64_t y;       /* f32 [T*k, H] */
-    uint64_t xf;      /* [T] bf16 hi/lo fragment images of x for the grouped gate/up */
+    uint64_t xf;      /* [T] bf16 hi/lo images of x for the prefill GEMM (size 0 without it) */
+    uint64_t xd;      /* [T] digit images of x for the grouped kernels (per 32 columns 16-bit
+                         fixed point as two int8 digits, a seed and a scale) */
     uint64_t sh_et;   /* shared MLP: its expert entry (size 0 without one) */
     uint64_t sh_perm; /* shared MLP: i32 [T] identity token list */
     uint64_t sh_act;  /* shared MLP: f32 [T, shared_inter] */

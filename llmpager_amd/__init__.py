@@ -56,7 +56,7 @@ class WsLayout(C.Structure):
     """lp_moe_ws_layout: byte offsets of the workspace parts."""
 
     _fields_ = [(n, C.c_uint64) for n in (
-        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y", "xf",
+        "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y", "xf", "xd",
         "sh_et", "sh_perm", "sh_act", "sh_y", "tiles", "actimg", "xlo", "disp", "total")]
 
 
@@ -241,6 +241,13 @@ def route_expf_sweep(first: int, stride: int, n: int) -> np.ndarray:
     out = np.zeros(n, np.float32)
     lib().lp_route_expf_sweep(first, stride, n, _ptr(out))
     return out
+
+
+def dimage_bytes(cols: int) -> int:
+    """Bytes of one row's digit image in the workspace's xd part: per padded
+    32-column sub-group 32 B of hi digits, 32 B of lo digits, an 8-byte seed
+    pair and a 4-byte scale."""
+    return 76 * 4 * (((cols >> 5) + 3) >> 2)
 
 
 def ws_layout(desc: LayerDesc, T: int) -> WsLayout:

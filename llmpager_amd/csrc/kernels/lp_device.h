@@ -110,26 +110,40 @@ __device__ __forceinline__ LP_GLOBAL T* gptr_w(uint64_t a) {
 // (q[row, c] - 8) * x[t][c] in fp32.  Sub-groups are 32 columns; one f16
 // scale covers 2^rs sub-groups (rs = log2(group / 32)).
 //
-// MFMA v_mfma_f32_16x16x32_bf16 (C[m][n] += sum_k A[m][k] B[k][n]):
+// Activations are integer digits: per (token, sub-group) the 32 values are
+// 16-bit fixed point against their largest magnitude m, xq = rint(x * 32639
+// / m) with sigma = m / 32639, written as two int8 digits hi = (xq + 128) >>
+// 8 and lo = xq - 256 hi.  The stored nibbles n = q + 8 (0 .. 15) are the
+// weight operand as they are, one AND (even columns) or a shift and an AND
+// (odd columns) per four.
+//
+// MFMA v_mfma_i32_16x16x64_i8 (C[m][n] += sum_k A[m][k] B[k][n]):
 //   B (weights): lane l = (n = l % 16, kb = l / 16).  At step c the four
 //     lanes of row n load sub-groups 4c..4c+3 (64 contiguous bytes of the row,
-//     16 per lane); MFMA d (0..3) takes the d-th 32-bit word of each load.
-//   A (activations): row m = 4*slot + th, th = 2*token + part, part 0 =
-//     bf16(x), part 1 = bf16(x - bf16(x)).  Element (m, k = 8*kbA + i) is
-//     non-zero only when slot == kbA, so the 16 MFMA output rows keep four
-//     sub-groups x four (token, part) apart.  Lanes whose slot is not their
-//     kb read a zero block, so every LDS read is unconditional.
+//     16 per lane: words w0..w3 = columns 0-7, 8-15, 16-23, 24-31); MFMA h
+//     (0, 1) takes w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F of words 2h and
+//     2h + 1, i.e. byte t of the lane's 16 holds column
+//     16h + 8 (t >> 3) + 2 (t & 3) + ((t >> 2) & 1)  (digit_col).
+//   A (activations): row m = 4*slot + th, th = 2*token + digit (0 = hi, 1 =
+//     lo).  Element (m, k = 16*kbA + t) is non-zero only when slot == kbA, so
+//     the 16 output rows keep four sub-groups x four (token, digit) apart.
+//     Lanes whose slot is not their kb read a zero block, so every LDS read
+//     is unconditional.
 //   C: lane l holds C[4*(l/16) + i][l % 16]: its own sub-group (slot = kb),
-//     th = i.  With n = q + 8 the stored nibble, the weight operand is
-//     128 + n, so sum_k (128 + n_k) x_k = sum_k (n_k - 8) x_k + 136 sum_k x_k;
-//     the accumulator is therefore seeded with -136 * sum_k x_k of the part.
-// Products of bf16 values are exact in fp32 and x = part0 + part1 to 16
-// significant bits, so the only roundings are the fp32 accumulations.
+//     th = i.  Seeded with (0, -8 sum xq) per token, the row pair gives
+//     V = 256 C[hi] + C[lo] = sum_k (n_k - 8) xq_k exactly in int32, and the
+//     lane adds s * sigma * V to the token's fp32 sum.
+// The digits carry x to within sigma / 2 (2^-16 of the sub-group's largest
+// magnitude); the products and their sums are exact integers, so the only
+// roundings are that quantisation and the fp32 accumulation.
 //
 // LDS (see lpk::frag_lds_bytes): zero block, then per token pair p
-//   frag[p][th][g][d] : uint4 (8 bf16 in element order i), g < ngp
-//   off [p][g][th]    : float, -136 * sum of the th part over sub-group g
+//   frag[p][th][g] : 32 B (MFMA h = 0 bytes, then h = 1), g < ngp
+//   off [p][g]     : int4 (0, seed of token 2p, 0, seed of token 2p + 1)
+//   sig [p][g]     : float2 (sigma of token 2p, sigma of token 2p + 1)
 // ---------------------------------------------------------------------------
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 struct Frags {
     uint8_t* lds;  // start of the fragment area (zero block first)
@@ -145,13 +159,20 @@ __device__ __forceinline__ Frags frags_at(uint8_t* lds, int cols) {
     return F;
 }
 
-__device__ __forceinline__ uint8_t* frag_ptr(const Frags& F, int p, int th, int g) {
-    return F.lds + lpk::kZeroBytes + p * lpk::frag_pair_bytes(F.ngp) + th * lpk::frag_th_stride(F.ngp) + g * 64;
+__device__ __forceinline__ uint8_t* pair_base(const Frags& F, int p) {
+    return F.lds + lpk::kZeroBytes + p * lpk::frag_pair_bytes(F.ngp);
 }
 
-__device__ __forceinline__ float* off_ptr(const Frags& F, int p, int g) {
-    return reinterpret_cast<float*>(F.lds + lpk::kZeroBytes + p * lpk::frag_pair_bytes(F.ngp) +
-                                    4 * lpk::frag_th_stride(F.ngp) + g * 16);
+__device__ __forceinline__ uint8_t* frag_ptr(const Frags& F, int p, int th, int g) {
+    return pair_base(F, p) + th * lpk::frag_th_stride(F.ngp) + g * 32;
+}
+
+__device__ __forceinline__ int32_t* off_ptr(const Frags& F, int p, int g) {
+    return reinterpret_cast<int32_t*>(pair_base(F, p) + lpk::frag_off_bytes(F.ngp) + g * 16);
+}
+
+__device__ __forceinline__ float* sig_ptr(const Frags& F, int p, int g) {
+    return reinterpret_cast<float*>(pair_base(F, p) + lpk::frag_sig_bytes(F.ngp) + g * 8);
 }
 
 // Zero the idle-lane block (once per workgroup, before the first barrier).
@@ -160,10 +181,120 @@ __device__ __forceinline__ void zero_block(const Frags& F, int tid, int nthreads
         reinterpret_cast<uint4*>(F.lds)[i] = make_uint4(0, 0, 0, 0);
 }
 
-// One 32-column sub-group of an fp32 row as fragment words: the bf16 parts
-// hi = bf16(x) and lo = bf16(x - hi) in fragment order (32-bit word w of
-// uint4 d pairs columns 8d + w and 8d + w + 4) and each part's sum.  p == 0
-// gives zeros (padding sub-groups, missing tokens).
+// Column (within a 32-column sub-group) of digit byte t of MFMA h.
+__device__ __forceinline__ constexpr int digit_col(int h, int t) {
+    return 16 * h + 8 * (t >> 3) + 2 * (t & 3) + ((t >> 2) & 1);
+}
+
+// The largest magnitude below which a sub-group's digits are all zero (its
+// contribution is below fp32's reach next to any other sub-group's).
+constexpr float kDigitMin = 1.0e-30f;
+
+// 16-bit fixed point of one value against inv = 32639 / m, as hi and lo
+// digits; returns xq.
+__device__ __forceinline__ int digit_split(float x, float inv, int& hi, int& lo) {
+    const int xq = (int)rintf(x * inv);
+    hi = (xq + 128) >> 8;
+    lo = xq - (hi << 8);
+    return xq;
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 255) | ((uint32_t)(b & 255) << 8) | ((uint32_t)(c & 255) << 16) | ((uint32_t)d << 24);
+}
+
+// One 32-column sub-group of an fp32 row as digits in operand order, its
+// seed -8 * sum xq and sigma.  p == 0 gives zeros (padding sub-groups,
+// missing tokens).
+struct DigitGroup {
+    uint4 hi[2], lo[2];
+    int32_t seed;
+    float sigma;
+};
+
+__device__ __forceinline__ DigitGroup digit_group(const LP_GLOBAL float4* p) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float4 f = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (p) f = p[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+    DigitGroup q;
+    const bool live = m >= kDigitMin;
+    const float inv = live ? 32639.0f / m : 0.0f;
+    q.sigma = live ? m / 32639.0f : 0.0f;
+    int hi[32], lo[32], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) sum += digit_split(v[i], inv, hi[i], lo[i]);
+    q.seed = -8 * sum;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t wh[4], wl[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int c0 = digit_col(h, 4 * w), c1 = digit_col(h, 4 * w + 1), c2 = digit_col(h, 4 * w + 2),
+                      c3 = digit_col(h, 4 * w + 3);
+            wh[w] = pack_i8x4(hi[c0], hi[c1], hi[c2], hi[c3]);
+            wl[w] = pack_i8x4(lo[c0], lo[c1], lo[c2], lo[c3]);
+        }
+        q.hi[h] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        q.lo[h] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    }
+    return q;
+}
+
+// Stage ntok activation rows into fragment pairs 0 .. ceil(ntok/2)-1.
+// row_of(t) returns the f32 row of token t.  Work units (token, sub-group)
+// are spread over the `nthreads` participating threads; a missing second
+// token of the last pair and the padding sub-groups are written as zeros.
+template <typename RowOf>
+__device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int tid, int nthreads) {
+    const int units = ((ntok + 1) & ~1) * F.ngp;
+    for (int u = tid; u < units; u += nthreads) {
+        const int t = u / F.ngp;
+        const int g = u - t * F.ngp;
+        const int pair = t >> 1, tk = t & 1;
+        const bool live = t < ntok && g < F.ng;
+        const DigitGroup q =
+            digit_group(live ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 0, g) + h * 16) = q.hi[h];
+            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 1, g) + h * 16) = q.lo[h];
+        }
+        int32_t* of = off_ptr(F, pair, g);
+        of[2 * tk + 0] = 0;
+        of[2 * tk + 1] = q.seed;
+        sig_ptr(F, pair, g)[tk] = q.sigma;
+    }
+}
+
+// Sub-group g of an fp32 row of `cols` columns into the row's digit image
+// (lpk::dimage_bytes layout).
+__device__ __forceinline__ void write_dimage_group(const float* row, int cols, int g, uint8_t* img) {
+    const int ng = cols >> 5, ngp = lpk::frag_ngp(cols);
+    const DigitGroup q =
+        digit_group(g < ng ? gptr<float4>(reinterpret_cast<uint64_t>(row + (size_t)g * 32)) : nullptr);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        reinterpret_cast<uint4*>(img + (size_t)g * 32)[h] = q.hi[h];
+        reinterpret_cast<uint4*>(img + (size_t)ngp * 32 + (size_t)g * 32)[h] = q.lo[h];
+    }
+    reinterpret_cast<int2*>(img + lpk::dimage_seed_off(ngp))[g] = make_int2(0, q.seed);
+    reinterpret_cast<float*>(img + lpk::dimage_sigma_off(ngp))[g] = q.sigma;
+}
+
+// One 32-column sub-group of an fp32 row as bf16 fragment words (the prefill
+// GEMM's A operand): the parts hi = bf16(x) and lo = bf16(x - hi) in
+// fragment order (32-bit word w of uint4 d pairs columns 8d + w and 8d + w +
+// 4) and each part's sum.  p == 0 gives zeros.
 struct GroupFrag {
     uint4 hi[4], lo[4];
     float shi, slo;
@@ -198,31 +329,6 @@ __device__ __forceinline__ GroupFrag convert_group(const LP_GLOBAL float4* p) {
                              lo[3] | (lo[7] << 16));
     }
     return q;
-}
-
-// Stage ntok activation rows into fragment pairs 0 .. ceil(ntok/2)-1.
-// row_of(t) returns the f32 row of token t.  Work units (token, sub-group)
-// are spread over the `nthreads` participating threads; a missing second
-// token of the last pair and the padding sub-groups are written as zeros.
-template <typename RowOf>
-__device__ inline void stage_rows(const Frags& F, int ntok, RowOf row_of, int tid, int nthreads) {
-    const int units = ((ntok + 1) & ~1) * F.ngp;
-    for (int u = tid; u < units; u += nthreads) {
-        const int t = u / F.ngp;
-        const int g = u - t * F.ngp;
-        const int pair = t >> 1, tk = t & 1;
-        const bool live = t < ntok && g < F.ng;
-        const GroupFrag q =
-            convert_group(live ? gptr<float4>(reinterpret_cast<uint64_t>(row_of(t) + (size_t)g * 32)) : nullptr);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 0, g) + d * 16) = q.hi[d];
-            *reinterpret_cast<uint4*>(frag_ptr(F, pair, 2 * tk + 1, g) + d * 16) = q.lo[d];
-        }
-        float* of = off_ptr(F, pair, g);
-        of[2 * tk + 0] = -136.0f * q.shi;
-        of[2 * tk + 1] = -136.0f * q.slo;
-    }
 }
 
 // Sub-group g of an fp32 row of `cols` columns into the row's fragment image
@@ -273,49 +379,55 @@ __device__ __forceinline__ uint32_t lds_addr_of(const uint8_t* p) {
         (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p);
 }
 
-// Copy the fragment images of nt tokens (img_of(t): device address of token
-// t's image) into fragment pairs 0 .. ceil(nt/2)-1.  Part blocks go straight
+// Copy the digit images of nt tokens (img_of(t): device address of token t's
+// image) into fragment pairs 0 .. ceil(nt/2)-1.  Digit blocks go straight
 // from memory into LDS (64 lanes fill 1 KB per instruction, no registers, no
-// LDS store), one instruction per wave in turn; the seeds go through
-// registers.  Ends with every load of the calling thread complete; the
-// caller's barrier then publishes the copy.  The second token of an odd last
-// pair is left as it is: its MFMA output rows are separate and never stored.
+// LDS store), one instruction per wave in turn; the seeds and scales go
+// through registers.  Ends with every load of the calling thread complete;
+// the caller's barrier then publishes the copy.  The second token of an odd
+// last pair is left as it is: its MFMA output rows are separate and never
+// stored.
 template <typename ImgOf>
 __device__ inline void load_images(const Frags& F, int nt, ImgOf img_of) {
     const int lane = lane_id(), wave = threadIdx.x >> 6, W = blockDim.x >> 6;
-    const int q4 = 4 * F.ngp;          // 16-byte units per part block
-    const int ipb = (q4 + 63) >> 6;    // DMA instructions per part block
+    const int q4 = 2 * F.ngp;          // 16-byte units per digit block
+    const int ipb = (q4 + 63) >> 6;    // DMA instructions per digit block
     for (int i = wave; i < 2 * nt * ipb; i += W) {
-        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + part
+        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + digit
         const int t = blk >> 1, part = blk & 1;
         const int q = r * 64 + lane;
-        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)r * 1024);
+        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 32 + (uint64_t)r * 1024);
         const uint32_t dst = lds_addr_of(frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024);
         if (q < q4) lds_copy16(base, (uint32_t)lane * 16u, dst);
     }
     for (int f = threadIdx.x; f < nt * F.ngp; f += blockDim.x) {
         const int t = f / F.ngp, g = f - t * F.ngp;
-        const uint2 sd = gptr<uint2>(img_of(t) + (uint64_t)F.ngp * 128)[g];
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(off_ptr(F, t >> 1, g)) + (t & 1) * 8) = sd;
+        const uint64_t img = img_of(t);
+        const int2 sd = gptr<int2>(img + lpk::dimage_seed_off(F.ngp))[g];
+        const float sg = gptr<float>(img + lpk::dimage_sigma_off(F.ngp))[g];
+        reinterpret_cast<int2*>(off_ptr(F, t >> 1, g))[t & 1] = sd;
+        sig_ptr(F, t >> 1, g)[t & 1] = sg;
     }
     __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct loads have landed
 }
 
-// load_images without registers and without the final wait: the seeds, too,
-// are gathered straight into LDS (one 4-byte copy per lane: dword d of pair
-// p's seed block is seed (d & 1) of token 2p + ((d >> 1) & 1) at sub-group
-// d >> 2; a missing second token repeats the first).  The caller waits for
-// every load of the thread (vmcnt 0) before its barrier, so these may be
-// issued ahead of other loads that the same wait then covers.
+// load_images without registers and without the final wait: the seeds and
+// scales, too, are gathered straight into LDS (one 4-byte copy per lane:
+// dword d of pair p's seed block is word (d & 1) of token 2p + ((d >> 1) & 1)
+// at sub-group d >> 2, dword d of its scale block the scale of token
+// 2p + (d & 1) at sub-group d >> 1; a missing second token repeats the
+// first).  The caller waits for every load of the thread (vmcnt 0) before its
+// barrier, so these may be issued ahead of other loads that the same wait
+// then covers.
 template <typename ImgOf>
 __device__ inline void issue_images(const Frags& F, int nt, ImgOf img_of) {
     const int lane = lane_id(), wave = threadIdx.x >> 6, W = blockDim.x >> 6;
-    const int q4 = 4 * F.ngp;          // 16-byte units per part block
-    const int ipb = (q4 + 63) >> 6;    // copies per part block
+    const int q4 = 2 * F.ngp;          // 16-byte units per digit block
+    const int ipb = (q4 + 63) >> 6;    // copies per digit block
     for (int i = wave; i < 2 * nt * ipb; i += W) {
-        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + part
+        const int blk = i / ipb, r = i - blk * ipb;  // blk = 2 * token + digit
         const int t = blk >> 1, part = blk & 1;
-        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 64 + (uint64_t)r * 1024);
+        const uint64_t base = uniform_u64(img_of(t) + (uint64_t)part * F.ngp * 32 + (uint64_t)r * 1024);
         const uint32_t dst = lds_addr_of(frag_ptr(F, t >> 1, 2 * (t & 1) + part, 0) + r * 1024);
         if (r * 64 + lane < q4) lds_copy16(base, (uint32_t)lane * 16u, dst);
     }
@@ -327,7 +439,18 @@ __device__ inline void issue_images(const Frags& F, int nt, ImgOf img_of) {
         const int g = d >> 2;
         const int t = min(2 * p + ((d >> 1) & 1), nt - 1);
         const uint32_t dst = lds_addr_of(reinterpret_cast<const uint8_t*>(off_ptr(F, p, 0)) + r * 256);
-        if (g < F.ngp) lds_copy4(img_of(t) + (uint64_t)F.ngp * 128 + (uint64_t)g * 8 + (uint64_t)(d & 1) * 4, dst);
+        if (g < F.ngp)
+            lds_copy4(img_of(t) + (uint64_t)lpk::dimage_seed_off(F.ngp) + (uint64_t)g * 8 + (uint64_t)(d & 1) * 4,
+                      dst);
+    }
+    const int gpp = (F.ngp * 2 + 63) >> 6;  // scale copies per pair
+    for (int i = wave; i < npair * gpp; i += W) {
+        const int p = i / gpp, r = i - p * gpp;
+        const int d = r * 64 + lane;
+        const int g = d >> 1;
+        const int t = min(2 * p + (d & 1), nt - 1);
+        const uint32_t dst = lds_addr_of(reinterpret_cast<const uint8_t*>(sig_ptr(F, p, 0)) + r * 256);
+        if (g < F.ngp) lds_copy4(img_of(t) + (uint64_t)lpk::dimage_sigma_off(F.ngp) + (uint64_t)g * 4, dst);
     }
 }
 
@@ -448,11 +571,13 @@ __device__ __forceinline__ void opaque(WRegs<NS, SL>& R) {
     }
 }
 
-// Per-lane LDS bases for the A operand and the accumulator seeds of pair p
-// at step chunk c0 (steps are 256 B apart in frag, 64 B apart in off).
+// Per-lane LDS bases for the A operand, the accumulator seeds and the token
+// scales of pair p at step chunk c0 (steps are 128 B apart in frag, 64 B in
+// off, 32 B in sig).
 struct ABase {
     const uint8_t* a;
     const uint8_t* o;
+    const uint8_t* sg;
 };
 
 __device__ __forceinline__ ABase abase(const Frags& F, int p, int c0) {
@@ -462,7 +587,16 @@ __device__ __forceinline__ ABase abase(const Frags& F, int p, int c0) {
     ABase b;
     b.a = live ? frag_ptr(F, p, m & 3, 4 * c0 + kb) : F.lds;
     b.o = reinterpret_cast<const uint8_t*>(off_ptr(F, p, 4 * c0 + kb));
+    b.sg = reinterpret_cast<const uint8_t*>(sig_ptr(F, p, 4 * c0 + kb));
     return b;
+}
+
+// The two B operands of one 16-byte nibble load: bytes in digit_col order.
+__device__ __forceinline__ void q4_digits(const uint4& w, i32x4_t& b0, i32x4_t& b1) {
+    b0 = i32x4_t{(int)(w.x & 0x0F0F0F0Fu), (int)((w.x >> 4) & 0x0F0F0F0Fu), (int)(w.y & 0x0F0F0F0Fu),
+                 (int)((w.y >> 4) & 0x0F0F0F0Fu)};
+    b1 = i32x4_t{(int)(w.z & 0x0F0F0F0Fu), (int)((w.z >> 4) & 0x0F0F0F0Fu), (int)(w.w & 0x0F0F0F0Fu),
+                 (int)((w.w >> 4) & 0x0F0F0F0Fu)};
 }
 
 // MFMAs of one loaded chunk for M weight tiles that share the same staged
@@ -481,6 +615,7 @@ __device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&
     for (int j = 0; j < NS; ++j) {
         if (j < rem) {  // uniform
             float s[M];
+            i32x4_t b[M][2];
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 if constexpr (SL)
@@ -489,36 +624,22 @@ __device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&
                 else
                     s[m] = f16_bits_to_f32(R[m].s[j]);
                 if (j == rem - 1 && !R[m].lastok) s[m] = 0.0f;
+                q4_digits(R[m].w[j], b[m][0], b[m][1]);
             }
 #pragma unroll
             for (int p = 0; p < P; ++p) {
                 if (p > 0 && p >= np) break;  // uniform: pairs staged in this token group
-                const float4 o = *reinterpret_cast<const float4*>(B[p].o + j * 64);
-                f32x4_t c[M];
+                const i32x4_t o = *reinterpret_cast<const i32x4_t*>(B[p].o + j * 64);
+                const float2 sg = *reinterpret_cast<const float2*>(B[p].sg + j * 32);
+                const i32x4_t a0 = *reinterpret_cast<const i32x4_t*>(B[p].a + j * 128);
+                const i32x4_t a1 = *reinterpret_cast<const i32x4_t*>(B[p].a + j * 128 + 16);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    c[m][0] = o.x;
-                    c[m][1] = o.y;
-                    c[m][2] = o.z;
-                    c[m][3] = o.w;
-                }
-                // one A fragment and one decoded weight word per MFMA keeps
-                // the step's temporaries to a few registers beside the chunk
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint4 a = *reinterpret_cast<const uint4*>(B[p].a + j * 256 + d * 16);
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const uint32_t w = d == 0 ? R[m].w[j].x : d == 1 ? R[m].w[j].y
-                                         : d == 2 ? R[m].w[j].z : R[m].w[j].w;
-                        c[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8_t, a), q4_word_to_bf16x8(w), c[m], 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    acc[m][p][0] = __builtin_fmaf(s[m], c[m][0] + c[m][1], acc[m][p][0]);
-                    acc[m][p][1] = __builtin_fmaf(s[m], c[m][2] + c[m][3], acc[m][p][1]);
+                    i32x4_t c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b[m][0], o, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b[m][1], c, 0, 0, 0);
+                    const int v0 = (c[0] << 8) + c[1], v1 = (c[2] << 8) + c[3];
+                    acc[m][p][0] = __builtin_fmaf(s[m] * sg.x, (float)v0, acc[m][p][0]);
+                    acc[m][p][1] = __builtin_fmaf(s[m] * sg.y, (float)v1, acc[m][p][1]);
                 }
             }
         }

@@ -44,12 +44,12 @@ __device__ __forceinline__ float div_rn(float a, float b) { return (float)((doub
 // ---------------------------------------------------------------------------
 namespace {
 
-// Token t's image, by the whole workgroup, and its lo flag (W.xlo[t]).
-// Token t's image from its row staged in LDS, by the whole workgroup: thread
-// u takes sub-group u / 4, columns 8 (u % 4) .. 8 (u % 4) + 7, writes their
-// bf16 parts, and the four threads of a sub-group add their part sums by
-// quad permutations ((s0 + s1) + (s2 + s3); the seed's rounding may differ
-// from the sequential sum of write_image_group in the last place).
+// Token t's bf16 image (the prefill GEMM's A operand) from its row staged in
+// LDS, by the whole workgroup, and its lo flag (W.xlo[t]): thread u takes
+// sub-group u / 4, columns 8 (u % 4) .. 8 (u % 4) + 7, writes their bf16
+// parts, and the four threads of a sub-group add their part sums by quad
+// permutations ((s0 + s1) + (s2 + s3); the seed's rounding may differ from
+// the sequential sum of write_image_group in the last place).
 __device__ __forceinline__ void write_image_lds(const RouteArgs& a, int t, const float* row) {
     const int H = a.L.hidden, ng = H >> 5, ngp = frag_ngp(H);
     uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
@@ -92,14 +92,72 @@ __device__ __forceinline__ void write_image_lds(const RouteArgs& a, int t, const
     if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo_any ? 1 : 0;
 }
 
+// Token t's digit image (the grouped kernels' A operand) from its row staged
+// in LDS, by the whole workgroup: the four threads of a sub-group take eight
+// columns each, share the sub-group's largest magnitude and their sum of xq
+// by quad permutations (exact: a maximum and an integer sum), and write their
+// eight columns' digits, which are contiguous in operand order (even columns,
+// then odd).  The same bytes as write_dimage_group.
+__device__ __forceinline__ void write_dimage_lds(const RouteArgs& a, int t, const float* row) {
+    const int H = a.L.hidden, ng = H >> 5, ngp = frag_ngp(H);
+    uint8_t* img = dptr<uint8_t>(a.W.xd) + (size_t)t * dimage_bytes(H);
+    for (int u = threadIdx.x; u < 4 * ngp; u += blockDim.x) {  // whole quads together
+        const int g = u >> 2, d = u & 3;
+        float v[8];
+        if (g < ng) {
+            const float4 f0 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8);
+            const float4 f1 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8 + 4);
+            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+            v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xb1, 0xf, 0xf, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4e, 0xf, 0xf, false)));
+        const bool live = m >= kDigitMin;
+        const float inv = live ? 32639.0f / m : 0.0f;
+        int hi[8], lo[8], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += digit_split(v[i], inv, hi[i], lo[i]);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0xb1, 0xf, 0xf, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x4e, 0xf, 0xf, false);
+        // columns 8d + {0, 2, 4, 6}, then 8d + {1, 3, 5, 7}
+        *reinterpret_cast<uint2*>(img + (size_t)g * 32 + d * 8) =
+            make_uint2(pack_i8x4(hi[0], hi[2], hi[4], hi[6]), pack_i8x4(hi[1], hi[3], hi[5], hi[7]));
+        *reinterpret_cast<uint2*>(img + (size_t)ngp * 32 + (size_t)g * 32 + d * 8) =
+            make_uint2(pack_i8x4(lo[0], lo[2], lo[4], lo[6]), pack_i8x4(lo[1], lo[3], lo[5], lo[7]));
+        if (d == 0) {
+            reinterpret_cast<int2*>(img + dimage_seed_off(ngp))[g] = make_int2(0, -8 * sum);
+            reinterpret_cast<float*>(img + dimage_sigma_off(ngp))[g] = live ? m / 32639.0f : 0.0f;
+        }
+    }
+}
+
+// Token t's images from its row in memory, by the whole workgroup.
 __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
     const int H = a.L.hidden;
     const float* row = dptr<const float>(a.x) + (size_t)t * H;
-    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-    bool lo = false;
-    for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) lo |= write_image_group(row, H, g, img);
-    lo = __syncthreads_or(lo);
-    if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
+    if (a.make_xf & kImgDigits) {
+        uint8_t* img = dptr<uint8_t>(a.W.xd) + (size_t)t * dimage_bytes(H);
+        for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) write_dimage_group(row, H, g, img);
+    }
+    if (a.make_xf & kImgBf16) {
+        uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
+        bool lo = false;
+        for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) lo |= write_image_group(row, H, g, img);
+        lo = __syncthreads_or(lo);
+        if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
+    }
+}
+
+// Token t's images from its row staged in LDS.
+__device__ __forceinline__ void write_images_lds(const RouteArgs& a, int t, const float* row) {
+    if (a.make_xf & kImgDigits) write_dimage_lds(a, t, row);
+    if (a.make_xf & kImgBf16) write_image_lds(a, t, row);
 }
 
 
@@ -318,19 +376,25 @@ __device__ __forceinline__ void router_rows(const RouteArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs a) { router_rows(a); }
 
-// Fragment images of x alone (callers that route from their own logits, and
-// the large-batch router): one wave per token, lane l converting sub-groups
-// l, l + 64, ...; W.xlo[t] from a wave vote.  Grid (ceil(T / 4)), 256 threads.
+// Images of x alone (callers that route from their own logits, and the
+// large-batch router): one wave per token, lane l converting sub-groups l,
+// l + 64, ...; W.xlo[t] from a wave vote.  Grid (ceil(T / 4)), 256 threads.
 extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs a) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
     const int H = a.L.hidden, lane = lane_id();
     const float* row = dptr<const float>(a.x) + (size_t)t * H;
-    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-    bool lo = false;
-    for (int g = lane; g < frag_ngp(H); g += 64) lo |= write_image_group(row, H, g, img);
-    lo = __any(lo);
-    if (lane == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
+    if (a.make_xf & kImgDigits) {
+        uint8_t* img = dptr<uint8_t>(a.W.xd) + (size_t)t * dimage_bytes(H);
+        for (int g = lane; g < frag_ngp(H); g += 64) write_dimage_group(row, H, g, img);
+    }
+    if (a.make_xf & kImgBf16) {
+        uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
+        bool lo = false;
+        for (int g = lane; g < frag_ngp(H); g += 64) lo |= write_image_group(row, H, g, img);
+        lo = __any(lo);
+        if (lane == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1063,7 +1127,7 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
         const bool staged = nt * a.L.hidden * 4 <= kRouteXLds;
         for (int t = first; t < nt; t += step) {
             if (staged)
-                write_image_lds(a, t0 + t, xs + (size_t)t * a.L.hidden);
+                write_images_lds(a, t0 + t, xs + (size_t)t * a.L.hidden);
             else
                 write_image(a, t0 + t);
         }
@@ -1230,8 +1294,8 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
     const WTile<RS> TG = wtile<RS>(x.blob + L.gate_off, I, H, n0);
     const WTile<RS> TU = wtile<RS>(x.blob + L.up_off, I, H, n0);
     const int* perm = dptr<const int>(a.W.perm);
-    const uint64_t xf = a.W.xf;
-    const uint64_t ib = (uint64_t)image_bytes(H);
+    const uint64_t xf = a.W.xd;
+    const uint64_t ib = (uint64_t)dimage_bytes(H);
     const int cap = min(kMaxPairs, a.pairs_cap);
     // The first token group's images (tokens from the entry: no lookup) are
     // copied first, the weights loaded after them; one wait then covers both
@@ -1387,7 +1451,7 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     uint64_t sblob[2];
     int sp0[2], snt[2];
     const LP_GLOBAL int* perm = gptr<int>(a.W.perm);
-    const uint64_t xf = a.W.xf, ib = (uint64_t)image_bytes(H);
+    const uint64_t xf = a.W.xd, ib = (uint64_t)dimage_bytes(H);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const ExpertEntry x = P.x[s];

@@ -36,23 +36,37 @@ constexpr int kDownChunk = 8;          // steps per chunk in the two-tile groupe
 constexpr int kDownWideChunk = 16;     // one-tile down: tiles up to this many steps in one piece
 constexpr int kDownLoopChunk = 8;      // steps per chunk of longer one-tile down tiles
 constexpr int kGemvChunk = 8;          // steps per chunk in the 1:1 q4 GEMV
-constexpr int kZeroBytes = 256 * kMaxChunk;  // LDS zero block read by idle MFMA lanes
+constexpr int kZeroBytes = 128 * kMaxChunk;  // LDS zero block read by idle MFMA lanes
 
-// LDS bytes of the fragment area for `pairs` token pairs over `cols` columns:
-// a zero block, then per pair four (token, part) blocks of ngp sub-groups x
-// 64 B (+16 B to stagger banks) and ngp x 16 B of accumulator seeds, with
-// ngp = 4 * ceil(cols / 128) sub-groups (zero padded).
+// LDS bytes of the digit fragment area of the grouped q4 kernels for `pairs`
+// token pairs over `cols` columns: a zero block, then per pair four
+// (token, digit) blocks of ngp sub-groups x 32 B (+16 B to stagger banks),
+// ngp x 16 B of accumulator seeds (int32: 0, seed of the pair's first token,
+// 0, seed of its second) and ngp x 8 B of the two tokens' sub-group scales,
+// with ngp = 4 * ceil(cols / 128) sub-groups (zero padded).
 LPK_HD constexpr int frag_ngp(int cols) { return 4 * (((cols >> 5) + 3) >> 2); }
-LPK_HD constexpr int frag_th_stride(int ngp) { return ngp * 64 + 16; }
-LPK_HD constexpr int frag_pair_bytes(int ngp) { return 4 * frag_th_stride(ngp) + ngp * 16; }
+LPK_HD constexpr int frag_th_stride(int ngp) { return ngp * 32 + 16; }
+LPK_HD constexpr int frag_off_bytes(int ngp) { return 4 * frag_th_stride(ngp); }
+LPK_HD constexpr int frag_sig_bytes(int ngp) { return frag_off_bytes(ngp) + ngp * 16; }
+LPK_HD constexpr int frag_pair_bytes(int ngp) { return frag_sig_bytes(ngp) + ngp * 8; }
 LPK_HD constexpr int frag_lds_bytes(int cols, int pairs) {
     return kZeroBytes + pairs * frag_pair_bytes(frag_ngp(cols));
 }
 
-// A token row's fragment image in device memory, the form the grouped gate/up
-// kernel copies straight into LDS: part 0 (bf16(x)) and part 1
-// (bf16(x - bf16(x))) as [ngp][64 B] blocks in fragment order, then the
-// accumulator seeds [ngp][2] f32 (-136 * the part's sum over the sub-group).
+// A token row's digit image in device memory, the form the grouped q4
+// kernels copy straight into LDS.  Each 32-column sub-group g is held as
+// 16-bit fixed point against its own largest magnitude m: xq = rint(x *
+// 32639 / m), split into digits hi = (xq + 128) >> 8 and lo = xq - 256 hi
+// (both int8), with sigma = m / 32639; the blocks are hi [ngp][32 B] and lo
+// [ngp][32 B] in MFMA operand order, then [ngp][2] int32 (0, -8 * sum xq)
+// and sigma [ngp] f32.
+LPK_HD constexpr int dimage_bytes(int cols) { return 76 * frag_ngp(cols); }
+LPK_HD constexpr int dimage_seed_off(int ngp) { return 64 * ngp; }
+LPK_HD constexpr int dimage_sigma_off(int ngp) { return 72 * ngp; }
+
+// A token row's bf16 fragment image, the A operand of the prefill GEMM: part
+// 0 (bf16(x)) and part 1 (bf16(x - bf16(x))) as [ngp][64 B] blocks, then
+// [ngp][2] f32 seeds (-136 * the parts' sum over the sub-group, 0).
 LPK_HD constexpr int image_bytes(int cols) { return 136 * frag_ngp(cols); }
 
 // The grouped kernels read a one-chunk tile's scales from a per-wave LDS
@@ -246,7 +260,8 @@ struct Workspace {
     uint64_t et;         // ExpertEntry [E]
     uint64_t act;        // f32 [T * k, I] expert-major activations
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
-    uint64_t xf;         // [T] fragment images of the layer input (image_bytes(H) each)
+    uint64_t xf;         // [T] bf16 images of the layer input for the prefill GEMM (image_bytes(H) each)
+    uint64_t xd;         // [T] digit images of the layer input for the grouped kernels (dimage_bytes(H) each)
     uint64_t sh_et;      // shared MLP: shared_entries(T) ExpertEntry (consecutive tokens)
     uint64_t sh_perm;    // shared MLP: i32 [T], t
     uint64_t sh_act;     // shared MLP: f32 [T, shared_inter]
@@ -262,12 +277,15 @@ struct Workspace {
 // one entry of all T tokens above 64.
 LPK_HD constexpr int shared_entries(int T) { return T <= 64 ? (T + kEntryToks - 1) / kEntryToks : 1; }
 
+constexpr int kImgBf16 = 1;    // RouteArgs::make_xf bits
+constexpr int kImgDigits = 2;
+
 struct RouteArgs {
     LayerView L;
     Workspace W;
     uint64_t x;          // f32 [T, H]
     int32_t T;
-    int32_t make_xf;     // router: also write the fragment images of x into W.xf
+    int32_t make_xf;     // router: also write images of x: kImgBf16 into W.xf, kImgDigits into W.xd
     uint64_t sync;       // fused routing: kSyncWords arrival counters, zero between launches
 };
 

@@ -765,6 +765,13 @@ static bool use_gemm(const lp_moe_layer_desc* d, int T) {
     return pairs >= (long)kGemmMinPairsPerExpert * std::min<long>(d->experts, pairs);
 }
 
+// The images of x a layer's expert kernels read: bf16 images for the prefill
+// GEMM, digit images for the grouped kernels (every shared MLP included).
+static int image_kinds(const lp_moe_layer_desc* d, int T) {
+    const bool gemm = use_gemm(d, T);
+    return (gemm ? kImgBf16 : 0) | (!gemm || d->shared_blob ? kImgDigits : 0);
+}
+
 static int gemm_max_tiles(const lp_moe_layer_desc* d, int T) {
     const int pairs = T * d->top_k;
     return pairs / kGemmBM + std::min(d->experts, pairs) + 1;
@@ -799,7 +806,8 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->et = take(E * sizeof(ExpertEntry));
     out->act = take(t * k * I * 4);
     out->y = take(t * k * H * 4);
-    out->xf = take(t * (uint64_t)image_bytes((int)H));
+    out->xf = take(use_gemm(d, T) ? t * (uint64_t)image_bytes((int)H) : 0);
+    out->xd = take(t * (uint64_t)dimage_bytes((int)H));
     const bool sh = d->shared_blob != 0;
     const uint64_t Is = sh ? (uint64_t)d->shared_inter : 0;
     out->sh_et = take(sh ? (uint64_t)shared_entries(T) * sizeof(ExpertEntry) : 0);
@@ -893,6 +901,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->act = ws + lay.act;
     W->y = ws + lay.y;
     W->xf = ws + lay.xf;
+    W->xd = ws + lay.xd;
     W->sh_et = ws + lay.sh_et;
     W->sh_perm = ws + lay.sh_perm;
     W->sh_act = ws + lay.sh_act;
@@ -920,6 +929,14 @@ static int sync_slot(lp_ctx* c, lp_stream s) {
     return free_slot;
 }
 
+// A workspace address the kernels may write lp_moe_ws_layout's parts at: not
+// null (an allocation of zero bytes), and 256-byte aligned like every part.
+static int check_ws(uint64_t ws) {
+    if (ws == 0) return fail(LP_E_INVALID, "null workspace");
+    if (ws % 256) return fail(LP_E_UNSUPPORTED, "the workspace must be 256-byte aligned");
+    return LP_OK;
+}
+
 static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     const int T = ra.T;
     // up to kTopkFusedMaxT tokens: one workgroup does both (one token per
@@ -937,12 +954,13 @@ static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
 int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws,
                  lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
+    if (int r = check_ws(ws)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.x = x;
     ra.T = T;
-    ra.make_xf = 1;
+    ra.make_xf = image_kinds(d, T);
     if (T > kTopkDispatchMaxT) {
         // large batch: the MFMA router, then the images of x on their own
         dim3 g((unsigned)((T + 15) / 16), (unsigned)((d->experts + 127) / 128));
@@ -970,6 +988,7 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
 int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, int T,
                         uint64_t ws, lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
+    if (int r = check_ws(ws)) return r;
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.T = T;
@@ -1056,6 +1075,7 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
 static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                         uint64_t ws, lp_stream s, bool have_images) {
     if (int r = check_desc(c, d, T)) return r;
+    if (int r = check_ws(ws)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
     if (h % 16) return fail(LP_E_UNSUPPORTED, "h must be 16-byte aligned");
     if (!have_images) {
@@ -1063,7 +1083,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         fill_views(d, ws, T, &ra.L, &ra.W);
         ra.x = x;
         ra.T = T;
-        ra.make_xf = 1;
+        ra.make_xf = image_kinds(d, T);
         if (int r = launch(c, kXImage, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
     }
     GroupedArgs ga{};
@@ -1137,6 +1157,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
 
 int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
+    if (int r = check_ws(ws)) return r;
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.T = T;
@@ -1158,6 +1179,7 @@ int lp_moe_stack_forward(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layer
                          uint64_t ws, lp_stream s) {
     if (int r = check_ctx(c)) return r;
     if (!layers || n_layers <= 0) return fail(LP_E_INVALID, "lp_moe_stack_forward: no layers");
+    if (int r = check_ws(ws)) return r;
     // every layer's shape is checked before the first launch, so a bad
     // descriptor part-way down the stack leaves h untouched
     for (int l = 0; l < n_layers; ++l)
@@ -1221,6 +1243,7 @@ void lp_graph_destroy(lp_graph* g) {
 int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T, lp_stream s,
                        int32_t* unique_count, int32_t* error_flags) {
     if (int r = check_ctx(c)) return r;
+    if (int r = check_ws(ws)) return r;
     lp_moe_ws_layout lay;
     if (int r = lp_moe_ws_layout_get(d, T, &lay)) return r;
     int32_t meta[2] = {0, 0};

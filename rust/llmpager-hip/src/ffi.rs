@@ -98,6 +98,7 @@ pub struct lp_moe_ws_layout {
     pub act: u64,
     pub y: u64,
     pub xf: u64,
+    pub xd: u64,
     pub sh_et: u64,
     pub sh_perm: u64,
     pub sh_act: u64,

@@ -146,6 +146,10 @@ def test_ws_layout_alignment_and_size():
         assert all(o % 256 == 0 for o in offs)
         assert offs == sorted(offs)
         assert lay.total >= lay.y + T * 8 * 2048 * 4
+        # the digit images of x fill their part; the bf16 images only exist
+        # for the prefill GEMM (T = 2048 here)
+        assert lay.sh_et - lay.xd >= T * lp.dimage_bytes(2048) > lay.sh_et - lay.xd - 256
+        assert (lay.xd - lay.xf > 0) == (T == 2048)
 
 
 def _c_struct_fields(text, name):

@@ -1,13 +1,13 @@
 """Parity of the paths the benchmark runs with full-precision activations.
 
-Every layer test elsewhere feeds bf16-exact activations, so the low half of
-the kernels' hi/lo activation split (x = bf16(x) + bf16(x - bf16(x))) is zero
-there.  A stacked decode (decode.rs:277-343 restricted to the MoE block; the
-layer input is the previous layer's residual) feeds fp32 values, so these
-tests use N(0, 1) fp32 activations that are not bf16-exact:
+Every layer test elsewhere feeds bf16-exact activations.  A stacked decode
+(decode.rs:277-343 restricted to the MoE block; the layer input is the
+previous layer's residual) feeds fp32 values, so these tests use N(0, 1) fp32
+activations that are not bf16-exact: the grouped kernels' int8 digit images
+then carry both digits, and the prefill GEMM's bf16 images a live lo part.
 
   - one config-1 layer (H2048/I768/E128/top-8/g32) at T = 1, 8, 32: the
-    balanced gate/up and down kernels with live lo parts;
+    balanced gate/up and down kernels;
   - a 4-layer in-place stack at the config-1 shape (x and h the same buffer,
     as the benchmark runs it), checked layer by layer against the oracle
     given the device's input to that layer;
@@ -25,6 +25,7 @@ import pytest
 
 import llmpager_amd as lp
 import _oracle as O
+from _digits import assert_digit_images
 from _gpu import DeviceLayer, align, rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -44,7 +45,8 @@ def _routing_equal(g_ids, g_wts, g_cnt, ids, wts, cnt):
 
 
 def _layer_once(cuda, L: DeviceLayer, x: np.ndarray, h: np.ndarray, inplace: bool = False):
-    """Run one layer on the device; returns (h', logits, ids, wts, cnt, xlo, status)."""
+    """Run one layer on the device; returns (h', logits, ids, wts, cnt, xd, status), xd the
+    digit images of x the grouped kernels read."""
     T, H, E, k = x.shape[0], L.H, L.E, L.k
     lay = lp.ws_layout(L.desc, T)
     ws = cuda.alloc_device(lay.total)
@@ -54,7 +56,7 @@ def _layer_once(cuda, L: DeviceLayer, x: np.ndarray, h: np.ndarray, inplace: boo
     dl = lambda off, shape, dt: cuda.download(ws + off, shape, dt)
     out = (cuda.download(dh, (T, H), np.float32), dl(lay.logits, (T, E), np.float32),
            dl(lay.ids, (T, k), np.int32), dl(lay.wts, (T, k), np.float32), dl(lay.cnt, (T,), np.int32),
-           dl(lay.xlo, (T,), np.int32), L.layer.status(ws, T))
+           dl(lay.xd, (T, lp.dimage_bytes(H)), np.uint8), L.layer.status(ws, T))
     for p in {ws, dh, dx}:
         cuda.free_device(p)
     return out
@@ -65,8 +67,8 @@ def test_layer_config1_fp32_activations(cuda, T):
     L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=31)
     x = fp32_normal(T * 2048, 100 + T).reshape(T, 2048)
     h = fp32_normal(T * 2048, 200 + T).reshape(T, 2048)
-    gh, glog, gids, gw, gcnt, xlo, status = _layer_once(cuda, L, x, h)
-    assert xlo.tolist() == [1] * T          # the lo parts are live
+    gh, glog, gids, gw, gcnt, xd, status = _layer_once(cuda, L, x, h)
+    assert_digit_images(xd, x)              # both digits live
     assert status[1] == 0
     want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h, threads=8)
     assert np.array_equal(glog.view(np.uint32), wlog.view(np.uint32))
@@ -142,8 +144,9 @@ def test_layer_config4_shape(cuda, T):
     L = DeviceLayer(cuda, H=P_H, I=P_I, E=P_E, k=P_K, group=P_G, seed=61)
     x = fp32_normal(T * P_H, 400 + T).reshape(T, P_H)
     h = fp32_normal(T * P_H, 500 + T).reshape(T, P_H)
-    gh, glog, gids, gw, gcnt, xlo, status = _layer_once(cuda, L, x, h)
-    assert status[1] == 0 and xlo.min() == 1
+    gh, glog, gids, gw, gcnt, xd, status = _layer_once(cuda, L, x, h)
+    assert status[1] == 0
+    assert_digit_images(xd, x)
     want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h, threads=8)
     assert np.array_equal(glog.view(np.uint32), wlog.view(np.uint32))
     _routing_equal(gids, gw, gcnt, wids, ww, wcnt)

@@ -46,12 +46,14 @@ def test_q4_gemv_batch(cuda, rows, cols, group, experts, x_stride):
     for e in range(experts):
         want = O.q4_gemv(regions[e], x[e * x_stride: e * x_stride + cols], rows, cols, group)
         assert worst_rel(y[e], want) <= 1e-3
-        assert rel_l2(y[e], want) <= 1e-5
+        # the MFMA path carries x as 16-bit fixed point per 32 columns
+        # (within 2^-16 of each sub-group's largest magnitude): rel-L2 ~2e-5
+        assert rel_l2(y[e], want) <= 1e-4
     # single-matrix form
     k.q4g64_gemv(arena + 32, d_x, d_y, rows, cols, group)
     y1 = cuda.download(d_y, (rows,), np.float32)
     want = O.q4_gemv(regions[0], x[:cols], rows, cols, group)
-    assert rel_l2(y1, want) <= 1e-5
+    assert rel_l2(y1, want) <= 1e-4
     for p in (arena, d_ptrs, d_x, d_y):
         cuda.free_device(p)
 

@@ -148,6 +148,19 @@ def test_layer_shared_expert_g64_softmax(cuda):
     L.free()
 
 
+def test_null_workspace_rejected(cuda):
+    # a zero-byte allocation comes back as a null address: every entry that
+    # writes the workspace refuses it before launching anything
+    L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=32, seed=1)
+    dx = cuda.upload(np.zeros((1, 128), np.float32))
+    for call in (lambda: L.layer.route(dx, 1, 0), lambda: L.layer.forward(dx, dx, 1, 0),
+                 lambda: L.layer.experts(dx, dx, 1, 0), lambda: L.layer.route(dx, 1, 64)):
+        with pytest.raises(lp.LpError):
+            call()
+    cuda.free_device(dx)
+    L.free()
+
+
 def test_layer_missing_expert_flags(cuda):
     # A routed expert with no slot raises the error flag and contributes 0.
     slots = np.arange(8, dtype=np.int32)
