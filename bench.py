@@ -743,7 +743,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "i8 MFMA (q4 weights x 16-bit fixed-point activations as two int8 digits per 32 columns), fp32 accumulate",
         "data": "synthetic",
         "config": {
             "workload": f"config2: {LAYERS}-layer Qwen3-30B-A3B-shape MoE stack, lockstep decode "
