@@ -607,10 +607,13 @@ __device__ __forceinline__ void q4_digits(const uint4& w, i32x4_t& b0, i32x4_t& 
 // in the tile from this chunk: steps j >= rem are skipped (uniform branch),
 // and at step rem - 1 lanes without a sub-group (cols % 128 != 0) take a
 // zero scale.  One code path serves every np, so the loaded chunk keeps its
-// registers whatever the token count.
-template <int NS, bool SL, int P, int M>
+// registers whatever the token count.  NF > 0 instead takes exactly the
+// first NF pairs (np unused): no branch between pairs, so their MFMA chains
+// interleave.
+template <int NS, bool SL, int P, int M, int NF = 0>
 __device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&B)[P], int rem, int np,
                                      float (&acc)[M][P][2]) {
+    static_assert(NF <= P, "NF pairs of at most P");
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         if (j < rem) {  // uniform
@@ -627,8 +630,8 @@ __device__ __forceinline__ void wmma(const WRegs<NS, SL> (&R)[M], const ABase (&
                 q4_digits(R[m].w[j], b[m][0], b[m][1]);
             }
 #pragma unroll
-            for (int p = 0; p < P; ++p) {
-                if (p > 0 && p >= np) break;  // uniform: pairs staged in this token group
+            for (int p = 0; p < (NF > 0 ? NF : P); ++p) {
+                if (NF == 0 && p > 0 && p >= np) break;  // uniform: pairs staged in this token group
                 const i32x4_t o = *reinterpret_cast<const i32x4_t*>(B[p].o + j * 64);
                 const float2 sg = *reinterpret_cast<const float2*>(B[p].sg + j * 32);
                 const i32x4_t a0 = *reinterpret_cast<const i32x4_t*>(B[p].a + j * 128);
@@ -655,6 +658,28 @@ __device__ __forceinline__ float tile_reduce(float v) {
     v += shfl_xor(v, 32);
     return v;
 }
+
+// The same sums for several tokens at once, by register swaps between lanes
+// (no LDS round trip), each token's sum landing in one row of 16 lanes.
+// pair_rows(a, b): rows 0 and 1 hold a's partials of rows {0, 2} and {1, 3},
+// rows 2 and 3 the same of b (v_permlane32_swap trades the first operand's
+// upper 32 lanes for the second's lower 32).
+__device__ __forceinline__ float pair_rows(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// quad_rows(pair_rows(a, b), pair_rows(c, d)): rows 0, 1, 2, 3 hold the full
+// sums of a, c, b, d (v_permlane16_swap trades the first operand's odd rows
+// for the second's even rows).
+__device__ __forceinline__ float quad_rows(float s, float t) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(t), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Token (0..3, of a, b = tokens 0, 1 and c, d = tokens 2, 3) in row r of a
+// quad_rows result.
+__device__ __forceinline__ constexpr int quad_row_tok(int r) { return 2 * (r & 1) + (r >> 1); }
 
 __device__ __forceinline__ int ilog2_pow2(int v) { return 31 - __builtin_clz(v); }
 

@@ -1327,11 +1327,11 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
 // kBalWaves waves per CU.  Work is cut into units of 8 rows of gate plus the
 // same 8 rows of up over the whole of K (one MFMA tile: lanes n < 8 carry gate
 // row r0 + n, lanes n >= 8 up row r0 + n - 8), for each "virtual expert" =
-// (routed expert, group of up to 4 of its tokens).  Virtual experts are
+// (routed expert, group of up to kBalToks = 4 of its tokens).  Virtual experts are
 // numbered by a prefix sum over the expert table and every workgroup takes
 // an equal contiguous range of the V * R units (R = ceil(I / 8)); with V no
 // larger than the grid a range touches at most two virtual experts, whose
-// token images are staged once, into pair slots 0-1 and 2-3.  Each wave then
+// token images are staged once, into two slots of kBalPairs pairs.  Each wave then
 // walks its units (every W-th of the range, W waves) with the next unit's
 // weights in flight while the current one is multiplied: two register
 // buffers, loads unconditional (a past-the-end unit reads a zero-size
@@ -1367,7 +1367,7 @@ __device__ __forceinline__ WTile<RS> wtile_gu(uint64_t blob, bool valid, uint64_
 }
 
 // The workgroup's share of a balanced launch: the entries' virtual experts
-// (ceil(ntok / 4) each) numbered by a prefix sum over the expert table,
+// (ceil(ntok / kBalToks) each) numbered by a prefix sum over the expert table,
 // then the workgroup's contiguous range [lo, hi) of the V * R units and the
 // (at most two) virtual experts it touches.  Returns false for an empty
 // range (the whole workgroup).  The LDS meta area follows the fragments of
@@ -1375,8 +1375,8 @@ __device__ __forceinline__ WTile<RS> wtile_gu(uint64_t blob, bool valid, uint64_
 struct BalPlan {
     int lo, hi, v0, nslot;
     ExpertEntry x[2];  // slot 1 repeats slot 0 when the range has one virtual expert
-    int tg[2];         // token group of the slot's expert (tokens 4 tg .. 4 tg + 3)
-    int nt[2];         // tokens in the slot (1..4)
+    int tg[2];         // token group of the slot's expert (tokens kBalToks tg ..)
+    int nt[2];         // tokens in the slot (1..kBalToks)
 };
 
 __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, BalPlan& P) {
@@ -1390,7 +1390,7 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
     if (tid < maxu) {
         const ExpertEntry x = entry_of(a, tid);
         ent[tid] = x;
-        ng = (x.ntok + 3) >> 2;
+        ng = (x.ntok + kBalToks - 1) / kBalToks;
     }
     int inc = ng;
 #pragma unroll
@@ -1430,9 +1430,39 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
         const int q = s < P.nslot ? s : 0;
         P.x[s] = ent[sl[2 * q]];
         P.tg[s] = sl[2 * q + 1];
-        P.nt[s] = min(4, P.x[s].ntok - 4 * P.tg[s]);
+        P.nt[s] = min(kBalToks, P.x[s].ntok - kBalToks * P.tg[s]);
     }
     return true;
+}
+
+// The MFMAs of one balanced unit: np (1..kBalPairs, uniform) picks a
+// straight-line form for exactly that many token pairs.
+template <int NS, bool SL>
+__device__ __forceinline__ void bal_wmma(const WRegs<NS, SL> (&R)[1], const ABase (&B)[kBalPairs], int rem, int np,
+                                         float (&acc)[1][kBalPairs][2]) {
+    static_assert(kBalPairs == 2 || kBalPairs == 4, "one form per pair count");
+    if constexpr (kBalPairs == 2) {
+        if (np == 1) wmma<NS, SL, kBalPairs, 1, 1>(R, B, rem, np, acc);
+        else wmma<NS, SL, kBalPairs, 1, 2>(R, B, rem, np, acc);
+    } else {
+        switch (np) {
+            case 1: wmma<NS, SL, kBalPairs, 1, 1>(R, B, rem, np, acc); break;
+            case 2: wmma<NS, SL, kBalPairs, 1, 2>(R, B, rem, np, acc); break;
+            case 3: wmma<NS, SL, kBalPairs, 1, 3>(R, B, rem, np, acc); break;
+            default: wmma<NS, SL, kBalPairs, 1, 4>(R, B, rem, np, acc); break;
+        }
+    }
+}
+
+// The token sums over K of a balanced unit's kBalPairs pairs (acc[0][p][h] =
+// lane partials of token 2p + h): row r of X holds token quad_row_tok(r), row
+// r of Y token 4 + quad_row_tok(r) (zero with two pairs).
+__device__ __forceinline__ void bal_sums(const float (&acc)[1][kBalPairs][2], float& X, float& Y) {
+    X = quad_rows(pair_rows(acc[0][0][0], acc[0][0][1]), pair_rows(acc[0][1][0], acc[0][1][1]));
+    if constexpr (kBalPairs == 4)
+        Y = quad_rows(pair_rows(acc[0][2][0], acc[0][2][1]), pair_rows(acc[0][3][0], acc[0][3][1]));
+    else
+        Y = 0.0f;
 }
 
 template <int NS, int RS, bool SL>
@@ -1440,7 +1470,10 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
     const int H = L.hidden, I = L.inter, k = L.top_k;
-    const int lane = lane_id(), wave = (int)threadIdx.x >> 6, W = (int)(blockDim.x >> 6);
+    // the wave index said to be uniform: unit indices, slots and token counts
+    // then live in SGPRs and the pair loop branches on them
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int W = (int)(blockDim.x >> 6);
     const int R = (I + 7) >> 3;
     const Frags F = frags_at(lds, H);
     zero_block(F, threadIdx.x, blockDim.x);
@@ -1457,13 +1490,13 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         const ExpertEntry x = P.x[s];
         const int tg = P.tg[s];
         sblob[s] = x.blob;
-        sp0[s] = x.p0 + 4 * tg;
+        sp0[s] = x.p0 + kBalToks * tg;
         snt[s] = P.nt[s];
         if (s < P.nslot) {
             Frags Fs = F;
-            Fs.lds = F.lds + 2 * s * frag_pair_bytes(F.ngp);
+            Fs.lds = F.lds + kBalPairs * s * frag_pair_bytes(F.ngp);
             issue_images(Fs, snt[s], [&](int t) {
-                const int i = 4 * tg + t;
+                const int i = kBalToks * tg + t;
                 const int tok = i < kEntryToks ? entry_tok(x, i) : perm[x.p0 + i] / k;
                 return xf + (uint64_t)tok * ib;
             });
@@ -1504,8 +1537,6 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
         const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
         const int np = (qnt + 1) >> 1;
-        const int row = r0 + (lane & 15);
-        const bool out = lane < 32 && (lane & 15) < 8 && row < I;
         missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
         WRegs<NS, SL> Rm[1] = {B};
         if constexpr (SL) {
@@ -1515,27 +1546,29 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
             asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B.w[0].x));
             Rm[0].sbase += z;
         }
-        float acc[1][kMaxPairs][2];
+        float acc[1][kBalPairs][2];
 #pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
-        ABase Bs[kMaxPairs];
+        for (int p = 0; p < kBalPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
+        ABase Bs[kBalPairs];
 #pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) Bs[p] = abase(F, 2 * s + p, 0);
-        wmma(Rm, Bs, Sx, np, acc);
-#pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) {
-            const float g0 = tile_reduce(acc[0][p][0]), g1 = tile_reduce(acc[0][p][1]);
-            // up of row n sits in lane n + 8 of the same 16
-            const float u0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(g0), 0x128, 0xf, 0xf, false));
-            const float u1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(g1), 0x128, 0xf, 0xf, false));
-            const int t = 2 * p + (lane >> 4);
-            const float g = lane < 16 ? g0 : g1;
-            const float u = lane < 16 ? u0 : u1;
-            const float v = qblob == 0 ? 0.0f : g / (1.0f + expf(-g)) * u;
-            const bool st = out && p < np && t < qnt;
-            const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)I + (uint32_t)row) * 4u : act_bytes;
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), act_rs, (int)off, 0, 0);
-        }
+        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * s + p, 0);
+        bal_wmma(Rm, Bs, Sx, np, acc);
+        // the tokens' sums over K (bal_sums); in each row the gate of weight
+        // row r0 + n sits in lane n < 8, its up in lane n + 8.  Lanes n < 8
+        // finish X's tokens, lanes n >= 8 Y's (their gate brought over by a
+        // rotation of the row by 8): one SiLU and one store per lane.
+        float X, Y;
+        bal_sums(acc, X, Y);
+        const float rX = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(X), 0x128, 0xf, 0xf, false));
+        const float rY = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(Y), 0x128, 0xf, 0xf, false));
+        const bool hy = (lane & 15) >= 8;
+        const float g = hy ? rY : X, u = hy ? Y : rX;
+        const int t = (hy ? 4 : 0) + quad_row_tok(lane >> 4);
+        const int row = r0 + (lane & 7);
+        const float v = qblob == 0 ? 0.0f : g / (1.0f + expf(-g)) * u;
+        const bool st = row < I && t < qnt;
+        const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)I + (uint32_t)row) * 4u : act_bytes;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), act_rs, (int)off, 0, 0);
     };
     WRegs<NS, SL> RA, RB;
     load(RA, 0, swin);
@@ -1582,7 +1615,8 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
     const int H = L.hidden, I = L.inter, k = L.top_k;
-    const int lane = lane_id(), wave = (int)threadIdx.x >> 6, W = (int)(blockDim.x >> 6);
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int W = (int)(blockDim.x >> 6);
     const int R = (H + 15) >> 4;
     const Frags F = frags_at(lds, I);
     zero_block(F, threadIdx.x, blockDim.x);
@@ -1595,11 +1629,11 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         sblob[s] = P.x[s].blob;
-        sp0[s] = P.x[s].p0 + 4 * P.tg[s];
+        sp0[s] = P.x[s].p0 + kBalToks * P.tg[s];
         snt[s] = P.nt[s];
         if (s < P.nslot) {
             Frags Fs = F;
-            Fs.lds = F.lds + 2 * s * frag_pair_bytes(F.ngp);
+            Fs.lds = F.lds + kBalPairs * s * frag_pair_bytes(F.ngp);
             const int p0 = sp0[s];
             stage_rows(Fs, snt[s], [&](int t) { return actp + (size_t)(p0 + t) * I; }, threadIdx.x, blockDim.x);
         }
@@ -1635,7 +1669,7 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
         const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
         const int np = (qnt + 1) >> 1;
         const int row = r0 + (lane & 15);
-        const bool out = lane < 32 && row < H;
+        const bool out = row < H;
         missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
         WRegs<NS, SL> Rm[1] = {B};
         if constexpr (SL) {
@@ -1645,19 +1679,22 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
             asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B.w[0].x));
             Rm[0].sbase += z;
         }
-        float acc[1][kMaxPairs][2];
+        float acc[1][kBalPairs][2];
 #pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
-        ABase Bs[kMaxPairs];
+        for (int p = 0; p < kBalPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
+        ABase Bs[kBalPairs];
 #pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) Bs[p] = abase(F, 2 * s + p, 0);
-        wmma(Rm, Bs, Sx, np, acc);
+        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * s + p, 0);
+        bal_wmma(Rm, Bs, Sx, np, acc);
+        // the tokens' sums over K (bal_sums): one store per lane and group of
+        // four tokens
+        float X, Y;
+        bal_sums(acc, X, Y);
 #pragma unroll
-        for (int p = 0; p < kMaxPairs; ++p) {
-            const float y0 = tile_reduce(acc[0][p][0]), y1 = tile_reduce(acc[0][p][1]);
-            const int t = 2 * p + (lane >> 4);
-            const float v = qblob == 0 ? 0.0f : lane < 16 ? y0 : y1;
-            const bool st = out && p < np && t < qnt;
+        for (int h = 0; h < kBalPairs / 2; ++h) {
+            const int t = 4 * h + quad_row_tok(lane >> 4);
+            const float v = qblob == 0 ? 0.0f : h ? Y : X;
+            const bool st = out && t < qnt;
             const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)H + (uint32_t)row) * 4u : y_bytes;
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, (int)off, 0, 0);
         }
@@ -1807,23 +1844,30 @@ lp_moe_gateup(const GroupedArgs a) {
 // experts than workgroups, kBalWaves waves).
 extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_gateup_bal(const GroupedArgs a) {
-    if (tile_steps(a.L.hidden) > 8) {
-        if (scales_in_lds(a.L.group, a.L.hidden)) {
-            gateup_bal_body<16, 0, true>(a);
-        } else {
+    gateup_bal_body<16, 0, true>(a);
+}
+
+// The same with tiles of at most 8 steps (hidden <= 1024), and for groups
+// whose scales are not read through LDS windows (64, 128, or rows not 16-byte
+// aligned).  Each form is a kernel of its own, so that each keeps its own
+// register budget (together in one function they spill).
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup_bal8(const GroupedArgs a) {
+    gateup_bal_body<8, 0, true>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup_bal_rs(const GroupedArgs a) {
 #define LP_GATEUP(rs) gateup_bal_body<16, rs, false>(a)
-            LP_BY_RS(a.L.group, LP_GATEUP)
+    LP_BY_RS(a.L.group, LP_GATEUP)
 #undef LP_GATEUP
-        }
-    } else {
-        if (scales_in_lds(a.L.group, a.L.hidden)) {
-            gateup_bal_body<8, 0, true>(a);
-        } else {
+}
+
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup_bal_rs8(const GroupedArgs a) {
 #define LP_GATEUP(rs) gateup_bal_body<8, rs, false>(a)
-            LP_BY_RS(a.L.group, LP_GATEUP)
+    LP_BY_RS(a.L.group, LP_GATEUP)
 #undef LP_GATEUP
-        }
-    }
 }
 
 // Balanced down (decode batches; the host checks what lp_moe_gateup_bal

@@ -78,6 +78,9 @@ enum Fn {
     kDispatch,
     kRouteFused,
     kGateupBal,
+    kGateupBal8,
+    kGateupBalRs,
+    kGateupBalRs8,
     kDownBal,
     kDownBal6,
     kRmsNorm,
@@ -117,7 +120,8 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
-    {"lp_moe.hsaco", "lp_moe_gateup_bal"},
+    {"lp_moe.hsaco", "lp_moe_gateup_bal"},  {"lp_moe.hsaco", "lp_moe_gateup_bal8"},
+    {"lp_moe.hsaco", "lp_moe_gateup_bal_rs"},  {"lp_moe.hsaco", "lp_moe_gateup_bal_rs8"},
     {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
     {"lp_attn.hsaco", "lp_rmsnorm"},       {"lp_attn.hsaco", "lp_scale_add"},
     {"lp_attn.hsaco", "lp_kv_append_f32"}, {"lp_attn.hsaco", "lp_kv_append_f16"},
@@ -301,7 +305,7 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     {
         // the loaded code objects must take the balanced kernels' fixed
         // workgroup size (their launch bound)
-        for (Fn f : {kGateupBal, kDownBal, kDownBal6}) {
+        for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6}) {
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[f]) != hipSuccess ||
                 mt < 64 * kBalWaves) {
@@ -1002,10 +1006,10 @@ static int tile_steps_host(int cols) { return ((cols >> 5) + 3) >> 2; }
 
 // Whether lp_moe_gateup_bal takes the gate/up of ga's routed experts: one
 // chunk of K, an expert table it can hold, no more virtual experts (groups
-// of up to 4 tokens of one expert) than CUs, and its LDS.
+// of up to kBalToks = 4 tokens of one expert) than CUs, and its LDS.
 static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int H = ga.L.hidden, pairs = ga.T * ga.L.top_k;
-    const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
+    const int maxv = std::min(pairs, (pairs + (kBalToks - 1) * maxu) / kBalToks);
     const int nw = tile_steps_host(H) > 8 ? 16 : 8;
     return tile_steps_host(H) <= kGateupChunk && maxu <= kBalMaxU && maxv <= c->cus &&
            (size_t)bal_lds_bytes(H, nw, kBalWaves) <= c->max_lds && ga.L.slot_span < (1ull << 31) &&
@@ -1018,7 +1022,7 @@ static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
 // pairs the one-shot kernel is faster: too few units to share.
 static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int I = ga.L.inter, pairs = ga.T * ga.L.top_k;
-    const int maxv = std::min(pairs, (pairs + 3 * maxu) / 4);
+    const int maxv = std::min(pairs, (pairs + (kBalToks - 1) * maxu) / kBalToks);
     return pairs >= 32 && tile_steps_host(I) <= 8 && scales_in_lds(ga.L.group, I) && maxu <= kBalMaxU &&
            maxv <= c->cus &&
            (size_t)bal_lds_bytes(I, 8, kBalWaves) <= c->max_lds &&
@@ -1042,8 +1046,11 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
         return 1;
     };
     if (c->gateup_bal && gateup_balanced(c, ga, maxu)) {
-        const int nw = tile_steps_host(H) > 8 ? 16 : 8;
-        if (int r = launch(c, kGateupBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
+        const bool t16 = tile_steps_host(H) > 8;
+        const int nw = t16 ? 16 : 8;
+        const Fn f = scales_in_lds(ga.L.group, H) ? (t16 ? kGateupBal : kGateupBal8)
+                                                  : (t16 ? kGateupBalRs : kGateupBalRs8);
+        if (int r = launch(c, f, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
                            (size_t)bal_lds_bytes(H, nw, kBalWaves), s, ga))
             return r;
     } else {
