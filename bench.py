@@ -708,7 +708,7 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
-    mla = None if a.no_mla or a.paged_only else run_mla(cuda, s, (1, 16), a.steps)
+    mla = None if a.no_mla or a.paged_only or a.prefill_only else run_mla(cuda, s, (1, 16), a.steps)
     if a.mla_only:
         print(json.dumps({"mla": _rounded(mla)}), flush=True)
         cuda.close()

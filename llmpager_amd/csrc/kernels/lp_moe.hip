@@ -1366,26 +1366,45 @@ __device__ __forceinline__ WTile<RS> wtile_gu(uint64_t blob, bool valid, uint64_
     return T;
 }
 
-// The workgroup's share of a balanced launch: the entries' virtual experts
-// (ceil(ntok / kBalToks) each) numbered by a prefix sum over the expert table,
-// then the workgroup's contiguous range [lo, hi) of the V * R units and the
-// (at most two) virtual experts it touches.  Returns false for an empty
-// range (the whole workgroup).  The LDS meta area follows the fragments of
-// `cols`-wide rows (bal_meta_off).
+// The workgroup's share of a balanced launch.  An entry's tokens form
+// ceil(ntok / kBalToks) token groups ("virtual experts", numbered by a prefix
+// sum over the expert table); runs of up to kBalGroups groups of one entry
+// form a block whose units are ordered row-major: unit i of the block is row
+// unit i / g of token group i % g (g groups), so the units that read the same
+// weight rows for different token groups are neighbours, taken by
+// neighbouring waves of one workgroup at the same time, and the rows come
+// from HBM once.  The workgroup takes the contiguous range [lo, hi) of the
+// V * R units; with V no larger than the grid a range is at most R units
+// long and a block at least R, so it touches at most two blocks, whose
+// tokens are staged into two LDS slots of kBalGroups * kBalPairs pairs.
+// Returns false for an empty range (the whole workgroup).  The LDS meta area
+// follows the fragments of `cols`-wide rows (bal_meta_off).
 struct BalPlan {
-    int lo, hi, v0, nslot;
-    ExpertEntry x[2];  // slot 1 repeats slot 0 when the range has one virtual expert
-    int tg[2];         // token group of the slot's expert (tokens kBalToks tg ..)
-    int nt[2];         // tokens in the slot (1..kBalToks)
+    int lo, hi, nslot;
+    ExpertEntry x[2];  // the slots' entries (slot 1 repeats slot 0 when the range has one block)
+    int start[2];      // first unit of the slot's block
+    int tg0[2];        // first token group of the block (tokens kBalToks tg0 ..)
+    int gq[2];         // token groups in the block (1..kBalGroups)
+    int ns[2];         // tokens in the block (1..kBalToks kBalGroups)
+
+    // Unit un (uniform): slot s, row unit u, token group gl within the block.
+    __device__ __forceinline__ void unit(int un, int& s, int& u, int& gl) const {
+        s = nslot == 2 && un >= start[1] ? 1 : 0;
+        const int i = un - (s ? start[1] : start[0]);
+        const int g = s ? gq[1] : gq[0];
+        u = g == 3 ? (i * 43691) >> 17 : i >> (g >> 1);  // i / g for g in 1..4, i < 2^16
+        gl = i - u * g;
+    }
 };
+static_assert(kBalGroups <= 4, "BalPlan::unit divides by at most 4");
 
 __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, BalPlan& P) {
     const int tid = (int)threadIdx.x, lane = lane_id(), wave = tid >> 6, W = (int)(blockDim.x >> 6);
     const int maxu = a.maxu;
     int* tot = reinterpret_cast<int*>(lds + bal_meta_off(cols));  // [kBalWaves] wave totals
-    int* sl = tot + kBalWaves;                                      // [2][2]: expert, token group
+    int* sl = tot + kBalWaves;  // [2][3]: entry, first token group, first unit of the blocks of lo and hi - 1
     ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(cols) + 128);
-    if (tid < 4) sl[tid] = 0;
+    if (tid < 6) sl[tid] = 0;
     int ng = 0;
     if (tid < maxu) {
         const ExpertEntry x = entry_of(a, tid);
@@ -1406,31 +1425,35 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
         before += w < wave ? t : 0;
         V += t;
     }
-    const int pre = before + inc - ng;  // this entry's first virtual expert
+    const int pre = before + inc - ng;  // this entry's first token group
     const long N = (long)V * R;
     P.lo = (int)(N * blockIdx.x / gridDim.x);
     P.hi = (int)(N * (blockIdx.x + 1) / gridDim.x);
     if (P.lo >= P.hi) return false;
-    const int v0 = P.lo / R, v1 = (P.hi - 1) / R;  // v1 <= v0 + 1
-    if (tid < maxu) {
-        if (pre <= v0 && v0 < pre + ng) {
-            sl[0] = tid;
-            sl[1] = v0 - pre;
-        }
-        if (v1 != v0 && pre <= v1 && v1 < pre + ng) {
-            sl[2] = tid;
-            sl[3] = v1 - pre;
+    if (tid < maxu && ng > 0) {
+        const int u0 = R * pre, u1 = R * (pre + ng);  // the entry's units
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int un = e == 0 ? P.lo : P.hi - 1;
+            if (u0 <= un && un < u1) {
+                const int q = (un - u0) / (R * kBalGroups);
+                sl[3 * e] = tid;
+                sl[3 * e + 1] = q * kBalGroups;
+                sl[3 * e + 2] = u0 + q * R * kBalGroups;
+            }
         }
     }
     __syncthreads();
-    P.v0 = v0;
-    P.nslot = v1 != v0 ? 2 : 1;
+    P.nslot = sl[2] != sl[5] ? 2 : 1;  // two blocks: their first units differ
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const int q = s < P.nslot ? s : 0;
-        P.x[s] = ent[sl[2 * q]];
-        P.tg[s] = sl[2 * q + 1];
-        P.nt[s] = min(kBalToks, P.x[s].ntok - kBalToks * P.tg[s]);
+        P.x[s] = ent[sl[3 * q]];
+        P.tg0[s] = sl[3 * q + 1];
+        P.start[s] = sl[3 * q + 2];
+        const int ngx = (P.x[s].ntok + kBalToks - 1) / kBalToks;
+        P.gq[s] = min(kBalGroups, ngx - P.tg0[s]);
+        P.ns[s] = min(kBalToks * kBalGroups, P.x[s].ntok - kBalToks * P.tg0[s]);
     }
     return true;
 }
@@ -1479,8 +1502,8 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     zero_block(F, threadIdx.x, blockDim.x);
     BalPlan P;
     if (!bal_plan(a, lds, H, R, P)) return;
-    const int lo = P.lo, hi = P.hi, v0 = P.v0;
-    // the two slots' blob, first dispatch position and token count
+    const int lo = P.lo, hi = P.hi;
+    // the two slots' blob, dispatch position and token count of the block
     uint64_t sblob[2];
     int sp0[2], snt[2];
     const LP_GLOBAL int* perm = gptr<int>(a.W.perm);
@@ -1488,15 +1511,15 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const ExpertEntry x = P.x[s];
-        const int tg = P.tg[s];
+        const int tb = kBalToks * P.tg0[s];
         sblob[s] = x.blob;
-        sp0[s] = x.p0 + kBalToks * tg;
-        snt[s] = P.nt[s];
+        sp0[s] = x.p0 + tb;
+        snt[s] = x.ntok - tb;
         if (s < P.nslot) {
             Frags Fs = F;
-            Fs.lds = F.lds + kBalPairs * s * frag_pair_bytes(F.ngp);
-            issue_images(Fs, snt[s], [&](int t) {
-                const int i = kBalToks * tg + t;
+            Fs.lds = F.lds + kBalGroups * kBalPairs * s * frag_pair_bytes(F.ngp);
+            issue_images(Fs, P.ns[s], [&](int t) {
+                const int i = tb + t;
                 const int tok = i < kEntryToks ? entry_tok(x, i) : perm[x.p0 + i] / k;
                 return xf + (uint64_t)tok * ib;
             });
@@ -1509,18 +1532,13 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(H) +
                           (uint32_t)(2 * wave * scale_window_bytes<NS>());
     LP_GLOBAL float* act = gptr_w<float>(a.W.act);
-    auto unit_of = [&](int j, int& s, int& r0) {
-        const int un = lo + wave + W * j;
-        const int v = un / R;
-        s = v - v0;
-        r0 = 8 * (un - v * R);
-    };
     auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
-        int s, r0;
-        unit_of(j, s, r0);
+        int s, u, gl;
+        P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
         const bool valid = j < J && blob != 0;
-        const WTile<RS> T = wtile_gu<RS>(blob, valid, dummy, (uint32_t)L.gate_off, (uint32_t)L.up_off, I, H, r0);
+        const WTile<RS> T =
+            wtile_gu<RS>(blob, valid, dummy, (uint32_t)L.gate_off, (uint32_t)L.up_off, I, H, 8 * u);
         wload(B, T, 0, win);
     };
     // act through a raw buffer: a lane with nothing to store writes at its end,
@@ -1532,10 +1550,12 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.act), (short)0, (int)act_bytes, kBufferWord3);
     bool missing = false;
     auto compute = [&](const WRegs<NS, SL>& B, int j) {
-        int s, r0;
-        unit_of(j, s, r0);
+        int s, ru, gl;
+        P.unit(lo + wave + W * j, s, ru, gl);
+        const int r0 = 8 * ru;
         const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
-        const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
+        const int qp0 = (s == 0 ? sp0[0] : sp0[1]) + kBalToks * gl;
+        const int qnt = min(kBalToks, (s == 0 ? snt[0] : snt[1]) - kBalToks * gl);
         const int np = (qnt + 1) >> 1;
         missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
         WRegs<NS, SL> Rm[1] = {B};
@@ -1551,7 +1571,7 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         for (int p = 0; p < kBalPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
         ABase Bs[kBalPairs];
 #pragma unroll
-        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * s + p, 0);
+        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * (kBalGroups * s + gl) + p, 0);
         bal_wmma(Rm, Bs, Sx, np, acc);
         // the tokens' sums over K (bal_sums); in each row the gate of weight
         // row r0 + n sits in lane n < 8, its up in lane n + 8.  Lanes n < 8
@@ -1622,20 +1642,21 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     zero_block(F, threadIdx.x, blockDim.x);
     BalPlan P;
     if (!bal_plan(a, lds, I, R, P)) return;
-    const int lo = P.lo, hi = P.hi, v0 = P.v0;
+    const int lo = P.lo, hi = P.hi;
     uint64_t sblob[2];
     int sp0[2], snt[2];
     const float* actp = dptr<const float>(a.W.act);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
+        const int tb = kBalToks * P.tg0[s];
         sblob[s] = P.x[s].blob;
-        sp0[s] = P.x[s].p0 + kBalToks * P.tg[s];
-        snt[s] = P.nt[s];
+        sp0[s] = P.x[s].p0 + tb;
+        snt[s] = P.x[s].ntok - tb;
         if (s < P.nslot) {
             Frags Fs = F;
-            Fs.lds = F.lds + kBalPairs * s * frag_pair_bytes(F.ngp);
+            Fs.lds = F.lds + kBalGroups * kBalPairs * s * frag_pair_bytes(F.ngp);
             const int p0 = sp0[s];
-            stage_rows(Fs, snt[s], [&](int t) { return actp + (size_t)(p0 + t) * I; }, threadIdx.x, blockDim.x);
+            stage_rows(Fs, P.ns[s], [&](int t) { return actp + (size_t)(p0 + t) * I; }, threadIdx.x, blockDim.x);
         }
     }
     // this wave's units: lo + wave + W * j < hi
@@ -1644,18 +1665,12 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     const uint64_t dummy = L.router_w;
     const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(I) +
                           (uint32_t)(2 * wave * scale_window_bytes<NS>());
-    auto unit_of = [&](int j, int& s, int& r0) {
-        const int un = lo + wave + W * j;
-        const int v = un / R;
-        s = v - v0;
-        r0 = 16 * (un - v * R);
-    };
     auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
-        int s, r0;
-        unit_of(j, s, r0);
+        int s, u, gl;
+        P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
         const bool valid = j < J && blob != 0;
-        const WTile<RS> T = wtile_dn<RS>(blob, valid, dummy, (uint32_t)L.down_off, H, I, r0);
+        const WTile<RS> T = wtile_dn<RS>(blob, valid, dummy, (uint32_t)L.down_off, H, I, 16 * u);
         wload(B, T, 0, win);
     };
     const uint32_t y_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)H * 4u;
@@ -1663,12 +1678,13 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.y), (short)0, (int)y_bytes, kBufferWord3);
     bool missing = false;
     auto compute = [&](const WRegs<NS, SL>& B, int j) {
-        int s, r0;
-        unit_of(j, s, r0);
+        int s, u, gl;
+        P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
-        const int qp0 = s == 0 ? sp0[0] : sp0[1], qnt = s == 0 ? snt[0] : snt[1];
+        const int qp0 = (s == 0 ? sp0[0] : sp0[1]) + kBalToks * gl;
+        const int qnt = min(kBalToks, (s == 0 ? snt[0] : snt[1]) - kBalToks * gl);
         const int np = (qnt + 1) >> 1;
-        const int row = r0 + (lane & 15);
+        const int row = 16 * u + (lane & 15);
         const bool out = row < H;
         missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
         WRegs<NS, SL> Rm[1] = {B};
@@ -1684,7 +1700,7 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
         for (int p = 0; p < kBalPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
         ABase Bs[kBalPairs];
 #pragma unroll
-        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * s + p, 0);
+        for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * (kBalGroups * s + gl) + p, 0);
         bal_wmma(Rm, Bs, Sx, np, acc);
         // the tokens' sums over K (bal_sums): one store per lane and group of
         // four tokens

@@ -302,10 +302,10 @@ struct GroupedArgs {
 
 // Balanced decode gate/up (lp_moe_gateup_bal): one workgroup of kBalWaves
 // waves per CU (the kernels' launch bound; the only size they are built and
-// tested for).  LDS: the zero block and two slots of kBalPairs token pairs
-// (frag_lds_bytes(H, 2 kBalPairs)), 128 bytes of counters (kBalWaves wave totals, then
-// four slot words), the expert table (kBalMaxU entries), then two scale
-// windows per wave.
+// tested for).  LDS: the zero block and two slots of kBalGroups * kBalPairs
+// token pairs (frag_lds_bytes(H, 2 kBalGroups kBalPairs)), 128 bytes of
+// counters (kBalWaves wave totals, then six slot words), the expert table
+// (kBalMaxU entries), then two scale windows per wave.
 constexpr int kBalWaves = 8;
 // A virtual expert of the balanced kernels: up to kBalPairs token pairs of
 // one routed expert, whose weights one pass over the expert serves.  Four
@@ -314,9 +314,14 @@ constexpr int kBalWaves = 8;
 // fourfold in MFMA work.
 constexpr int kBalPairs = 2;
 constexpr int kBalToks = 2 * kBalPairs;
+// Token groups of one expert whose units the balanced kernels interleave
+// (neighbouring units read the same weight rows for different groups).
+constexpr int kBalGroups = 2;
 constexpr int kBalMaxU = 64 * kBalWaves;
-static_assert(4 * kBalWaves + 16 <= 128, "bal_plan's counters fit their 128 bytes");
-LPK_HD constexpr int bal_meta_off(int hidden) { return (frag_lds_bytes(hidden, 2 * kBalPairs) + 15) & ~15; }
+static_assert(4 * kBalWaves + 24 <= 128, "bal_plan's counters fit their 128 bytes");
+LPK_HD constexpr int bal_meta_off(int hidden) {
+    return (frag_lds_bytes(hidden, 2 * kBalGroups * kBalPairs) + 15) & ~15;
+}
 LPK_HD constexpr int bal_win_off(int hidden) { return bal_meta_off(hidden) + 128 + kBalMaxU * 32; }
 LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
     return bal_win_off(hidden) + waves * 2 * 64 * 2 * window_steps;
