@@ -2018,3 +2018,82 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
     }
     *h = v;
 }
+
+// ---------------------------------------------------------------------------
+// Down and combine of a one-token batch in one launch (lp_moe_down_comb):
+// workgroup b owns rows [16 b, 16 b + 16) of h, wave w the token's pick w
+// (w < cnt, at most kCombWaves picks).  Each wave stages its pick's act row
+// as digit fragments in its own pair slot, loads the 16 rows of its
+// expert's down matrix (one tile of at most NS steps, scales through an LDS
+// window) and leaves the 16 row sums in LDS; after a barrier the first 16
+// threads fold them in pick order, h += sum_j w_j y_j, with the fused
+// multiply-adds of lp_moe_combine, so h is bit-identical to the down kernel
+// followed by the combine.  For layers without a shared MLP, group 32 and
+// tile_steps(inter) <= 16 (the host checks).
+// ---------------------------------------------------------------------------
+namespace {
+
+__host__ __device__ constexpr int comb_part_off(int inter) { return (frag_lds_bytes(inter, kCombWaves) + 15) & ~15; }
+
+template <int NS>
+__device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LayerView& L = a.L;
+    const int H = L.hidden, I = L.inter;
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int n0 = kTileRows * (int)blockIdx.x;
+    const int c = gptr<int>(a.W.cnt)[0];
+    const Frags F = frags_at(lds, I);
+    float* part = reinterpret_cast<float*>(lds + comb_part_off(I));  // [kCombWaves][16]
+    const uint32_t swin = lds_addr_of(lds) + (uint32_t)(comb_part_off(I) + kCombWaves * 64) +
+                          (uint32_t)(wave * scale_window_bytes<NS>());
+    zero_block(F, threadIdx.x, blockDim.x);
+    // the pick's dispatch position; with one token, entry p of the expert
+    // table holds position p alone
+    const int p = wave < c ? gptr<int>(a.W.inv)[wave] : 0;
+    const uint64_t blob = wave < c ? entry_of(a, p).blob : 0;
+    WRegs<NS, true> D;
+    if (blob != 0) {
+        const WTile<0> T = wtile<0>(blob + L.down_off, H, I, n0);
+        wload(D, T, 0, swin);
+        Frags Fw = F;
+        Fw.lds = F.lds + wave * frag_pair_bytes(F.ngp);
+        const float* actp = dptr<const float>(a.W.act);
+        stage_rows(Fw, 1, [&](int) { return actp + (size_t)p * I; }, lane, 64);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the tile, its scale window and the staged row
+    __syncthreads();
+    float yv = 0.0f;
+    if (blob != 0) {
+        float acc[1][1][2] = {{{0.0f, 0.0f}}};
+        const ABase B[1] = {abase(F, wave, 0)};
+        const WRegs<NS, true> Rm[1] = {D};
+        wmma(Rm, B, tile_steps(I), 1, acc);
+        yv = tile_reduce(acc[0][0][0]);
+    } else if (wave < c && lane == 0) {
+        atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);  // not resident: zero output
+    }
+    if (lane < 16) part[wave * 16 + lane] = yv;
+    __syncthreads();
+    const int row = n0 + (int)threadIdx.x;
+    if (threadIdx.x < 16 && row < H) {
+        const LP_GLOBAL float* w = gptr<float>(a.W.wts);
+        float acc = 0.0f;
+        for (int j = 0; j < c; ++j) acc = __builtin_fmaf(w[j], part[j * 16 + threadIdx.x], acc);
+        LP_GLOBAL float* h = gptr_w<float>(a.h);
+        h[row] = h[row] + acc;
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(64 * kCombWaves) lp_moe_down_comb(const GroupedArgs a) {
+    if (tile_steps(a.L.inter) == 6)
+        down_comb_body<6>(a);  // inter 768 loads only its own 6 steps
+    else
+        down_comb_body<8>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(64 * kCombWaves) lp_moe_down_comb16(const GroupedArgs a) {
+    down_comb_body<16>(a);
+}

@@ -327,6 +327,9 @@ LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
     return bal_win_off(hidden) + waves * 2 * 64 * 2 * window_steps;
 }
 
+// One-token down + combine (lp_moe_down_comb): one wave per pick.
+constexpr int kCombWaves = 8;
+
 // Prefill grouped GEMM (lp_gemm.hip).
 constexpr int kGemmBM = 128;           // tokens per tile
 constexpr int kGemmBN = 128;           // weight rows per tile (gate/up: 64 gate + the same 64 up)

@@ -83,6 +83,8 @@ enum Fn {
     kGateupBalRs8,
     kDownBal,
     kDownBal6,
+    kDownComb,
+    kDownComb16,
     kRmsNorm,
     kScaleAdd,
     kKvAppendF32,
@@ -123,6 +125,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_gateup_bal"},  {"lp_moe.hsaco", "lp_moe_gateup_bal8"},
     {"lp_moe.hsaco", "lp_moe_gateup_bal_rs"},  {"lp_moe.hsaco", "lp_moe_gateup_bal_rs8"},
     {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
+    {"lp_moe.hsaco", "lp_moe_down_comb"},  {"lp_moe.hsaco", "lp_moe_down_comb16"},
     {"lp_attn.hsaco", "lp_rmsnorm"},       {"lp_attn.hsaco", "lp_scale_add"},
     {"lp_attn.hsaco", "lp_kv_append_f32"}, {"lp_attn.hsaco", "lp_kv_append_f16"},
     {"lp_attn.hsaco", "lp_rope"},          {"lp_attn.hsaco", "lp_bf16_row_to_f32"},
@@ -305,7 +308,9 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     {
         // the loaded code objects must take the balanced kernels' fixed
         // workgroup size (their launch bound)
-        for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6}) {
+        static_assert(kCombWaves == kBalWaves, "one workgroup size checked");
+        for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6, kDownComb,
+                     kDownComb16}) {
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[f]) != hipSuccess ||
                 mt < 64 * kBalWaves) {
@@ -1035,7 +1040,8 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
 // `routed`: the routed experts (the balanced down may take them; the
 // balanced gate/up takes the shared MLP too, as ceil(T / 4) virtual experts
 // whose weight rows neighbouring workgroups of one XCD read together).
-static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s) {
+static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s,
+                       bool with_down = true) {
     GroupedArgs ga = ga0;
     ga.maxu = maxu;
     const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
@@ -1062,6 +1068,7 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
                            (size_t)(frag_lds_bytes(H, cap) + win), s, ga))
             return r;
     }
+    if (!with_down) return 0;
     const int steps = tile_steps_host(I);
     if (routed && c->gateup_bal && down_balanced(c, ga, maxu)) {
         return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
@@ -1075,6 +1082,15 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
     const int win = steps <= kDownWideChunk && scales_in_lds(ga.L.group, I) ? scale_window_lds(w, tw, ns) : 0;
     return launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), (size_t)(frag_lds_bytes(I, cap) + win),
                   s, ga);
+}
+
+// LDS of lp_moe_down_comb(16): the picks' fragment pairs, their row sums
+// (kCombWaves x 16 floats), then a scale window per wave (6, 8 or 16 steps
+// wide: tile steps 6, 7..8, 9..16).
+static int comb_lds(int inter, int steps) {
+    const int ns = steps == 6 ? 6 : steps <= 8 ? 8 : 16;
+    const int win = 64 * 2 * ((ns + 7) / 8 * 8);
+    return ((frag_lds_bytes(inter, kCombWaves) + 15) & ~15) + kCombWaves * 64 + kCombWaves * win;
 }
 
 // The grouped expert kernels and the combine; the fragment images of x are
@@ -1138,8 +1154,17 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gm.nblocks = (d->hidden + kGemmBN - 1) / kGemmBN;
         if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
             return r;
-    } else if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s)) {
-        return r;
+    } else {
+        // one token without a shared MLP: down and combine in one launch
+        const int Si = tile_steps_host(d->inter);
+        const bool comb = T == 1 && !d->shared_blob && d->top_k <= kCombWaves &&
+                          scales_in_lds(d->group, d->inter) && Si <= 16 && (size_t)comb_lds(d->inter, Si) <= c->max_lds;
+        if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb)) return r;
+        if (comb) {
+            ga.maxu = std::min(d->top_k, d->experts);
+            return launch(c, Si <= 8 ? kDownComb : kDownComb16, dim3((unsigned)((d->hidden + kTileRows - 1) / kTileRows)),
+                          dim3(64 * kCombWaves), (size_t)comb_lds(d->inter, Si), s, ga);
+        }
     }
     if (d->shared_blob) {
         // the shared MLP through the same kernels: its own width, group and

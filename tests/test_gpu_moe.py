@@ -206,11 +206,12 @@ def _zero_expert_blob(L: DeviceLayer, blob: np.ndarray) -> np.ndarray:
     return z
 
 
-@pytest.mark.parametrize("T", [4, 32])
+@pytest.mark.parametrize("T", [1, 4, 32])
 def test_layer_missing_expert_matches_zero_expert(cuda, T):
     # Experts without a slot contribute zero (flag raised); the rest of the
-    # layer, at decode batch sizes through both the one-shot and the balanced
-    # grouped kernels, matches the oracle with those experts zeroed.
+    # layer, at decode batch sizes through the one-token down + combine, the
+    # one-shot and the balanced grouped kernels, matches the oracle with
+    # those experts zeroed.
     slots = np.arange(128, dtype=np.int32)
     slots[::3] = -1
     L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=2, slots=slots)
