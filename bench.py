@@ -39,14 +39,19 @@ EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 # The grouped gate/up launch of a layer is the dominant kernel.
-GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal")
-DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide", "lp_moe_down_bal", "lp_moe_down_bal6")
+GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal", "lp_moe_gateup_bal8", "lp_moe_gateup_bal_rs",
+                  "lp_moe_gateup_bal_rs8")
+# lp_moe_down_comb (one token) also folds the combine into the same launch
+DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide", "lp_moe_down_bal", "lp_moe_down_bal6", "lp_moe_down_comb",
+                "lp_moe_down_comb16")
 CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
 # HBM bytes per dominant-kernel launch at B = 32 (FETCH_SIZE + WRITE_SIZE,
 # each scaled by the factor the same counter reads for the calibration copy),
-# from the rocprofv3 --pmc runs recorded in profiles/ for that kernel.
+# from the rocprofv3 --pmc runs recorded in profiles/ for that kernel: the
+# 256 MiB copy reads FETCH_SIZE 131,093 KiB (factor 2.0) and WRITE_SIZE
+# 262,144 KiB (factor 1.0); lp_moe_gateup_bal averages 91,641 and 899 KiB.
 # Re-measure whenever the kernel changes.
-TRAFFIC_B32 = {"lp_moe_gateup": 181_856_889, "lp_moe_gateup_bal": 209_553_912}
+TRAFFIC_B32 = {"lp_moe_gateup_bal": (2 * 91_641 + 899) * 1024}
 KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
            "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
            "lp_moe_combine")
