@@ -2049,9 +2049,11 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
                           (uint32_t)(wave * scale_window_bytes<NS>());
     zero_block(F, threadIdx.x, blockDim.x);
     // the pick's dispatch position; with one token, entry p of the expert
-    // table holds position p alone
-    const int p = wave < c ? gptr<int>(a.W.inv)[wave] : 0;
-    const uint64_t blob = wave < c ? entry_of(a, p).blob : 0;
+    // table holds position p alone.  Read without waiting for the count
+    // (clamped into the table: positions of dropped picks are stale).
+    const int p = min(max(gptr<int>(a.W.inv)[min(wave, L.top_k - 1)], 0), a.maxu - 1);
+    const uint64_t eb = entry_of(a, p).blob;
+    const uint64_t blob = wave < c ? eb : 0;
     WRegs<NS, true> D;
     if (blob != 0) {
         const WTile<0> T = wtile<0>(blob + L.down_off, H, I, n0);

@@ -308,15 +308,15 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     {
         // the loaded code objects must take the balanced kernels' fixed
         // workgroup size (their launch bound)
-        static_assert(kCombWaves == kBalWaves, "one workgroup size checked");
         for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6, kDownComb,
                      kDownComb16}) {
+            const int need = 64 * (f == kDownComb || f == kDownComb16 ? kCombWaves : kBalWaves);
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[f]) != hipSuccess ||
-                mt < 64 * kBalWaves) {
+                mt < need) {
                 lp_destroy(c);
                 return fail(LP_E_LOAD, std::string(kSpecs[f].name) + ": code object does not take " +
-                                           std::to_string(64 * kBalWaves) + "-thread workgroups");
+                                           std::to_string(need) + "-thread workgroups");
             }
         }
     }
