@@ -437,7 +437,8 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
     renormalisation, as DeepSeek-V2-Lite) of width 1408 plus the always-on
     shared MLP of width 2816 (2 shared experts), g32, stacked over 26 layers
     (8.4 GB of distinct weights, so the 256 MB MALL cannot serve repeats) in
-    lockstep decode; tok/s and algorithmic GB/s at each batch."""
+    lockstep decode, each step a replayed graph of the 26 layers
+    (lp_moe_stack_capture); tok/s and algorithmic GB/s at each batch."""
     import llmpager_amd as lp
     span = align(lp.blob_bytes(D_H, D_I, D_G))
     go, uo, do = lp.blob_offsets(D_H, D_I, D_G)
@@ -460,21 +461,29 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
         layers.append(lp.MoeLayer(cuda, desc))
     expert_bytes = 3 * D_I * (D_H // D_G) * 2 + 3 * D_I * D_H // 2
     shared_bytes = 3 * D_SH * (D_H // D_G) * 2 + 3 * D_SH * D_H // 2
+    stack = lp.MoeStack(cuda, [L.desc for L in layers])
     out = {}
     for B in batches:
-        ws = cuda.alloc_device(lp.ws_layout(layers[0].desc, B).total)
+        # each step: the step's B token rows into the residual buffer, then
+        # the 26 layers replayed as one captured graph (as config 2's steps)
+        ws = cuda.alloc_device(stack.ws_bytes(B))
+        tok_bytes = B * D_H * 4
         h0 = cuda.upload(lp.synth_f32_bf16((steps + warmup) * B * D_H, 1.0, 5, 2), s)
+        hcur = cuda.alloc_device(tok_bytes)
+        graph = stack.capture(hcur, B, ws, s)
         for i in range(warmup):
-            for L in layers:
-                L.forward(h0 + (steps + i) * B * D_H * 4, h0 + (steps + i) * B * D_H * 4, B, ws, s)
+            cuda.dtod_async(hcur, h0 + (steps + i) * tok_bytes, tok_bytes, s)
+            graph.launch(s)
         e0, e1 = cuda.event(), cuda.event()
         cuda.sync()
         cuda.record_event(e0, s)
         for i in range(steps):
-            for L in layers:
-                L.forward(h0 + i * B * D_H * 4, h0 + i * B * D_H * 4, B, ws, s)
+            cuda.dtod_async(hcur, h0 + i * tok_bytes, tok_bytes, s)
+            graph.launch(s)
         cuda.record_event(e1, s)
         cuda.sync()
+        graph.close()
+        cuda.free_device(hcur)
         sec = cuda.elapsed_ms(e0, e1) / 1e3 / steps
         L0 = layers[0]
         L0.forward(h0, h0, B, ws, s)
@@ -690,6 +699,7 @@ def main() -> int:
     ap.add_argument("--paged-only", action="store_true")
     ap.add_argument("--no-mla", action="store_true", help="skip the config-5 MLA attention leg")
     ap.add_argument("--mla-only", action="store_true")
+    ap.add_argument("--shared-only", action="store_true")
     ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
     ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
     a = ap.parse_args()
@@ -713,18 +723,22 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
-    mla = None if a.no_mla or a.paged_only or a.prefill_only else run_mla(cuda, s, (1, 16), a.steps)
+    mla = None if a.no_mla or a.paged_only or a.prefill_only or a.shared_only else run_mla(cuda, s, (1, 16), a.steps)
     if a.mla_only:
         print(json.dumps({"mla": _rounded(mla)}), flush=True)
         cuda.close()
         return 0
-    prefill = None if a.no_prefill or a.paged_only else run_prefill(cuda, s, a.steps, a.warmup)
+    prefill = None if a.no_prefill or a.paged_only or a.shared_only else run_prefill(cuda, s, a.steps, a.warmup)
     if a.prefill_only:
         print(json.dumps({"prefill": prefill}), flush=True)
         cuda.close()
         return 0
-    paged = None if a.no_paged else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
+    paged = None if a.no_paged or a.shared_only else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
     shared = None if a.no_shared or a.paged_only else run_shared(cuda, s, (1, 16), a.steps, a.warmup)
+    if a.shared_only:
+        print(json.dumps({"shared": _rounded(shared)}), flush=True)
+        cuda.close()
+        return 0
     if a.paged_only:
         print(json.dumps({"paged": paged}), flush=True)
         cuda.close()

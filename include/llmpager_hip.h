@@ -476,9 +476,9 @@ int lp_pack_read_range(lp_pack* p, uint64_t offset, void* buf, uint64_t n);
 
 /* ---- measurement ------------------------------------------------------------ */
 
-/* When enabled, every kernel launch through this context is bracketed by a
- * pair of hipEvents on its stream (a measurement aid; it adds two event
- * records per launch).  lp_profile_read_sync waits for the recorded work and
+/* When enabled, every kernel launch through this context carries a start and
+ * a stop hipEvent on its own dispatch (a measurement aid: the kernel's begin
+ * and end timestamps, no separate event packets).  lp_profile_read_sync waits for the recorded work and
  * returns, for the kernel named `kernel` (e.g. "lp_moe_grouped"), the summed
  * elapsed milliseconds and launch count since the last reset. */
 int lp_profile_enable(lp_ctx* ctx, int enable);

@@ -27,9 +27,9 @@ __device__ __forceinline__ uint32_t ordered_key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// IEEE binary32 division, correctly rounded: the binary64 quotient of two
-// binary32 values rounds to the same binary32 as the exact quotient (53 >= 2*24+2).
-__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
+// IEEE binary32 division, correctly rounded (the compiler's fdiv sequence:
+// div_scale, a reciprocal refined by fused multiply-adds, div_fmas, div_fixup).
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
 
 }  // namespace
 

@@ -220,6 +220,22 @@ void prof_drain(lp_ctx* c) {
     c->prof_recs.clear();
 }
 
+}  // namespace
+
+// hip_ext.h's launch with events attached to the dispatch (declared here:
+// that header also holds templates only the HIP compiler takes).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ,
+                                               size_t sharedMemBytes, hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
+
+namespace {
+
+// Launch f; when profiling, the dispatch itself carries a start and a stop
+// event (hipExtModuleLaunchKernel takes the kernel's own begin and end
+// timestamps, not those of separate event packets around it).
 template <typename A>
 int launch(lp_ctx* c, Fn f, dim3 grid, dim3 block, size_t lds, lp_stream s, const A& args) {
     void* params[] = {const_cast<A*>(&args)};
@@ -228,14 +244,26 @@ int launch(lp_ctx* c, Fn f, dim3 grid, dim3 block, size_t lds, lp_stream s, cons
         std::lock_guard<std::mutex> g(c->prof_mu);
         e0 = prof_event(c);
         e1 = prof_event(c);
-        if (e0) (void)hipEventRecord(e0, (hipStream_t)s);
     }
-    hipError_t e = hipModuleLaunchKernel(c->fns[f], grid.x, grid.y, grid.z, block.x, block.y,
-                                         block.z, (unsigned)lds, (hipStream_t)s, params, nullptr);
-    if (c->prof && e0 && e1) {
+    hipError_t e;
+    if (e0 && e1) {
+        e = hipExtModuleLaunchKernel(c->fns[f], grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
+                                     block.y, block.z, lds, (hipStream_t)s, params, nullptr, e0, e1, 0);
         std::lock_guard<std::mutex> g(c->prof_mu);
-        (void)hipEventRecord(e1, (hipStream_t)s);
-        c->prof_recs.push_back(ProfRec{(int)f, e0, e1});
+        if (e == hipSuccess) {
+            c->prof_recs.push_back(ProfRec{(int)f, e0, e1});
+        } else {
+            c->prof_pool.push_back(e0);
+            c->prof_pool.push_back(e1);
+        }
+    } else {
+        if (e0 || e1) {
+            std::lock_guard<std::mutex> g(c->prof_mu);
+            if (e0) c->prof_pool.push_back(e0);
+            if (e1) c->prof_pool.push_back(e1);
+        }
+        e = hipModuleLaunchKernel(c->fns[f], grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)lds,
+                                  (hipStream_t)s, params, nullptr);
     }
     if (e != hipSuccess) return hip_fail(e, kSpecs[f].name);
     return LP_OK;
