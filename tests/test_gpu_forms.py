@@ -1,0 +1,71 @@
+"""Every form of the decode kernels against the oracle, with fp32 activations.
+
+The balanced gate/up comes as four kernels (16- or 8-step tiles; scales
+through LDS windows for group 32, or read per lane for groups 64 and 128,
+the reference's own q4g64 among them), the balanced down as two (6 steps, up
+to 8), and a one-token batch takes down and combine in one launch
+(`lp_moe_down_comb`, up to 8 steps, `_comb16` for 9..16).  Each case names
+the kernels it must reach; the per-kernel launch counts of the profiling
+mode show that it did.  Layer outputs within rel-L2 1e-3 on the delta
+h' - h, routing bit-exact given the device's logits (decode.rs:303-342)."""
+import numpy as np
+import pytest
+
+import llmpager_amd as lp
+import _oracle as O
+from _gpu import DeviceLayer, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def fp32_normal(n: int, seed: int) -> np.ndarray:
+    return np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+
+
+FORMS = [
+    # H, I, group, T, kernels that must run
+    (2048, 768, 64, 1, ("lp_moe_gateup_bal_rs", "lp_moe_down", "lp_moe_combine")),
+    (2048, 768, 64, 32, ("lp_moe_gateup_bal_rs", "lp_moe_down")),
+    (2048, 768, 128, 8, ("lp_moe_gateup_bal_rs",)),
+    (1024, 512, 32, 1, ("lp_moe_gateup_bal8", "lp_moe_down_comb")),
+    (1024, 512, 32, 32, ("lp_moe_gateup_bal8", "lp_moe_down_bal")),
+    (1024, 512, 64, 32, ("lp_moe_gateup_bal_rs8",)),
+    (2048, 1536, 32, 1, ("lp_moe_gateup_bal", "lp_moe_down_comb16")),
+    (2048, 1024, 32, 32, ("lp_moe_gateup_bal", "lp_moe_down_bal")),
+    (2048, 768, 32, 32, ("lp_moe_gateup_bal", "lp_moe_down_bal6")),
+]
+
+
+@pytest.mark.parametrize("H,I,group,T,kernels", FORMS)
+def test_decode_kernel_forms(cuda, H, I, group, T, kernels):
+    E, k = 64, 8
+    L = DeviceLayer(cuda, H=H, I=I, E=E, k=k, group=group, seed=H + I + group + T)
+    x = fp32_normal(T * H, 7 * T + group).reshape(T, H)
+    h = fp32_normal(T * H, 11 * T + group).reshape(T, H)
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    dx, dh = cuda.upload(x), cuda.upload(h)
+    cuda.profile_reset()
+    cuda.profile(True)
+    L.layer.forward(dx, dh, T, ws)
+    cuda.sync()
+    counts = {kn: cuda.profile_read(kn)[1] for kn in kernels}
+    cuda.profile(False)
+    got = cuda.download(dh, (T, H), np.float32)
+    logits = cuda.download(ws + lay.logits, (T, E), np.float32)
+    ids = cuda.download(ws + lay.ids, (T, k), np.int32)
+    wts = cuda.download(ws + lay.wts, (T, k), np.float32)
+    cnt = cuda.download(ws + lay.cnt, (T,), np.int32)
+    assert L.layer.status(ws, T)[1] == 0
+    for p in (ws, dx, dh):
+        cuda.free_device(p)
+    assert all(n == 1 for n in counts.values()), counts
+    want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h, threads=8)
+    L.free()
+    assert np.array_equal(logits.view(np.uint32), wlog.view(np.uint32))
+    assert np.array_equal(cnt, wcnt)
+    for t in range(T):
+        c = cnt[t]
+        assert np.array_equal(ids[t, :c], wids[t, :c]), t
+        assert np.array_equal(wts[t, :c].view(np.uint32), ww[t, :c].view(np.uint32)), t
+    assert rel_l2(got - h, want - h) <= 1e-3
