@@ -1326,12 +1326,13 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
 // Balanced gate/up for decode batches (lp_moe_gateup_bal).  One workgroup of
 // kBalWaves waves per CU.  Work is cut into units of 8 rows of gate plus the
 // same 8 rows of up over the whole of K (one MFMA tile: lanes n < 8 carry gate
-// row r0 + n, lanes n >= 8 up row r0 + n - 8), for each "virtual expert" =
-// (routed expert, group of up to kBalToks = 4 of its tokens).  Virtual experts are
-// numbered by a prefix sum over the expert table and every workgroup takes
-// an equal contiguous range of the V * R units (R = ceil(I / 8)); with V no
-// larger than the grid a range touches at most two virtual experts, whose
-// token images are staged once, into two slots of kBalPairs pairs.  Each wave then
+// row r0 + n, lanes n >= 8 up row r0 + n - 8), for each token group
+// (routed expert, up to kBalToks = 4 of its tokens), in blocks of up to
+// kBalGroups groups of one expert ordered row unit by row unit (BalPlan).
+// Every workgroup takes an equal contiguous range of the V * R units (V
+// groups, R = ceil(I / 8)); with V no larger than the grid a range touches
+// at most two blocks, whose tokens' images are staged once, into two LDS
+// slots.  Each wave then
 // walks its units (every W-th of the range, W waves) with the next unit's
 // weights in flight while the current one is multiplied: two register
 // buffers, loads unconditional (a past-the-end unit reads a zero-size

@@ -307,11 +307,11 @@ struct GroupedArgs {
 // counters (kBalWaves wave totals, then six slot words), the expert table
 // (kBalMaxU entries), then two scale windows per wave.
 constexpr int kBalWaves = 8;
-// A virtual expert of the balanced kernels: up to kBalPairs token pairs of
-// one routed expert, whose weights one pass over the expert serves.  Four
-// pairs read fewer weight bytes (experts of 5-8 tokens once instead of twice)
-// but measured slower at 32 tokens: units of one range then differ up to
-// fourfold in MFMA work.
+// A token group of the balanced kernels: up to kBalPairs token pairs of one
+// routed expert, which one unit's MFMAs serve.  Groups of four pairs were
+// measured slower at 32 tokens: the units of one range then differ up to
+// fourfold in MFMA work (the row-major blocks below save the weight bytes
+// instead).
 constexpr int kBalPairs = 2;
 constexpr int kBalToks = 2 * kBalPairs;
 // Token groups of one expert whose units the balanced kernels interleave

@@ -1038,8 +1038,8 @@ int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, 
 static int tile_steps_host(int cols) { return ((cols >> 5) + 3) >> 2; }
 
 // Whether lp_moe_gateup_bal takes the gate/up of ga's routed experts: one
-// chunk of K, an expert table it can hold, no more virtual experts (groups
-// of up to kBalToks = 4 tokens of one expert) than CUs, and its LDS.
+// chunk of K, an expert table it can hold, no more token groups (up to
+// kBalToks = 4 tokens of one expert each) than CUs, and its LDS.
 static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int H = ga.L.hidden, pairs = ga.T * ga.L.top_k;
     const int maxv = std::min(pairs, (pairs + (kBalToks - 1) * maxu) / kBalToks);
@@ -1066,8 +1066,9 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
 // (maxu entries): workgroup width chosen so that there are about two work
 // items per CU, down with two tiles per wave when the inner size allows.
 // `routed`: the routed experts (the balanced down may take them; the
-// balanced gate/up takes the shared MLP too, as ceil(T / 4) virtual experts
-// whose weight rows neighbouring workgroups of one XCD read together).
+// balanced gate/up takes the shared MLP too, as ceil(T / 4) one-group
+// entries of one blob, whose weight rows neighbouring workgroups of one XCD
+// read together).
 static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s,
                        bool with_down = true) {
     GroupedArgs ga = ga0;
