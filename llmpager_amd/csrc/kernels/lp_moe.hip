@@ -2026,17 +2026,18 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
 // (w < cnt, at most kCombWaves picks).  Each wave stages its pick's act row
 // as digit fragments in its own pair slot, loads the 16 rows of its
 // expert's down matrix (one tile of at most NS steps, scales through an LDS
-// window) and leaves the 16 row sums in LDS; after a barrier the first 16
+// window for group 32 with 16-byte aligned scale rows (SL), else read per
+// lane) and leaves the 16 row sums in LDS; after a barrier the first 16
 // threads fold them in pick order, h += sum_j w_j y_j, with the fused
-// multiply-adds of lp_moe_combine, so h is bit-identical to the down kernel
-// followed by the combine.  For layers without a shared MLP, group 32 and
-// tile_steps(inter) <= 16 (the host checks).
+// multiply-adds of lp_moe_combine, then add the shared MLP's row (already
+// computed) as the combine does, so h is bit-identical to the down kernel
+// followed by the combine.  For tile_steps(inter) <= 16 (the host checks).
 // ---------------------------------------------------------------------------
 namespace {
 
 __host__ __device__ constexpr int comb_part_off(int inter) { return (frag_lds_bytes(inter, kCombWaves) + 15) & ~15; }
 
-template <int NS>
+template <int NS, int RS, bool SL>
 __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -2055,9 +2056,9 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
     const int p = min(max(gptr<int>(a.W.inv)[min(wave, L.top_k - 1)], 0), a.maxu - 1);
     const uint64_t eb = entry_of(a, p).blob;
     const uint64_t blob = wave < c ? eb : 0;
-    WRegs<NS, true> D;
+    WRegs<NS, SL> D;
     if (blob != 0) {
-        const WTile<0> T = wtile<0>(blob + L.down_off, H, I, n0);
+        const WTile<RS> T = wtile<RS>(blob + L.down_off, H, I, n0);
         wload(D, T, 0, swin);
         Frags Fw = F;
         Fw.lds = F.lds + wave * frag_pair_bytes(F.ngp);
@@ -2070,7 +2071,7 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
     if (blob != 0) {
         float acc[1][1][2] = {{{0.0f, 0.0f}}};
         const ABase B[1] = {abase(F, wave, 0)};
-        const WRegs<NS, true> Rm[1] = {D};
+        const WRegs<NS, SL> Rm[1] = {D};
         wmma(Rm, B, tile_steps(I), 1, acc);
         yv = tile_reduce(acc[0][0][0]);
     } else if (wave < c && lane == 0) {
@@ -2084,7 +2085,9 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
         float acc = 0.0f;
         for (int j = 0; j < c; ++j) acc = __builtin_fmaf(w[j], part[j * 16 + threadIdx.x], acc);
         LP_GLOBAL float* h = gptr_w<float>(a.h);
-        h[row] = h[row] + acc;
+        float v = h[row] + acc;
+        if (L.shared_blob) v = v + gptr<float>(a.W.sh_y)[row];
+        h[row] = v;
     }
 }
 
@@ -2092,11 +2095,18 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(64 * kCombWaves) lp_moe_down_comb(const GroupedArgs a) {
     if (tile_steps(a.L.inter) == 6)
-        down_comb_body<6>(a);  // inter 768 loads only its own 6 steps
+        down_comb_body<6, 0, true>(a);  // inter 768 loads only its own 6 steps
     else
-        down_comb_body<8>(a);
+        down_comb_body<8, 0, true>(a);
 }
 
 extern "C" __global__ void __launch_bounds__(64 * kCombWaves) lp_moe_down_comb16(const GroupedArgs a) {
-    down_comb_body<16>(a);
+    down_comb_body<16, 0, true>(a);
+}
+
+// Scales read per lane (groups 64 and 128, or scale rows not 16-byte aligned).
+extern "C" __global__ void __launch_bounds__(64 * kCombWaves) lp_moe_down_comb_rs(const GroupedArgs a) {
+#define LP_DOWN(rs) down_comb_body<16, rs, false>(a)
+    LP_BY_RS(a.L.group, LP_DOWN)
+#undef LP_DOWN
 }

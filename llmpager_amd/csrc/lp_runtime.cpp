@@ -85,6 +85,7 @@ enum Fn {
     kDownBal6,
     kDownComb,
     kDownComb16,
+    kDownCombRs,
     kRmsNorm,
     kScaleAdd,
     kKvAppendF32,
@@ -126,6 +127,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_gateup_bal_rs"},  {"lp_moe.hsaco", "lp_moe_gateup_bal_rs8"},
     {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
     {"lp_moe.hsaco", "lp_moe_down_comb"},  {"lp_moe.hsaco", "lp_moe_down_comb16"},
+    {"lp_moe.hsaco", "lp_moe_down_comb_rs"},
     {"lp_attn.hsaco", "lp_rmsnorm"},       {"lp_attn.hsaco", "lp_scale_add"},
     {"lp_attn.hsaco", "lp_kv_append_f32"}, {"lp_attn.hsaco", "lp_kv_append_f16"},
     {"lp_attn.hsaco", "lp_rope"},          {"lp_attn.hsaco", "lp_bf16_row_to_f32"},
@@ -337,8 +339,8 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
         // the loaded code objects must take the balanced kernels' fixed
         // workgroup size (their launch bound)
         for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6, kDownComb,
-                     kDownComb16}) {
-            const int need = 64 * (f == kDownComb || f == kDownComb16 ? kCombWaves : kBalWaves);
+                     kDownComb16, kDownCombRs}) {
+            const int need = 64 * (f == kDownComb || f == kDownComb16 || f == kDownCombRs ? kCombWaves : kBalWaves);
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->fns[f]) != hipSuccess ||
                 mt < need) {
@@ -1113,13 +1115,30 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
                   s, ga);
 }
 
-// LDS of lp_moe_down_comb(16): the picks' fragment pairs, their row sums
-// (kCombWaves x 16 floats), then a scale window per wave (6, 8 or 16 steps
-// wide: tile steps 6, 7..8, 9..16).
-static int comb_lds(int inter, int steps) {
+// LDS of lp_moe_down_comb(16, _rs): the picks' fragment pairs, their row
+// sums (kCombWaves x 16 floats), then (scales in LDS windows) a window per
+// wave (6, 8 or 16 steps wide: tile steps 6, 7..8, 9..16).
+static int comb_lds(int inter, int steps, bool sl) {
     const int ns = steps == 6 ? 6 : steps <= 8 ? 8 : 16;
-    const int win = 64 * 2 * ((ns + 7) / 8 * 8);
+    const int win = sl ? 64 * 2 * ((ns + 7) / 8 * 8) : 0;
     return ((frag_lds_bytes(inter, kCombWaves) + 15) & ~15) + kCombWaves * 64 + kCombWaves * win;
+}
+
+// The shared MLP through the grouped kernels: its own width, group and
+// regions, an expert table of consecutive token groups (written by dispatch).
+static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& ga, int T, lp_stream s) {
+    GroupedArgs gs = ga;
+    gs.L.inter = d->shared_inter;
+    gs.L.group = d->shared_group;
+    gs.L.gate_off = d->sh_gate_off;
+    gs.L.up_off = d->sh_up_off;
+    gs.L.down_off = d->sh_down_off;
+    gs.L.top_k = 1;
+    gs.W.et = ga.W.sh_et;
+    gs.W.perm = ga.W.sh_perm;
+    gs.W.act = ga.W.sh_act;
+    gs.W.y = ga.W.sh_y;
+    return grouped_ffn(c, gs, shared_entries(T), false, s);
 }
 
 // The grouped expert kernels and the combine; the fragment images of x are
@@ -1184,34 +1203,24 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
             return r;
     } else {
-        // one token without a shared MLP: down and combine in one launch
+        // one token: down and combine in one launch (after the shared MLP,
+        // whose row it adds)
         const int Si = tile_steps_host(d->inter);
-        const bool comb = T == 1 && !d->shared_blob && d->top_k <= kCombWaves &&
-                          scales_in_lds(d->group, d->inter) && Si <= 16 && (size_t)comb_lds(d->inter, Si) <= c->max_lds;
+        const bool sl = scales_in_lds(d->group, d->inter);
+        const bool comb = T == 1 && d->top_k <= kCombWaves && Si <= 16 &&
+                          (size_t)comb_lds(d->inter, Si, sl) <= c->max_lds;
         if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb)) return r;
         if (comb) {
+            if (d->shared_blob)
+                if (int r = shared_ffn(c, d, ga, T, s)) return r;
             ga.maxu = std::min(d->top_k, d->experts);
-            return launch(c, Si <= 8 ? kDownComb : kDownComb16, dim3((unsigned)((d->hidden + kTileRows - 1) / kTileRows)),
-                          dim3(64 * kCombWaves), (size_t)comb_lds(d->inter, Si), s, ga);
+            const Fn f = !sl ? kDownCombRs : Si <= 8 ? kDownComb : kDownComb16;
+            return launch(c, f, dim3((unsigned)((d->hidden + kTileRows - 1) / kTileRows)), dim3(64 * kCombWaves),
+                          (size_t)comb_lds(d->inter, Si, sl), s, ga);
         }
     }
-    if (d->shared_blob) {
-        // the shared MLP through the same kernels: its own width, group and
-        // regions, an expert table of consecutive token groups (written by
-        // dispatch)
-        GroupedArgs gs = ga;
-        gs.L.inter = Is;
-        gs.L.group = d->shared_group;
-        gs.L.gate_off = d->sh_gate_off;
-        gs.L.up_off = d->sh_up_off;
-        gs.L.down_off = d->sh_down_off;
-        gs.L.top_k = 1;
-        gs.W.et = ga.W.sh_et;
-        gs.W.perm = ga.W.sh_perm;
-        gs.W.act = ga.W.sh_act;
-        gs.W.y = ga.W.sh_y;
-        if (int r = grouped_ffn(c, gs, shared_entries(T), false, s)) return r;
-    }
+    if (d->shared_blob)
+        if (int r = shared_ffn(c, d, ga, T, s)) return r;
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 1023) / 1024), (unsigned)T), dim3(256), 0,
                   s, ga);
 }

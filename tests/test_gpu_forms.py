@@ -4,7 +4,8 @@ The balanced gate/up comes as four kernels (16- or 8-step tiles; scales
 through LDS windows for group 32, or read per lane for groups 64 and 128,
 the reference's own q4g64 among them), the balanced down as two (6 steps, up
 to 8), and a one-token batch takes down and combine in one launch
-(`lp_moe_down_comb`, up to 8 steps, `_comb16` for 9..16).  Each case names
+(`lp_moe_down_comb`, up to 8 steps, `_comb16` for 9..16, `_comb_rs` with
+per-lane scales: groups 64 and 128, or scale rows not 16-byte aligned).  Each case names
 the kernels it must reach; the per-kernel launch counts of the profiling
 mode show that it did.  Layer outputs within rel-L2 1e-3 on the delta
 h' - h, routing bit-exact given the device's logits (decode.rs:303-342)."""
@@ -24,7 +25,8 @@ def fp32_normal(n: int, seed: int) -> np.ndarray:
 
 FORMS = [
     # H, I, group, T, kernels that must run
-    (2048, 768, 64, 1, ("lp_moe_gateup_bal_rs", "lp_moe_down", "lp_moe_combine")),
+    (2048, 768, 64, 1, ("lp_moe_gateup_bal_rs", "lp_moe_down_comb_rs")),
+    (2048, 1408, 32, 1, ("lp_moe_gateup_bal", "lp_moe_down_comb_rs")),
     (2048, 768, 64, 32, ("lp_moe_gateup_bal_rs", "lp_moe_down")),
     (2048, 768, 128, 8, ("lp_moe_gateup_bal_rs",)),
     (1024, 512, 32, 1, ("lp_moe_gateup_bal8", "lp_moe_down_comb")),
