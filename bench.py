@@ -213,7 +213,7 @@ def run_batch(cuda, stack: Stack, B: int, steps: int, warmup: int) -> dict:
 PREFILL_T = 2048
 DISPATCH_KERNELS = ("lp_moe_topk", "lp_moe_disp_count", "lp_moe_disp_scan", "lp_moe_disp_scatter")
 PREFILL_KERNELS = ("lp_moe_router", "lp_gemm_router", *DISPATCH_KERNELS, "lp_moe_ximage", "lp_gemm_tiles",
-                   "lp_gemm_gateup", "lp_gemm_actimg", "lp_gemm_down", "lp_moe_combine")
+                   "lp_gemm_gateup", "lp_gemm_down", "lp_moe_combine")
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 
 

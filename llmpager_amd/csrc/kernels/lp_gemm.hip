@@ -95,6 +95,19 @@ __device__ __forceinline__ int tile_row(const GemmTile& g, int r) {
     return min(g.n0 + (MODE == 0 ? (r & 63) : r), g.NR - 1);
 }
 
+// Sum over the 16 lanes of a row, in every lane of the row: quad_perm
+// [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+
 template <int MODE, int RS, bool LO>
 __device__ __forceinline__ void gemm_main(const GemmArgs& a, const GemmTile& G) {
     // Sub-groups per stage: an A slot holds one sub-group's hi and lo parts,
@@ -333,22 +346,67 @@ __device__ __forceinline__ void gemm_main(const GemmArgs& a, const GemmTile& G) 
     }
 
     // epilogue: lane holds C rows 4 akb + i (tokens) of column lane & 15 of each tile
-    float* out = dptr<float>(a.out);
+    if constexpr (MODE == 0) {
+        // act = silu(gate) * up straight into the down GEMM's A image (a.out
+        // is the image base; lpk::image_bytes layout, as lp_device.h's
+        // write_image_group): the wave's 32 columns n0 + 32 wn .. + 31 are
+        // sub-group g of each of its token rows, held by the 16 lanes of one
+        // row (column 16 t + am in register t).  Fragment word (d, w) pairs
+        // columns 8d + w and 8d + w + 4, so lane am (bit 2 clear) packs its
+        // hi part with lane am + 4's (a row shift by 4) and writes the hi
+        // word, lane am + 4 the lo word; the seed -136 (sum hi) - 136 (sum
+        // lo) comes from a sum over the row's lanes (quad swaps, then the
+        // half-row and row mirrors).  All lane exchanges are DPP moves.
+        LP_GLOBAL uint8_t* img = gptr_w<uint8_t>(a.out);
+        const int g = (G.n0 >> 5) + wn;
+        const bool live_g = g < (G.NR >> 5);
+        const int ngp = frag_ngp(G.NR);
+        const size_t ib = (size_t)image_bytes(G.NR);
+        const bool low = (am & 4) == 0;
+        const uint32_t part = low ? (uint32_t)g * 64u : (uint32_t)(ngp + g) * 64u;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 16 * (2 * mt + wm) + 4 * akb + i;
-            if (m >= G.mvalid) continue;
-            float* orow = out + (size_t)(G.x.p0 + G.m0 + m) * G.NR;
-            if (MODE == 0) {
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * (2 * mt + wm) + 4 * akb + i;
+                LP_GLOBAL uint8_t* row = img + (size_t)(G.x.p0 + G.m0 + min(m, G.mvalid - 1)) * ib;
+                const bool st = m < G.mvalid && live_g;  // the same for lanes am and am ^ 4
+                float shi = 0.0f, slo = 0.0f;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    const int r = G.n0 + 32 * wn + 16 * t + am;
                     const float gg = acc[mt][t][i], uu = acc[mt][t + 2][i];
-                    if (r < G.NR) orow[r] = gg / (1.0f + expf(-gg)) * uu;
+                    const float v = gg / (1.0f + expf(-gg)) * uu;
+                    const uint32_t h16 = f32_to_bf16_rne(v);
+                    const uint32_t l16 = f32_to_bf16_rne(v - bf16_to_f32(h16));
+                    shi += bf16_to_f32(h16);
+                    slo += bf16_to_f32(l16);
+                    // both moves with every lane on (a DPP source lane that is
+                    // off reads as zero): pinned here by the empty asm, so that
+                    // the select below cannot become a branch around each
+                    const int send = (int)(low ? l16 : h16);
+                    int up4 = __builtin_amdgcn_mov_dpp(send, 0x104, 0xf, 0xf, true);  // row_shl:4, lane am + 4
+                    int dn4 = __builtin_amdgcn_mov_dpp(send, 0x114, 0xf, 0xf, true);  // row_shr:4, lane am - 4
+                    asm volatile("" : "+v"(up4), "+v"(dn4));
+                    const uint32_t recv = (uint32_t)(low ? up4 : dn4);
+                    const uint32_t word = low ? (h16 | (recv << 16)) : (recv | (l16 << 16));
+                    const uint32_t off = part + 16u * (uint32_t)(2 * t + (am >> 3)) + 4u * (uint32_t)(am & 3);
+                    if (st) *reinterpret_cast<LP_GLOBAL uint32_t*>(row + off) = word;
                 }
-            } else {
+                shi = row_sum16(shi);
+                slo = row_sum16(slo);
+                if (st && am == 0)
+                    reinterpret_cast<LP_GLOBAL float2*>(row + (size_t)ngp * 128)[g] = make_float2(-136.0f * shi + -136.0f * slo, 0.0f);
+            }
+        }
+    } else {
+        float* out = dptr<float>(a.out);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * (2 * mt + wm) + 4 * akb + i;
+                if (m >= G.mvalid) continue;
+                float* orow = out + (size_t)(G.x.p0 + G.m0 + m) * G.NR;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int r = G.n0 + 64 * wn + 16 * t + am;
@@ -387,11 +445,31 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const int tid = threadIdx.x;
     if (G.x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
         if (tid == 0 && nb == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
-        const int cols = MODE == 0 ? kGemmBN / 2 : kGemmBN;
-        float* out = dptr<float>(a.out);
-        for (int e = tid; e < G.mvalid * cols; e += blockDim.x) {
-            const int m = e / cols, r = G.n0 + e - m * cols;
-            if (r < G.NR) out[(size_t)(G.x.p0 + G.m0 + m) * G.NR + r] = 0.0f;
+        if (MODE == 0) {
+            // zero act: the tile's two sub-groups of each token row's image
+            // (both parts, and the seeds)
+            uint8_t* img = dptr<uint8_t>(a.out);
+            const int ngp = frag_ngp(G.NR);
+            const size_t ib = (size_t)image_bytes(G.NR);
+            for (int e = tid; e < G.mvalid * 18; e += blockDim.x) {
+                // item (m, sub-group gi, w): w < 8 one 16-byte quarter of
+                // part w >> 2, w = 8 the seeds
+                const int m = e / 18, q = e - m * 18, gi = q / 9, w = q - gi * 9;
+                const int g = (G.n0 >> 5) + gi;
+                if (g >= (G.NR >> 5)) continue;
+                uint8_t* row = img + (size_t)(G.x.p0 + G.m0 + m) * ib;
+                if (w < 8)
+                    reinterpret_cast<uint4*>(row + (size_t)((w >> 2) * ngp + g) * 64)[w & 3] = make_uint4(0u, 0u, 0u, 0u);
+                else
+                    reinterpret_cast<float2*>(row + (size_t)ngp * 128)[g] = make_float2(0.0f, 0.0f);
+            }
+        } else {
+            const int cols = kGemmBN;
+            float* out = dptr<float>(a.out);
+            for (int e = tid; e < G.mvalid * cols; e += blockDim.x) {
+                const int m = e / cols, r = G.n0 + e - m * cols;
+                if (r < G.NR) out[(size_t)(G.x.p0 + G.m0 + m) * G.NR + r] = 0.0f;
+            }
         }
         return;
     }
@@ -536,18 +614,6 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_tiles(const GemmArgs a
         __syncthreads();
     }
     if (tid == 0) dptr<int>(a.W.meta)[2] = min(base, a.max_tiles);
-}
-
-// act rows (dispatch order) into fragment images for the down GEMM: 8 rows
-// per workgroup, 32 sub-groups per row at a time.
-extern "C" __global__ void __launch_bounds__(256) lp_gemm_actimg(const GemmArgs a) {
-    const int I = a.L.inter;
-    const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
-    const int total = a.T * a.L.top_k;
-    if (row >= total) return;
-    const float* src = dptr<const float>(a.W.act) + (size_t)row * I;
-    uint8_t* img = dptr<uint8_t>(a.W.actimg) + (size_t)row * image_bytes(I);
-    for (int g = threadIdx.x & 31; g < frag_ngp(I); g += 32) (void)write_image_group(src, I, g, img);
 }
 
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) lp_gemm_gateup(const GemmArgs a) {

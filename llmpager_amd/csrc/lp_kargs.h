@@ -356,7 +356,7 @@ struct GemmArgs {
     LayerView L;
     Workspace W;
     uint64_t a_img;      // A images: gate/up = W.xf (token rows through perm); down = act images
-    uint64_t out;        // gate/up: act f32 [T*k, I]; down: y f32 [T*k, H]
+    uint64_t out;        // gate/up: act images [T*k] (image_bytes(I) each); down: y f32 [T*k, H]
     uint64_t tiles;      // i32 [max_tiles]: (expert entry << 16) | token block; count in meta[2]
     int32_t T;
     int32_t max_tiles;

@@ -69,7 +69,6 @@ enum Fn {
     kResolve,
     kGemmTiles,
     kGemmGateup,
-    kGemmActImg,
     kGemmDown,
     kDispCount,
     kDispScan,
@@ -119,7 +118,7 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_topk_dispatch"}, {"lp_basic.hsaco", "lp_expf_wave"},
     {"lp_moe.hsaco", "lp_moe_resolve"},
     {"lp_gemm.hsaco", "lp_gemm_tiles"},    {"lp_gemm.hsaco", "lp_gemm_gateup"},
-    {"lp_gemm.hsaco", "lp_gemm_actimg"},   {"lp_gemm.hsaco", "lp_gemm_down"},
+    {"lp_gemm.hsaco", "lp_gemm_down"},
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
@@ -843,7 +842,7 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->uniq = take(E * 4);
     out->meta = take(64);
     out->et = take(E * sizeof(ExpertEntry));
-    out->act = take(t * k * I * 4);
+    out->act = take(use_gemm(d, T) ? 0 : t * k * I * 4);  // the prefill GEMM writes act as images (actimg)
     out->y = take(t * k * H * 4);
     out->xf = take(use_gemm(d, T) ? t * (uint64_t)image_bytes((int)H) : 0);
     out->xd = take(t * (uint64_t)dimage_bytes((int)H));
@@ -1190,12 +1189,11 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         gm.tiles = ga.W.tiles;
         gm.max_tiles = gemm_max_tiles(d, T);
         if (int r = launch(c, kGemmTiles, dim3(1), dim3(256), 0, s, gm)) return r;
+        // gate/up writes act as the down GEMM's bf16 fragment images
         gm.a_img = ga.W.xf;
-        gm.out = ga.W.act;
+        gm.out = ga.W.actimg;
         gm.nblocks = (d->inter + kGemmBN / 2 - 1) / (kGemmBN / 2);
         if (int r = launch(c, kGemmGateup, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
-            return r;
-        if (int r = launch(c, kGemmActImg, dim3((unsigned)((T * d->top_k + 7) / 8)), dim3(256), 0, s, gm))
             return r;
         gm.a_img = ga.W.actimg;
         gm.out = ga.W.y;
