@@ -510,14 +510,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 // so every product is exact and the sums are fp32 in the matrix core (the
 // GEMV router's lane order is not kept: its results agree to fp32 rounding).
 // The mid and lo MFMAs run only when some lane's x has such a part (never for
-// bf16-valued activations).  Grid (ceil(T / 16), ceil(E / 128)), 256 threads:
-// wave w takes 16 tokens x experts 128 y + 32 w .. + 31; no LDS, no barriers.
+// bf16-valued activations).  Grid (ceil(T / 16), ceil(E / 32)), 256 threads:
+// the workgroup takes 16 tokens x experts 32 y .. 32 y + 31, wave w the w-th
+// quarter of the hidden dimension (its loads four 32-column steps at a time),
+// and the four partial tiles meet in LDS, summed in wave order.
 extern "C" __global__ void __launch_bounds__(256) lp_gemm_router(const RouteArgs a) {
+    __shared__ f32x4_t part[3][2][64];  // waves 1..3: their two partial C tiles per lane
     const int H = a.L.hidden, E = a.L.experts, T = a.T;
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     const int m = lane & 15, kb = lane >> 4;
-    const int e0 = blockIdx.y * 128 + wave * 32;
-    if (e0 >= E) return;
+    const int e0 = blockIdx.y * 32;
+    if (e0 >= E) return;  // the whole workgroup
     const int t = min((int)blockIdx.x * 16 + m, T - 1);  // rows past the batch repeat its last token
     const float* xr = dptr<const float>(a.x) + (size_t)t * H + 8 * kb;
     const uint16_t* w0 = dptr<const uint16_t>(a.L.router_w) + (size_t)min(e0 + m, E - 1) * H + 8 * kb;
@@ -555,9 +558,12 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_router(const RouteArgs
             c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wb, c1, 0, 0, 0);
         }
     };
-    // four k-steps' loads in flight before their MFMAs (H is a multiple of 32)
-    int h = 0;
-    for (; h + 128 <= H; h += 128) {
+    // this wave's quarter of the 32-column steps (H is a multiple of 32),
+    // four steps' loads in flight before their MFMAs
+    const int ns = H >> 5;
+    const int hend = 32 * ((ns * (wave + 1)) >> 2);
+    int h = 32 * ((ns * wave) >> 2);
+    for (; h + 128 <= hend; h += 128) {
         float4 xa[4], xb[4];
         uint4 wa[4], wb[4];
 #pragma unroll
@@ -570,9 +576,20 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_router(const RouteArgs
 #pragma unroll
         for (int q = 0; q < 4; ++q) step(xa[q], xb[q], wa[q], wb[q]);
     }
-    for (; h < H; h += 32)
+    for (; h < hend; h += 32)
         step(*reinterpret_cast<const float4*>(xr + h), *reinterpret_cast<const float4*>(xr + h + 4),
              *reinterpret_cast<const uint4*>(w0 + h), *reinterpret_cast<const uint4*>(w1 + h));
+    if (wave > 0) {
+        part[wave - 1][0][lane] = c0;
+        part[wave - 1][1][lane] = c1;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+        c0 += part[w][0][lane];
+        c1 += part[w][1][lane];
+    }
     // lane holds C rows 4 kb + i (tokens) of column m (experts e0 + m, e0 + 16 + m)
     float* logits = dptr<float>(a.W.logits);
 #pragma unroll

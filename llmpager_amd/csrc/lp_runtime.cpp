@@ -1001,7 +1001,7 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
     ra.make_xf = image_kinds(d, T);
     if (T > kTopkDispatchMaxT) {
         // large batch: the MFMA router, then the images of x on their own
-        dim3 g((unsigned)((T + 15) / 16), (unsigned)((d->experts + 127) / 128));
+        dim3 g((unsigned)((T + 15) / 16), (unsigned)((d->experts + 31) / 32));
         if (int r = launch(c, kGemmRouter, g, dim3(256), 0, s, ra)) return r;
         if (int r = launch(c, kXImage, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, ra)) return r;
         return route_tail(c, ra, s);
