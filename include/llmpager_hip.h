@@ -219,7 +219,7 @@ typedef struct lp_moe_ws_layout {
     uint64_t uniq;    /* i32 [E] experts with picks, ascending */
     uint64_t meta;    /* i32 [16]: [0] unique count, [1] error flags */
     uint64_t et;      /* 32-byte expert entries [E] for the grouped kernels */
-    uint64_t act;     /* f32 [T*k, I] */
+    uint64_t act;     /* f32 [T*k, I] (size 0 on the prefill GEMM path, which keeps act in actimg) */
     uint64_t y;       /* f32 [T*k, H] */
     uint64_t xf;      /* [T] bf16 hi/lo images of x for the prefill GEMM (size 0 without it) */
     uint64_t xd;      /* [T] digit images of x for the grouped kernels (per 32 columns 16-bit
