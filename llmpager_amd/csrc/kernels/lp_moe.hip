@@ -1333,12 +1333,14 @@ __device__ __forceinline__ void gateup_body(const GroupedArgs& a) {
 // groups, R = ceil(I / 8)); with V no larger than the grid a range touches
 // at most two blocks, whose tokens' images are staged once, into two LDS
 // slots.  Each wave then
-// walks its units (every W-th of the range, W waves) with the next unit's
-// weights in flight while the current one is multiplied: two register
-// buffers, loads unconditional (a past-the-end unit reads a zero-size
-// buffer) and every store issued (a dropped one past the end of act), so
-// that the compiler's wait before each unit counts only the other buffer's
-// loads.  No barrier after the start.
+// walks its units (every W-th of the range, W waves), one at a time: a
+// unit's loads, then its MFMAs, the workgroup's waves overlapping one
+// another's loads and math (a second register buffer, the next unit's
+// weights in flight during the current one's MFMAs, measured slower: the
+// extra loads only lengthen the memory system's queues).  Loads and stores
+// are issued unconditionally (a missing expert's unit reads a zero-size
+// buffer, a lane with nothing to store writes past the end of act, which
+// the hardware drops).  No barrier after the start.
 // ---------------------------------------------------------------------------
 
 // The merged gate/up tile of rows [r0, r0 + 8) of an expert blob; `valid`
@@ -1531,7 +1533,7 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     const int Sx = tile_steps(H);
     const uint64_t dummy = L.router_w;
     const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(H) +
-                          (uint32_t)(2 * wave * scale_window_bytes<NS>());
+                          (uint32_t)(wave * scale_window_bytes<NS>());
     LP_GLOBAL float* act = gptr_w<float>(a.W.act);
     auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
         int s, u, gl;
@@ -1544,8 +1546,6 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     };
     // act through a raw buffer: a lane with nothing to store writes at its end,
     // which the hardware drops, so every unit issues the same memory operations
-    // (branch-free stores keep the compiler's count of outstanding loads exact:
-    // it then waits for one buffer's loads only, not for the other's)
     const uint32_t act_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)I * 4u;
     const __amdgpu_buffer_rsrc_t act_rs =
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.act), (short)0, (int)act_bytes, kBufferWord3);
@@ -1591,16 +1591,13 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)I + (uint32_t)row) * 4u : act_bytes;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), act_rs, (int)off, 0, 0);
     };
-    WRegs<NS, SL> RA, RB;
+    WRegs<NS, SL> RA;
     load(RA, 0, swin);
     __builtin_amdgcn_s_waitcnt(0);  // images, seeds and the first unit have landed
     __syncthreads();
-    for (int j = 0; j < J; j += 2) {
-        load(RB, j + 1, swin + scale_window_bytes<NS>());
+    for (int j = 0; j < J; ++j) {
+        if (j > 0) load(RA, j, swin);
         compute(RA, j);
-        if (j + 1 >= J) break;
-        load(RA, j + 2, swin);
-        compute(RB, j + 1);
     }
     if (missing && lane == 0) atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);
     __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) unit's loads
@@ -1608,8 +1605,8 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
 
 // Balanced down for decode batches (lp_moe_down_bal): the plan of the
 // balanced gate/up over units of 16 rows of down (all of K = inter), the
-// slots' act rows staged as fragments, two register buffers in turn and
-// branch-free stores into y (a dropped one past its end).
+// slots' act rows staged as fragments, one unit at a time per wave as in the
+// gate/up, and branch-free stores into y (a dropped one past its end).
 template <int RS>
 __device__ __forceinline__ WTile<RS> wtile_dn(uint64_t blob, bool valid, uint64_t dummy, uint32_t off, int rows,
                                               int cols, int r0) {
@@ -1665,7 +1662,7 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     const int Sx = tile_steps(I);
     const uint64_t dummy = L.router_w;
     const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(I) +
-                          (uint32_t)(2 * wave * scale_window_bytes<NS>());
+                          (uint32_t)(wave * scale_window_bytes<NS>());
     auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
         int s, u, gl;
         P.unit(lo + wave + W * j, s, u, gl);
@@ -1716,16 +1713,13 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, (int)off, 0, 0);
         }
     };
-    WRegs<NS, SL> RA, RB;
+    WRegs<NS, SL> RA;
     load(RA, 0, swin);
     __builtin_amdgcn_s_waitcnt(0);  // the first unit has landed
     __syncthreads();                // and the staged act rows are in place
-    for (int j = 0; j < J; j += 2) {
-        load(RB, j + 1, swin + scale_window_bytes<NS>());
+    for (int j = 0; j < J; ++j) {
+        if (j > 0) load(RA, j, swin);
         compute(RA, j);
-        if (j + 1 >= J) break;
-        load(RA, j + 2, swin);
-        compute(RB, j + 1);
     }
     if (missing && lane == 0) atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);
     __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) unit's loads

@@ -305,7 +305,7 @@ struct GroupedArgs {
 // tested for).  LDS: the zero block and two slots of kBalGroups * kBalPairs
 // token pairs (frag_lds_bytes(H, 2 kBalGroups kBalPairs)), 128 bytes of
 // counters (kBalWaves wave totals, then six slot words), the expert table
-// (kBalMaxU entries), then two scale windows per wave.
+// (kBalMaxU entries), then one scale window per wave.
 constexpr int kBalWaves = 8;
 // A token group of the balanced kernels: up to kBalPairs token pairs of one
 // routed expert, which one unit's MFMAs serve.  Groups of four pairs were
@@ -324,7 +324,7 @@ LPK_HD constexpr int bal_meta_off(int hidden) {
 }
 LPK_HD constexpr int bal_win_off(int hidden) { return bal_meta_off(hidden) + 128 + kBalMaxU * 32; }
 LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
-    return bal_win_off(hidden) + waves * 2 * 64 * 2 * window_steps;
+    return bal_win_off(hidden) + waves * 64 * 2 * window_steps;
 }
 
 // One-token down + combine (lp_moe_down_comb): one wave per pick.
