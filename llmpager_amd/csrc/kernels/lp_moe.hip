@@ -2026,10 +2026,23 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
 // multiply-adds of lp_moe_combine, then add the shared MLP's row (already
 // computed) as the combine does, so h is bit-identical to the down kernel
 // followed by the combine.  For tile_steps(inter) <= 16 (the host checks).
+//
+// With sh_fused (lp_moe_down_comb_rs only; top_k <= kCombWaves -
+// kCombShWaves, the shared MLP's group equal to the routed one) the last
+// two waves, otherwise idle, also take the shared MLP's down for the same
+// rows: its act row (already computed by the shared gate/up) staged once
+// into a fragment area of its own, wave q the q-th half of its K steps,
+// and the fold adds the two halves' row sums in place of the shared row.
 // ---------------------------------------------------------------------------
 namespace {
 
 __host__ __device__ constexpr int comb_part_off(int inter) { return (frag_lds_bytes(inter, kCombWaves) + 15) & ~15; }
+
+// The fused shared down's LDS (its fragment pair, then the halves' row sums)
+// after the routed part's: fragments, row sums, the scale windows (SL).
+__host__ __device__ constexpr int comb_sh_off(int inter, int ns, bool sl) {
+    return comb_part_off(inter) + kCombWaves * 64 + (sl ? kCombWaves * 64 * 2 * ((ns + 7) / 8 * 8) : 0);
+}
 
 template <int NS, int RS, bool SL>
 __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
@@ -2050,6 +2063,18 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
     const int p = min(max(gptr<int>(a.W.inv)[min(wave, L.top_k - 1)], 0), a.maxu - 1);
     const uint64_t eb = entry_of(a, p).blob;
     const uint64_t blob = wave < c ? eb : 0;
+    // the fused shared down (sh_fused, per-lane scales only): wave q of the
+    // last kCombShWaves takes steps [q hs, q hs + hs) of its tile
+    constexpr bool kSh = !SL && NS == 16;
+    const bool fused = kSh && a.sh_fused != 0;
+    const bool shw = fused && wave >= kCombWaves - kCombShWaves;
+    const int q = wave - (kCombWaves - kCombShWaves);
+    const int Is = fused ? L.shared_inter : 32;
+    const int Ss = tile_steps(Is), hs = (Ss + kCombShWaves - 1) / kCombShWaves;
+    uint8_t* sh_lds = lds + comb_sh_off(I, NS, SL);
+    const Frags Fs = frags_at(sh_lds, Is);
+    float* psh = reinterpret_cast<float*>(sh_lds + ((frag_lds_bytes(Is, 1) + 15) & ~15));  // [kCombShWaves][16]
+    if (fused) zero_block(Fs, threadIdx.x, blockDim.x);
     WRegs<NS, SL> D;
     if (blob != 0) {
         const WTile<RS> T = wtile<RS>(blob + L.down_off, H, I, n0);
@@ -2058,6 +2083,12 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
         Fw.lds = F.lds + wave * frag_pair_bytes(F.ngp);
         const float* actp = dptr<const float>(a.W.act);
         stage_rows(Fw, 1, [&](int) { return actp + (size_t)p * I; }, lane, 64);
+    } else if (shw) {
+        const WTile<RS> T = wtile<RS>(L.shared_blob + L.sh_down_off, H, Is, n0);
+        wload(D, T, q * hs, swin);
+        const float* sact = dptr<const float>(a.W.sh_act);
+        stage_rows(Fs, 1, [&](int) { return sact; }, (int)threadIdx.x - 64 * (kCombWaves - kCombShWaves),
+                   64 * kCombShWaves);
     }
     __builtin_amdgcn_s_waitcnt(0);  // the tile, its scale window and the staged row
     __syncthreads();
@@ -2070,6 +2101,16 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
         yv = tile_reduce(acc[0][0][0]);
     } else if (wave < c && lane == 0) {
         atomicOr(gptr_w<int>(a.W.meta) + 1, kErrMissingExpert);  // not resident: zero output
+    } else if (shw) {
+        // this half's steps only: the first half never reaches the tile's
+        // last step, whose lanes past the last sub-group take a zero scale
+        float acc[1][1][2] = {{{0.0f, 0.0f}}};
+        const ABase B[1] = {abase(Fs, 0, q * hs)};
+        WRegs<NS, SL> Rm[1] = {D};
+        if (q + 1 < kCombShWaves) Rm[0].lastok = true;
+        wmma(Rm, B, min(hs, Ss - q * hs), 1, acc);
+        const float ys = tile_reduce(acc[0][0][0]);
+        if (lane < 16) psh[q * 16 + lane] = ys;
     }
     if (lane < 16) part[wave * 16 + lane] = yv;
     __syncthreads();
@@ -2080,7 +2121,14 @@ __device__ __forceinline__ void down_comb_body(const GroupedArgs& a) {
         for (int j = 0; j < c; ++j) acc = __builtin_fmaf(w[j], part[j * 16 + threadIdx.x], acc);
         LP_GLOBAL float* h = gptr_w<float>(a.h);
         float v = h[row] + acc;
-        if (L.shared_blob) v = v + gptr<float>(a.W.sh_y)[row];
+        if (L.shared_blob) {
+            float sy;
+            if (fused)
+                sy = psh[threadIdx.x] + psh[16 + threadIdx.x];
+            else
+                sy = gptr<float>(a.W.sh_y)[row];
+            v = v + sy;
+        }
         h[row] = v;
     }
 }

@@ -297,7 +297,7 @@ struct GroupedArgs {
     int32_t T;
     int32_t pairs_cap;   // token pairs the dynamic LDS holds at once
     int32_t maxu;        // expert-table entries (balanced kernels)
-    int32_t pad0;
+    int32_t sh_fused;    // lp_moe_down_comb_rs: also the shared MLP's down (its act row in W.sh_act)
 };
 
 // Balanced decode gate/up (lp_moe_gateup_bal): one workgroup of kBalWaves
@@ -327,8 +327,10 @@ LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
     return bal_win_off(hidden) + waves * 64 * 2 * window_steps;
 }
 
-// One-token down + combine (lp_moe_down_comb): one wave per pick.
+// One-token down + combine (lp_moe_down_comb): one wave per pick; with the
+// shared MLP's down fused in, its two halves of K on the last two waves.
 constexpr int kCombWaves = 8;
+constexpr int kCombShWaves = 2;
 
 // Prefill grouped GEMM (lp_gemm.hip).
 constexpr int kGemmBM = 128;           // tokens per tile

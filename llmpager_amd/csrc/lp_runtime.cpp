@@ -1123,9 +1123,16 @@ static int comb_lds(int inter, int steps, bool sl) {
     return ((frag_lds_bytes(inter, kCombWaves) + 15) & ~15) + kCombWaves * 64 + kCombWaves * win;
 }
 
+// ... with the shared MLP's down fused in: its fragment pair and the two
+// halves' row sums after the routed part.
+static int comb_sh_lds(int inter, int steps, bool sl, int shared_inter) {
+    return comb_lds(inter, steps, sl) + ((frag_lds_bytes(shared_inter, 1) + 15) & ~15) + kCombShWaves * 64;
+}
+
 // The shared MLP through the grouped kernels: its own width, group and
 // regions, an expert table of consecutive token groups (written by dispatch).
-static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& ga, int T, lp_stream s) {
+static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& ga, int T, lp_stream s,
+                      bool with_down = true) {
     GroupedArgs gs = ga;
     gs.L.inter = d->shared_inter;
     gs.L.group = d->shared_group;
@@ -1137,7 +1144,7 @@ static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& 
     gs.W.perm = ga.W.sh_perm;
     gs.W.act = ga.W.sh_act;
     gs.W.y = ga.W.sh_y;
-    return grouped_ffn(c, gs, shared_entries(T), false, s);
+    return grouped_ffn(c, gs, shared_entries(T), false, s, with_down);
 }
 
 // The grouped expert kernels and the combine; the fragment images of x are
@@ -1209,12 +1216,21 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
                           (size_t)comb_lds(d->inter, Si, sl) <= c->max_lds;
         if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb)) return r;
         if (comb) {
-            if (d->shared_blob)
-                if (int r = shared_ffn(c, d, ga, T, s)) return r;
-            ga.maxu = std::min(d->top_k, d->experts);
             const Fn f = !sl ? kDownCombRs : Si <= 8 ? kDownComb : kDownComb16;
+            // the shared MLP's down on the comb kernel's idle waves: per-lane
+            // scales, the routed group, at most 2 x 16 steps, the LDS
+            size_t lds = (size_t)comb_lds(d->inter, Si, sl);
+            const size_t lds_sh = (size_t)comb_sh_lds(d->inter, Si, sl, d->shared_inter);
+            const bool fuse = d->shared_blob && f == kDownCombRs && d->top_k <= kCombWaves - kCombShWaves &&
+                              d->shared_group == d->group && tile_steps_host(d->shared_inter) <= 32 &&
+                              lds_sh <= c->max_lds;
+            if (d->shared_blob)
+                if (int r = shared_ffn(c, d, ga, T, s, !fuse)) return r;
+            ga.maxu = std::min(d->top_k, d->experts);
+            ga.sh_fused = fuse ? 1 : 0;
+            if (fuse) lds = lds_sh;
             return launch(c, f, dim3((unsigned)((d->hidden + kTileRows - 1) / kTileRows)), dim3(64 * kCombWaves),
-                          (size_t)comb_lds(d->inter, Si, sl), s, ga);
+                          lds, s, ga);
         }
     }
     if (d->shared_blob)

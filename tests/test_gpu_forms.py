@@ -5,7 +5,8 @@ through LDS windows for group 32, or read per lane for groups 64 and 128,
 the reference's own q4g64 among them), the balanced down as two (6 steps, up
 to 8), and a one-token batch takes down and combine in one launch
 (`lp_moe_down_comb`, up to 8 steps, `_comb16` for 9..16, `_comb_rs` with
-per-lane scales: groups 64 and 128, or scale rows not 16-byte aligned).  Each case names
+per-lane scales: groups 64 and 128, or scale rows not 16-byte aligned; it
+also takes a shared MLP's down on its idle waves).  Each case names
 the kernels it must reach; the per-kernel launch counts of the profiling
 mode show that it did.  Layer outputs within rel-L2 1e-3 on the delta
 h' - h, routing bit-exact given the device's logits (decode.rs:303-342)."""
@@ -38,10 +39,27 @@ FORMS = [
 ]
 
 
-@pytest.mark.parametrize("H,I,group,T,kernels", FORMS)
-def test_decode_kernel_forms(cuda, H, I, group, T, kernels):
-    E, k = 64, 8
-    L = DeviceLayer(cuda, H=H, I=I, E=E, k=k, group=group, seed=H + I + group + T)
+# One token with a shared MLP (config 5's layout): top-6 leaves two of the
+# one-token down + combine's waves idle, and they take the shared MLP's down
+# (its group the routed one's) — no lp_moe_down_wide launch; with another
+# group the shared down runs on its own.
+SHARED5 = dict(E=64, k=6, gating=lp.GATING_SIGMOID, renorm=True, routed_scaling=2.5, min_weight=0.0,
+               router_std=0.05)
+
+
+@pytest.mark.parametrize("H,I,group,T,kernels,extra", [f + ({},) for f in FORMS] + [
+    (2048, 1408, 32, 1, {"lp_moe_gateup_bal": 2, "lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 0},
+     dict(SHARED5, shared=(2816, 32))),
+    (2048, 1408, 32, 1, {"lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 1}, dict(SHARED5, shared=(2816, 64))),
+    (2048, 768, 64, 1, {"lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 0}, dict(SHARED5, shared=(1536, 64))),
+])
+def test_decode_kernel_forms(cuda, H, I, group, T, kernels, extra):
+    extra = dict(extra)
+    E, k = extra.pop("E", 64), extra.pop("k", 8)
+    bias = None
+    if extra.get("gating") == lp.GATING_SIGMOID:
+        bias = np.random.default_rng(T).standard_normal(E).astype(np.float32) * 0.05
+    L = DeviceLayer(cuda, H=H, I=I, E=E, k=k, group=group, seed=H + I + group + T, bias=bias, **extra)
     x = fp32_normal(T * H, 7 * T + group).reshape(T, H)
     h = fp32_normal(T * H, 11 * T + group).reshape(T, H)
     lay = lp.ws_layout(L.desc, T)
@@ -61,8 +79,10 @@ def test_decode_kernel_forms(cuda, H, I, group, T, kernels):
     assert L.layer.status(ws, T)[1] == 0
     for p in (ws, dx, dh):
         cuda.free_device(p)
-    assert all(n == 1 for n in counts.values()), counts
-    want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h, threads=8)
+    want_n = kernels if isinstance(kernels, dict) else dict.fromkeys(kernels, 1)
+    assert counts == want_n, counts
+    want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h, threads=8,
+                                             shared_blob=L.shared)
     L.free()
     assert np.array_equal(logits.view(np.uint32), wlog.view(np.uint32))
     assert np.array_equal(cnt, wcnt)
