@@ -39,7 +39,7 @@ EXPERT_BYTES = 3 * REGION_BYTES                      # 2,654,208
 ACT_BYTES = H * 2 + H * 4 * 2                      # x (bf16) + h read and write
 PEAK_GBPS = 8000.0
 # The grouped gate/up launch of a layer is the dominant kernel.
-GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal", "lp_moe_gateup_bal8", "lp_moe_gateup_bal_rs",
+GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal", "lp_moe_gateup_bal_sh", "lp_moe_gateup_bal8", "lp_moe_gateup_bal_rs",
                   "lp_moe_gateup_bal_rs8")
 # lp_moe_down_comb (one token) also folds the combine into the same launch
 DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide", "lp_moe_down_bal", "lp_moe_down_bal6", "lp_moe_down_comb",
@@ -52,7 +52,7 @@ CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-co
 # 262,144 KiB (factor 1.0); lp_moe_gateup_bal averages 91,995 and 918 KiB.
 # Re-measure whenever the kernel changes.
 TRAFFIC_B32 = {"lp_moe_gateup_bal": (2 * 91_995 + 918) * 1024}
-KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
+KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
            "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
            "lp_moe_combine")
 

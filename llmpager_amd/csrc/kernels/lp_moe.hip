@@ -580,11 +580,13 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
     }
 }
 
-// Top-k of token t with the candidate count per lane the expert count needs;
-// ids_l / cnt_l (may be null) receive LDS copies of the picks.
+// Top-k of token t with the candidate count per lane the expert count needs
+// (PMAX 2: at most 128 experts, the only form compiled); ids_l / cnt_l (may
+// be null) receive LDS copies of the picks.
+template <int PMAX = kMaxExperts / 64>
 __device__ __forceinline__ void topk_any(const RouteArgs& a, int t, float* sv, int* ids_l = nullptr,
                                          int* cnt_l = nullptr) {
-    if (a.L.experts <= 128)
+    if (PMAX == 2 || a.L.experts <= 128)
         topk_token<2>(a, t, sv, ids_l, cnt_l);
     else if (a.L.experts <= 256)
         topk_token<4>(a, t, sv, ids_l, cnt_l);
@@ -1095,7 +1097,8 @@ __device__ __forceinline__ bool last_arrival(int* cnt, int n, int* flag) {
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const RouteArgs a) {
+template <int PMAX>
+__device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
     constexpr int kTopkLds = 8 * kMaxExperts * 4;
     __shared__ __align__(16) uint8_t sm[kDispatchSmem > kTopkLds ? kDispatchSmem : kTopkLds];
     __shared__ __align__(16) float xs[kRouteXLds / 4];
@@ -1142,7 +1145,7 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     // one token block: the picks also go to LDS (token t = wave)
     const bool one = gridDim.y == 1;
     if (wave < nt)
-        topk_any(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts, one ? ids_l : nullptr,
+        topk_any<PMAX>(a, t0 + wave, reinterpret_cast<float*>(sm) + wave * kMaxExperts, one ? ids_l : nullptr,
                  one ? cnt_l : nullptr);
     if (one) {
         // ranked by this workgroup: no second arrival, and the tables come
@@ -1160,6 +1163,13 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
     dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l);
 }
 
+extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const RouteArgs a) { route_fused_body<kMaxExperts / 64>(a); }
+
+// The same for at most 128 experts: only that top-k form compiled, a kernel
+// of about half the code (the whole fused kernel outgrows the instruction
+// cache).
+extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused128(const RouteArgs a) { route_fused_body<2>(a); }
+
 // ---------------------------------------------------------------------------
 // Grouped expert projections.  A workgroup of W waves takes one work item =
 // (routed expert u, run of rows); every wave owns 16-row tiles of that run and
@@ -1175,6 +1185,20 @@ extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const Route
 // slot raises kErrMissingExpert in meta[1] and its outputs are zero.
 // ---------------------------------------------------------------------------
 namespace {
+
+__device__ __forceinline__ ExpertEntry entry_at(uint64_t table, int u) {
+    const LP_GLOBAL uint4* p = gptr<uint4>(table + (uint64_t)u * sizeof(ExpertEntry));
+    const uint4 lo = p[0], hi = p[1];
+    ExpertEntry x;
+    x.blob = (uint64_t)lo.x | ((uint64_t)lo.y << 32);
+    x.p0 = (int)lo.z;
+    x.ntok = (int)lo.w;
+    x.tok[0] = (int)hi.x;
+    x.tok[1] = (int)hi.y;
+    x.tok[2] = (int)hi.z;
+    x.tok[3] = (int)hi.w;
+    return x;
+}
 
 __device__ __forceinline__ ExpertEntry entry_of(const GroupedArgs& a, int u) {
     const LP_GLOBAL uint4* p = gptr<uint4>(a.W.et + (uint64_t)u * sizeof(ExpertEntry));
@@ -1389,6 +1413,7 @@ struct BalPlan {
     int tg0[2];        // first token group of the block (tokens kBalToks tg0 ..)
     int gq[2];         // token groups in the block (1..kBalGroups)
     int ns[2];         // tokens in the block (1..kBalToks kBalGroups)
+    int sh[2];         // the block is the shared MLP's (an entry of W.sh_et)
 
     // Unit un (uniform): slot s, row unit u, token group gl within the block.
     __device__ __forceinline__ void unit(int un, int& s, int& u, int& gl) const {
@@ -1401,20 +1426,24 @@ struct BalPlan {
 };
 static_assert(kBalGroups <= 4, "BalPlan::unit divides by at most 4");
 
-__device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, BalPlan& P) {
+// The routed entries (R units per token group) and, with SH and a.sh_maxu,
+// the shared MLP's entries after them (Rs units per group: its own width).
+template <bool SH = false>
+__device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int cols, int R, int Rs, BalPlan& P) {
     const int tid = (int)threadIdx.x, lane = lane_id(), wave = tid >> 6, W = (int)(blockDim.x >> 6);
-    const int maxu = a.maxu;
+    const int maxu = a.maxu, nent = SH ? a.maxu + a.sh_maxu : a.maxu;
     int* tot = reinterpret_cast<int*>(lds + bal_meta_off(cols));  // [kBalWaves] wave totals
     int* sl = tot + kBalWaves;  // [2][3]: entry, first token group, first unit of the blocks of lo and hi - 1
     ExpertEntry* ent = reinterpret_cast<ExpertEntry*>(lds + bal_meta_off(cols) + 128);
     if (tid < 6) sl[tid] = 0;
     int ng = 0;
-    if (tid < maxu) {
-        const ExpertEntry x = entry_of(a, tid);
+    const int Re = !SH || tid < maxu ? R : Rs;  // this entry's units per token group
+    if (tid < nent) {
+        const ExpertEntry x = !SH || tid < maxu ? entry_of(a, tid) : entry_at(a.W.sh_et, tid - maxu);
         ent[tid] = x;
         ng = (x.ntok + kBalToks - 1) / kBalToks;
     }
-    int inc = ng;
+    int inc = ng * Re;  // units, prefix-summed
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
         const int o = __shfl_up(inc, d, 64);
@@ -1422,27 +1451,26 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
     }
     if (lane == 63) tot[wave] = inc;
     __syncthreads();
-    int before = 0, V = 0;
+    int before = 0, N = 0;
     for (int w = 0; w < W; ++w) {
         const int t = tot[w];
         before += w < wave ? t : 0;
-        V += t;
+        N += t;
     }
-    const int pre = before + inc - ng;  // this entry's first token group
-    const long N = (long)V * R;
-    P.lo = (int)(N * blockIdx.x / gridDim.x);
-    P.hi = (int)(N * (blockIdx.x + 1) / gridDim.x);
+    const int u0 = before + inc - ng * Re;  // this entry's first unit
+    P.lo = (int)((long)N * blockIdx.x / gridDim.x);
+    P.hi = (int)((long)N * (blockIdx.x + 1) / gridDim.x);
     if (P.lo >= P.hi) return false;
-    if (tid < maxu && ng > 0) {
-        const int u0 = R * pre, u1 = R * (pre + ng);  // the entry's units
+    if (tid < nent && ng > 0) {
+        const int u1 = u0 + Re * ng;  // the entry's units
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int un = e == 0 ? P.lo : P.hi - 1;
             if (u0 <= un && un < u1) {
-                const int q = (un - u0) / (R * kBalGroups);
+                const int q = (un - u0) / (Re * kBalGroups);
                 sl[3 * e] = tid;
                 sl[3 * e + 1] = q * kBalGroups;
-                sl[3 * e + 2] = u0 + q * R * kBalGroups;
+                sl[3 * e + 2] = u0 + q * Re * kBalGroups;
             }
         }
     }
@@ -1457,6 +1485,7 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
         const int ngx = (P.x[s].ntok + kBalToks - 1) / kBalToks;
         P.gq[s] = min(kBalGroups, ngx - P.tg0[s]);
         P.ns[s] = min(kBalToks * kBalGroups, P.x[s].ntok - kBalToks * P.tg0[s]);
+        P.sh[s] = SH && sl[3 * q] >= maxu;
     }
     return true;
 }
@@ -1491,7 +1520,7 @@ __device__ __forceinline__ void bal_sums(const float (&acc)[1][kBalPairs][2], fl
         Y = 0.0f;
 }
 
-template <int NS, int RS, bool SL>
+template <int NS, int RS, bool SL, bool SH = false>
 __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const LayerView& L = a.L;
@@ -1501,29 +1530,39 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int W = (int)(blockDim.x >> 6);
     const int R = (I + 7) >> 3;
+    const int Ish = SH && a.sh_maxu ? L.shared_inter : I;  // the shared MLP's entries (SH) have their own width
     const Frags F = frags_at(lds, H);
     zero_block(F, threadIdx.x, blockDim.x);
     BalPlan P;
-    if (!bal_plan(a, lds, H, R, P)) return;
+    if (!bal_plan<SH>(a, lds, H, R, (Ish + 7) >> 3, P)) return;
     const int lo = P.lo, hi = P.hi;
-    // the two slots' blob, dispatch position and token count of the block
+    // the two slots' blob, dispatch position and token count of the block,
+    // and (a shared MLP block) its width, regions and act rows
     uint64_t sblob[2];
-    int sp0[2], snt[2];
-    const LP_GLOBAL int* perm = gptr<int>(a.W.perm);
+    int sp0[2], snt[2], sI[2];
+    uint32_t sgo[2], suo[2];
     const uint64_t xf = a.W.xd, ib = (uint64_t)dimage_bytes(H);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const ExpertEntry x = P.x[s];
         const int tb = kBalToks * P.tg0[s];
+        const bool sh = SH && P.sh[s] != 0;
         sblob[s] = x.blob;
         sp0[s] = x.p0 + tb;
         snt[s] = x.ntok - tb;
+        sI[s] = sh ? Ish : I;
+        sgo[s] = (uint32_t)(sh ? L.sh_gate_off : L.gate_off);
+        suo[s] = (uint32_t)(sh ? L.sh_up_off : L.up_off);
         if (s < P.nslot) {
             Frags Fs = F;
             Fs.lds = F.lds + kBalGroups * kBalPairs * s * frag_pair_bytes(F.ngp);
+            // shared entries hold consecutive tokens (all in tok[] for up to
+            // kEntryToks; a routed entry's later ones through perm)
+            const LP_GLOBAL int* perm = gptr<int>(sh ? a.W.sh_perm : a.W.perm);
+            const int kk = sh ? 1 : k;
             issue_images(Fs, P.ns[s], [&](int t) {
                 const int i = tb + t;
-                const int tok = i < kEntryToks ? entry_tok(x, i) : perm[x.p0 + i] / k;
+                const int tok = i < kEntryToks ? entry_tok(x, i) : perm[x.p0 + i] / kk;
                 return xf + (uint64_t)tok * ib;
             });
         }
@@ -1540,8 +1579,8 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
         const bool valid = j < J && blob != 0;
-        const WTile<RS> T =
-            wtile_gu<RS>(blob, valid, dummy, (uint32_t)L.gate_off, (uint32_t)L.up_off, I, H, 8 * u);
+        const WTile<RS> T = wtile_gu<RS>(blob, valid, dummy, s == 0 ? sgo[0] : sgo[1], s == 0 ? suo[0] : suo[1],
+                                         s == 0 ? sI[0] : sI[1], H, 8 * u);
         wload(B, T, 0, win);
     };
     // act through a raw buffer: a lane with nothing to store writes at its end,
@@ -1549,6 +1588,9 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
     const uint32_t act_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)I * 4u;
     const __amdgpu_buffer_rsrc_t act_rs =
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.act), (short)0, (int)act_bytes, kBufferWord3);
+    const uint32_t sh_bytes = SH && a.sh_maxu ? (uint32_t)a.T * (uint32_t)Ish * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t sh_rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.sh_act), (short)0, (int)sh_bytes, kBufferWord3);
     bool missing = false;
     auto compute = [&](const WRegs<NS, SL>& B, int j) {
         int s, ru, gl;
@@ -1587,9 +1629,12 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         const int t = (hy ? 4 : 0) + quad_row_tok(lane >> 4);
         const int row = r0 + (lane & 7);
         const float v = qblob == 0 ? 0.0f : g / (1.0f + expf(-g)) * u;
-        const bool st = row < I && t < qnt;
-        const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)I + (uint32_t)row) * 4u : act_bytes;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), act_rs, (int)off, 0, 0);
+        const bool shb = SH && (s == 0 ? P.sh[0] : P.sh[1]) != 0;  // uniform
+        const int Iq = shb ? Ish : I;
+        const bool st = row < Iq && t < qnt;
+        const uint32_t lim = shb ? sh_bytes : act_bytes;
+        const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)Iq + (uint32_t)row) * 4u : lim;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), shb ? sh_rs : act_rs, (int)off, 0, 0);
     };
     WRegs<NS, SL> RA;
     load(RA, 0, swin);
@@ -1639,7 +1684,7 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     const Frags F = frags_at(lds, I);
     zero_block(F, threadIdx.x, blockDim.x);
     BalPlan P;
-    if (!bal_plan(a, lds, I, R, P)) return;
+    if (!bal_plan(a, lds, I, R, R, P)) return;
     const int lo = P.lo, hi = P.hi;
     uint64_t sblob[2];
     int sp0[2], snt[2];
@@ -1856,6 +1901,14 @@ lp_moe_gateup(const GroupedArgs a) {
 extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
 lp_moe_gateup_bal(const GroupedArgs a) {
     gateup_bal_body<16, 0, true>(a);
+}
+
+// lp_moe_gateup_bal with the shared MLP's entries (W.sh_et, a.sh_maxu of
+// them, its own width and regions, act rows into W.sh_act) planned after
+// the routed ones: one launch for both.
+extern "C" __global__ void __launch_bounds__(64 * kBalWaves) __attribute__((amdgpu_waves_per_eu(2)))
+lp_moe_gateup_bal_sh(const GroupedArgs a) {
+    gateup_bal_body<16, 0, true, true>(a);
 }
 
 // The same with tiles of at most 8 steps (hidden <= 1024), and for groups

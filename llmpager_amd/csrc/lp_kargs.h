@@ -298,6 +298,8 @@ struct GroupedArgs {
     int32_t pairs_cap;   // token pairs the dynamic LDS holds at once
     int32_t maxu;        // expert-table entries (balanced kernels)
     int32_t sh_fused;    // lp_moe_down_comb_rs: also the shared MLP's down (its act row in W.sh_act)
+    int32_t sh_maxu;     // balanced gate/up: the shared MLP's W.sh_et entries taken after the routed ones
+    int32_t pad0;
 };
 
 // Balanced decode gate/up (lp_moe_gateup_bal): one workgroup of kBalWaves

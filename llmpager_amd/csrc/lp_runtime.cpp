@@ -76,10 +76,12 @@ enum Fn {
     kGemmRouter,
     kDispatch,
     kRouteFused,
+    kRouteFused128,
     kGateupBal,
     kGateupBal8,
     kGateupBalRs,
     kGateupBalRs8,
+    kGateupBalSh,
     kDownBal,
     kDownBal6,
     kDownComb,
@@ -122,8 +124,10 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_moe.hsaco", "lp_moe_disp_count"}, {"lp_moe.hsaco", "lp_moe_disp_scan"},
     {"lp_moe.hsaco", "lp_moe_disp_scatter"}, {"lp_gemm.hsaco", "lp_gemm_router"},
     {"lp_moe.hsaco", "lp_moe_dispatch"},   {"lp_moe.hsaco", "lp_moe_route_fused"},
+    {"lp_moe.hsaco", "lp_moe_route_fused128"},
     {"lp_moe.hsaco", "lp_moe_gateup_bal"},  {"lp_moe.hsaco", "lp_moe_gateup_bal8"},
     {"lp_moe.hsaco", "lp_moe_gateup_bal_rs"},  {"lp_moe.hsaco", "lp_moe_gateup_bal_rs8"},
+    {"lp_moe.hsaco", "lp_moe_gateup_bal_sh"},
     {"lp_moe.hsaco", "lp_moe_down_bal"},   {"lp_moe.hsaco", "lp_moe_down_bal6"},
     {"lp_moe.hsaco", "lp_moe_down_comb"},  {"lp_moe.hsaco", "lp_moe_down_comb16"},
     {"lp_moe.hsaco", "lp_moe_down_comb_rs"},
@@ -337,7 +341,7 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     {
         // the loaded code objects must take the balanced kernels' fixed
         // workgroup size (their launch bound)
-        for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kDownBal, kDownBal6, kDownComb,
+        for (Fn f : {kGateupBal, kGateupBal8, kGateupBalRs, kGateupBalRs8, kGateupBalSh, kDownBal, kDownBal6, kDownComb,
                      kDownComb16, kDownCombRs}) {
             const int need = 64 * (f == kDownComb || f == kDownComb16 || f == kDownCombRs ? kCombWaves : kBalWaves);
             int mt = 0;
@@ -1020,7 +1024,7 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
     ra.sync = reinterpret_cast<uint64_t>(c->sync) + (uint64_t)slot * kSyncWords * 4;
     dim3 g((unsigned)((d->experts + 8 * kRouteEPW - 1) / (8 * kRouteEPW)),
            (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
-    return launch(c, kRouteFused, g, dim3(512), 0, s, ra);
+    return launch(c, d->experts <= 128 ? kRouteFused128 : kRouteFused, g, dim3(512), 0, s, ra);
 }
 
 int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, int T,
@@ -1045,9 +1049,16 @@ static bool gateup_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int H = ga.L.hidden, pairs = ga.T * ga.L.top_k;
     const int maxv = std::min(pairs, (pairs + (kBalToks - 1) * maxu) / kBalToks);
     const int nw = tile_steps_host(H) > 8 ? 16 : 8;
-    return tile_steps_host(H) <= kGateupChunk && maxu <= kBalMaxU && maxv <= c->cus &&
+    // with the shared MLP's entries (one token group each): at most the
+    // grid's worth of units of the shorter width per workgroup, so that a
+    // range still touches at most two blocks
+    const int nsh = ga.sh_maxu;
+    const long R = (ga.L.inter + 7) / 8, Rs = nsh ? (ga.L.shared_inter + 7) / 8 : R;
+    const bool units_ok = (long)maxv * R + (long)nsh * Rs <= (long)c->cus * std::min(R, Rs);
+    return tile_steps_host(H) <= kGateupChunk && maxu + nsh <= kBalMaxU && maxv <= c->cus && units_ok &&
            (size_t)bal_lds_bytes(H, nw, kBalWaves) <= c->max_lds && ga.L.slot_span < (1ull << 31) &&
-           (uint64_t)pairs * ga.L.inter * 4 < (1ull << 31);
+           (uint64_t)pairs * ga.L.inter * 4 < (1ull << 31) &&
+           (uint64_t)ga.T * (nsh ? ga.L.shared_inter : 0) * 4 < (1ull << 31);
 }
 
 // Whether lp_moe_down_bal(6) takes the down projection of ga's routed
@@ -1070,10 +1081,12 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
 // balanced gate/up takes the shared MLP too, as ceil(T / 4) one-group
 // entries of one blob, whose weight rows neighbouring workgroups of one XCD
 // read together).
-static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s,
-                       bool with_down = true) {
+// The grouped down projection of ga's entries (maxu): balanced for routed
+// decode batches when it can, else the one-shot kernels.
+static int grouped_down(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s) {
     GroupedArgs ga = ga0;
     ga.maxu = maxu;
+    ga.sh_maxu = 0;
     const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
     auto pick_w = [&](int rows, int tw) {
         for (int w = 4; w > 1; w >>= 1)
@@ -1081,24 +1094,6 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
                 return w;
         return 1;
     };
-    if (c->gateup_bal && gateup_balanced(c, ga, maxu)) {
-        const bool t16 = tile_steps_host(H) > 8;
-        const int nw = t16 ? 16 : 8;
-        const Fn f = scales_in_lds(ga.L.group, H) ? (t16 ? kGateupBal : kGateupBal8)
-                                                  : (t16 ? kGateupBalRs : kGateupBalRs8);
-        if (int r = launch(c, f, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
-                           (size_t)bal_lds_bytes(H, nw, kBalWaves), s, ga))
-            return r;
-    } else {
-        const int w = pick_w(I, 1);
-        const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
-        const int win = tile_steps_host(H) <= kGateupChunk && scales_in_lds(ga.L.group, H)
-                            ? scale_window_lds(w, 2, kGateupChunk) : 0;
-        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w),
-                           (size_t)(frag_lds_bytes(H, cap) + win), s, ga))
-            return r;
-    }
-    if (!with_down) return 0;
     const int steps = tile_steps_host(I);
     if (routed && c->gateup_bal && down_balanced(c, ga, maxu)) {
         return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
@@ -1112,6 +1107,52 @@ static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed,
     const int win = steps <= kDownWideChunk && scales_in_lds(ga.L.group, I) ? scale_window_lds(w, tw, ns) : 0;
     return launch(c, f, dim3((unsigned)(maxu * chunks)), dim3(64 * w), (size_t)(frag_lds_bytes(I, cap) + win),
                   s, ga);
+}
+
+
+// sh_maxu > 0 (routed only): the balanced gate/up also takes the shared
+// MLP's entries when it can; *sh_done says whether it did.
+static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s,
+                       bool with_down = true, int sh_maxu = 0, bool* sh_done = nullptr) {
+    GroupedArgs ga = ga0;
+    ga.maxu = maxu;
+    ga.sh_maxu = 0;
+    if (sh_done) *sh_done = false;
+    // (the 16-step form with scales in LDS windows only: its own kernel)
+    if (sh_maxu > 0 && c->gateup_bal && tile_steps_host(ga.L.hidden) > 8 && scales_in_lds(ga.L.group, ga.L.hidden)) {
+        GroupedArgs gs = ga;
+        gs.sh_maxu = sh_maxu;
+        if (gateup_balanced(c, gs, maxu)) ga.sh_maxu = sh_maxu;
+    }
+    const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
+    auto pick_w = [&](int rows, int tw) {
+        for (int w = 4; w > 1; w >>= 1)
+            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= 2L * c->cus)
+                return w;
+        return 1;
+    };
+    if (c->gateup_bal && gateup_balanced(c, ga, maxu)) {
+        const bool t16 = tile_steps_host(H) > 8;
+        const int nw = t16 ? 16 : 8;
+        const Fn f = ga.sh_maxu ? kGateupBalSh
+                     : scales_in_lds(ga.L.group, H) ? (t16 ? kGateupBal : kGateupBal8)
+                                                    : (t16 ? kGateupBalRs : kGateupBalRs8);
+        if (int r = launch(c, f, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
+                           (size_t)bal_lds_bytes(H, nw, kBalWaves), s, ga))
+            return r;
+        if (sh_done) *sh_done = ga.sh_maxu > 0;
+        ga.sh_maxu = 0;
+    } else {
+        const int w = pick_w(I, 1);
+        const int chunks = (I + kTileRows * w - 1) / (kTileRows * w);
+        const int win = tile_steps_host(H) <= kGateupChunk && scales_in_lds(ga.L.group, H)
+                            ? scale_window_lds(w, 2, kGateupChunk) : 0;
+        if (int r = launch(c, kGateup, dim3((unsigned)(maxu * chunks)), dim3(64 * w),
+                           (size_t)(frag_lds_bytes(H, cap) + win), s, ga))
+            return r;
+    }
+    if (!with_down) return 0;
+    return grouped_down(c, ga0, maxu, routed, s);
 }
 
 // LDS of lp_moe_down_comb(16, _rs): the picks' fragment pairs, their row
@@ -1132,7 +1173,7 @@ static int comb_sh_lds(int inter, int steps, bool sl, int shared_inter) {
 // The shared MLP through the grouped kernels: its own width, group and
 // regions, an expert table of consecutive token groups (written by dispatch).
 static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& ga, int T, lp_stream s,
-                      bool with_down = true) {
+                      bool with_down = true, bool with_gateup = true) {
     GroupedArgs gs = ga;
     gs.L.inter = d->shared_inter;
     gs.L.group = d->shared_group;
@@ -1144,6 +1185,11 @@ static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& 
     gs.W.perm = ga.W.sh_perm;
     gs.W.act = ga.W.sh_act;
     gs.W.y = ga.W.sh_y;
+    if (!with_gateup) {
+        // gate/up already done with the routed experts': the down alone
+        if (!with_down) return 0;
+        return grouped_down(c, gs, shared_entries(T), false, s);
+    }
     return grouped_ffn(c, gs, shared_entries(T), false, s, with_down);
 }
 
@@ -1182,6 +1228,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     if (lds_for(1) > c->max_lds)
         return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
     ga.pairs_cap = cap;
+    bool sh_gu = false;  // the shared MLP's gate/up done by the routed launch
     if (use_gemm(d, T)) {
         if ((size_t)kGemmLds > c->max_lds) return fail(LP_E_UNSUPPORTED, "GEMM stages exceed the LDS");
         // the GEMM loads address images and weights as 32-bit offsets from a base
@@ -1214,7 +1261,11 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         const bool sl = scales_in_lds(d->group, d->inter);
         const bool comb = T == 1 && d->top_k <= kCombWaves && Si <= 16 &&
                           (size_t)comb_lds(d->inter, Si, sl) <= c->max_lds;
-        if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb)) return r;
+        // the shared MLP's gate/up rides on the routed balanced launch when
+        // the groups agree (sh_gu: it did)
+        const int shm = d->shared_blob && d->shared_group == d->group ? shared_entries(T) : 0;
+        if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb, shm, &sh_gu))
+            return r;
         if (comb) {
             const Fn f = !sl ? kDownCombRs : Si <= 8 ? kDownComb : kDownComb16;
             // the shared MLP's down on the comb kernel's idle waves: per-lane
@@ -1225,7 +1276,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
                               d->shared_group == d->group && tile_steps_host(d->shared_inter) <= 32 &&
                               lds_sh <= c->max_lds;
             if (d->shared_blob)
-                if (int r = shared_ffn(c, d, ga, T, s, !fuse)) return r;
+                if (int r = shared_ffn(c, d, ga, T, s, !fuse, !sh_gu)) return r;
             ga.maxu = std::min(d->top_k, d->experts);
             ga.sh_fused = fuse ? 1 : 0;
             if (fuse) lds = lds_sh;
@@ -1234,7 +1285,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         }
     }
     if (d->shared_blob)
-        if (int r = shared_ffn(c, d, ga, T, s)) return r;
+        if (int r = shared_ffn(c, d, ga, T, s, true, !sh_gu)) return r;
     return launch(c, kCombine, dim3((unsigned)((d->hidden + 1023) / 1024), (unsigned)T), dim3(256), 0,
                   s, ga);
 }

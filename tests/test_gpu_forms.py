@@ -39,17 +39,19 @@ FORMS = [
 ]
 
 
-# One token with a shared MLP (config 5's layout): top-6 leaves two of the
-# one-token down + combine's waves idle, and they take the shared MLP's down
-# (its group the routed one's) — no lp_moe_down_wide launch; with another
-# group the shared down runs on its own.
+# One token with a shared MLP (config 5's layout): its gate/up rides on the
+# routed experts' balanced launch, and top-6 leaves two of the one-token
+# down + combine's waves idle, which take its down (its group the routed
+# one's) — one gate/up launch, no lp_moe_down_wide; with another group the
+# shared MLP runs on its own.
 SHARED5 = dict(E=64, k=6, gating=lp.GATING_SIGMOID, renorm=True, routed_scaling=2.5, min_weight=0.0,
                router_std=0.05)
 
 
 @pytest.mark.parametrize("H,I,group,T,kernels,extra", [f + ({},) for f in FORMS] + [
-    (2048, 1408, 32, 1, {"lp_moe_gateup_bal": 2, "lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 0},
-     dict(SHARED5, shared=(2816, 32))),
+    (2048, 1408, 32, 1, {"lp_moe_gateup_bal_sh": 1, "lp_moe_gateup_bal": 0, "lp_moe_down_comb_rs": 1,
+                         "lp_moe_down_wide": 0}, dict(SHARED5, shared=(2816, 32))),
+    (2048, 1408, 32, 16, {"lp_moe_gateup_bal_sh": 1, "lp_moe_gateup_bal": 0}, dict(SHARED5, shared=(2816, 32))),
     (2048, 1408, 32, 1, {"lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 1}, dict(SHARED5, shared=(2816, 64))),
     (2048, 768, 64, 1, {"lp_moe_down_comb_rs": 1, "lp_moe_down_wide": 0}, dict(SHARED5, shared=(1536, 64))),
 ])
