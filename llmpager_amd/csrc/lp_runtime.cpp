@@ -1088,9 +1088,14 @@ static int grouped_down(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed
     ga.maxu = maxu;
     ga.sh_maxu = 0;
     const int H = ga.L.hidden, I = ga.L.inter, cap = ga.pairs_cap;
+    // Waves per workgroup: the most that still give every CU two workgroups
+    // (routed) or one (the shared MLP: its few entries' act rows, staged by
+    // each workgroup, cost more than the lost occupancy: a config-5 layer of
+    // 16 tokens took 98.9 us with 2 waves, 102.2 with 1 and 100.0 with 4).
+    const long want = routed ? 2L * c->cus : (long)c->cus;
     auto pick_w = [&](int rows, int tw) {
         for (int w = 4; w > 1; w >>= 1)
-            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= 2L * c->cus)
+            if ((long)maxu * ((rows + kTileRows * w * tw - 1) / (kTileRows * w * tw)) >= want)
                 return w;
         return 1;
     };
