@@ -1490,32 +1490,32 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
     return true;
 }
 
-// The MFMAs of one balanced unit: np (1..kBalPairs, uniform) picks a
-// straight-line form for exactly that many token pairs.
-template <int NS, bool SL>
-__device__ __forceinline__ void bal_wmma(const WRegs<NS, SL> (&R)[1], const ABase (&B)[kBalPairs], int rem, int np,
-                                         float (&acc)[1][kBalPairs][2]) {
+// The MFMAs of one balanced unit of M weight tiles: np (1..kBalPairs,
+// uniform) picks a straight-line form for exactly that many token pairs.
+template <int NS, bool SL, int M>
+__device__ __forceinline__ void bal_wmma(const WRegs<NS, SL> (&R)[M], const ABase (&B)[kBalPairs], int rem, int np,
+                                         float (&acc)[M][kBalPairs][2]) {
     static_assert(kBalPairs == 2 || kBalPairs == 4, "one form per pair count");
     if constexpr (kBalPairs == 2) {
-        if (np == 1) wmma<NS, SL, kBalPairs, 1, 1>(R, B, rem, np, acc);
-        else wmma<NS, SL, kBalPairs, 1, 2>(R, B, rem, np, acc);
+        if (np == 1) wmma<NS, SL, kBalPairs, M, 1>(R, B, rem, np, acc);
+        else wmma<NS, SL, kBalPairs, M, 2>(R, B, rem, np, acc);
     } else {
         switch (np) {
-            case 1: wmma<NS, SL, kBalPairs, 1, 1>(R, B, rem, np, acc); break;
-            case 2: wmma<NS, SL, kBalPairs, 1, 2>(R, B, rem, np, acc); break;
-            case 3: wmma<NS, SL, kBalPairs, 1, 3>(R, B, rem, np, acc); break;
-            default: wmma<NS, SL, kBalPairs, 1, 4>(R, B, rem, np, acc); break;
+            case 1: wmma<NS, SL, kBalPairs, M, 1>(R, B, rem, np, acc); break;
+            case 2: wmma<NS, SL, kBalPairs, M, 2>(R, B, rem, np, acc); break;
+            case 3: wmma<NS, SL, kBalPairs, M, 3>(R, B, rem, np, acc); break;
+            default: wmma<NS, SL, kBalPairs, M, 4>(R, B, rem, np, acc); break;
         }
     }
 }
 
-// The token sums over K of a balanced unit's kBalPairs pairs (acc[0][p][h] =
+// The token sums over K of a balanced tile's kBalPairs pairs (acc[p][h] =
 // lane partials of token 2p + h): row r of X holds token quad_row_tok(r), row
 // r of Y token 4 + quad_row_tok(r) (zero with two pairs).
-__device__ __forceinline__ void bal_sums(const float (&acc)[1][kBalPairs][2], float& X, float& Y) {
-    X = quad_rows(pair_rows(acc[0][0][0], acc[0][0][1]), pair_rows(acc[0][1][0], acc[0][1][1]));
+__device__ __forceinline__ void bal_sums(const float (&acc)[kBalPairs][2], float& X, float& Y) {
+    X = quad_rows(pair_rows(acc[0][0], acc[0][1]), pair_rows(acc[1][0], acc[1][1]));
     if constexpr (kBalPairs == 4)
-        Y = quad_rows(pair_rows(acc[0][2][0], acc[0][2][1]), pair_rows(acc[0][3][0], acc[0][3][1]));
+        Y = quad_rows(pair_rows(acc[2][0], acc[2][1]), pair_rows(acc[3][0], acc[3][1]));
     else
         Y = 0.0f;
 }
@@ -1621,7 +1621,7 @@ __device__ __forceinline__ void gateup_bal_body(const GroupedArgs& a) {
         // finish X's tokens, lanes n >= 8 Y's (their gate brought over by a
         // rotation of the row by 8): one SiLU and one store per lane.
         float X, Y;
-        bal_sums(acc, X, Y);
+        bal_sums(acc[0], X, Y);
         const float rX = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(X), 0x128, 0xf, 0xf, false));
         const float rY = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(Y), 0x128, 0xf, 0xf, false));
         const bool hy = (lane & 15) >= 8;
@@ -1680,7 +1680,8 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     const int H = L.hidden, I = L.inter, k = L.top_k;
     const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int W = (int)(blockDim.x >> 6);
-    const int R = (H + 15) >> 4;
+    constexpr int TW = kDownBalTiles;  // row tiles per unit
+    const int R = (H + 16 * TW - 1) / (16 * TW);
     const Frags F = frags_at(lds, I);
     zero_block(F, threadIdx.x, blockDim.x);
     BalPlan P;
@@ -1707,58 +1708,70 @@ __device__ __forceinline__ void down_bal_body(const GroupedArgs& a) {
     const int Sx = tile_steps(I);
     const uint64_t dummy = L.router_w;
     const uint32_t swin = lds_addr_of(lds) + (uint32_t)bal_win_off(I) +
-                          (uint32_t)(wave * scale_window_bytes<NS>());
-    auto load = [&](WRegs<NS, SL>& B, int j, uint32_t win) {
+                          (uint32_t)(TW * wave * scale_window_bytes<NS>());
+    auto load = [&](WRegs<NS, SL> (&B)[TW], int j, uint32_t win) {
         int s, u, gl;
         P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t blob = s == 0 ? sblob[0] : sblob[1];
         const bool valid = j < J && blob != 0;
-        const WTile<RS> T = wtile_dn<RS>(blob, valid, dummy, (uint32_t)L.down_off, H, I, 16 * u);
-        wload(B, T, 0, win);
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            const WTile<RS> T = wtile_dn<RS>(blob, valid, dummy, (uint32_t)L.down_off, H, I, 16 * (TW * u + t));
+            wload(B[t], T, 0, win + (uint32_t)(t * scale_window_bytes<NS>()));
+        }
     };
     const uint32_t y_bytes = (uint32_t)a.T * (uint32_t)k * (uint32_t)H * 4u;
     const __amdgpu_buffer_rsrc_t y_rs =
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a.W.y), (short)0, (int)y_bytes, kBufferWord3);
     bool missing = false;
-    auto compute = [&](const WRegs<NS, SL>& B, int j) {
+    auto compute = [&](const WRegs<NS, SL> (&B)[TW], int j) {
         int s, u, gl;
         P.unit(lo + wave + W * j, s, u, gl);
         const uint64_t qblob = s == 0 ? sblob[0] : sblob[1];
         const int qp0 = (s == 0 ? sp0[0] : sp0[1]) + kBalToks * gl;
         const int qnt = min(kBalToks, (s == 0 ? snt[0] : snt[1]) - kBalToks * gl);
         const int np = (qnt + 1) >> 1;
-        const int row = 16 * u + (lane & 15);
-        const bool out = row < H;
         missing |= qblob == 0;  // not resident: zero outputs, flag raised after the loop
-        WRegs<NS, SL> Rm[1] = {B};
-        if constexpr (SL) {
-            // read the scale window only once B's first nibble load has landed,
-            // and with it the window copies issued before that load
-            uint32_t z;
-            asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B.w[0].x));
-            Rm[0].sbase += z;
-        }
-        float acc[1][kBalPairs][2];
+        WRegs<NS, SL> Rm[TW];
 #pragma unroll
-        for (int p = 0; p < kBalPairs; ++p) acc[0][p][0] = acc[0][p][1] = 0.0f;
+        for (int t = 0; t < TW; ++t) {
+            Rm[t] = B[t];
+            if constexpr (SL) {
+                // read the scale window only once the tile's first nibble load
+                // has landed, and with it the window copies issued before it
+                uint32_t z;
+                asm("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(B[t].w[0].x));
+                Rm[t].sbase += z;
+            }
+        }
+        float acc[TW][kBalPairs][2];
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int p = 0; p < kBalPairs; ++p) acc[t][p][0] = acc[t][p][1] = 0.0f;
         ABase Bs[kBalPairs];
 #pragma unroll
         for (int p = 0; p < kBalPairs; ++p) Bs[p] = abase(F, kBalPairs * (kBalGroups * s + gl) + p, 0);
         bal_wmma(Rm, Bs, Sx, np, acc);
-        // the tokens' sums over K (bal_sums): one store per lane and group of
-        // four tokens
-        float X, Y;
-        bal_sums(acc, X, Y);
+        // the tokens' sums over K (bal_sums): one store per lane, tile and
+        // group of four tokens
 #pragma unroll
-        for (int h = 0; h < kBalPairs / 2; ++h) {
-            const int t = 4 * h + quad_row_tok(lane >> 4);
-            const float v = qblob == 0 ? 0.0f : h ? Y : X;
-            const bool st = out && t < qnt;
-            const uint32_t off = st ? ((uint32_t)(qp0 + t) * (uint32_t)H + (uint32_t)row) * 4u : y_bytes;
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, (int)off, 0, 0);
+        for (int t = 0; t < TW; ++t) {
+            float X, Y;
+            bal_sums(acc[t], X, Y);
+            const int row = 16 * (TW * u + t) + (lane & 15);
+            const bool out = row < H;
+#pragma unroll
+            for (int h = 0; h < kBalPairs / 2; ++h) {
+                const int tk = 4 * h + quad_row_tok(lane >> 4);
+                const float v = qblob == 0 ? 0.0f : h ? Y : X;
+                const bool st = out && tk < qnt;
+                const uint32_t off = st ? ((uint32_t)(qp0 + tk) * (uint32_t)H + (uint32_t)row) * 4u : y_bytes;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, (int)off, 0, 0);
+            }
         }
     };
-    WRegs<NS, SL> RA;
+    WRegs<NS, SL> RA[TW];
     load(RA, 0, swin);
     __builtin_amdgcn_s_waitcnt(0);  // the first unit has landed
     __syncthreads();                // and the staged act rows are in place

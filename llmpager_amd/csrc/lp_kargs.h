@@ -320,6 +320,10 @@ constexpr int kBalToks = 2 * kBalPairs;
 // (neighbouring units read the same weight rows for different groups).
 constexpr int kBalGroups = 2;
 constexpr int kBalMaxU = 64 * kBalWaves;
+// Row tiles (16 rows of down, all of K) in one unit of the balanced down.
+// Two (12 KB of nibbles per unit at inter 768, half the units) measured
+// slower: 26.3 against 25.1 us at 32 tokens.
+constexpr int kDownBalTiles = 1;
 static_assert(4 * kBalWaves + 24 <= 128, "bal_plan's counters fit their 128 bytes");
 LPK_HD constexpr int bal_meta_off(int hidden) {
     return (frag_lds_bytes(hidden, 2 * kBalGroups * kBalPairs) + 15) & ~15;

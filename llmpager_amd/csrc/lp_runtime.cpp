@@ -1070,7 +1070,7 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
     const int maxv = std::min(pairs, (pairs + (kBalToks - 1) * maxu) / kBalToks);
     return pairs >= 32 && tile_steps_host(I) <= 8 && scales_in_lds(ga.L.group, I) && maxu <= kBalMaxU &&
            maxv <= c->cus &&
-           (size_t)bal_lds_bytes(I, 8, kBalWaves) <= c->max_lds &&
+           (size_t)bal_lds_bytes(I, 8 * kDownBalTiles, kBalWaves) <= c->max_lds &&
            (uint64_t)pairs * ga.L.hidden * 4 < (1ull << 31);
 }
 
@@ -1102,7 +1102,7 @@ static int grouped_down(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed
     const int steps = tile_steps_host(I);
     if (routed && c->gateup_bal && down_balanced(c, ga, maxu)) {
         return launch(c, steps == 6 ? kDownBal6 : kDownBal, dim3((unsigned)c->cus), dim3(64 * kBalWaves),
-                      (size_t)bal_lds_bytes(I, 8, kBalWaves), s, ga);
+                      (size_t)bal_lds_bytes(I, 8 * kDownBalTiles, kBalWaves), s, ga);
     }
     const Fn f = steps <= kDownChunk ? kDown : kDownWide;
     const int tw = steps <= kDownChunk ? 2 : 1;
