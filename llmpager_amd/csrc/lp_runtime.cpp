@@ -1074,13 +1074,6 @@ static bool down_balanced(const lp_ctx* c, const GroupedArgs& ga, int maxu) {
            (uint64_t)pairs * ga.L.hidden * 4 < (1ull << 31);
 }
 
-// Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
-// (maxu entries): workgroup width chosen so that there are about two work
-// items per CU, down with two tiles per wave when the inner size allows.
-// `routed`: the routed experts (the balanced down may take them; the
-// balanced gate/up takes the shared MLP too, as ceil(T / 4) one-group
-// entries of one blob, whose weight rows neighbouring workgroups of one XCD
-// read together).
 // The grouped down projection of ga's entries (maxu): balanced for routed
 // decode batches when it can, else the one-shot kernels.
 static int grouped_down(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s) {
@@ -1114,7 +1107,13 @@ static int grouped_down(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed
                   s, ga);
 }
 
-
+// Grouped gate/up (+ SiLU) and down over the work items of ga's expert table
+// (maxu entries): workgroup width chosen so that there are about two work
+// items per CU, down with two tiles per wave when the inner size allows.
+// `routed`: the routed experts (the balanced down may take them; the
+// balanced gate/up takes the shared MLP too, as ceil(T / 4) one-group
+// entries of one blob, whose weight rows neighbouring workgroups of one XCD
+// read together).
 // sh_maxu > 0 (routed only): the balanced gate/up also takes the shared
 // MLP's entries when it can; *sh_done says whether it did.
 static int grouped_ffn(lp_ctx* c, const GroupedArgs& ga0, int maxu, bool routed, lp_stream s,
