@@ -1458,8 +1458,12 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
         N += t;
     }
     const int u0 = before + inc - ng * Re;  // this entry's first unit
-    P.lo = (int)((long)N * blockIdx.x / gridDim.x);
-    P.hi = (int)((long)N * (blockIdx.x + 1) / gridDim.x);
+    // workgroups of one XCD (dispatched round-robin over the 8) take
+    // neighbouring shares
+    const int G = (int)gridDim.x;
+    const int b = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    P.lo = (int)((long)N * b / G);
+    P.hi = (int)((long)N * (b + 1) / G);
     if (P.lo >= P.hi) return false;
     if (tid < nent && ng > 0) {
         const int u1 = u0 + Re * ng;  // the entry's units
