@@ -49,9 +49,9 @@ CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-co
 # each scaled by the factor the same counter reads for the calibration copy),
 # from the rocprofv3 --pmc runs recorded in profiles/ for that kernel: the
 # 256 MiB copy reads FETCH_SIZE 131,093 KiB (factor 2.0) and WRITE_SIZE
-# 262,144 KiB (factor 1.0); lp_moe_gateup_bal averages 91,995 and 918 KiB.
+# 262,144 KiB (factor 1.0); lp_moe_gateup_bal averages 89,353 and 908 KiB.
 # Re-measure whenever the kernel changes.
-TRAFFIC_B32 = {"lp_moe_gateup_bal": (2 * 91_995 + 918) * 1024}
+TRAFFIC_B32 = {"lp_moe_gateup_bal": (2 * 89_353 + 908) * 1024}
 KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
            "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
            "lp_moe_combine")
