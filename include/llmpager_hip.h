@@ -161,7 +161,8 @@ int lp_strided_copy(lp_ctx* ctx, uint64_t src, int src_stride, int src_off, uint
  * reference calls mla_attn_decode once per sequence, kimi.rs:892-939):
  * q f32 [batch][heads][qk_dim]; sequence b's cache rows (bf16 [seq, qk_dim])
  * at cache + b * cache_stride bytes; seq_lens device i32 [batch], each in
- * 1..max_seq; ctx_out f32 [batch][heads][c_dim].  heads <= 16, qk_dim =
+ * 1..max_seq (a larger value is taken as max_seq: no row past a sequence's
+ * max_seq rows is read); ctx_out f32 [batch][heads][c_dim].  heads <= 16, qk_dim =
  * 32 x {3,4,6,8,12,16,18,20}, c_dim a multiple of 64 up to 512.  The
  * workspace holds lp_mla_batch_ws_bytes(ctx, batch, c_dim, max_seq) bytes. */
 uint64_t lp_mla_batch_ws_bytes(lp_ctx* ctx, int batch, int c_dim, int max_seq);
@@ -237,6 +238,16 @@ typedef struct lp_moe_ws_layout {
 
 int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* out);
 
+/* Every entry point below that takes a workspace also takes its size in
+ * bytes (ws_bytes) and refuses, before any launch, a workspace that is null,
+ * not 256-byte aligned or smaller than lp_moe_ws_layout_get(d, T).total (for
+ * a stack: than the largest layer's).  This is that check on its own, with no
+ * context and no device: LP_OK, or the error the entry points would give.
+ * (No counterpart in the reference, whose engine sizes its buffers itself,
+ * decode.rs:165-199.) */
+int lp_moe_workspace_check(const lp_moe_layer_desc* layers, int n_layers, int T, uint64_t workspace,
+                           uint64_t ws_bytes);
+
 /* Routing for T tokens without the host round trip of decode.rs:305-331:
  * router logits (T <= 64: GEMV in the canonical fp32 FMA order; larger T: an
  * MFMA GEMM over exact products, equal to fp32 rounding), softmax or sigmoid
@@ -244,26 +255,27 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
  * given the same logits), and the stable token->expert dispatch.
  * x: f32 [T, H], 16-byte aligned. */
 int lp_moe_route(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t workspace,
-                 lp_stream s);
+                 uint64_t ws_bytes, lp_stream s);
 /* Routing from caller-supplied logits (f32 [T, E], copied into the
  * workspace): the "given identical fp32 router logits" contract. */
 int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits, int T,
-                        uint64_t workspace, lp_stream s);
+                        uint64_t workspace, uint64_t ws_bytes, lp_stream s);
 /* Expert half of the layer after lp_moe_route*: fragment images of x,
  * grouped gate/up + SiLU, grouped down, and h[t] += sum_j w[t][j] * y[t][j]
  * in pick order.  x and h 16-byte aligned. */
 int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                   uint64_t workspace, lp_stream s);
+                   uint64_t workspace, uint64_t ws_bytes, lp_stream s);
 /* Paged flow (decode.rs:305-331 order: route, then request the picks, then
  * compute): after lp_moe_route* and the pager's requests for the picked
  * experts, re-resolve the expert table's blob addresses through the layer's
  * now-current slot table, before lp_moe_experts. */
-int lp_moe_resolve(lp_ctx* ctx, const lp_moe_layer_desc* d, int T, uint64_t workspace, lp_stream s);
+int lp_moe_resolve(lp_ctx* ctx, const lp_moe_layer_desc* d, int T, uint64_t workspace, uint64_t ws_bytes,
+                   lp_stream s);
 /* The whole layer (decode.rs:303-337 for one token, 469-531 for many):
  * lp_moe_route followed by lp_moe_experts, with the fragment images of x
  * written by the router kernel.  h: f32 [T, H], updated in place. */
 int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                   uint64_t workspace, lp_stream s);
+                   uint64_t workspace, uint64_t ws_bytes, lp_stream s);
 /* The layer-stack driver (decode.rs:277-343 restricted to the MoE block;
  * the batched layer loop decode.rs:431-532): lp_moe_forward over
  * layers[0 .. n_layers), in order, the layer input being the residual itself
@@ -273,17 +285,20 @@ int lp_moe_forward(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t
  * first launch.  No host synchronisation between layers (the reference reads
  * the router logits back and syncs once per layer, decode.rs:306-307). */
 int lp_moe_stack_forward(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
-                         uint64_t workspace, lp_stream s);
+                         uint64_t workspace, uint64_t ws_bytes, lp_stream s);
 /* The same stack captured once into a HIP graph (no counterpart in the
  * reference, whose launches are issued one by one from the host): every
  * kernel node keeps the arguments given here (h, T, workspace, the
  * descriptors' tables), so a replay reruns exactly this stack.  s must be a
- * created stream (the null stream cannot be captured); the routing kernels'
- * arrival counters are those of s, so replays must not overlap one another
- * or routing launches on s.  The graph holds no memset nodes. */
+ * created stream (the null stream cannot be captured).  The graph holds a
+ * set of the routing kernels' arrival counters of its own until
+ * lp_graph_destroy (so s may be destroyed, and other streams may route, while
+ * it lives): replays of one graph must not overlap one another.  Destroy
+ * graphs before their context; lp_graph_destroy waits for the device first.
+ * The graph holds no memset nodes. */
 typedef struct lp_graph lp_graph;
 int lp_moe_stack_capture(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
-                         uint64_t workspace, lp_stream s, lp_graph** out);
+                         uint64_t workspace, uint64_t ws_bytes, lp_stream s, lp_graph** out);
 int lp_graph_launch(lp_ctx* ctx, lp_graph* g, lp_stream s);
 void lp_graph_destroy(lp_graph* g);
 /* lp_moe_forward without a workspace argument and without any allocation:
@@ -301,7 +316,7 @@ int lp_moe_forward_noalloc(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, 
 /* LP_NOALLOC_SCRATCH_BYTES, as built into the library. */
 uint64_t lp_noalloc_scratch_bytes(void);
 /* Synchronising readback of meta[0..1] (unique count, error flags). */
-int lp_moe_status_sync(lp_ctx* ctx, uint64_t workspace, const lp_moe_layer_desc* d, int T,
+int lp_moe_status_sync(lp_ctx* ctx, uint64_t workspace, uint64_t ws_bytes, const lp_moe_layer_desc* d, int T,
                        lp_stream s, int32_t* unique_count, int32_t* error_flags);
 
 /* ---- expert-slot bookkeeping: cache::ExpertCache (cache.rs:58-241) -------- */
@@ -372,6 +387,10 @@ typedef struct lp_pager_config {
     uint32_t ring_slots;        /* pinned staging buffers of one span per worker; 0 = 2 */
     uint32_t stage_threads;     /* threads sharing one blob's staging copy or read; 0 = 4 */
     uint64_t ram_bytes;         /* PACK: host-RAM expert tier in bytes, 0 = none (PagerConfig::ram_bytes, :42-45) */
+    uint64_t reserve_bytes;     /* device memory to leave free, 0 = none (PagerConfig::reserve_bytes, :46-50):
+                                   slots_per_layer is lowered until the arena and slot tables leave this much
+                                   free (lp_pager_slots_per_layer gives the result); refused if not even one
+                                   slot per layer fits */
 } lp_pager_config;
 
 typedef struct lp_pager_metrics {

@@ -28,6 +28,17 @@ GATING_SIGMOID = 1
 _lib = None
 
 
+class DevPtr(int):
+    """A device address (an int, as the C ABI takes it) that remembers the
+    size of its allocation, so entry points that need a buffer's size (the
+    workspace) can pass it on."""
+
+    def __new__(cls, addr: int, nbytes: int):
+        o = super().__new__(cls, addr)
+        o.nbytes = int(nbytes)
+        return o
+
+
 class LpError(RuntimeError):
     """A non-zero return from the C ABI, with lp_last_error()'s text."""
 
@@ -108,18 +119,19 @@ def _sig(lib):
         "lp_mla_batch_ws_bytes": (u64, [vp, i32, i32, i32]),
         "lp_mla_attn_decode_batch": (i32, [vp, u64, u64, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
         "lp_moe_ws_layout_get": (i32, [P(LayerDesc), i32, P(WsLayout)]),
-        "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
-        "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, vp]),
-        "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
-        "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, vp]),
-        "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, vp]),
+        "lp_moe_workspace_check": (i32, [P(LayerDesc), i32, i32, u64, u64]),
+        "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, u64, vp]),
+        "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, u64, vp]),
+        "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, u64, vp]),
+        "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, u64, vp]),
+        "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, u64, vp]),
         "lp_moe_forward_noalloc": (i32, [vp, P(LayerDesc), u64, u64, i32, vp]),
-        "lp_moe_stack_forward": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, vp]),
-        "lp_moe_stack_capture": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, vp, P(vp)]),
+        "lp_moe_stack_forward": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, u64, vp]),
+        "lp_moe_stack_capture": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, u64, vp, P(vp)]),
         "lp_graph_launch": (i32, [vp, vp, vp]),
         "lp_graph_destroy": (None, [vp]),
         "lp_noalloc_scratch_bytes": (u64, []),
-        "lp_moe_status_sync": (i32, [vp, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
+        "lp_moe_status_sync": (i32, [vp, u64, u64, P(LayerDesc), i32, vp, P(C.c_int32), P(C.c_int32)]),
         "lp_q4_bytes": (u64, [i32, i32, i32]),
         "lp_blob_bytes": (u64, [i32, i32, i32]),
         "lp_blob_offsets": (None, [i32, i32, i32, P(u64), P(u64), P(u64)]),
@@ -285,10 +297,10 @@ class Cuda:
         _check(lib().lp_mem_info(self.ctx, C.byref(f), C.byref(t)))
         return f.value, t.value
 
-    def alloc_device(self, nbytes: int) -> int:
+    def alloc_device(self, nbytes: int) -> "DevPtr":
         p = C.c_uint64()
         _check(lib().lp_alloc_device(self.ctx, nbytes, C.byref(p)))
-        return p.value
+        return DevPtr(p.value, nbytes)
 
     def free_device(self, p: int) -> None:
         _check(lib().lp_free_device(self.ctx, p))
@@ -479,7 +491,7 @@ class PagerConfig(C.Structure):
         ("host_blobs", C.c_void_p), ("host_stride", C.c_uint64), ("copy_streams", C.c_int32),
         ("global_pool", C.c_int32), ("pool_decay_tokens", C.c_uint32), ("source", C.c_int32),
         ("direct", C.c_int32), ("io_threads", C.c_uint32), ("ring_slots", C.c_uint32),
-        ("stage_threads", C.c_uint32), ("ram_bytes", C.c_uint64),
+        ("stage_threads", C.c_uint32), ("ram_bytes", C.c_uint64), ("reserve_bytes", C.c_uint64),
     ]
 
 
@@ -602,6 +614,11 @@ class Pager:
     def slot_table(self, layer: int) -> int:
         return int(lib().lp_pager_slot_table(self.p, layer))
 
+    @property
+    def slots_per_layer(self) -> int:
+        """Slots per layer in use (after any reserve_bytes clamp)."""
+        return int(lib().lp_pager_slots_per_layer(self.p))
+
     def request(self, layer: int, experts, stream=None) -> np.ndarray:
         ex = np.ascontiguousarray(experts, np.uint16)
         out = np.zeros(len(ex), np.uint32)
@@ -642,36 +659,58 @@ class Pager:
             self.p = None
 
 
+def _ws_bytes(ws: int, ws_bytes: int | None) -> int:
+    """The workspace's size: given, or carried by a DevPtr from alloc_device."""
+    if ws_bytes is not None:
+        return ws_bytes
+    n = getattr(ws, "nbytes", None)
+    if n is None:
+        raise TypeError("workspace size unknown: pass ws_bytes or a DevPtr from Cuda.alloc_device")
+    return n
+
+
+def workspace_check(descs, T: int, ws: int, ws_bytes: int) -> int:
+    """lp_moe_workspace_check (host only): 0, or the code the entry points
+    would return for this workspace."""
+    arr = (LayerDesc * len(descs))(*descs)
+    return lib().lp_moe_workspace_check(arr, len(descs), T, ws, ws_bytes)
+
+
 class MoeLayer:
-    """The fused layer entry points for one layer descriptor."""
+    """The fused layer entry points for one layer descriptor.  `ws` is a
+    DevPtr from Cuda.alloc_device (its size travels with it) or an address
+    with `ws_bytes` given."""
 
     def __init__(self, cuda: Cuda, desc: LayerDesc):
         self.cuda = cuda
         self.desc = desc
 
-    def route(self, x: int, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_route(self.cuda.ctx, C.byref(self.desc), x, T, ws, stream))
+    def route(self, x: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_route(self.cuda.ctx, C.byref(self.desc), x, T, ws, _ws_bytes(ws, ws_bytes), stream))
 
-    def route_logits(self, logits: int, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_route_logits(self.cuda.ctx, C.byref(self.desc), logits, T, ws, stream))
+    def route_logits(self, logits: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_route_logits(self.cuda.ctx, C.byref(self.desc), logits, T, ws,
+                                         _ws_bytes(ws, ws_bytes), stream))
 
-    def resolve(self, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_resolve(self.cuda.ctx, C.byref(self.desc), T, ws, stream))
+    def resolve(self, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_resolve(self.cuda.ctx, C.byref(self.desc), T, ws, _ws_bytes(ws, ws_bytes), stream))
 
-    def experts(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_experts(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))
+    def experts(self, x: int, h: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_experts(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, _ws_bytes(ws, ws_bytes),
+                                    stream))
 
-    def forward(self, x: int, h: int, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_forward(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, stream))
+    def forward(self, x: int, h: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_forward(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, _ws_bytes(ws, ws_bytes),
+                                    stream))
 
     def forward_noalloc(self, x: int, h: int, T: int, stream=None) -> None:
         """lp_moe_forward_noalloc: the layer with the library's built-in
         per-device scratch as its workspace (no allocation)."""
         _check(lib().lp_moe_forward_noalloc(self.cuda.ctx, C.byref(self.desc), x, h, T, stream))
 
-    def status(self, ws: int, T: int, stream=None) -> tuple[int, int]:
+    def status(self, ws: int, T: int, stream=None, ws_bytes: int | None = None) -> tuple[int, int]:
         u, e = C.c_int32(), C.c_int32()
-        _check(lib().lp_moe_status_sync(self.cuda.ctx, ws, C.byref(self.desc), T, stream,
+        _check(lib().lp_moe_status_sync(self.cuda.ctx, ws, _ws_bytes(ws, ws_bytes), C.byref(self.desc), T, stream,
                                         C.byref(u), C.byref(e)))
         return u.value, e.value
 
@@ -689,12 +728,14 @@ class MoeStack:
     def ws_bytes(self, T: int) -> int:
         return max(ws_layout(d, T).total for d in self.descs)
 
-    def forward(self, h: int, T: int, ws: int, stream=None) -> None:
-        _check(lib().lp_moe_stack_forward(self.cuda.ctx, self.descs, self.n, h, T, ws, stream))
+    def forward(self, h: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
+        _check(lib().lp_moe_stack_forward(self.cuda.ctx, self.descs, self.n, h, T, ws, _ws_bytes(ws, ws_bytes),
+                                          stream))
 
-    def capture(self, h: int, T: int, ws: int, stream) -> "Graph":
+    def capture(self, h: int, T: int, ws: int, stream, ws_bytes: int | None = None) -> "Graph":
         g = C.c_void_p()
-        _check(lib().lp_moe_stack_capture(self.cuda.ctx, self.descs, self.n, h, T, ws, stream, C.byref(g)))
+        _check(lib().lp_moe_stack_capture(self.cuda.ctx, self.descs, self.n, h, T, ws, _ws_bytes(ws, ws_bytes),
+                                          stream, C.byref(g)))
         return Graph(self.cuda, g.value)
 
 

@@ -364,7 +364,9 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
     uint4* qlo = qhi + STEPS * 64;
     uint8_t* ct = lds + 2 * STEPS * 1024;  // transposed chunk: [CD][kMlaColStride]
     float* sl = reinterpret_cast<float*>(ct + CD * kMlaColStride);  // [16][64]
-    const int seq = dptr<const int>(a.seq_lens)[b];
+    // a length past the cache is cut to the cache (rows beyond max_seq
+    // belong to the next sequence, or to no allocation at all)
+    const int seq = min(dptr<const int>(a.seq_lens)[b], a.max_seq);
     const int p0 = sp * a.span;
     const int p1 = min(seq, p0 + a.span);
     const int nchunks = p1 > p0 ? (p1 - p0 + kMlaRows - 1) / kMlaRows : 0;

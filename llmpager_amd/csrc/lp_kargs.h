@@ -211,7 +211,7 @@ struct MlaBatchArgs {
     uint64_t part;                  // f32 [batch][splits] partial records
     int32_t batch, heads, qk_dim, c_dim, splits, span;
     float scale;
-    int32_t pad0;
+    int32_t max_seq;                // rows per cache: seq_lens[b] is clamped to it on the device
 };
 
 // ---- fused MoE layer ---------------------------------------------------------

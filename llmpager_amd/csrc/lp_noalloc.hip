@@ -71,7 +71,7 @@ extern "C" int lp_moe_forward_noalloc(lp_ctx* ctx, const lp_moe_layer_desc* d, u
         ws = dev >= 0 && dev < kMaxDevices ? g_ptr[dev] : 0;
     }
     if (!ws) return lpi::set_error(LP_E_LOAD, "lp_moe_forward_noalloc: scratch not set up on this device");
-    return lp_moe_forward(ctx, d, x, h, T, ws, s);
+    return lp_moe_forward(ctx, d, x, h, T, ws, kScratchBytes, s);
 }
 
 extern "C" uint64_t lp_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -10,8 +10,11 @@
 // and index (pack.rs:67-150); the reader keeps the index in memory and reads
 // a blob's whole aligned span with pread, optionally through O_DIRECT
 // (pack.rs:152-260).  Compressed packs (zstd frames) are refused.
+#include <errno.h>
 #include <fcntl.h>
+#include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -75,6 +78,20 @@ bool json_field(const std::string& js, const char* key, std::string* out) {
     while (end < js.size() && js[end] != ',' && js[end] != '}') ++end;
     *out = js.substr(at, end - at);
     while (!out->empty() && (out->back() == ' ' || out->back() == '\n')) out->pop_back();
+    return true;
+}
+
+// A JSON unsigned integer: digits only (no sign, no fraction, no exponent),
+// at most 20 of them, parsed without exceptions or wrap-around.
+bool parse_count(const std::string& v, uint64_t* out) {
+    if (v.empty() || v.size() > 20) return false;
+    for (char ch : v)
+        if (ch < '0' || ch > '9') return false;
+    errno = 0;
+    char* end = nullptr;
+    const unsigned long long x = strtoull(v.c_str(), &end, 10);
+    if (errno != 0 || !end || *end != '\0') return false;
+    *out = (uint64_t)x;
     return true;
 }
 
@@ -202,24 +219,41 @@ int lp_pack_open(const char* path, int direct, lp_pack** out) {
     if (ver != kVersion) return bad("unsupported pack version " + std::to_string(ver));
     if (jl > kAlign - 16) return bad("metadata JSON overruns the header");
     const std::string js(reinterpret_cast<const char*>(head.data() + 16), jl);
+    // PackMeta (pack.rs:29-48) holds num_layers and experts_per_layer as
+    // u16: anything else is not a pack this format can describe
     std::string v;
+    uint64_t nl = 0, ne = 0;
     if (!json_field(js, "num_layers", &v)) return bad("metadata has no num_layers");
-    p->layers = (uint32_t)std::stoul(v);
+    if (!parse_count(v, &nl) || nl > 65535) return bad("num_layers is not an integer in 0..65535");
     if (!json_field(js, "experts_per_layer", &v)) return bad("metadata has no experts_per_layer");
-    p->experts = (uint32_t)std::stoul(v);
+    if (!parse_count(v, &ne) || ne > 65535) return bad("experts_per_layer is not an integer in 0..65535");
+    p->layers = (uint32_t)nl;
+    p->experts = (uint32_t)ne;
     if (json_field(js, "dtype", &v)) p->dtype = v;
     if (json_field(js, "model", &v)) p->model = v;
     if (json_field(js, "compression", &v) && v != "null") return bad("compressed packs are not supported");
     if (p->layers == 0 || p->experts == 0) return bad("empty pack");
+    // at most 65535^2 entries of 16 bytes: no overflow in 64 bits
     const uint64_t total = (uint64_t)p->layers * p->experts;
     const uint64_t span = align_up(total * 16);
+    struct stat st;
+    if (fstat(fd, &st) != 0) return bad("cannot stat the file");
+    const uint64_t fsize = (uint64_t)st.st_size;
+    if (fsize < kAlign + span) return bad("the file is shorter than its index");
     void* ib = nullptr;
     if (posix_memalign(&ib, kAlign, span) != 0) return bad("out of memory");
     const bool iok = pread_full(fd, ib, span, kAlign);
-    p->index.assign(static_cast<const uint64_t*>(ib), static_cast<const uint64_t*>(ib) + 2 * total);
+    if (iok) p->index.assign(static_cast<const uint64_t*>(ib), static_cast<const uint64_t*>(ib) + 2 * total);
     free(ib);
     if (!iok) return bad("cannot read the index");
-    for (uint64_t i = 0; i < total; ++i) p->max_blob = std::max(p->max_blob, p->index[2 * i + 1]);
+    // every blob starts on a 4096 boundary past the index and its aligned
+    // span lies inside the file (the reads take whole spans)
+    for (uint64_t i = 0; i < total; ++i) {
+        const uint64_t off = p->index[2 * i], n = p->index[2 * i + 1];
+        if (off % kAlign || off < kAlign + span || n > fsize || align_up(n) > fsize || off > fsize - align_up(n))
+            return bad("index entry " + std::to_string(i) + " lies outside the file or is not 4096-aligned");
+        p->max_blob = std::max(p->max_blob, n);
+    }
     *out = p;
     return LP_OK;
 }

@@ -469,7 +469,31 @@ int pager_init(lp_ctx* ctx, const lp_pager_config* cfg, lp_pack* pack, lp_pager*
         lp_pager_free(p);
         return fail(LP_E_INVALID, "lp_pager_new: span must hold a blob and be 256-byte (pack: 4096-byte) aligned");
     }
-    const uint32_t L = cfg->layers, E = cfg->experts_per_layer, S = cfg->slots_per_layer;
+    const uint32_t L = cfg->layers, E = cfg->experts_per_layer;
+    if (cfg->reserve_bytes > 0) {
+        // The arena is a cache, the first thing to give up for a co-tenant
+        // of the card (PagerConfig::reserve_bytes, pager.rs:46-50): keep at
+        // most as many slots per layer as leave reserve_bytes of device
+        // memory free once the arena and the slot tables are allocated.
+        size_t free_b = 0, total_b = 0;
+        const hipError_t me = hipMemGetInfo(&free_b, &total_b);
+        if (me != hipSuccess) {
+            lp_pager_free(p);
+            return hip_fail(me, "lp_pager: hipMemGetInfo");
+        }
+        const uint64_t tables = (uint64_t)L * E * 4, layer_slot = (uint64_t)L * p->span;
+        const uint64_t room = (uint64_t)free_b > cfg->reserve_bytes + tables
+                                  ? (uint64_t)free_b - cfg->reserve_bytes - tables : 0;
+        const uint64_t fit = room / layer_slot;
+        if (fit == 0) {
+            lp_pager_free(p);
+            return fail(LP_E_UNSUPPORTED, "lp_pager: " + std::to_string(free_b) + " bytes of device memory free; "
+                                          "keeping " + std::to_string(cfg->reserve_bytes) + " free leaves no room "
+                                          "for one slot per layer (" + std::to_string(layer_slot) + " bytes)");
+        }
+        if (fit < p->cfg.slots_per_layer) p->cfg.slots_per_layer = (uint32_t)fit;
+    }
+    const uint32_t S = p->cfg.slots_per_layer;
     const uint64_t total = (uint64_t)L * S;
     // pager.rs:331-343: per-layer pools (decay by insertions), or one pool
     // whose decay is driven by lp_pager_tick
@@ -664,7 +688,11 @@ int lp_pager_request_handles(lp_pager* p, uint16_t layer, const uint16_t* expert
         out[i].expert = experts[i];
         out[i].slot = slots[(size_t)i];
         out[i].dev = slot_dev(p, slots[(size_t)i]);
-        out[i].len = p->cfg.blob_bytes;
+        // a pack's blobs differ in size: the handle carries this one's
+        // (pager.rs:595-603 takes it from the pack index)
+        uint64_t nb = p->cfg.blob_bytes;
+        if (p->pack) lp_pack_entry(p->pack, layer, experts[i], nullptr, &nb);
+        out[i].len = nb;
     }
     return LP_OK;
 }

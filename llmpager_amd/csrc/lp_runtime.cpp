@@ -186,10 +186,17 @@ struct lp_ctx {
     // first kSyncSlots streams that route through the context get one each):
     // launches on one stream run one after another, so they may share it,
     // and launches on different streams never do.
+    // A graph captured by lp_moe_stack_capture keeps a slot of its own for
+    // its whole life (its kernel nodes hold the slot's address), so that
+    // destroying the capture stream and routing on a stream created later
+    // never shares counters with the graph's replays.
     int32_t* sync = nullptr;
     std::mutex sync_mu;
     hipStream_t sync_owner[kSyncSlots] = {};  // slot i belongs to sync_owner[i] when sync_used[i]
     bool sync_used[kSyncSlots] = {};
+    bool sync_graph[kSyncSlots] = {};         // slot i belongs to a graph (sync_owner unused)
+    hipStream_t cap_stream = nullptr;         // a capture in progress on this stream ...
+    int cap_slot = -1;                        // ... routes through this (the graph's) slot
     // decode gate/up through lp_moe_gateup_bal (LLMPAGER_HIP_GATEUP_BAL=0 at
     // lp_init turns it off, for comparison)
     bool gateup_bal = true;
@@ -442,7 +449,7 @@ int lp_stream_destroy(lp_ctx* c, lp_stream s) {
         // done, so a stream created later may take them
         std::lock_guard<std::mutex> g(c->sync_mu);
         for (int i = 0; i < kSyncSlots; ++i) {
-            if (c->sync_used[i] && c->sync_owner[i] == (hipStream_t)s) {
+            if (c->sync_used[i] && !c->sync_graph[i] && c->sync_owner[i] == (hipStream_t)s) {
                 HIPCHK(hipStreamSynchronize((hipStream_t)s));
                 c->sync_used[i] = false;
                 break;
@@ -792,6 +799,7 @@ int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cac
     a.qk_dim = qk_dim;
     a.c_dim = c_dim;
     a.scale = scale;
+    a.max_seq = max_seq;
     mla_plan(c, batch, max_seq, &a.splits, &a.span);
     if (int r = launch(c, kMlaSplit, dim3((unsigned)a.splits, (unsigned)batch), dim3(256), lds, s, a)) return r;
     return launch(c, kMlaCombine, dim3((unsigned)heads, (unsigned)batch, (unsigned)(c_dim / 64)), dim3(256), 0, s,
@@ -865,8 +873,8 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     return LP_OK;
 }
 
-static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
-    if (int r = check_ctx(c)) return r;
+// The layer descriptor and T as the kernels assume them (no device state).
+static int check_desc_shape(const lp_moe_layer_desc* d, int T) {
     if (!d) return fail(LP_E_INVALID, "null layer descriptor");
     if (T <= 0) return fail(LP_E_INVALID, "T must be >= 1");
     if (d->experts <= 0 || d->experts > kMaxExperts)
@@ -901,6 +909,11 @@ static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
             return fail(LP_E_UNSUPPORTED, "shared MLP nibble rows must be 16-byte aligned");
     }
     return LP_OK;
+}
+
+static int check_desc(lp_ctx* c, const lp_moe_layer_desc* d, int T) {
+    if (int r = check_ctx(c)) return r;
+    return check_desc_shape(d, T);
 }
 
 static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView* L, Workspace* W) {
@@ -959,9 +972,10 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
 static int sync_slot(lp_ctx* c, lp_stream s) {
     std::lock_guard<std::mutex> g(c->sync_mu);
     const hipStream_t hs = (hipStream_t)s;
+    if (c->cap_slot >= 0 && c->cap_stream == hs) return c->cap_slot;
     int free_slot = -1;
     for (int i = 0; i < kSyncSlots; ++i) {
-        if (c->sync_used[i] && c->sync_owner[i] == hs) return i;
+        if (c->sync_used[i] && !c->sync_graph[i] && c->sync_owner[i] == hs) return i;
         if (!c->sync_used[i] && free_slot < 0) free_slot = i;
     }
     if (free_slot >= 0) {
@@ -971,11 +985,17 @@ static int sync_slot(lp_ctx* c, lp_stream s) {
     return free_slot;
 }
 
-// A workspace address the kernels may write lp_moe_ws_layout's parts at: not
-// null (an allocation of zero bytes), and 256-byte aligned like every part.
-static int check_ws(uint64_t ws) {
+// A workspace the kernels may write lp_moe_ws_layout's parts of layer d at,
+// for T tokens: not null, 256-byte aligned like every part, and at least the
+// layout's total bytes long (the kernels write up to its end unchecked).
+static int check_ws(const lp_moe_layer_desc* d, int T, uint64_t ws, uint64_t ws_bytes) {
     if (ws == 0) return fail(LP_E_INVALID, "null workspace");
     if (ws % 256) return fail(LP_E_UNSUPPORTED, "the workspace must be 256-byte aligned");
+    lp_moe_ws_layout lay;
+    if (int r = lp_moe_ws_layout_get(d, T, &lay)) return r;
+    if (ws_bytes < lay.total)
+        return fail(LP_E_INVALID, "workspace of " + std::to_string(ws_bytes) + " bytes; this layer needs " +
+                                      std::to_string(lay.total) + " for T = " + std::to_string(T));
     return LP_OK;
 }
 
@@ -993,10 +1013,20 @@ static int route_tail(lp_ctx* c, const RouteArgs& ra, lp_stream s) {
     return launch(c, kDispScatter, dim3(nb), dim3(kDispTok), 0, s, ra);
 }
 
-int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws,
+int lp_moe_workspace_check(const lp_moe_layer_desc* layers, int n_layers, int T, uint64_t ws, uint64_t ws_bytes) {
+    if (!layers || n_layers <= 0) return fail(LP_E_INVALID, "no layers");
+    for (int l = 0; l < n_layers; ++l) {
+        int r = check_desc_shape(&layers[l], T);
+        if (!r) r = check_ws(&layers[l], T, ws, ws_bytes);
+        if (r) return n_layers > 1 ? fail(r, "layer " + std::to_string(l) + ": " + g_err) : r;
+    }
+    return LP_OK;
+}
+
+int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint64_t ws, uint64_t ws_bytes,
                  lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
-    if (int r = check_ws(ws)) return r;
+    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
@@ -1028,9 +1058,9 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
 }
 
 int lp_moe_route_logits(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t logits, int T,
-                        uint64_t ws, lp_stream s) {
+                        uint64_t ws, uint64_t ws_bytes, lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
-    if (int r = check_ws(ws)) return r;
+    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.T = T;
@@ -1200,9 +1230,9 @@ static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& 
 // The grouped expert kernels and the combine; the fragment images of x are
 // written first unless the router kernel of lp_moe_forward already did.
 static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                        uint64_t ws, lp_stream s, bool have_images) {
+                        uint64_t ws, uint64_t ws_bytes, lp_stream s, bool have_images) {
     if (int r = check_desc(c, d, T)) return r;
-    if (int r = check_ws(ws)) return r;
+    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
     if (h % 16) return fail(LP_E_UNSUPPORTED, "h must be 16-byte aligned");
     if (!have_images) {
@@ -1294,9 +1324,9 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
                   s, ga);
 }
 
-int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, lp_stream s) {
+int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, uint64_t ws_bytes, lp_stream s) {
     if (int r = check_desc(c, d, T)) return r;
-    if (int r = check_ws(ws)) return r;
+    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
     RouteArgs ra{};
     fill_views(d, ws, T, &ra.L, &ra.W);
     ra.T = T;
@@ -1304,58 +1334,103 @@ int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, lp
 }
 
 int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                   uint64_t ws, lp_stream s) {
-    return experts_impl(c, d, x, h, T, ws, s, false);
+                   uint64_t ws, uint64_t ws_bytes, lp_stream s) {
+    return experts_impl(c, d, x, h, T, ws, ws_bytes, s, false);
 }
 
 int lp_moe_forward(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                   uint64_t ws, lp_stream s) {
-    if (int r = lp_moe_route(c, d, x, T, ws, s)) return r;
-    return experts_impl(c, d, x, h, T, ws, s, true);
+                   uint64_t ws, uint64_t ws_bytes, lp_stream s) {
+    if (int r = lp_moe_route(c, d, x, T, ws, ws_bytes, s)) return r;
+    return experts_impl(c, d, x, h, T, ws, ws_bytes, s, true);
 }
 
 int lp_moe_stack_forward(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
-                         uint64_t ws, lp_stream s) {
+                         uint64_t ws, uint64_t ws_bytes, lp_stream s) {
     if (int r = check_ctx(c)) return r;
-    if (!layers || n_layers <= 0) return fail(LP_E_INVALID, "lp_moe_stack_forward: no layers");
-    if (int r = check_ws(ws)) return r;
-    // every layer's shape is checked before the first launch, so a bad
-    // descriptor part-way down the stack leaves h untouched
+    // every layer's shape and workspace need are checked before the first
+    // launch, so a bad descriptor part-way down the stack leaves h untouched
+    if (int r = lp_moe_workspace_check(layers, n_layers, T, ws, ws_bytes))
+        return fail(r, "lp_moe_stack_forward: " + g_err);
     for (int l = 0; l < n_layers; ++l)
-        if (int r = check_desc(c, &layers[l], T))
-            return fail(r, "lp_moe_stack_forward: layer " + std::to_string(l) + ": " + g_err);
-    for (int l = 0; l < n_layers; ++l)
-        if (int r = lp_moe_forward(c, &layers[l], h, h, T, ws, s)) return r;
+        if (int r = lp_moe_forward(c, &layers[l], h, h, T, ws, ws_bytes, s)) return r;
     return LP_OK;
 }
 
 struct lp_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    lp_ctx* ctx = nullptr;
+    int slot = -1;  // the graph's own arrival-counter slot, freed with it
 };
 
+// A slot of arrival counters for a graph about to be captured on s (the
+// routing launches of the capture use it); -1 when none is free.
+static int graph_slot_take(lp_ctx* c, lp_stream s) {
+    std::lock_guard<std::mutex> g(c->sync_mu);
+    for (int i = 0; i < kSyncSlots; ++i) {
+        if (!c->sync_used[i]) {
+            c->sync_used[i] = true;
+            c->sync_graph[i] = true;
+            c->sync_owner[i] = nullptr;
+            c->cap_stream = (hipStream_t)s;
+            c->cap_slot = i;
+            return i;
+        }
+    }
+    return -1;
+}
+
+static void graph_slot_free(lp_ctx* c, int slot) {
+    std::lock_guard<std::mutex> g(c->sync_mu);
+    if (slot < 0 || slot >= kSyncSlots) return;
+    c->sync_used[slot] = false;
+    c->sync_graph[slot] = false;
+}
+
+static void capture_end(lp_ctx* c) {
+    std::lock_guard<std::mutex> g(c->sync_mu);
+    c->cap_stream = nullptr;
+    c->cap_slot = -1;
+}
+
 int lp_moe_stack_capture(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
-                         uint64_t ws, lp_stream s, lp_graph** out) {
+                         uint64_t ws, uint64_t ws_bytes, lp_stream s, lp_graph** out) {
     if (int r = check_ctx(c)) return r;
     if (!out) return fail(LP_E_INVALID, "lp_moe_stack_capture: null out");
     *out = nullptr;
     if (!s) return fail(LP_E_INVALID, "lp_moe_stack_capture: the null stream cannot be captured");
+    if (int r = lp_moe_workspace_check(layers, n_layers, T, ws, ws_bytes))
+        return fail(r, "lp_moe_stack_capture: " + g_err);
+    // the graph's own arrival counters (routing in the captured launches)
+    const int slot = graph_slot_take(c, s);
+    if (slot < 0)
+        return fail(LP_E_UNSUPPORTED, "lp_moe_stack_capture: every slot of arrival counters is taken (" +
+                                          std::to_string(kSyncSlots) + " streams and graphs)");
     // no profiling events inside the graph
     const bool prof = c->prof;
     c->prof = false;
-    HIPCHK(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal));
-    const int r = lp_moe_stack_forward(c, layers, n_layers, h, T, ws, s);
+    const hipError_t be = hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal);
+    if (be != hipSuccess) {
+        c->prof = prof;
+        capture_end(c);
+        graph_slot_free(c, slot);
+        return hip_fail(be, "hipStreamBeginCapture");
+    }
+    const int r = lp_moe_stack_forward(c, layers, n_layers, h, T, ws, ws_bytes, s);
     const std::string err = g_err;
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture((hipStream_t)s, &g);
     c->prof = prof;
-    if (r != LP_OK) {
+    capture_end(c);
+    if (r != LP_OK || e != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
-        return fail(r, err);
+        graph_slot_free(c, slot);
+        return r != LP_OK ? fail(r, err) : hip_fail(e, "hipStreamEndCapture");
     }
-    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
     lp_graph* G = new lp_graph();
     G->graph = g;
+    G->ctx = c;
+    G->slot = slot;
     const hipError_t ie = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
     if (ie != hipSuccess) {
         lp_graph_destroy(G);
@@ -1374,15 +1449,21 @@ int lp_graph_launch(lp_ctx* c, lp_graph* g, lp_stream s) {
 
 void lp_graph_destroy(lp_graph* g) {
     if (!g) return;
-    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->exec) {
+        // replays still in flight hold the graph's counters
+        (void)hipDeviceSynchronize();
+        (void)hipGraphExecDestroy(g->exec);
+    }
     if (g->graph) (void)hipGraphDestroy(g->graph);
+    if (g->ctx) graph_slot_free(g->ctx, g->slot);
     delete g;
 }
 
-int lp_moe_status_sync(lp_ctx* c, uint64_t ws, const lp_moe_layer_desc* d, int T, lp_stream s,
+int lp_moe_status_sync(lp_ctx* c, uint64_t ws, uint64_t ws_bytes, const lp_moe_layer_desc* d, int T, lp_stream s,
                        int32_t* unique_count, int32_t* error_flags) {
     if (int r = check_ctx(c)) return r;
-    if (int r = check_ws(ws)) return r;
+    if (int r = check_desc_shape(d, T)) return r;
+    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
     lp_moe_ws_layout lay;
     if (int r = lp_moe_ws_layout_get(d, T, &lay)) return r;
     int32_t meta[2] = {0, 0};

@@ -130,6 +130,7 @@ pub struct lp_pager_config {
     pub ring_slots: u32,
     pub stage_threads: u32,
     pub ram_bytes: u64,
+    pub reserve_bytes: u64,
 }
 
 #[repr(C)]
@@ -237,26 +238,33 @@ extern "C" {
 
     // ---- the fused MoE layer ----
     pub fn lp_moe_ws_layout_get(d: *const lp_moe_layer_desc, t: c_int, out: *mut lp_moe_ws_layout) -> c_int;
+    pub fn lp_moe_workspace_check(
+        layers: *const lp_moe_layer_desc, n_layers: c_int, t: c_int, workspace: u64, ws_bytes: u64,
+    ) -> c_int;
     pub fn lp_moe_route(
-        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, t: c_int, ws: u64, s: lp_stream,
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, t: c_int, ws: u64, ws_bytes: u64, s: lp_stream,
     ) -> c_int;
     pub fn lp_moe_route_logits(
-        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, logits: u64, t: c_int, ws: u64, s: lp_stream,
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, logits: u64, t: c_int, ws: u64, ws_bytes: u64, s: lp_stream,
     ) -> c_int;
     pub fn lp_moe_experts(
-        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, s: lp_stream,
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, ws_bytes: u64,
+        s: lp_stream,
     ) -> c_int;
-    pub fn lp_moe_resolve(ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, t: c_int, ws: u64, s: lp_stream) -> c_int;
+    pub fn lp_moe_resolve(
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, t: c_int, ws: u64, ws_bytes: u64, s: lp_stream,
+    ) -> c_int;
     pub fn lp_moe_forward(
-        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, s: lp_stream,
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, ws_bytes: u64,
+        s: lp_stream,
     ) -> c_int;
     pub fn lp_moe_stack_forward(
         ctx: *mut lp_ctx, layers: *const lp_moe_layer_desc, n_layers: c_int, h: u64, t: c_int, ws: u64,
-        s: lp_stream,
+        ws_bytes: u64, s: lp_stream,
     ) -> c_int;
     pub fn lp_moe_stack_capture(
         ctx: *mut lp_ctx, layers: *const lp_moe_layer_desc, n_layers: c_int, h: u64, t: c_int, ws: u64,
-        s: lp_stream, out: *mut *mut lp_graph,
+        ws_bytes: u64, s: lp_stream, out: *mut *mut lp_graph,
     ) -> c_int;
     pub fn lp_graph_launch(ctx: *mut lp_ctx, g: *mut lp_graph, s: lp_stream) -> c_int;
     pub fn lp_graph_destroy(g: *mut lp_graph);
@@ -265,8 +273,8 @@ extern "C" {
     ) -> c_int;
     pub fn lp_noalloc_scratch_bytes() -> u64;
     pub fn lp_moe_status_sync(
-        ctx: *mut lp_ctx, ws: u64, d: *const lp_moe_layer_desc, t: c_int, s: lp_stream, unique_count: *mut i32,
-        error_flags: *mut i32,
+        ctx: *mut lp_ctx, ws: u64, ws_bytes: u64, d: *const lp_moe_layer_desc, t: c_int, s: lp_stream,
+        unique_count: *mut i32, error_flags: *mut i32,
     ) -> c_int;
 
     // ---- expert-slot bookkeeping: cache::ExpertCache ----

@@ -206,31 +206,47 @@ impl Kernels {
         Ok(out)
     }
 
-    /// Routing alone: router GEMV, top-k, dispatch groups into `ws`.
-    pub fn moe_route(&self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream) -> Result<()> {
-        check(unsafe { ffi::lp_moe_route(cuda.ctx, d, x, t, ws, stream) }, "moe_route")
+    /// The workspace check every MoE entry point makes before launching
+    /// (`ws_bytes` at least the largest layer's layout total), on its own.
+    pub fn moe_workspace_check(&self, layers: &[lp_moe_layer_desc], t: i32, ws: CUdeviceptr, ws_bytes: u64) -> Result<()> {
+        let rc = unsafe { ffi::lp_moe_workspace_check(layers.as_ptr(), layers.len() as i32, t, ws, ws_bytes) };
+        check(rc, "moe_workspace_check")
+    }
+
+    /// Routing alone: router GEMV, top-k, dispatch groups into `ws`
+    /// (`ws_bytes` long).
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_route(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, t: i32, ws: CUdeviceptr, ws_bytes: u64,
+        stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_route(cuda.ctx, d, x, t, ws, ws_bytes, stream) }, "moe_route")
     }
 
     /// Routing from caller-supplied router logits (f32 [t, experts]).
+    #[allow(clippy::too_many_arguments)]
     pub fn moe_route_logits(
-        &self, cuda: &Cuda, d: &lp_moe_layer_desc, logits: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, logits: CUdeviceptr, t: i32, ws: CUdeviceptr, ws_bytes: u64,
+        stream: CUstream,
     ) -> Result<()> {
-        check(unsafe { ffi::lp_moe_route_logits(cuda.ctx, d, logits, t, ws, stream) }, "moe_route_logits")
+        check(unsafe { ffi::lp_moe_route_logits(cuda.ctx, d, logits, t, ws, ws_bytes, stream) }, "moe_route_logits")
     }
 
     /// Paged flow: after routing and the pager's requests for the picks,
     /// re-resolve the expert entries through the now-current slot table.
-    pub fn moe_resolve(&self, cuda: &Cuda, d: &lp_moe_layer_desc, t: i32, ws: CUdeviceptr, stream: CUstream) -> Result<()> {
-        check(unsafe { ffi::lp_moe_resolve(cuda.ctx, d, t, ws, stream) }, "moe_resolve")
+    pub fn moe_resolve(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, t: i32, ws: CUdeviceptr, ws_bytes: u64, stream: CUstream,
+    ) -> Result<()> {
+        check(unsafe { ffi::lp_moe_resolve(cuda.ctx, d, t, ws, ws_bytes, stream) }, "moe_resolve")
     }
 
     /// The expert half of a routed layer: `h += sum_k w * expert_k(x)`.
     #[allow(clippy::too_many_arguments)]
     pub fn moe_experts(
         &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, ws: CUdeviceptr,
-        stream: CUstream,
+        ws_bytes: u64, stream: CUstream,
     ) -> Result<()> {
-        check(unsafe { ffi::lp_moe_experts(cuda.ctx, d, x, h, t, ws, stream) }, "moe_experts")
+        check(unsafe { ffi::lp_moe_experts(cuda.ctx, d, x, h, t, ws, ws_bytes, stream) }, "moe_experts")
     }
 
     /// One whole MoE layer: route, gate/up, SiLU, down, weighted combine
@@ -238,9 +254,9 @@ impl Kernels {
     #[allow(clippy::too_many_arguments)]
     pub fn moe_forward(
         &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, ws: CUdeviceptr,
-        stream: CUstream,
+        ws_bytes: u64, stream: CUstream,
     ) -> Result<()> {
-        check(unsafe { ffi::lp_moe_forward(cuda.ctx, d, x, h, t, ws, stream) }, "moe_forward")
+        check(unsafe { ffi::lp_moe_forward(cuda.ctx, d, x, h, t, ws, ws_bytes, stream) }, "moe_forward")
     }
 
     /// [`Self::moe_forward`] with its workspace in the library's own
@@ -252,20 +268,28 @@ impl Kernels {
     }
 
     /// A stack of MoE layers over the residual `h` (f32 [t, hidden]).
+    #[allow(clippy::too_many_arguments)]
     pub fn stack_forward(
-        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, ws_bytes: u64,
+        stream: CUstream,
     ) -> Result<()> {
-        let rc = unsafe { ffi::lp_moe_stack_forward(cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, stream) };
+        let rc = unsafe {
+            ffi::lp_moe_stack_forward(cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, ws_bytes, stream)
+        };
         check(rc, "stack_forward")
     }
 
     /// [`Self::stack_forward`] captured once into a HIP graph.
+    #[allow(clippy::too_many_arguments)]
     pub fn stack_capture(
-        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, stream: CUstream,
+        &self, cuda: &Cuda, layers: &[lp_moe_layer_desc], h: CUdeviceptr, t: i32, ws: CUdeviceptr, ws_bytes: u64,
+        stream: CUstream,
     ) -> Result<Graph> {
         let mut g = std::ptr::null_mut();
         let rc = unsafe {
-            ffi::lp_moe_stack_capture(cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, stream, &mut g)
+            ffi::lp_moe_stack_capture(
+                cuda.ctx, layers.as_ptr(), layers.len() as i32, h, t, ws, ws_bytes, stream, &mut g,
+            )
         };
         check(rc, "stack_capture")?;
         Ok(Graph { g })
@@ -277,9 +301,11 @@ impl Kernels {
 
     /// Synchronise `stream` and read the layer's (unique experts, error
     /// flags); a non-zero flag word is an error.
-    pub fn moe_status(&self, cuda: &Cuda, ws: CUdeviceptr, d: &lp_moe_layer_desc, t: i32, stream: CUstream) -> Result<i32> {
+    pub fn moe_status(
+        &self, cuda: &Cuda, ws: CUdeviceptr, ws_bytes: u64, d: &lp_moe_layer_desc, t: i32, stream: CUstream,
+    ) -> Result<i32> {
         let (mut uniq, mut flags) = (0i32, 0i32);
-        let rc = unsafe { ffi::lp_moe_status_sync(cuda.ctx, ws, d, t, stream, &mut uniq, &mut flags) };
+        let rc = unsafe { ffi::lp_moe_status_sync(cuda.ctx, ws, ws_bytes, d, t, stream, &mut uniq, &mut flags) };
         check(rc, "moe_status")?;
         anyhow::ensure!(flags == 0, "MoE layer reported error flags {flags:#x}");
         Ok(uniq)

@@ -1,14 +1,14 @@
 //! Expert pager over the C ABI: the surface of `pager::Pager`
 //! (`crates/llmpager-cuda/src/pager.rs`).  The workers, staging rings, RAM
-//! tier and slot cache live in the library (`lp_pager_open`); this module
-//! keeps the reference's types and method names and applies the VRAM
-//! reserve clamp (`pager.rs:266-294`) before the arena is allocated.
+//! tier, slot cache and the VRAM reserve (`lp_pager_config::reserve_bytes`)
+//! live in the library (`lp_pager_open`); this module keeps the reference's
+//! types and method names.
 use std::ffi::CString;
 use std::os::unix::ffi::OsStrExt;
 use std::path::Path;
 use std::sync::Arc;
 
-use anyhow::{bail, Result};
+use anyhow::Result;
 
 use crate::driver::{CUdeviceptr, CUstream, Cuda};
 use crate::ffi::{self, check};
@@ -61,14 +61,35 @@ pub struct Metrics {
     pub latency_ms_buckets: [u64; 7],
 }
 
+/// Upper edges (ms) of the fetch-time buckets; the last bucket is open.
+const LATENCY_EDGES_MS: [u32; 6] = [1, 2, 5, 10, 20, 50];
+
 impl Metrics {
+    /// Hits over all lookups; 0 before the first lookup.
     pub fn hit_rate(&self) -> f64 {
-        self.hits as f64 / (self.hits + self.misses).max(1) as f64
+        match self.hits + self.misses {
+            0 => 0.0,
+            lookups => self.hits as f64 / lookups as f64,
+        }
     }
 
+    /// The fetch-time buckets as `<edge>ms:count` pairs, the open last one
+    /// as `>=50ms:count`.
     pub fn histogram(&self) -> String {
-        const LABELS: [&str; 7] = ["<1ms", "<2ms", "<5ms", "<10ms", "<20ms", "<50ms", ">=50ms"];
-        LABELS.iter().zip(self.latency_ms_buckets.iter()).map(|(l, n)| format!("{l}:{n}")).collect::<Vec<_>>().join(" ")
+        let mut out = String::new();
+        for (i, count) in self.latency_ms_buckets.iter().enumerate() {
+            let label = match LATENCY_EDGES_MS.get(i) {
+                Some(edge) => format!("<{edge}ms"),
+                None => format!(">={}ms", LATENCY_EDGES_MS[LATENCY_EDGES_MS.len() - 1]),
+            };
+            if i > 0 {
+                out.push(' ');
+            }
+            out.push_str(&label);
+            out.push(':');
+            out.push_str(&count.to_string());
+        }
+        out
     }
 }
 
@@ -84,11 +105,13 @@ unsafe impl Send for Pager {}
 unsafe impl Sync for Pager {}
 
 impl Pager {
-    /// `pager.rs:260-388`: open `pack`, clamp the slot count to the VRAM
-    /// reserve, allocate the arena and start `io_threads` workers.
+    /// `pager.rs:260-388`: open `pack`, allocate the arena (its slot count
+    /// lowered by the library until `reserve_bytes` stay free: read it back
+    /// with [`Pager::slots_per_layer`]) and start `io_threads` workers.
     /// `LLMPAGER_GLOBAL_POOL=1` selects one pool shared by every layer.
     pub fn new(cuda: Arc<Cuda>, pack: &Path, cfg: PagerConfig) -> Result<Self> {
         let path = CString::new(pack.as_os_str().as_bytes())?;
+        // the pack's shape (for expert_stats); the library reads it again
         let (mut layers, mut experts, mut max_blob) = (0u32, 0u32, 0u64);
         {
             let mut pk = std::ptr::null_mut();
@@ -97,35 +120,11 @@ impl Pager {
             unsafe { ffi::lp_pack_close(pk) };
             check(rc, "lp_pack_info")?;
         }
-        let span = max_blob.div_ceil(4096) * 4096;
-        let mut slots = cfg.slots_per_layer;
-        if cfg.reserve_bytes > 0 {
-            let (free, total) = cuda.mem_info()?;
-            let per_slot = layers as u64 * span;
-            let fits = (free.saturating_sub(cfg.reserve_bytes) / per_slot.max(1)) as u32;
-            if fits < slots {
-                if fits == 0 {
-                    bail!(
-                        "cannot honour a {} MB VRAM reserve: {} MB free of {} MB, and one slot per layer needs {} MB",
-                        cfg.reserve_bytes / 1_000_000,
-                        free / 1_000_000,
-                        total / 1_000_000,
-                        per_slot / 1_000_000
-                    );
-                }
-                eprintln!(
-                    "vram reserve: {slots} slots/layer -> {fits} (leaving {} MB free of {} MB)",
-                    cfg.reserve_bytes / 1_000_000,
-                    total / 1_000_000
-                );
-                slots = fits;
-            }
-        }
         let global_pool = std::env::var("LLMPAGER_GLOBAL_POOL").ok().as_deref() == Some("1");
         let c = ffi::lp_pager_config {
             layers,
             experts_per_layer: experts,
-            slots_per_layer: slots,
+            slots_per_layer: cfg.slots_per_layer,
             decay_interval: cfg.decay_interval,
             blob_bytes: 0,
             span: 0,
@@ -140,6 +139,7 @@ impl Pager {
             ring_slots: 0,
             stage_threads: 0,
             ram_bytes: cfg.ram_bytes,
+            reserve_bytes: cfg.reserve_bytes,
         };
         let mut p = std::ptr::null_mut();
         check(unsafe { ffi::lp_pager_open(cuda.ctx, path.as_ptr(), &c, &mut p) }, "lp_pager_open")?;

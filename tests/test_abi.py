@@ -152,6 +152,62 @@ def test_ws_layout_alignment_and_size():
         assert (lay.xd - lay.xf > 0) == (T == 2048)
 
 
+def test_workspace_check_rejects_undersized_workspaces():
+    """lp_moe_workspace_check, the pre-launch check of every MoE entry point
+    that takes a workspace: null, misaligned and short workspaces are refused
+    (a short one would be written past its end by the kernels), for one layer
+    and for a stack sized by its largest layer."""
+    d = lp.LayerDesc(hidden=2048, inter=768, experts=128, top_k=8, group=32, router_w=1 << 20,
+                     slot_table=2 << 20, arena_base=1 << 30, slot_span=2658304,
+                     gate_off=32, up_off=884768, down_off=1769504)
+    for T in (1, 8, 32, 2048):
+        need = lp.ws_layout(d, T).total
+        ws = 1 << 32
+        assert lp.workspace_check([d], T, ws, need) == 0
+        assert lp.workspace_check([d], T, ws, need + 4096) == 0
+        assert lp.workspace_check([d], T, ws, need - 1) == -1
+        assert "needs %d" % need in lp.lib().lp_last_error().decode()
+        assert lp.workspace_check([d], T, ws, 0) == -1
+        assert lp.workspace_check([d], T, 0, need) == -1
+        assert lp.workspace_check([d], T, ws + 16, need) == -2
+    # a stack: the largest layer decides; the failing layer is named
+    big = lp.LayerDesc(**{f: getattr(d, f) for f, _ in lp.LayerDesc._fields_})
+    big.inter = 1536
+    big.up_off, big.down_off = lp.blob_offsets(2048, 1536, 32)[1:]
+    T = 32
+    need = max(lp.ws_layout(x, T).total for x in (d, big))
+    assert need > lp.ws_layout(d, T).total
+    assert lp.workspace_check([d, big], T, 1 << 32, need) == 0
+    assert lp.workspace_check([d, big], T, 1 << 32, lp.ws_layout(d, T).total) == -1
+    assert lp.lib().lp_last_error().decode().startswith("layer 1:")
+    # a bad descriptor is refused before the size is looked at
+    bad = lp.LayerDesc(**{f: getattr(d, f) for f, _ in lp.LayerDesc._fields_})
+    bad.top_k = 0
+    assert lp.workspace_check([d, bad], T, 1 << 32, 1 << 40) == -2
+    # the Python wrappers take the size from an allocation, or refuse
+    with pytest.raises(TypeError):
+        lp._ws_bytes(1 << 32, None)
+    assert lp._ws_bytes(lp.DevPtr(1 << 32, 4096), None) == 4096
+
+
+def _c_decl_args(text):
+    """{name: argument count} of the header's function declarations."""
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(lp_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def _rs_decl_args(text):
+    out = {}
+    for m in re.finditer(r"pub fn (lp_[a-z0-9_]+)\((.*?)\)\s*(->[^;]*)?;", text, flags=re.S):
+        args = [a for a in m.group(2).split(",") if a.strip()]
+        out[m.group(1)] = len(args)
+    return out
+
+
 def _c_struct_fields(text, name):
     body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
@@ -173,6 +229,10 @@ def test_rust_bindings_follow_the_header():
     fns = set(re.findall(r"pub fn (lp_[a-z0-9_]+)\(", rs))
     assert len(fns) > 80
     assert not fns - set(declared_functions())
+    # and each with the header's number of arguments
+    c_args, rs_args = _c_decl_args(hdr), _rs_decl_args(rs)
+    assert set(rs_args) == fns
+    assert {n: rs_args[n] for n in fns} == {n: c_args[n] for n in fns}
     for st in ("lp_moe_layer_desc", "lp_moe_ws_layout", "lp_pager_config", "lp_pager_metrics", "lp_expert_handle"):
         body = re.search(r"pub struct %s \{(.*?)\n\}" % st, rs, flags=re.S).group(1)
         rs_fields = re.findall(r"pub ([a-z0-9_]+):", body)

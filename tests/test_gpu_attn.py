@@ -157,13 +157,13 @@ def test_bf16_gemv_batch(cuda, K, rows, cols, batch, xs):
     _free(cuda, dw, dx, dy)
 
 
-def _mla_batch(cuda, K, heads, qk, cd, seqs, ms, scale, qstd, seed):
+def _mla_batch(cuda, K, heads, qk, cd, seqs, ms, scale, qstd, seed, device_seqs=None):
     rng = np.random.default_rng(seed)
     B = len(seqs)
     q = (rng.standard_normal(B * heads * qk) * qstd).astype(np.float32)
     cache = _bf16(rng.standard_normal(B * ms * qk).astype(np.float32))   # N(0, 1) latent KV
     dq, dc = cuda.upload(q), cuda.upload(cache)
-    dsl = cuda.upload(np.asarray(seqs, np.int32))
+    dsl = cuda.upload(np.asarray(seqs if device_seqs is None else device_seqs, np.int32))
     dctx = cuda.alloc_device(B * heads * cd * 4)
     ws = cuda.alloc_device(K.mla_batch_ws_bytes(B, cd, ms))
     K.mla_attn_decode_batch(dq, dc, ms * qk * 2, dsl, dctx, ws, B, heads, qk, cd, ms, scale)
@@ -180,6 +180,13 @@ def test_mla_batch_small_shapes(cuda, K):
     # 4 heads (padded to the 16-row tile), qk 96, c_dim 64; ragged lengths
     # (one position, a partial chunk, several chunks)
     _mla_batch(cuda, K, 4, 96, 64, [1, 63, 200], 256, 0.2, 1.0, 1)
+
+
+def test_mla_batch_lengths_past_the_cache_are_clamped(cuda, K):
+    # device lengths above max_seq (256) read only the sequence's own 256
+    # rows: the result is that of a full-length sequence (unclamped, the
+    # first two would also read the following sequences' rows)
+    _mla_batch(cuda, K, 4, 96, 64, [256, 256, 63], 256, 0.2, 1.0, 2, device_seqs=[1000, 257, 63])
 
 
 @pytest.mark.parametrize("B,qstd", [(1, 0.05), (1, 1.0), (16, 0.05), (16, 1.0)])

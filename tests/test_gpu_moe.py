@@ -140,6 +140,38 @@ def test_layer_shared_expert(cuda, T):
     L.free()
 
 
+@pytest.mark.parametrize("T", [1, 16])
+def test_layer_config5_as_benchmarked(cuda, T):
+    # Config 5's MoE layer exactly as bench.py runs it: softmax gating without
+    # renormalisation (DeepSeek-V2-Lite), 64 routed experts top-6 of width
+    # 1408, the shared MLP of width 2816, g32, router N(0, 0.02), the layer
+    # input being the residual itself (one buffer, as in the captured stack)
+    L = DeviceLayer(cuda, H=2048, I=1408, E=64, k=6, group=32, seed=5, gating=lp.GATING_SOFTMAX,
+                    renorm=False, router_std=0.02, shared=(2816, 32))
+    h = lp.synth_f32_bf16(T * 2048, 1.0, 5, 2).reshape(T, 2048)
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    dh = cuda.upload(h)
+    L.layer.forward(dh, dh, T, ws)
+    got = cuda.download(dh, (T, 2048), np.float32)
+    dl = lambda off, shape, dt: cuda.download(ws + off, shape, dt)
+    glog, gids = dl(lay.logits, (T, 64), np.float32), dl(lay.ids, (T, 6), np.int32)
+    gw, gcnt = dl(lay.wts, (T, 6), np.float32), dl(lay.cnt, (T,), np.int32)
+    assert L.layer.status(ws, T)[1] == 0
+    want, wlog, wids, ww, wcnt = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), h, h.copy(), threads=8,
+                                             shared_blob=L.shared)
+    assert np.array_equal(glog.view(np.uint32), wlog.view(np.uint32))
+    assert np.array_equal(gcnt, wcnt) and np.all(wcnt == 6)
+    assert np.array_equal(gids, wids)
+    assert np.array_equal(gw.view(np.uint32), ww.view(np.uint32))
+    assert np.all(ww.sum(axis=1) < 1.0)   # softmax mass of the top 6 only: no renormalisation
+    err = rel_l2(got - h, want - h)
+    assert err <= 1e-3, err
+    for p in (ws, dh):
+        cuda.free_device(p)
+    L.free()
+
+
 def test_layer_shared_expert_g64_softmax(cuda):
     # a g64 shared MLP beside g32 routed experts, softmax gating, small shape
     L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=32, seed=8, router_std=0.2, shared=(128, 64))
@@ -150,13 +182,24 @@ def test_layer_shared_expert_g64_softmax(cuda):
 
 def test_null_workspace_rejected(cuda):
     # a zero-byte allocation comes back as a null address: every entry that
-    # writes the workspace refuses it before launching anything
+    # writes the workspace refuses it before launching anything, and so it
+    # does a misaligned one or one shorter than the layout
     L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=32, seed=1)
-    dx = cuda.upload(np.zeros((1, 128), np.float32))
-    for call in (lambda: L.layer.route(dx, 1, 0), lambda: L.layer.forward(dx, dx, 1, 0),
-                 lambda: L.layer.experts(dx, dx, 1, 0), lambda: L.layer.route(dx, 1, 64)):
+    h0 = np.arange(128, dtype=np.float32).reshape(1, 128)
+    dx = cuda.upload(h0)
+    need = lp.ws_layout(L.desc, 1).total
+    short = cuda.alloc_device(need - 256)
+    big = 1 << 20
+    for call in (lambda: L.layer.route(dx, 1, 0, ws_bytes=big), lambda: L.layer.forward(dx, dx, 1, 0, ws_bytes=big),
+                 lambda: L.layer.experts(dx, dx, 1, 0, ws_bytes=big), lambda: L.layer.route(dx, 1, 64, ws_bytes=big),
+                 lambda: L.layer.route(dx, 1, short), lambda: L.layer.route_logits(dx, 1, short),
+                 lambda: L.layer.forward(dx, dx, 1, short), lambda: L.layer.experts(dx, dx, 1, short),
+                 lambda: L.layer.resolve(1, short), lambda: L.layer.status(short, 1)):
         with pytest.raises(lp.LpError):
             call()
+    cuda.sync()
+    assert np.array_equal(cuda.download(dx, (1, 128), np.float32), h0)
+    cuda.free_device(short)
     cuda.free_device(dx)
     L.free()
 

@@ -44,13 +44,17 @@ class HostPack:
         o = (l * E + e) * self.span
         return self.view[o:o + self.blob]
 
-    def pager(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256, ram_bytes: int = 0) -> lp.Pager:
+    def pager_config(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256,
+                     ram_bytes: int = 0) -> lp.PagerConfig:
         src = {"pinned": lp.PAGER_SRC_PINNED, "host": lp.PAGER_SRC_HOST, "pack": lp.PAGER_SRC_PACK}[self.source]
-        cfg = lp.PagerConfig(layers=self.layers, experts_per_layer=E, slots_per_layer=slots,
-                             decay_interval=decay, blob_bytes=self.blob, span=0,
-                             host_blobs=self.pin or self.view.ctypes.data, host_stride=self.span,
-                             copy_streams=streams, global_pool=glob, source=src, io_threads=3, ring_slots=2,
-                             ram_bytes=ram_bytes)
+        return lp.PagerConfig(layers=self.layers, experts_per_layer=E, slots_per_layer=slots,
+                              decay_interval=decay, blob_bytes=self.blob, span=0,
+                              host_blobs=self.pin or self.view.ctypes.data, host_stride=self.span,
+                              copy_streams=streams, global_pool=glob, source=src, io_threads=3, ring_slots=2,
+                              ram_bytes=ram_bytes)
+
+    def pager(self, slots: int, streams: int = 2, glob: int = 0, decay: int = 256, ram_bytes: int = 0) -> lp.Pager:
+        cfg = self.pager_config(slots, streams, glob, decay, ram_bytes)
         if self.source == "pack":
             cfg.host_blobs, cfg.blob_bytes, cfg.host_stride = None, 0, 0
             return lp.Pager(self.cuda, cfg, pack_path=self.path)
@@ -268,4 +272,71 @@ def test_pager_expert_stats_and_prewarm(cuda, tmp_path):
     pg2.release(got)
     pg2.sync()
     pg2.close()
+    cuda.destroy_stream(s)
+
+
+def test_pager_reserve_clamps_slots(cuda):
+    # PagerConfig::reserve_bytes (pager.rs:46-50): device memory to leave
+    # free.  The slot count drops until the arena and the slot tables leave
+    # that much; a reserve that leaves no room for one slot per layer is an
+    # error.  Memory is measured just before the pager allocates, so the
+    # reserve is set to leave room for about 3 slots per layer.
+    pk = HostPack(cuda, 2, seed=12, source="pinned")
+    try:
+        per_slot = 2 * pk.span
+        free, _ = cuda.mem_info()
+        cfg_slots = 6
+        pg = pk.pager(slots=cfg_slots)
+        assert pg.slots_per_layer == cfg_slots      # no reserve: as configured
+        pg.close()
+        cfg = lp.PagerConfig.from_buffer_copy(pk.pager_config(slots=cfg_slots))
+        free, _ = cuda.mem_info()
+        cfg.reserve_bytes = free - 3 * per_slot - 2 * E * 4 - 4096
+        pg = lp.Pager(cuda, cfg)
+        assert 1 <= pg.slots_per_layer <= 3, pg.slots_per_layer
+        free_after, _ = cuda.mem_info()
+        assert free_after >= cfg.reserve_bytes - (8 << 20)   # within allocation granularity
+        # the clamped pager still works: fill and read back one expert
+        s = cuda.stream()
+        sl = pg.request(0, [5], s)
+        cuda.sync_stream(s)
+        assert np.array_equal(cuda.download(pg.arena + int(sl[0]) * pg.span, (pk.blob,), np.uint8),
+                              pk.blob_of(0, 5))
+        pg.release(sl)
+        pg.sync()
+        pg.close()
+        cuda.destroy_stream(s)
+        free, _ = cuda.mem_info()
+        cfg.reserve_bytes = free + (1 << 30)
+        with pytest.raises(lp.LpError, match="no room"):
+            lp.Pager(cuda, cfg)
+    finally:
+        pk.free()
+
+
+def test_pack_handles_carry_each_blobs_length(cuda, tmp_path):
+    # ExpertHandle.len is the expert's own blob length from the pack index
+    # (pager.rs:595-603), not the largest blob's: blobs of mixed sizes
+    path = str(tmp_path / "mixed.llmpk")
+    blob = lp.synth_blob(H, I, G, 3, 0, 0)
+    w = lp.PackWriter(path, 1, E)
+    lens = [blob.size + 100 * e for e in range(E)]
+    for e in range(E):
+        w.add_blob(np.concatenate([blob, np.full(lens[e] - blob.size, e, np.uint8)]))
+    w.finish()
+    cfg = lp.PagerConfig(slots_per_layer=4, decay_interval=256, io_threads=2, ring_slots=2)
+    pg = lp.Pager(cuda, cfg, pack_path=path)
+    s = cuda.stream()
+    for group in ([0, 7, 3], [5, 1]):
+        hs = pg.request_handles(0, group)
+        assert [h.len for h in hs] == [lens[e] for e in group]
+        for h in hs:
+            pg.wait_stream(h, s)
+        cuda.sync_stream(s)
+        for h in hs:
+            got = cuda.download(h.dev, (h.len,), np.uint8)
+            assert np.array_equal(got[:blob.size], blob) and np.all(got[blob.size:] == h.expert)
+        pg.release([h.slot for h in hs])
+    pg.sync()
+    pg.close()
     cuda.destroy_stream(s)

@@ -90,3 +90,58 @@ def test_stack_rejects_a_bad_layer_before_launching(cuda, layers):
     assert np.array_equal(cuda.download(dh, (T, H), np.float32), h0)
     for p in (ws, dh):
         cuda.free_device(p)
+
+
+def test_graph_keeps_its_counters_after_its_stream_is_gone(cuda, layers):
+    # A graph holds its own routing arrival counters for its whole life: its
+    # capture stream destroyed, a stream created afterwards (which would have
+    # taken the freed counters) routes while the graph replays on a third
+    # stream, with no ordering between the two; both stay bit-exact with the
+    # eager result.
+    T = 8
+    h0 = _fp32(T * H, 990).reshape(T, H)
+    st = lp.MoeStack(cuda, [L.desc for L in layers])
+    s = cuda.stream()
+    ws_g, ws_e = cuda.alloc_device(st.ws_bytes(T)), cuda.alloc_device(st.ws_bytes(T))
+    dg, de, saved = cuda.upload(h0), cuda.upload(h0), cuda.upload(h0)
+    cuda.sync()
+    st.forward(de, T, ws_e)
+    cuda.sync()
+    want = cuda.download(de, (T, H), np.float32)
+    g = st.capture(dg, T, ws_g, s)
+    cuda.destroy_stream(s)
+    s2, s3 = cuda.stream(), cuda.stream()
+    for rep in range(4):
+        cuda.dtod_async(dg, saved, h0.nbytes, s3)
+        cuda.dtod_async(de, saved, h0.nbytes, s2)
+        cuda.sync()
+        g.launch(s3)
+        st.forward(de, T, ws_e, s2)
+        cuda.sync()
+        got_g = cuda.download(dg, (T, H), np.float32)
+        got_e = cuda.download(de, (T, H), np.float32)
+        assert np.array_equal(got_g.view(np.uint32), want.view(np.uint32)), rep
+        assert np.array_equal(got_e.view(np.uint32), want.view(np.uint32)), rep
+    g.close()
+    for p in (ws_g, ws_e, dg, de, saved):
+        cuda.free_device(p)
+    cuda.destroy_stream(s2)
+    cuda.destroy_stream(s3)
+
+
+def test_stack_rejects_a_short_workspace(cuda, layers):
+    T = 8
+    h0 = _fp32(T * H, 991).reshape(T, H)
+    st = lp.MoeStack(cuda, [L.desc for L in layers])
+    ws = cuda.alloc_device(st.ws_bytes(T) - 256)
+    dh = cuda.upload(h0)
+    s = cuda.stream()
+    with pytest.raises(lp.LpError, match="workspace"):
+        st.forward(dh, T, ws)
+    with pytest.raises(lp.LpError, match="workspace"):
+        st.capture(dh, T, ws, s)
+    cuda.sync()
+    assert np.array_equal(cuda.download(dh, (T, H), np.float32), h0)
+    for p in (ws, dh):
+        cuda.free_device(p)
+    cuda.destroy_stream(s)

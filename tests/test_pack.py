@@ -69,3 +69,51 @@ def test_not_a_pack(tmp_path):
     path.write_bytes(b"\0" * 8192)
     with pytest.raises(lp.LpError):
         lp.Pack(str(path))
+
+
+def _raw_pack(path, meta_json: bytes, index=None, blobs_end=12288):
+    """A hand-made pack: header with the given metadata text, then the index
+    entries given (offset, nbytes), then zeros up to blobs_end."""
+    head = bytearray(4096)
+    head[:8] = b"LLMPK1\0\0"
+    head[8:16] = struct.pack("<II", 1, len(meta_json))
+    head[16:16 + len(meta_json)] = meta_json
+    body = bytearray(max(blobs_end - 4096, 0))
+    for i, (off, nb) in enumerate(index or []):
+        body[16 * i:16 * i + 16] = struct.pack("<QQ", off, nb)
+    path.write_bytes(bytes(head) + bytes(body))
+    return str(path)
+
+
+def _meta(layers, experts):
+    return ('{"model":"m","num_layers":%s,"experts_per_layer":%s,"dtype":"q4g32-gud"}' % (layers, experts)).encode()
+
+
+def test_malformed_metadata_is_an_error_not_an_abort(tmp_path):
+    """PackMeta (pack.rs:29-48) holds both counts as u16: text that is not an
+    unsigned integer, or a value past 65535, is refused with an error (the
+    C ABI never throws through its callers)."""
+    ok = _raw_pack(tmp_path / "ok.llmpk", _meta(1, 1), [(8192, 100)])
+    lp.Pack(ok).close()
+    for layers, experts in (('"x"', 1), ("true", 1), ("-1", 1), ("1.5", 1), ("1e3", 1), (1, "null"),
+                            (70000, 1), (1, 65536), ("99999999999999999999999", 1), (0, 1), (1, 0)):
+        p = _raw_pack(tmp_path / "bad.llmpk", _meta(layers, experts), [(8192, 100)])
+        with pytest.raises(lp.LpError):
+            lp.Pack(p)
+
+
+def test_oversized_counts_and_bad_index_rejected(tmp_path):
+    """Counts that fit u16 but whose index the file cannot hold, and index
+    entries outside the file or off the 4096 grid, are refused at open."""
+    # 65535 x 65535 entries (64 GiB of index) in a 12 KiB file
+    p = _raw_pack(tmp_path / "big.llmpk", _meta(65535, 65535))
+    with pytest.raises(lp.LpError, match="shorter than its index"):
+        lp.Pack(p)
+    for entry in ((4096, 10),          # inside the index
+                  (8192 + 512, 10),    # not 4096-aligned
+                  (8192, 8192),        # runs past the end of the file
+                  (1 << 62, 10),       # far outside
+                  (8192, 1 << 63)):    # absurd length
+        p = _raw_pack(tmp_path / "idx.llmpk", _meta(1, 1), [entry])
+        with pytest.raises(lp.LpError, match="index entry 0"):
+            lp.Pack(p)
