@@ -31,6 +31,22 @@ __device__ __forceinline__ uint32_t ordered_key(float f) {
 // div_scale, a reciprocal refined by fused multiply-adds, div_fmas, div_fixup).
 __device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
 
+// Data handed between workgroups of one launch: stores that write through to
+// agent scope (sc1) and loads that read at agent scope, so that a relaxed
+// arrival counter orders them without an L2 write-back or invalidate.
+template <typename T>
+__device__ __forceinline__ void store_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void store_agent(LP_GLOBAL T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_agent(const LP_GLOBAL T* p) {
+    return __hip_atomic_load(const_cast<LP_GLOBAL T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -244,7 +260,7 @@ __device__ __forceinline__ void router_dot(const RouteArgs& a, int e, int t0, in
     for (int t = 0; t < kRouterTokBlock; ++t) {
         float v = acc[t];
         for (int o = 32; o >= 1; o >>= 1) v += shfl_xor(v, o);
-        if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * E + e] = v;
+        if (lane == 0 && t < nt) store_agent(&logits[(size_t)(t0 + t) * E + e], v);
     }
 }
 
@@ -357,7 +373,8 @@ __device__ __forceinline__ void router_block(const RouteArgs& a, float* xs, int 
             const int e = e0 + wave * kRouteEPW + j;
 #pragma unroll
             for (int t = 0; t < kRouterTokBlock; ++t)
-                if (lane == 0 && e < E && t < nb) logits[(size_t)(t0 + tt + t) * E + e] = red[j * kRouterTokBlock + t];
+                if (lane == 0 && e < E && t < nb)
+                    store_agent(&logits[(size_t)(t0 + tt + t) * E + e], red[j * kRouterTokBlock + t]);
         }
     }
 }
@@ -431,7 +448,7 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
         const int i = lane + 64 * q;
-        v[q] = i < E ? lg[i] : 0.0f;
+        v[q] = i < E ? load_agent(lg + i) : 0.0f;
         key[q] = 0u;
         val[q] = 0.0f;
     }
@@ -570,12 +587,12 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
     }
     if (lane < k) {
         const int id = lane < kept ? out_pick : -1;
-        gptr_w<int>(a.W.ids)[(size_t)t * k + lane] = id;
-        gptr_w<float>(a.W.wts)[(size_t)t * k + lane] = lane < kept ? out_w : 0.0f;
+        store_agent(gptr_w<int>(a.W.ids) + (size_t)t * k + lane, id);
+        store_agent(gptr_w<float>(a.W.wts) + (size_t)t * k + lane, lane < kept ? out_w : 0.0f);
         if (ids_l) ids_l[t * k + lane] = id;
     }
     if (lane == 0) {
-        gptr_w<int>(a.W.cnt)[t] = kept;
+        store_agent(gptr_w<int>(a.W.cnt) + t, kept);
         if (cnt_l) cnt_l[t] = kept;
     }
 }
@@ -666,8 +683,10 @@ __device__ __forceinline__ void write_shared_table(const RouteArgs& a, int tid, 
     }
 }
 
+// in_global: ids_in / cnt_in are the workspace's (written by other
+// workgroups of this launch: read at agent scope), else LDS copies.
 __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, const int* ids_in,
-                                             const int* cnt_in, const int* slots_in) {
+                                             const int* cnt_in, const int* slots_in, bool in_global) {
     // T <= kTopkDispatchMaxT <= 64: expert e's picks are the set bits of
     // its token mask (a token picks an expert at most once), its count is
     // the mask's popcount and a pick's rank among them the bits below its
@@ -689,8 +708,8 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     LP_GLOBAL int* meta = gptr_w<int>(a.W.meta);
     // the picks and the slot table in LDS (one round trip when they are in
     // memory), the masks and first tokens cleared
-    for (int i = tid; i < P; i += nth) ids[i] = ids_in[i];
-    for (int i = tid; i < T; i += nth) cnt[i] = cnt_in[i];
+    for (int i = tid; i < P; i += nth) ids[i] = in_global ? load_agent(gptr<int>((uint64_t)ids_in) + i) : ids_in[i];
+    for (int i = tid; i < T; i += nth) cnt[i] = in_global ? load_agent(gptr<int>((uint64_t)cnt_in) + i) : cnt_in[i];
     for (int e = tid; e < E; e += nth) {
         slots[e] = slots_in[e];
         mlo[e] = 0u;
@@ -869,7 +888,7 @@ __device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids
 // over the picks in memory, one workgroup of 256.
 extern "C" __global__ void __launch_bounds__(256) lp_moe_dispatch(const RouteArgs a) {
     __shared__ __align__(16) uint8_t sm[kDispatchSmem];
-    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table));
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), dptr<const int>(a.L.slot_table), true);
 }
 
 // ---------------------------------------------------------------------------
@@ -1046,7 +1065,7 @@ extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const Ro
     float* sv = reinterpret_cast<float*>(sm) + wave * kMaxExperts;
     for (int t = wave; t < a.T; t += nw) topk_any(a, t, sv, ids_l, cnt_l);
     __syncthreads();
-    dispatch_all(a, sm, ids_l, cnt_l, slots_l);
+    dispatch_all(a, sm, ids_l, cnt_l, slots_l, false);
 }
 
 // ---------------------------------------------------------------------------
@@ -1057,34 +1076,26 @@ extern "C" __global__ void __launch_bounds__(1024) lp_moe_topk_dispatch(const Ro
 // for the tokens of block b (8b .. 8b+7).  The last workgroup of block b to
 // finish (an arrival counter) ranks the block's tokens, one per wave, while
 // the others write the block's fragment images (make_xf); the last block to
-// finish ranking builds the dispatch tables.  Release fences before each
-// arrival and acquire fences after it make the other workgroups' logits and
-// picks visible; the last arrival resets its counter, so every launch finds
-// them zero.
+// finish ranking builds the dispatch tables.  Logits and picks cross between
+// workgroups as agent-scope stores and loads (arrival_order); the last
+// arrival resets its counter, so every launch finds them zero.
 // ---------------------------------------------------------------------------
 namespace {
 
 // Add one arrival at *cnt; returns (in every thread) the workgroup's arrival
 // order, n - 1 for the last, which also resets the counter.  Every thread of
-// the workgroup must call it.  Each wave first waits until its own stores
-// have completed (reached this XCD's L2: the barrier alone does not wait for
-// global stores), then thread 0 alone carries them to agent scope: an
-// agent-scope release writes back the whole L2, and one per workgroup
-// instead of one per wave took 8 us off a 64-workgroup launch.  Thread 0 of
-// the last arrival likewise acquires for the workgroup before the second
-// barrier.
+// the workgroup must call it.  What one workgroup hands to another across an
+// arrival (logits, then picks) is written with agent-scope stores (they
+// write through this XCD's L2) and read with agent-scope loads, so each wave
+// only waits until its own stores have completed before the barrier and a
+// relaxed counter orders the rest: no L2 write-back or invalidate (each of
+// those costs microseconds).
 __device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt, expcnt and lgkmcnt all zero
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed at agent scope
     __syncthreads();
     if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __builtin_amdgcn_s_waitcnt(0);  // the L2 write-back done before the arrival counts
         const int o = atomicAdd(cnt, 1);
-        if (o == n - 1) {
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __builtin_amdgcn_s_waitcnt(0);  // the invalidate done before any wave loads
-        }
+        if (o == n - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = o;
     }
     __syncthreads();
@@ -1155,12 +1166,12 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         if (a.T * a.L.top_k <= kDispatchWaveMaxPicks) {
             if (wave == 0) dispatch_wave(a, ids_l, cnt_l, slots_l);
         } else {
-            dispatch_all(a, sm, ids_l, cnt_l, slots_l);
+            dispatch_all(a, sm, ids_l, cnt_l, slots_l, false);
         }
         return;
     }
     if (!last_arrival(cnt + 8, gridDim.y, &flag)) return;
-    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l);
+    dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l, true);
 }
 
 extern "C" __global__ void __launch_bounds__(512) lp_moe_route_fused(const RouteArgs a) { route_fused_body<kMaxExperts / 64>(a); }
