@@ -341,6 +341,80 @@ def zipf_trace(layers: int, tokens: int, E: int, k: int, s: float = P_ZIPF, seed
     return out
 
 
+def run_paged_batch(cuda, s, host, layers: int, trace: np.ndarray, B: int, slots: int, io_threads: int,
+                    stage_threads: int) -> dict:
+    """Config 4 in lockstep batches of B tokens (the reference's step_multi,
+    decode.rs:431-532): per layer the batch's picks (the trace's), their
+    union sorted by expert id, fetched and computed in waves of `slots`
+    experts (decode.rs:483-531): request the wave from the pager, re-resolve
+    the expert table, lp_moe_experts_wave (each token's picks inside the
+    wave added into h once), release after the stream passes.  A cold pager
+    over the same pageable host pack."""
+    import llmpager_amd as lp
+    blob = lp.blob_bytes(P_H, P_I, P_G)
+    cfg = lp.PagerConfig(layers=layers, experts_per_layer=P_E, slots_per_layer=slots, decay_interval=256,
+                         blob_bytes=blob, span=0, host_blobs=host.ctypes.data, host_stride=align(blob),
+                         copy_streams=1, global_pool=0, source=lp.PAGER_SRC_HOST, io_threads=io_threads,
+                         ring_slots=2, stage_threads=stage_threads)
+    pg = lp.Pager(cuda, cfg)
+    go, uo, do = lp.blob_offsets(P_H, P_I, P_G)
+    d_rw = cuda.upload(lp.synth_bf16(P_E * P_H, 0.02, 0, 1000), s)   # unused by route_logits
+    descs = [lp.LayerDesc(hidden=P_H, inter=P_I, experts=P_E, top_k=P_K, group=P_G, gating=lp.GATING_SOFTMAX,
+                          renorm=1, routed_scaling=1.0, min_weight=0.0, router_w=d_rw, router_bias=0,
+                          slot_table=pg.slot_table(l), arena_base=pg.arena, slot_span=pg.span,
+                          gate_off=go, up_off=uo, down_off=do) for l in range(layers)]
+    moe = [lp.MoeLayer(cuda, d) for d in descs]
+    tokens = trace.shape[0] // B * B
+    steps = tokens // B
+    lg = np.zeros((tokens, layers, P_E), np.float32)
+    np.put_along_axis(lg, trace[:tokens].astype(np.int64), (16.0 - np.arange(P_K, dtype=np.float32))[None, None, :],
+                      axis=2)
+    # [step][layer][token][E]: one route_logits call per (step, layer)
+    dlg = cuda.upload(np.ascontiguousarray(lg.reshape(steps, B, layers, P_E).transpose(0, 2, 1, 3)), s)
+    ws = cuda.alloc_device(lp.ws_layout(descs[0], B).total)
+    dx = cuda.upload(lp.synth_f32_bf16(B * P_H, 1.0, 0, 3), s)
+    dh = cuda.upload(lp.synth_f32_bf16(B * P_H, 1.0, 0, 4), s)
+    cuda.sync()
+    unions = [[sorted(set(int(e) for e in trace[st * B:(st + 1) * B, l].ravel())) for l in range(layers)]
+              for st in range(steps)]
+    n_waves = 0
+    t0 = time.time()
+    for st in range(steps):
+        for l in range(layers):
+            moe[l].route_logits(dlg + ((st * layers + l) * B * P_E) * 4, B, ws, s)
+            U = unions[st][l]
+            for u0 in range(0, len(U), slots):
+                wave = U[u0:u0 + slots]
+                got = pg.request(l, wave, s)
+                moe[l].resolve(B, ws, s)
+                moe[l].experts_wave(dx, dh, B, ws, u0, len(wave), False, s)
+                pg.release_after(got, s)
+                n_waves += 1
+        pg.tick()
+    cuda.sync()
+    pg.sync()
+    sec = time.time() - t0
+    m = pg.metrics()
+    uq, err = moe[-1].status(ws, B, s)
+    pg.close()
+    for p in (dlg, ws, dx, dh, d_rw):
+        cuda.free_device(p)
+    assert err == 0, f"paged batch decode reported error flags {err}"
+    assert uq == len(unions[-1][-1]), "the device's union differs from the trace's"
+    lookups = m["hits"] + m["misses"]
+    mean_union = float(np.mean([len(U) for row in unions for U in row]))
+    res = dict(
+        batch=B, steps=steps, tokens=tokens, tok_s=tokens / sec, seconds=sec, waves=n_waves,
+        waves_per_layer=n_waves / (steps * layers), mean_union=mean_union, hits=m["hits"], misses=m["misses"],
+        hit_rate=m["hits"] / max(lookups, 1), bytes_fetched=m["bytes_fetched"],
+        h2d_gbps=m["bytes_fetched"] / sec / 1e9, stalls=m["stalls"],
+        hbm_gbps=steps * layers * mean_union * (blob - 32) / sec / 1e9,
+    )
+    log(f"paged B={B} ({layers} layers, {slots} slots): {res['tok_s']:.1f} tok/s, {res['waves_per_layer']:.2f} "
+        f"waves per layer (union {mean_union:.1f}), hit rate {res['hit_rate']:.4f}, H2D {res['h2d_gbps']:.1f} GB/s")
+    return res
+
+
 def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4, stage_threads: int = 4) -> dict:
     """Workload config 4: H4096 / I1536 / E128 / top-8 / g32, `layers` layers,
     `slots` VRAM expert slots per layer; every expert blob sits in pageable
@@ -407,8 +481,10 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4
     pg.close()
     for p in (dlg, ws, dx, dh, d_rw):
         cuda.free_device(p)
-    del host
     assert err == 0, f"paged decode reported error flags {err}"
+    # the same trace in lockstep batches of 32, each layer's union in waves
+    batch = run_paged_batch(cuda, s, host, layers, trace, 32, slots, io_threads, stage_threads)
+    del host
     lookups = m["hits"] + m["misses"]
     # the experts' weights and scales (the trace replaces the router GEMV)
     compute_bytes = tokens * layers * P_K * (blob - 32)
@@ -421,6 +497,7 @@ def run_paged(cuda, s, layers: int, tokens: int, slots: int, io_threads: int = 4
         h2d_gbps=m["bytes_fetched"] / sec / 1e9, stalls=m["stalls"],
         fetch_latency_ms_buckets=dict(zip(("<1", "<2", "<5", "<10", "<20", "<50", ">=50"), m["latency_ms_buckets"])),
         hbm_gbps=compute_bytes / sec / 1e9,
+        batch32=batch,
     )
     log(f"paged ({layers} layers, {slots} slots, {tokens} tokens): {res['tok_s']:.1f} tok/s, hit rate "
         f"{res['hit_rate']:.4f}, {res['misses']} misses, H2D {res['h2d_gbps']:.1f} GB/s")

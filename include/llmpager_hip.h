@@ -265,6 +265,21 @@ int lp_moe_route_logits(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t logits
  * in pick order.  x and h 16-byte aligned. */
 int lp_moe_experts(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t workspace, uint64_t ws_bytes, lp_stream s);
+/* One wave of a paged multi-token step (decode.rs:483-531; Kimi
+ * kimi.rs:965-1021): when a layer's union of picked experts exceeds its slots,
+ * the reference fetches it in waves (`union.chunks(wave)`, the union sorted by
+ * expert id) and, per wave, adds each token's picks inside the wave, summed in
+ * pick order, into h once.  After lp_moe_route* (and, per wave, the pager's
+ * requests for the wave's experts and lp_moe_resolve): the routed experts
+ * uniq[u_first, u_first + u_count) of the dispatch's unique list (the `uniq`
+ * part of the workspace, ascending ids; its length is meta[0]) are computed
+ * and h[t] += sum over token t's picks among them; tokens with none are left
+ * as they are.  with_shared != 0 also adds the shared MLP's output after the
+ * routed sum (pass it with the last wave, as the reference adds the shared
+ * MLP after the routed part, kimi.rs:779).  x must not be h (every wave reads
+ * the same input); decode batches only (T <= 64). */
+int lp_moe_experts_wave(lp_ctx* ctx, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T, uint64_t workspace,
+                        uint64_t ws_bytes, int u_first, int u_count, int with_shared, lp_stream s);
 /* Paged flow (decode.rs:305-331 order: route, then request the picks, then
  * compute): after lp_moe_route* and the pager's requests for the picked
  * experts, re-resolve the expert table's blob addresses through the layer's

@@ -123,6 +123,7 @@ def _sig(lib):
         "lp_moe_route": (i32, [vp, P(LayerDesc), u64, i32, u64, u64, vp]),
         "lp_moe_route_logits": (i32, [vp, P(LayerDesc), u64, i32, u64, u64, vp]),
         "lp_moe_experts": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, u64, vp]),
+        "lp_moe_experts_wave": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, u64, i32, i32, i32, vp]),
         "lp_moe_resolve": (i32, [vp, P(LayerDesc), i32, u64, u64, vp]),
         "lp_moe_forward": (i32, [vp, P(LayerDesc), u64, u64, i32, u64, u64, vp]),
         "lp_moe_forward_noalloc": (i32, [vp, P(LayerDesc), u64, u64, i32, vp]),
@@ -702,6 +703,13 @@ class MoeLayer:
     def forward(self, x: int, h: int, T: int, ws: int, stream=None, ws_bytes: int | None = None) -> None:
         _check(lib().lp_moe_forward(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, _ws_bytes(ws, ws_bytes),
                                     stream))
+
+    def experts_wave(self, x: int, h: int, T: int, ws: int, u_first: int, u_count: int, with_shared: bool,
+                     stream=None, ws_bytes: int | None = None) -> None:
+        """lp_moe_experts_wave: the routed experts uniq[u_first : u_first +
+        u_count] of one wave of a paged union (decode.rs:483-531)."""
+        _check(lib().lp_moe_experts_wave(self.cuda.ctx, C.byref(self.desc), x, h, T, ws, _ws_bytes(ws, ws_bytes),
+                                         u_first, u_count, int(with_shared), stream))
 
     def forward_noalloc(self, x: int, h: int, T: int, stream=None) -> None:
         """lp_moe_forward_noalloc: the layer with the library's built-in

@@ -2033,10 +2033,11 @@ lp_moe_down_wide(const GroupedArgs a) {
 // fused multiply-adds, then one add (q4g64.cu:84-99); with a shared MLP its
 // output is added after that, unweighted (kimi.rs:779).  Grid (ceil(H/1024),
 // T): four columns per thread, eight picks' rows loaded before their FMAs;
-// picks past cnt load pick 0's row with weight 0, which leaves the sum as it
-// is.  The pick count, the first eight picks' rows and weights (in bounds
-// whatever the count), the residual and the shared output are loaded
-// together, so the picked rows are the only dependent round trip.
+// picks past cnt (or, for one wave of a paged union, outside it) add zeros
+// with weight 0, which leaves the sum as it is.  The pick count, the first
+// eight picks' rows and weights (in bounds whatever the count), the residual
+// and the shared output are loaded together, so the picked rows are the only
+// dependent round trip.
 // ---------------------------------------------------------------------------
 extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedArgs a) {
     const int t = blockIdx.y;
@@ -2059,27 +2060,36 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
             wv[q] = w[q];
         }
     }
+    // one wave of the union (decode.rs:489-531): only picks whose dispatch
+    // position lies in the wave's experts' range [p0, p1)
+    int p0 = 0, p1 = 0x7fffffff;
+    if (a.wave_n > 0) {
+        const int u1 = min(a.wave_u0 + a.wave_n, gptr<int>(a.W.meta)[0]);
+        const LP_GLOBAL int* uq = gptr<int>(a.W.uniq);
+        const LP_GLOBAL int* gs = gptr<int>(a.W.gs);
+        p0 = a.wave_u0 < u1 ? gs[uq[a.wave_u0]] : 0;
+        p1 = a.wave_u0 < u1 ? gs[uq[u1 - 1] + 1] : 0;
+    }
     float4 v = *h;
     float4 sy = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (a.L.shared_blob)
         sy = *reinterpret_cast<const LP_GLOBAL float4*>(gptr<float>(a.W.sh_y) + (size_t)t * H + i);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    bool any = false;
     if (c > 0) {
-        const int row0 = iv[0];
         for (int j0 = 0; j0 < c; j0 += 8) {
             float4 yv[8];
             float wl[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 const int j = j0 + q;
-                const bool live = j < c;
-                int r = row0;
-                wl[q] = 0.0f;
-                if (live) {
-                    r = j0 == 0 ? iv[q] : inv[j];
-                    wl[q] = j0 == 0 ? wv[q] : w[j];
-                }
-                yv[q] = *reinterpret_cast<const LP_GLOBAL float4*>(y + (size_t)r * H);
+                int r = 0;
+                if (j < c) r = j0 == 0 ? iv[q] : inv[j];
+                const bool live = j < c && r >= p0 && r < p1;
+                any |= live;
+                wl[q] = live ? (j0 == 0 ? wv[q] : w[j]) : 0.0f;
+                yv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (live) yv[q] = *reinterpret_cast<const LP_GLOBAL float4*>(y + (size_t)r * H);
             }
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -2090,10 +2100,14 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_combine(const GroupedAr
             }
         }
     }
-    v.x = v.x + acc.x;
-    v.y = v.y + acc.y;
-    v.z = v.z + acc.z;
-    v.w = v.w + acc.w;
+    // a wave without any of this token's picks leaves its row as it is
+    if (!any && a.wave_n > 0 && !a.L.shared_blob) return;
+    if (any || a.wave_n == 0) {
+        v.x = v.x + acc.x;
+        v.y = v.y + acc.y;
+        v.z = v.z + acc.z;
+        v.w = v.w + acc.w;
+    }
     if (a.L.shared_blob) {
         v.x = v.x + sy.x;
         v.y = v.y + sy.y;

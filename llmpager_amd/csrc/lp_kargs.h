@@ -299,6 +299,8 @@ struct GroupedArgs {
     int32_t maxu;        // expert-table entries (balanced kernels)
     int32_t sh_fused;    // lp_moe_down_comb_rs: also the shared MLP's down (its act row in W.sh_act)
     int32_t sh_maxu;     // balanced gate/up: the shared MLP's W.sh_et entries taken after the routed ones
+    int32_t wave_u0;     // combine of one wave (wave_n > 0): the routed experts uniq[wave_u0 ..
+    int32_t wave_n;      //   wave_u0 + wave_n) only; tokens without a pick among them are left as they are
     int32_t pad0;
 };
 

@@ -1229,12 +1229,19 @@ static int shared_ffn(lp_ctx* c, const lp_moe_layer_desc* d, const GroupedArgs& 
 
 // The grouped expert kernels and the combine; the fragment images of x are
 // written first unless the router kernel of lp_moe_forward already did.
-static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
-                        uint64_t ws, uint64_t ws_bytes, lp_stream s, bool have_images) {
-    if (int r = check_desc(c, d, T)) return r;
-    if (int r = check_ws(d, T, ws, ws_bytes)) return r;
+// wave_n > 0: only the routed experts uniq[wave_u0, wave_u0 + wave_n) (one
+// wave of a paged union), the shared MLP only when wave_shared.
+static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d0, uint64_t x, uint64_t h, int T,
+                        uint64_t ws, uint64_t ws_bytes, lp_stream s, bool have_images, int wave_u0 = 0,
+                        int wave_n = 0, bool wave_shared = true) {
+    if (int r = check_desc(c, d0, T)) return r;
+    if (int r = check_ws(d0, T, ws, ws_bytes)) return r;
     if (x % 16) return fail(LP_E_UNSUPPORTED, "x must be 16-byte aligned");
     if (h % 16) return fail(LP_E_UNSUPPORTED, "h must be 16-byte aligned");
+    const bool wave = wave_n > 0;
+    lp_moe_layer_desc dw = *d0;
+    if (wave && !wave_shared) dw.shared_blob = 0;
+    const lp_moe_layer_desc* d = &dw;
     if (!have_images) {
         RouteArgs ra{};
         fill_views(d, ws, T, &ra.L, &ra.W);
@@ -1248,6 +1255,14 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
     ga.x = x;
     ga.h = h;
     ga.T = T;
+    // the routed experts this call computes: every entry, or one wave's
+    const int maxu_all = std::min(T * d->top_k, d->experts);
+    if (wave) {
+        ga.W.et += (uint64_t)wave_u0 * sizeof(ExpertEntry);
+        ga.wave_u0 = wave_u0;
+        ga.wave_n = wave_n;
+    }
+    const int maxu = wave ? wave_n : maxu_all;
     const int H = d->hidden;
     const int Is = d->shared_blob ? d->shared_inter : 0;
     // Token pairs staged at once: enough for T tokens on one expert, bounded
@@ -1263,7 +1278,7 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         return fail(LP_E_UNSUPPORTED, "hidden/inter too large for one LDS fragment pair");
     ga.pairs_cap = cap;
     bool sh_gu = false;  // the shared MLP's gate/up done by the routed launch
-    if (use_gemm(d, T)) {
+    if (!wave && use_gemm(d, T)) {
         if ((size_t)kGemmLds > c->max_lds) return fail(LP_E_UNSUPPORTED, "GEMM stages exceed the LDS");
         // the GEMM loads address images and weights as 32-bit offsets from a base
         const uint64_t img_span = std::max((uint64_t)T * image_bytes(d->hidden),
@@ -1293,13 +1308,12 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint6
         // whose row it adds)
         const int Si = tile_steps_host(d->inter);
         const bool sl = scales_in_lds(d->group, d->inter);
-        const bool comb = T == 1 && d->top_k <= kCombWaves && Si <= 16 &&
+        const bool comb = !wave && T == 1 && d->top_k <= kCombWaves && Si <= 16 &&
                           (size_t)comb_lds(d->inter, Si, sl) <= c->max_lds;
         // the shared MLP's gate/up rides on the routed balanced launch when
         // the groups agree (sh_gu: it did)
-        const int shm = d->shared_blob && d->shared_group == d->group ? shared_entries(T) : 0;
-        if (int r = grouped_ffn(c, ga, std::min(T * d->top_k, d->experts), true, s, !comb, shm, &sh_gu))
-            return r;
+        const int shm = !wave && d->shared_blob && d->shared_group == d->group ? shared_entries(T) : 0;
+        if (int r = grouped_ffn(c, ga, maxu, true, s, !comb, shm, &sh_gu)) return r;
         if (comb) {
             const Fn f = !sl ? kDownCombRs : Si <= 8 ? kDownComb : kDownComb16;
             // the shared MLP's down on the comb kernel's idle waves: per-lane
@@ -1336,6 +1350,18 @@ int lp_moe_resolve(lp_ctx* c, const lp_moe_layer_desc* d, int T, uint64_t ws, ui
 int lp_moe_experts(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,
                    uint64_t ws, uint64_t ws_bytes, lp_stream s) {
     return experts_impl(c, d, x, h, T, ws, ws_bytes, s, false);
+}
+
+int lp_moe_experts_wave(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T, uint64_t ws,
+                        uint64_t ws_bytes, int u_first, int u_count, int with_shared, lp_stream s) {
+    if (int r = check_desc(c, d, T)) return r;
+    if (u_first < 0 || u_count <= 0 || u_first + u_count > std::min(T * d->top_k, d->experts))
+        return fail(LP_E_INVALID, "lp_moe_experts_wave: the wave must be a non-empty range of the unique list");
+    if (T > kTopkDispatchMaxT || use_gemm(d, T))
+        return fail(LP_E_UNSUPPORTED, "lp_moe_experts_wave: decode batches only (at most 64 tokens, the grouped "
+                                      "kernels' workspace)");
+    if (x == h) return fail(LP_E_INVALID, "lp_moe_experts_wave: x must not be h (every wave reads the same x)");
+    return experts_impl(c, d, x, h, T, ws, ws_bytes, s, false, u_first, u_count, with_shared != 0);
 }
 
 int lp_moe_forward(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, uint64_t h, int T,

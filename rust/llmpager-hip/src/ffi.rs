@@ -251,6 +251,10 @@ extern "C" {
         ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, ws_bytes: u64,
         s: lp_stream,
     ) -> c_int;
+    pub fn lp_moe_experts_wave(
+        ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, x: u64, h: u64, t: c_int, ws: u64, ws_bytes: u64,
+        u_first: c_int, u_count: c_int, with_shared: c_int, s: lp_stream,
+    ) -> c_int;
     pub fn lp_moe_resolve(
         ctx: *mut lp_ctx, d: *const lp_moe_layer_desc, t: c_int, ws: u64, ws_bytes: u64, s: lp_stream,
     ) -> c_int;

@@ -249,6 +249,21 @@ impl Kernels {
         check(unsafe { ffi::lp_moe_experts(cuda.ctx, d, x, h, t, ws, ws_bytes, stream) }, "moe_experts")
     }
 
+    /// One wave of a paged union (`decode.rs:483-531`): the routed experts
+    /// `uniq[u_first .. u_first + u_count)` of the dispatch's unique list,
+    /// each token's picks among them summed in pick order and added into `h`
+    /// once; `with_shared` adds the shared MLP after them (the last wave).
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_experts_wave(
+        &self, cuda: &Cuda, d: &lp_moe_layer_desc, x: CUdeviceptr, h: CUdeviceptr, t: i32, ws: CUdeviceptr,
+        ws_bytes: u64, u_first: i32, u_count: i32, with_shared: bool, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_moe_experts_wave(cuda.ctx, d, x, h, t, ws, ws_bytes, u_first, u_count, with_shared as i32, stream)
+        };
+        check(rc, "moe_experts_wave")
+    }
+
     /// One whole MoE layer: route, gate/up, SiLU, down, weighted combine
     /// into `h` (`x` = the normalised input, f32 [t, hidden]).
     #[allow(clippy::too_many_arguments)]

@@ -215,3 +215,107 @@ def test_paged_stack_config4_shape(cuda):
         cuda.free_device(p)
     cuda.destroy_stream(s)
     cuda.free_pinned(pin)
+
+
+def _union_waves(cuda, moe, ws, lay, T, k, wave):
+    """The routed union (the dispatch's unique list) and its waves."""
+    cuda.sync()
+    nu = int(cuda.download(ws + lay.meta, (1,), np.int32)[0])
+    uniq = cuda.download(ws + lay.uniq, (nu,), np.int32)
+    ids = cuda.download(ws + lay.ids, (T, k), np.int32)
+    cnt = cuda.download(ws + lay.cnt, (T,), np.int32)
+    want = sorted(set(int(e) for t in range(T) for e in ids[t, :cnt[t]]))
+    assert uniq.tolist() == want        # decode.rs:483-485: sorted, deduplicated
+    return uniq, [(u0, min(wave, nu - u0)) for u0 in range(0, nu, wave)]
+
+
+def test_paged_waves_config4_shape(cuda):
+    # Config 4's shape at 32 tokens with 64 slots per layer: the ~98 experts of
+    # the union do not fit, so the step runs in waves of 64 as decode.rs:489-531
+    # does (request the wave, re-resolve, compute the wave's experts, add each
+    # token's picks inside the wave into h once, release), against the oracle
+    # with the same waves.
+    T, slots, wave = 32, 64, 64
+    blob = lp.blob_bytes(P_H, P_I, P_G)
+    span = align(blob)
+    n = P_E * span
+    pin = cuda.alloc_pinned(n)
+    view = np.ctypeslib.as_array((C.c_uint8 * n).from_address(pin))
+    lp.synth_blobs(P_E, span, P_H, P_I, P_G, 8, 0, out=view)
+    cfg = lp.PagerConfig(layers=1, experts_per_layer=P_E, slots_per_layer=slots, decay_interval=256,
+                         blob_bytes=blob, span=0, host_blobs=pin, host_stride=span, copy_streams=2, global_pool=0)
+    pg = lp.Pager(cuda, cfg)
+    s = cuda.stream()
+    router = lp.synth_bf16(P_E * P_H, 0.02, 8, 1000)
+    d_router = cuda.upload(router)
+    go, uo, do = lp.blob_offsets(P_H, P_I, P_G)
+    desc = lp.LayerDesc(hidden=P_H, inter=P_I, experts=P_E, top_k=P_K, group=P_G, gating=lp.GATING_SOFTMAX,
+                        renorm=1, routed_scaling=1.0, router_w=d_router, slot_table=pg.slot_table(0),
+                        arena_base=pg.arena, slot_span=pg.span, gate_off=go, up_off=uo, down_off=do)
+    moe = lp.MoeLayer(cuda, desc)
+    lay = lp.ws_layout(desc, T)
+    ws = cuda.alloc_device(lay.total)
+    x = fp32_normal(T * P_H, 801).reshape(T, P_H)
+    h = fp32_normal(T * P_H, 802).reshape(T, P_H)
+    dx, dh = cuda.upload(x), cuda.upload(h)
+    moe.route(dx, T, ws, s)
+    uniq, waves = _union_waves(cuda, moe, ws, lay, T, P_K, wave)
+    assert len(waves) == 2 and len(uniq) > slots
+    glog = cuda.download(ws + lay.logits, (T, P_E), np.float32)
+    with pytest.raises(lp.LpError):
+        moe.experts_wave(dh, dh, T, ws, 0, 4, False, s)         # x aliasing h is refused
+    for i, (u0, nw) in enumerate(waves):
+        got = pg.request(0, uniq[u0:u0 + nw].tolist(), s)
+        moe.resolve(T, ws, s)
+        moe.experts_wave(dx, dh, T, ws, u0, nw, i == len(waves) - 1, s)
+        pg.release_after(got, s)
+    cuda.sync_stream(s)
+    out = cuda.download(dh, (T, P_H), np.float32)
+    assert moe.status(ws, T, s)[1] == 0
+    odesc = dict(hidden=P_H, inter=P_I, experts=P_E, top_k=P_K, group=P_G, gating=0, renorm=True,
+                 routed_scaling=1.0, min_weight=0.0, router_w=router, router_bias=None, offsets=(go, uo, do))
+    blobs = [view[e * span:e * span + blob] for e in range(P_E)]
+    want = O.moe_layer(odesc, blobs, x, h.copy(), logits_in=glog, wave=wave, threads=8)[0]
+    assert rel_l2(out - h, want - h) <= 1e-3
+    m = pg.metrics()
+    assert m["misses"] == len(uniq)
+    pg.sync()
+    pg.close()
+    for p in (d_router, ws, dx, dh):
+        cuda.free_device(p)
+    cuda.destroy_stream(s)
+    cuda.free_pinned(pin)
+
+
+@pytest.mark.parametrize("T,wave", [(5, 3), (16, 2)])
+def test_waves_with_shared_mlp(cuda, T, wave):
+    # every expert resident; the union computed wave by wave, the shared MLP
+    # added with the last wave (kimi.rs:779), against the oracle's waves; a
+    # token with no pick in a wave is left untouched by it
+    L = DeviceLayer(cuda, H=128, I=64, E=8, k=2, group=32, seed=14, router_std=0.2, shared=(128, 64))
+    lay = lp.ws_layout(L.desc, T)
+    ws = cuda.alloc_device(lay.total)
+    x = fp32_normal(T * 128, 900 + T).reshape(T, 128)
+    h = fp32_normal(T * 128, 901 + T).reshape(T, 128)
+    dx, dh = cuda.upload(x), cuda.upload(h)
+    L.layer.route(dx, T, ws)
+    uniq, waves = _union_waves(cuda, L.layer, ws, lay, T, 2, wave)
+    assert len(waves) >= 2
+    glog = cuda.download(ws + lay.logits, (T, 8), np.float32)
+    ids = cuda.download(ws + lay.ids, (T, 2), np.int32)
+    for i, (u0, nw) in enumerate(waves):
+        before = cuda.download(dh, (T, 128), np.float32)
+        L.layer.experts_wave(dx, dh, T, ws, u0, nw, i == len(waves) - 1)
+        after = cuda.download(dh, (T, 128), np.float32)
+        if i < len(waves) - 1:
+            idle = [t for t in range(T) if not set(ids[t].tolist()) & set(uniq[u0:u0 + nw].tolist())]
+            for t in idle:
+                assert np.array_equal(before[t].view(np.uint32), after[t].view(np.uint32)), t
+    out = cuda.download(dh, (T, 128), np.float32)
+    assert L.layer.status(ws, T)[1] == 0
+    want = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h.copy(), logits_in=glog, wave=wave, threads=8,
+                       shared_blob=L.shared)[0]
+    assert rel_l2(out - h, want - h) <= 1e-3
+    for p in (ws, dx, dh):
+        cuda.free_device(p)
+    L.free()
