@@ -45,13 +45,32 @@ GATEUP_KERNELS = ("lp_moe_gateup", "lp_moe_gateup_bal", "lp_moe_gateup_bal_sh", 
 DOWN_KERNELS = ("lp_moe_down", "lp_moe_down_wide", "lp_moe_down_bal", "lp_moe_down_bal6", "lp_moe_down_comb",
                 "lp_moe_down_comb16")
 CALIB_BYTES = 256 << 20   # one plain device copy of known size: the PMC byte-counter calibration
-# HBM bytes per dominant-kernel launch at B = 32 (FETCH_SIZE + WRITE_SIZE,
-# each scaled by the factor the same counter reads for the calibration copy),
-# from the rocprofv3 --pmc runs recorded in profiles/ for that kernel: the
-# 256 MiB copy reads FETCH_SIZE 131,093 KiB (factor 2.0) and WRITE_SIZE
-# 262,144 KiB (factor 1.0); lp_moe_gateup_bal averages 89,353 and 908 KiB.
-# Re-measure whenever the kernel changes.
-TRAFFIC_B32 = {"lp_moe_gateup_bal": (2 * 89_353 + 908) * 1024}
+# HBM bytes per dominant-kernel launch come from rocprofv3 --pmc runs of this
+# bench (FETCH_SIZE, then WRITE_SIZE, each scaled by the factor the same
+# counter reads for the calibration copy), recorded with the command that
+# made them and the SHA-256 of the kernel source they measured in
+# profiles/traffic.json.  A record whose source hash differs from the kernel
+# source in the tree is stale: traffic is then reported as null.
+TRAFFIC_RECORD = os.path.join(ROOT, "profiles", "traffic.json")
+KERNEL_SOURCE = os.path.join(ROOT, "llmpager_amd", "csrc", "kernels", "lp_moe.hip")
+
+
+def measured_traffic(kernel: str, batch: int):
+    """(bytes per launch, record) for `kernel` at `batch` from the committed
+    counter record, or (None, reason) when there is none for this source."""
+    import hashlib
+    try:
+        rec = json.load(open(TRAFFIC_RECORD))
+    except (OSError, ValueError):
+        return None, "no counter record"
+    sha = hashlib.sha256(open(KERNEL_SOURCE, "rb").read()).hexdigest()
+    for r in rec.get("records", []):
+        if r.get("kernel") == kernel and r.get("batch") == batch:
+            if r.get("source_sha256") != sha:
+                return None, "counter record is for another kernel source"
+            f = r["fetch_kib"] * r["fetch_factor"] + r["write_kib"] * r["write_factor"]
+            return int(round(f * 1024)), r
+    return None, "no counter record for this kernel and batch"
 KERNELS = ("lp_moe_router", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_topk_dispatch", "lp_moe_topk", "lp_moe_dispatch", "lp_moe_disp_count",
            "lp_moe_disp_scan", "lp_moe_disp_scatter", "lp_moe_ximage", *GATEUP_KERNELS, *DOWN_KERNELS,
            "lp_moe_combine")
@@ -562,15 +581,25 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
         graph.close()
         cuda.free_device(hcur)
         sec = cuda.elapsed_ms(e0, e1) / 1e3 / steps
-        L0 = layers[0]
-        L0.forward(h0, h0, B, ws, s)
-        u, err = L0.status(ws, B, s)
-        assert err == 0, f"config-5 step reported error flags {err}"
+        # the measured unique routed experts of every layer of every timed
+        # step (each layer's input the previous layer's output, as timed)
+        hstep = cuda.alloc_device(tok_bytes)
+        counts = []
+        for i in range(steps):
+            cuda.dtod_async(hstep, h0 + i * tok_bytes, tok_bytes, s)
+            for L in layers:
+                L.forward(hstep, hstep, B, ws, s)
+                u_l, err = L.status(ws, B, s)
+                assert err == 0, f"config-5 step reported error flags {err}"
+                counts.append(u_l)
+        cuda.free_device(hstep)
+        u = float(np.mean(counts))                          # per layer, over layers and steps
         step_bytes = D_LAYERS * (D_E * D_H * 2 + u * expert_bytes + shared_bytes + B * D_H * 12)
         out[str(B)] = dict(batch=B, tok_s=B / sec, us_per_layer=sec / D_LAYERS * 1e6, unique_experts=u,
+                           unique_experts_min=int(min(counts)), unique_experts_max=int(max(counts)),
                            hbm_gbps=step_bytes / sec / 1e9, hbm_frac=step_bytes / sec / 1e9 / PEAK_GBPS)
         log(f"config 5 B={B}: {B / sec:.1f} tok/s over {D_LAYERS} MoE layers, {sec / D_LAYERS * 1e6:.1f} us "
-            f"per layer, {step_bytes / sec / 1e9:.0f} GB/s (unique routed experts {u})")
+            f"per layer, {step_bytes / sec / 1e9:.0f} GB/s (unique routed experts {u:.1f} per layer)")
         for p in (ws, h0):
             cuda.free_device(p)
         for e in (e0, e1):
@@ -716,26 +745,34 @@ def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
                              routed_scaling=1.0, min_weight=0.0, router_w=rw.ctypes.data,
                              blobs=C.cast(ptrs, vp), gate_off=go, up_off=uo, down_off=do), ptrs))
 
-    def leg(batch: int, threads: int, seconds: float) -> dict:
+    def leg(batch: int, threads: int, seconds: float, min_passes: int = 20) -> dict:
+        # one untimed warm-up pass, then at least min_passes timed layer
+        # passes (more while the time share lasts); the median pass is the
+        # figure, with the spread beside it
         h = lp.synth_f32_bf16(batch * H, 1.0, 0, 2).reshape(batch, H)
         x = np.empty_like(h)
-        passes, t0 = 0, time.perf_counter()
-        while True:
+
+        def one(L):
+            x[:] = h
+            rc = lib.lpo_moe_layer(C.byref(L), x.ctypes.data, h.ctypes.data, batch, None, None, None,
+                                   None, None, 0, threads)
+            assert rc == 0
+
+        one(layers[0][0])
+        times, t0 = [], time.perf_counter()
+        while len(times) < min_passes or time.perf_counter() - t0 < seconds:
             for L, _ in layers:
-                x[:] = h
-                rc = lib.lpo_moe_layer(C.byref(L), x.ctypes.data, h.ctypes.data, batch, None, None, None,
-                                       None, None, 0, threads)
-                assert rc == 0
-                passes += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
+                p0 = time.perf_counter()
+                one(L)
+                times.append(time.perf_counter() - p0)
         dt = time.perf_counter() - t0
-        per_layer = dt / passes
-        per_step = per_layer * LAYERS
-        log(f"cpu baseline: batch {batch} on {threads} thread(s): {passes} layer passes in {dt:.1f} s, "
-            f"{per_layer * 1e3:.2f} ms per layer")
-        return dict(batch=batch, threads=threads, layer_passes=passes, seconds=round(dt, 3),
-                    ms_per_layer=per_layer * 1e3, tok_s=batch / per_step)
+        med = float(np.median(times))
+        per_step = med * LAYERS
+        log(f"cpu baseline: batch {batch} on {threads} thread(s): {len(times)} layer passes in {dt:.1f} s, "
+            f"median {med * 1e3:.2f} ms per layer (min {min(times) * 1e3:.2f}, max {max(times) * 1e3:.2f})")
+        return dict(batch=batch, threads=threads, layer_passes=len(times), seconds=round(dt, 3),
+                    ms_per_layer=med * 1e3, ms_per_layer_min=min(times) * 1e3, ms_per_layer_max=max(times) * 1e3,
+                    tok_s=batch / per_step)
 
     legs = {
         "config1_scalar": leg(1, 1, budget_s * 0.1),
@@ -745,9 +782,10 @@ def cpu_baseline(stack: Stack, B: int, budget_s: float) -> dict:
     }
     head = legs[f"config2_b{B}_omp"]
     return dict(value=head["tok_s"], unit="tok/s", cores=all_threads, kind="port",
-                sample=f"oracle lpo_moe_layer (the reference's CPU semantics in C, OpenMP over GEMV rows) "
-                       f"on {head['layer_passes']} layer passes of batch {B} over the first {len(layers)} "
-                       f"of the 48 layers, scaled to 48 layers; config-1 and single-thread legs in 'legs'",
+                sample=f"oracle lpo_moe_layer (the reference's CPU semantics in C, OpenMP over GEMV rows): "
+                       f"median of {head['layer_passes']} layer passes of batch {B} (after a warm-up pass) over "
+                       f"the first {len(layers)} of the 48 layers, scaled to 48 layers; config-1 and "
+                       f"single-thread legs in 'legs'",
                 cpu_model=cpu_model(), nproc=os.cpu_count(), affinity_cpus=share,
                 legs={k: _rounded(v) for k, v in legs.items()})
 
@@ -828,6 +866,9 @@ def main() -> int:
     hl = results[a.headline]
     cpu = None if a.no_cpu else cpu_baseline(stack, a.headline, a.cpu_seconds)
     dom = hl["dominant"]
+    traffic, trec = measured_traffic(dom["kernel"], a.headline)
+    traffic_src = (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE ({trec['command']}), scaled by the "
+                   f"calibration copy's factors" if traffic is not None else trec)
     line = {
         "metric": METRIC,
         "value": round(hl["tok_s"], 2),
@@ -857,7 +898,8 @@ def main() -> int:
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dom["frac"], 4),
-            "traffic": TRAFFIC_B32.get(dom["kernel"]) if a.headline == 32 else None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "avg_us": round(dom["avg_us"], 3),
         },
         "cpu_baseline": cpu,
