@@ -220,9 +220,11 @@ typedef struct lp_moe_ws_layout {
     uint64_t uniq;    /* i32 [E] experts with picks, ascending */
     uint64_t meta;    /* i32 [16]: [0] unique count, [1] error flags */
     uint64_t et;      /* 32-byte expert entries [E] for the grouped kernels */
-    uint64_t act;     /* f32 [T*k, I] (size 0 on the prefill GEMM path, which keeps act in actimg) */
+    uint64_t act;     /* f32 [T*k, I]; on the prefill GEMM path i32 [T*k][ceil(I/128)], the
+                         exponent of each 128-column chunk of the act images in actimg */
     uint64_t y;       /* f32 [T*k, H] */
-    uint64_t xf;      /* [T] bf16 hi/lo images of x for the prefill GEMM (size 0 without it) */
+    uint64_t xf;      /* [T] fp16 images of x for the prefill GEMM, each row scaled by 2^-xexp[t]
+                         (size 0 without it) */
     uint64_t xd;      /* [T] digit images of x for the grouped kernels (per 32 columns 16-bit
                          fixed point as two int8 digits, a seed and a scale) */
     uint64_t sh_et;   /* shared MLP: its expert entry (size 0 without one) */
@@ -230,8 +232,8 @@ typedef struct lp_moe_ws_layout {
     uint64_t sh_act;  /* shared MLP: f32 [T, shared_inter] */
     uint64_t sh_y;    /* shared MLP: f32 [T, H] */
     uint64_t tiles;   /* prefill GEMM tile list (size 0 on the decode path) */
-    uint64_t actimg;  /* prefill GEMM: images of the act rows (size 0 on the decode path) */
-    uint64_t xlo;     /* i32 [T]: 1 when a token's image in xf has a non-zero lo part */
+    uint64_t actimg;  /* prefill GEMM: fp16 images of the act rows (size 0 on the decode path) */
+    uint64_t xexp;    /* i32 [T]: prefill GEMM: the power-of-two exponent of each token's image in xf */
     uint64_t disp;    /* dispatch scratch of batches above 64 tokens */
     uint64_t total;   /* bytes */
 } lp_moe_ws_layout;

@@ -68,7 +68,7 @@ class WsLayout(C.Structure):
 
     _fields_ = [(n, C.c_uint64) for n in (
         "logits", "ids", "wts", "cnt", "gs", "perm", "inv", "uniq", "meta", "et", "act", "y", "xf", "xd",
-        "sh_et", "sh_perm", "sh_act", "sh_y", "tiles", "actimg", "xlo", "disp", "total")]
+        "sh_et", "sh_perm", "sh_act", "sh_y", "tiles", "actimg", "xexp", "disp", "total")]
 
 
 def _sig(lib):

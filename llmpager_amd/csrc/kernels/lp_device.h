@@ -291,68 +291,73 @@ __device__ __forceinline__ void write_dimage_group(const float* row, int cols, i
     reinterpret_cast<float*>(img + lpk::dimage_sigma_off(ngp))[g] = q.sigma;
 }
 
-// One 32-column sub-group of an fp32 row as bf16 fragment words (the prefill
-// GEMM's A operand): the parts hi = bf16(x) and lo = bf16(x - hi) in
-// fragment order (32-bit word w of uint4 d pairs columns 8d + w and 8d + w +
-// 4) and each part's sum.  p == 0 gives zeros.
-struct GroupFrag {
-    uint4 hi[4], lo[4];
-    float shi, slo;
-};
+// fp16 images (lpk::himage_bytes layout), the token operand of the prefill
+// GEMM.  The exponent e of a row (or act chunk) whose largest magnitude is m
+// puts m 2^-e in [2^14, 2^15), so every value down to 2^-28 m stays a normal
+// fp16; a zero or non-finite m gives e = 0 (zeros stay zero, inf and NaN
+// carry through).
+__device__ __forceinline__ int h16_exp(float m) {
+    return m > 0.0f && m <= 3.402823466e38f ? __builtin_amdgcn_frexp_expf(m) - 15 : 0;
+}
 
-__device__ __forceinline__ GroupFrag convert_group(const LP_GLOBAL float4* p) {
-    GroupFrag q;
-    q.shi = 0.0f;
-    q.slo = 0.0f;
+// Columns 8 j .. 8 j + 7 of a sub-group (v[0..7]) times 2^-e, rounded to fp16
+// (RNE), as the image's 16-byte word j: halves in the order (0, 4, 1, 5, 2, 6,
+// 3, 7), the order in which a q4 weight word unpacks.
+__device__ __forceinline__ uint4 h16_word(const float (&v)[8], int e) {
+    uint32_t h[8];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+    for (int i = 0; i < 8; ++i) h[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(v[i], -e));
+    return make_uint4(h[0] | (h[4] << 16), h[1] | (h[5] << 16), h[2] | (h[6] << 16), h[3] | (h[7] << 16));
+}
+
+// Largest |x| over columns 4 first, 4 (first + step), ... (four each) of an
+// fp32 row (cols % 4 == 0, 16-byte aligned), reduced over the wave: the
+// result in every lane.
+__device__ __forceinline__ float row_absmax_wave(const float* row, int cols, int first, int step) {
+    float m = 0.0f;
+    for (int c = 4 * first; c < cols; c += 4 * step) {
+        const float4 v = *reinterpret_cast<const float4*>(row + c);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    return m;
+}
+
+// Words first, first + step, ... of the fp16 image of an fp32 row with
+// exponent e (zero words for the padding sub-groups).
+__device__ __forceinline__ void write_h16_words(const float* row, int cols, int e, uint8_t* img, int first,
+                                                int step) {
+    const int ng = cols >> 5, nw = 4 * lpk::frag_ngp(cols);
+    for (int w = first; w < nw; w += step) {
+        const int g = w >> 2, j = w & 3;
         float v[8];
-        if (p) {
-            const float4 f0 = p[2 * d], f1 = p[2 * d + 1];
+        if (g < ng) {
+            const float4 f0 = *reinterpret_cast<const float4*>(row + g * 32 + j * 8);
+            const float4 f1 = *reinterpret_cast<const float4*>(row + g * 32 + j * 8 + 4);
             v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
             v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = 0.0f;
         }
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            hi[i] = f32_to_bf16_rne(v[i]);
-            lo[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hi[i]));
-            q.shi += bf16_to_f32(hi[i]);
-            q.slo += bf16_to_f32(lo[i]);
-        }
-        q.hi[d] = make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
-                             hi[3] | (hi[7] << 16));
-        q.lo[d] = make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
-                             lo[3] | (lo[7] << 16));
+        reinterpret_cast<uint4*>(img)[w] = h16_word(v, e);
     }
-    return q;
 }
 
-// Sub-group g of an fp32 row of `cols` columns into the row's fragment image
-// (lpk::image_bytes layout): part blocks [2][ngp][64 B], then seeds [ngp][2]:
-// [0] = -136 * sum(hi) + -136 * sum(lo), the whole sub-group's seed, and
-// [1] = 0 (a consumer that keeps the parts in separate accumulator rows seeds
-// the hi row with [0] and the lo row with [1]).  Returns whether any lo
-// element is non-zero.
-__device__ __forceinline__ bool write_image_group(const float* row, int cols, int g, uint8_t* img) {
-    const int ng = cols >> 5, ngp = lpk::frag_ngp(cols);
-    const GroupFrag q =
-        convert_group(g < ng ? gptr<float4>(reinterpret_cast<uint64_t>(row + (size_t)g * 32)) : nullptr);
-    uint4* hi = reinterpret_cast<uint4*>(img + (size_t)g * 64);
-    uint4* lo = reinterpret_cast<uint4*>(img + (size_t)ngp * 64 + (size_t)g * 64);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        hi[d] = q.hi[d];
-        lo[d] = q.lo[d];
-    }
-    reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * q.shi + -136.0f * q.slo, 0.0f);
-    uint32_t any = 0;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) any |= q.lo[d].x | q.lo[d].y | q.lo[d].z | q.lo[d].w;
-    return any != 0;
+// The fp16 image of an fp32 row (global memory or LDS) and its exponent
+// (*exp_out), by the whole workgroup (every thread calls it).
+__device__ __forceinline__ void write_h16_image(const float* row, int cols, uint8_t* img, int* exp_out) {
+    __shared__ float red[16];
+    const int wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    float m = row_absmax_wave(row, cols, threadIdx.x, blockDim.x);
+    if (lane_id() == 0) red[wave] = m;
+    __syncthreads();
+    for (int w = 0; w < nwaves; ++w) m = fmaxf(m, red[w]);
+    __syncthreads();  // red is free for the next row
+    const int e = h16_exp(m);
+    write_h16_words(row, cols, e, img, threadIdx.x, blockDim.x);
+    if (threadIdx.x == 0) *exp_out = e;
 }
 
 // Direct-to-LDS copy from inline assembly: lane l's 16 bytes at base + off

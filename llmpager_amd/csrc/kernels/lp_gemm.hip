@@ -3,32 +3,40 @@
 // the arithmetic each output restates is q4g64.cu:19-81's).
 //
 // A tile is (routed expert, block of kGemmBM = 128 of its tokens, block of
-// weight rows): gate/up tiles take 64 rows of gate and the same 64 rows of up
-// so that SiLU * up is the epilogue; down tiles take 128 rows.  Wave w owns
-// the 16-token blocks 2 mt + (w & 1), mt = 0..3, and one half of the rows
-// (w >> 1): 4 x 4 tiles of v_mfma_f32_16x16x32_bf16 (gate/up: two gate tiles
-// and the matching two up tiles).
+// kGemmBN = 256 weight rows), eight waves; wave w owns 32 rows (two 16-row
+// MFMA tiles) against all 128 tokens (eight 16-token tiles), so every weight
+// is dequantised once per tile.  Gate/up tiles take 128 act columns: wave w's
+// gate rows and the same up rows, so SiLU * up is the epilogue.
 //
-// K runs over 32-column sub-groups, one pipeline stage each.  Operands reach
-// LDS by direct-to-LDS loads (no registers, no LDS stores), each stream in
-// whole 64-byte pieces of memory:
-//   A: per stage, the 128 token rows' fragment blocks (bf16 hi = bf16(x), lo
-//      = bf16(x - hi), in MFMA operand order; gate/up gathers the token images
-//      through the dispatch permutation), lo only when a token of the tile has
-//      one; three slots, loads two stages ahead;
-//   B: per kGemmBGroups stages, 64 nibble bytes of each of the tile's 128
-//      weight rows; two slots;
-//   scales: per kGemmSGroups stages, a 16-scale window of each row; two slots.
-// Each wave turns its B words into bf16 128 + q (one v_bitop3_b32 per two
-// values); one MFMA of the A block against bf16(-136) gives -136 sum_k (hi +
-// lo)_k, which seeds the sub-group's MFMAs, so they return sum_k x_k (q_k - 8)
-// exactly up to fp32 rounding; the sub-group's scale is then applied in fp32.
+// The MFMA is v_mfma_f32_16x16x32_f16 with the weights as its first operand
+// and the tokens as its second: C[row][token], fp32 accumulation over all of
+// K.  Weights: each lane turns a q4 word into fp16 (q - 8) s with two packed
+// fp16 operations per two values (1024 + q by the 0x6400 exponent trick,
+// minus 1032, exact; times the group's fp16 scale, one rounding).  Tokens:
+// fp16 images of x (gate/up, through the dispatch permutation) or of act
+// (down), each row scaled by a power of two (lp_device.h's h16_exp).
+//
+// K runs in stages of 64 columns (two sub-groups).  Per stage, direct-to-LDS
+// loads (no registers, no LDS stores) bring 128 bytes of each token row and 32
+// bytes of each weight row into one of kGemmSlots slots, three stages ahead;
+// every fourth stage a 16-scale window of each row.  Within a stage lane (r,
+// kb) of an MFMA takes sub-group kb >> 1, words 2 (kb & 1) + j at step j, on
+// both operands.
+//
+// act leaves gate/up as fp16 images with one exponent per (row, 128 columns),
+// the tile's own maximum; the down GEMM rescales each staged chunk in LDS to
+// the row's largest exponent before its MFMAs and scales y back.
+#include <type_traits>
+
 #include "lp_device.h"
 
 using namespace lp;
 using namespace lpk;
 
 namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 template <typename T>
 __device__ __forceinline__ T* dptr(uint64_t a) {
@@ -51,19 +59,6 @@ __device__ __forceinline__ ExpertEntry load_entry(uint64_t et, int u) {
 
 __shared__ __align__(16) uint8_t g_lds[kGemmLds];
 
-// Chunk kb (16 bytes) of token m's 64-byte block within a 16-token block of
-// LDS sits at slot 4 m + (kb ^ chunk_swz(m)): the MFMA operand read (lane =
-// 16 kb + m) then touches 16 distinct 16-byte bank groups per 16 lanes and 8
-// per 8 lanes, while each direct-load quad still copies one token's 64
-// contiguous bytes.
-__device__ __forceinline__ int chunk_swz(int m) { return ((m >> 1) ^ (m >> 3)) & 3; }
-
-// B slot: row r's kGemmBGroups 16-byte sub-group pieces sit at 64 r + 16 (j ^
-// b_swz(r)) for sub-group j of the load, so that the operand read (16 rows x
-// one 32-bit word) hits distinct banks; each direct-load quad still copies
-// one row's 64 contiguous bytes.
-__device__ __forceinline__ int b_swz(int r) { return (r >> 2) & 3; }
-
 __device__ __forceinline__ void dma16(uint64_t base, uint32_t off, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
@@ -75,424 +70,418 @@ __device__ __forceinline__ uint32_t lds_base() {
 
 // Wait until at most n vector-memory loads of this wave are outstanding and
 // its LDS reads are done; with the loads completing in issue order this is
-// "stage s has landed" when n counts the loads issued after stage s's.
+// "every load issued before the last n has landed".
 #define LP_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+__device__ __forceinline__ void wait_loads(int n) {
+    switch (n) {
+        case 0: LP_WAIT_VM_LGKM0(0); break;
+        case 1: LP_WAIT_VM_LGKM0(1); break;
+        case 2: LP_WAIT_VM_LGKM0(2); break;
+        case 3: LP_WAIT_VM_LGKM0(3); break;
+        case 4: LP_WAIT_VM_LGKM0(4); break;
+        case 5: LP_WAIT_VM_LGKM0(5); break;
+        case 6: LP_WAIT_VM_LGKM0(6); break;
+        case 7: LP_WAIT_VM_LGKM0(7); break;
+        case 8: LP_WAIT_VM_LGKM0(8); break;
+        case 9: LP_WAIT_VM_LGKM0(9); break;
+        case 10: LP_WAIT_VM_LGKM0(10); break;
+        case 11: LP_WAIT_VM_LGKM0(11); break;
+        default: LP_WAIT_VM_LGKM0(12); break;
+    }
+}
 
 // s_barrier as a compiler-level memory fence too: no LDS access or load moves
 // across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-struct GemmTile {
-    ExpertEntry x;
-    int m0, mvalid, n0;   // token block start and size; first matrix row of the tile
-    int K, NR, ng, ngp;   // reduction width, matrix rows, sub-groups, padded sub-groups
-    uint64_t off0, off1;  // byte offsets in the blob: gate/up: gate and up regions; down: down twice
-};
+// Token n's (n = tile token mod 16) 16-byte word c of a stage sits at
+// position c ^ tok_swz(n) of its 128-byte LDS row: an MFMA operand read (16
+// tokens, one word each) then touches 16 distinct 16-byte bank groups of 256
+// bytes, and 8 distinct of 128 bytes per 8 lanes.
+__device__ __forceinline__ int tok_swz(int n) { return (n ^ (n >> 3)) & 7; }
 
-// Matrix row (in 0 .. NR-1) behind row r of the tile's B buffer.
-template <int MODE>
-__device__ __forceinline__ int tile_row(const GemmTile& g, int r) {
-    return min(g.n0 + (MODE == 0 ? (r & 63) : r), g.NR - 1);
+// Weight row rho's two 16-byte sub-group pieces of a stage: piece h at
+// position h ^ w_swz(rho) (rows 8 apart then differ in their 8-byte reads).
+__device__ __forceinline__ int w_swz(int rho) { return (rho >> 3) & 1; }
+
+// The act column (0..15 within a wave's 16) of MFMA row r of a gate/up tile:
+// lane group kb of the C tile holds rows 4 kb .. 4 kb + 3, which are then the
+// columns of half kb & 1 of the image's word kb >> 1, in image order.
+__device__ __forceinline__ int act_col(int r) {
+    const int q = r >> 2, i = r & 3;
+    return 8 * (q >> 1) + 2 * (q & 1) + ((i & 1) << 2) + (i >> 1);
 }
 
-// Sum over the 16 lanes of a row, in every lane of the row: quad_perm
-// [1,0,3,2] and [2,3,0,1], then row_half_mirror and row_mirror.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+// A q4 word (8 values, nibble v of byte v / 2, low first) as fp16 (q - 8) s in
+// image order (0, 4, 1, 5, 2, 6, 3, 7): 1024 + q exactly from the exponent
+// trick, minus 1032 exactly, times s with one rounding.
+__device__ __forceinline__ f16x8_t q4_word_to_f16x8(uint32_t b, f16x2_t s) {
+    const f16x2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const f16x2_t h0 = (__builtin_bit_cast(f16x2_t, and_or(b, 0x000F000Fu, 0x64006400u)) - bias) * s;
+    const f16x2_t h1 = (__builtin_bit_cast(f16x2_t, and_or(b >> 4, 0x000F000Fu, 0x64006400u)) - bias) * s;
+    const f16x2_t h2 = (__builtin_bit_cast(f16x2_t, and_or(b >> 8, 0x000F000Fu, 0x64006400u)) - bias) * s;
+    const f16x2_t h3 = (__builtin_bit_cast(f16x2_t, and_or(b >> 12, 0x000F000Fu, 0x64006400u)) - bias) * s;
+    return f16x8_t{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += dpp_f<0x141>(v);
-    return v + dpp_f<0x140>(v);
-}
 
-template <int MODE, int RS, bool LO>
-__device__ __forceinline__ void gemm_main(const GemmArgs& a, const GemmTile& G) {
-    // Sub-groups per stage: an A slot holds one sub-group's hi and lo parts,
-    // or two sub-groups' hi parts when the tile has no lo.
-    constexpr int GPS = LO ? 1 : 2;
-    constexpr int OPS_A = 4;  // A loads per wave per stage (two 16-token blocks x two parts / sub-groups)
-    const int tid = threadIdx.x, lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA targets stay scalar
-    const int wm = wave & 1, wn = wave >> 1;
-    const int nst = (G.ng + GPS - 1) / GPS;
-    const uint32_t lds0 = lds_base();
-    const uint64_t part_bytes = (uint64_t)G.ngp * 64;
-    const int gpr = G.ng >> RS;
-    const uint32_t sbytes = (uint32_t)G.NR * gpr * 2;
-    const uint64_t* rowimg = reinterpret_cast<const uint64_t*>(g_lds + kGemmLdsRows);
+// A value the whole wave holds, as a scalar (so that branches on it stay
+// scalar branches).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-    // --- load sources: a uniform 64-bit base plus per-lane 32-bit offsets ---
-    const uint64_t a_base = a.a_img;
-    // (each half zero-extended: readfirstlane returns a signed int)
-    const uint64_t w_base = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)G.x.blob) |
-                            ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(G.x.blob >> 32)) << 32);
-    // A: block 2 w + j of 16 tokens; lane l copies chunk (l & 3) ^ swz of token l >> 2
-    uint32_t a_off[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int m = lane >> 2;
-        a_off[j] = (uint32_t)(rowimg[16 * (2 * wave + j) + m] - a_base) + (uint32_t)(((lane & 3) ^ chunk_swz(m)) * 16);
-    }
-    // B: rows 32 w + 16 i + (l >> 2); lane l copies the row's piece j = l & 3,
-    // i.e. sub-group kGemmBGroups S + (j ^ b_swz(row)) of load S
-    uint32_t b_row[2];
-    const int b_j = (lane & 3) ^ ((lane >> 4) & 3);  // j ^ b_swz(row): row bits 2-3 are lane bits 4-5
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 32 * wave + 16 * i + (lane >> 2);
-        const uint32_t mat = (uint32_t)((MODE == 0 && r >= 64) ? G.off1 : G.off0);
-        b_row[i] = mat + sbytes + (uint32_t)tile_row<MODE>(G, r) * G.ng * 16;
-    }
-    // scales: row 32 w + (l >> 1), 16-byte half l & 1 of the row's window
-    const int s_r = 32 * wave + (lane >> 1);
-    const uint32_t s_mat = (uint32_t)((MODE == 0 && s_r >= 64) ? G.off1 : G.off0) + 16 * (lane & 1);
-    const uint32_t s_idx = (uint32_t)tile_row<MODE>(G, s_r) * gpr;
-
-    // stage st into A slot `slot`: half q of the slot is part q of sub-group
-    // st (LO) or sub-group 2 st + q (no lo; a padding sub-group of the image
-    // past the last one reads as zeros)
-    auto issue_a = [&](int st, int slot) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                dma16(a_base + (LO ? q * part_bytes + (uint64_t)st * 64 : (uint64_t)(GPS * st + q) * 64), a_off[j],
-                      lds0 + slot * kGemmSlotA + q * kGemmBM * 64 + (2 * wave + j) * 1024);
-    };
-    auto issue_b = [&](int S, int slot) {
-        const uint32_t g = (uint32_t)min(kGemmBGroups * S + b_j, G.ng - 1);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            dma16(w_base, b_row[i] + g * 16, lds0 + kGemmLdsB + slot * kGemmSlotB + (32 * wave + 16 * i) * 64);
-    };
-    // the window starts at the 8-aligned scale index at or below the row's
-    // first scale of the load: 16 scales cover the 8 >> RS it needs
-    auto issue_s = [&](int S, int slot) {
-        const uint32_t c0 = (s_idx + (uint32_t)((kGemmSGroups * S) >> RS)) & ~7u;
-        dma16(w_base, s_mat + c0 * 2, lds0 + kGemmLdsS + slot * kGemmSlotS + wave * 1024);
-    };
-
-    // --- read side ---
-    // B / scale row of n-tile t: rbase + roff(t)
-    const int rbase = MODE == 0 ? 32 * wn + (lane & 15) : 64 * wn + (lane & 15);
-    auto roff = [](int t) { return MODE == 0 ? (t < 2 ? 16 * t : 64 + 16 * (t - 2)) : 16 * t; };
-    const int am = lane & 15, akb = lane >> 4;
-    // the wave's 16-token blocks are 2 mt + wm (mt = 0..3): both halves of a
-    // partly filled tile get about the same number of valid blocks
-    const uint8_t* a_rd = g_lds + wm * 1024 + (4 * am + (akb ^ chunk_swz(am))) * 16;
-    const uint8_t* b_rd = g_lds + kGemmLdsB + rbase * 64 + akb * 4;
-    const int b_x = b_swz(rbase) << 4;  // roff(t) is a multiple of 16: same swizzle for every t
-    uint32_t s_row[4];                   // the row's scale index at sub-group 0
-#pragma unroll
-    for (int t = 0; t < 4; ++t) s_row[t] = (uint32_t)tile_row<MODE>(G, rbase + roff(t)) * gpr;
-    int s_rd[4];                         // LDS byte offset of the window's first scale of the load
-    const int nmt = max(0, min(4, (((G.mvalid + 15) >> 4) - wm + 1) >> 1));  // valid blocks of the wave
-    const bf16x8_t k136 = __builtin_bit_cast(bf16x8_t, u32x4_t{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
-
-    f32x4_t acc[4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[mt][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // this stage's weight words (as bf16 128 + q) and scales
-    auto stage_b = [&](int g, bf16x8_t (&b)[4], float (&sc)[4], uint32_t (&w)[4]) {
-        const int b_slot = ((g / kGemmBGroups) & 1) * kGemmSlotB + (((g % kGemmBGroups) << 4) ^ b_x);
-        const int s_sub = (g >> RS) - ((kGemmSGroups * (g / kGemmSGroups)) >> RS);  // scale within the load
-        const int s_slot = ((g / kGemmSGroups) & 1) * kGemmSlotS + 2 * s_sub;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            w[t] = *reinterpret_cast<const uint32_t*>(b_rd + b_slot + roff(t) * 64);
-            sc[t] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(g_lds + s_rd[t] + s_slot));
-        }
-        (void)b;
-    };
-    auto mfma = [](const uint4& a, const bf16x8_t& b, const f32x4_t& c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), b, c, 0, 0, 0);
-    };
-
-    // Partly filled block set: one block at a time, FMAs right behind.
-    auto compute_part = [&](int g, int a_slot) {
-        if (nmt == 0) return;
-        bf16x8_t b[4];
-        float sc[4];
-        uint32_t w[4];
-        stage_b(g, b, sc, w);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) b[t] = q4_word_to_bf16x8(w[t]);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            if (mt < nmt) {
-                const uint4 ahi = *reinterpret_cast<const uint4*>(a_rd + a_slot + mt * 2048);
-                const uint4 alo = LO ? *reinterpret_cast<const uint4*>(a_rd + a_slot + kGemmBM * 64 + mt * 2048) : ahi;
-                f32x4_t c0 = mfma(ahi, k136, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
-                if (LO) c0 = mfma(alo, k136, c0);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    f32x4_t c = mfma(ahi, b[t], c0);
-                    if (LO) c = mfma(alo, b[t], c);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(sc[t], c[i], acc[mt][t][i]);
-                }
-            }
-        }
-    };
-
-    // All four blocks valid: a software pipeline in which each MFMA is
-    // followed by the four scale FMAs of an MFMA that finished long before,
-    // so the wave keeps its matrix and vector units busy together.  Block
-    // mt's FMAs run behind block mt + 1's MFMAs; block 3's behind the next
-    // stage's block 0 (cp / scp carry them).  Per stage:
-    //   seed MFMAs of the four blocks, each with a quarter of the nibble
-    //   decode behind it; then per block: per n-tile its MFMA(s), then the
-    //   lagging block's four FMAs of that n-tile.
-    f32x4_t cp[4];
-    float scp[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        cp[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        scp[t] = 0.0f;
-    }
-    auto compute_full = [&](int g, int a_slot) {
-        bf16x8_t b[4];
-        float sc[4];
-        uint32_t w[4];
-        stage_b(g, b, sc, w);
-        uint4 ahi[4], alo[4];
-        f32x4_t c0[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            ahi[mt] = *reinterpret_cast<const uint4*>(a_rd + a_slot + mt * 2048);
-            alo[mt] = LO ? *reinterpret_cast<const uint4*>(a_rd + a_slot + kGemmBM * 64 + mt * 2048) : ahi[mt];
-        }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            c0[mt] = mfma(ahi[mt], k136, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
-            if (LO) c0[mt] = mfma(alo[mt], k136, c0[mt]);
-            b[mt] = q4_word_to_bf16x8(w[mt]);
-            __builtin_amdgcn_sched_group_barrier(0x008, LO ? 2 : 1, 0);  // seed MFMA(s)
-            __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);           // a word's decode
-        }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            f32x4_t cc[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                cc[t] = mfma(ahi[mt], b[t], c0[mt]);
-                if (LO) cc[t] = mfma(alo[mt], b[t], cc[t]);
-                // the lagging block: mt - 1 of this sub-group, or block 3 of
-                // the previous one (with its scales; zeros before the first)
-                f32x4_t& dst = acc[mt == 0 ? 3 : mt - 1][t];
-                const float sl = mt == 0 ? scp[t] : sc[t];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) dst[i] = __builtin_fmaf(sl, cp[t][i], dst[i]);
-                __builtin_amdgcn_sched_group_barrier(0x008, LO ? 2 : 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-            }
-#pragma unroll
-            for (int t = 0; t < 4; ++t) cp[t] = cc[t];
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) scp[t] = sc[t];
-    };
-
-    // Stage st (sub-groups g0 = GPS st ..) needs A(st), B(g0 / 4) and
-    // scales(g0 / 8).  Everything issued before A(st + 1) is complete once at
-    // most OPS_A loads are outstanding (loads complete in issue order and
-    // A(st + 1) alone is OPS_A loads), and B / scale loads are issued at
-    // least one stage before the A(st + 1) that follows them; after the last
-    // A, wait for everything.
-    auto stage_begin = [&](int st) {
-        const int g = GPS * st;
-        if (st + 1 < nst) LP_WAIT_VM_LGKM0(OPS_A);
-        else LP_WAIT_VM_LGKM0(0);
-        stage_barrier();
-        if (st + 2 < nst) issue_a(st + 2, (st + 2) % kGemmASlots);
-        if (g % kGemmBGroups == 0 && g + kGemmBGroups < G.ng) issue_b(g / kGemmBGroups + 1, (g / kGemmBGroups + 1) & 1);
-        if (g % kGemmSGroups == 0) {
-            if (g + kGemmSGroups < G.ng) issue_s(g / kGemmSGroups + 1, (g / kGemmSGroups + 1) & 1);
-            const uint32_t first = (uint32_t)(g >> RS);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                s_rd[t] = kGemmLdsS + (rbase + roff(t)) * 32 + 2 * (int)((s_row[t] + first) & 7u);
-        }
-    };
-    issue_a(0, 0);
-    issue_b(0, 0);
-    issue_s(0, 0);
-    if (nst > 1) issue_a(1, 1);
-    if (nmt == 4) {
-        for (int st = 0; st < nst; ++st) {
-            stage_begin(st);
-            const int a_slot = (st % kGemmASlots) * kGemmSlotA;
-            compute_full(GPS * st, a_slot);
-            if (GPS == 2 && GPS * st + 1 < G.ng) compute_full(GPS * st + 1, a_slot + kGemmBM * 64);
-        }
-        // the last stage's block 3
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[3][t][i] = __builtin_fmaf(scp[t], cp[t][i], acc[3][t][i]);
-    } else {
-        for (int st = 0; st < nst; ++st) {
-            stage_begin(st);
-            const int a_slot = (st % kGemmASlots) * kGemmSlotA;
-            compute_part(GPS * st, a_slot);
-            if (GPS == 2 && GPS * st + 1 < G.ng) compute_part(GPS * st + 1, a_slot + kGemmBM * 64);
-        }
-    }
-
-    // epilogue: lane holds C rows 4 akb + i (tokens) of column lane & 15 of each tile
-    if constexpr (MODE == 0) {
-        // act = silu(gate) * up straight into the down GEMM's A image (a.out
-        // is the image base; lpk::image_bytes layout, as lp_device.h's
-        // write_image_group): the wave's 32 columns n0 + 32 wn .. + 31 are
-        // sub-group g of each of its token rows, held by the 16 lanes of one
-        // row (column 16 t + am in register t).  Fragment word (d, w) pairs
-        // columns 8d + w and 8d + w + 4, so lane am (bit 2 clear) packs its
-        // hi part with lane am + 4's (a row shift by 4) and writes the hi
-        // word, lane am + 4 the lo word; the seed -136 (sum hi) - 136 (sum
-        // lo) comes from a sum over the row's lanes (quad swaps, then the
-        // half-row and row mirrors).  All lane exchanges are DPP moves.
-        LP_GLOBAL uint8_t* img = gptr_w<uint8_t>(a.out);
-        const int g = (G.n0 >> 5) + wn;
-        const bool live_g = g < (G.NR >> 5);
-        const int ngp = frag_ngp(G.NR);
-        const size_t ib = (size_t)image_bytes(G.NR);
-        const bool low = (am & 4) == 0;
-        const uint32_t part = low ? (uint32_t)g * 64u : (uint32_t)(ngp + g) * 64u;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 16 * (2 * mt + wm) + 4 * akb + i;
-                LP_GLOBAL uint8_t* row = img + (size_t)(G.x.p0 + G.m0 + min(m, G.mvalid - 1)) * ib;
-                const bool st = m < G.mvalid && live_g;  // the same for lanes am and am ^ 4
-                float shi = 0.0f, slo = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const float gg = acc[mt][t][i], uu = acc[mt][t + 2][i];
-                    const float v = gg / (1.0f + expf(-gg)) * uu;
-                    const uint32_t h16 = f32_to_bf16_rne(v);
-                    const uint32_t l16 = f32_to_bf16_rne(v - bf16_to_f32(h16));
-                    shi += bf16_to_f32(h16);
-                    slo += bf16_to_f32(l16);
-                    // both moves with every lane on (a DPP source lane that is
-                    // off reads as zero): pinned here by the empty asm, so that
-                    // the select below cannot become a branch around each
-                    const int send = (int)(low ? l16 : h16);
-                    int up4 = __builtin_amdgcn_mov_dpp(send, 0x104, 0xf, 0xf, true);  // row_shl:4, lane am + 4
-                    int dn4 = __builtin_amdgcn_mov_dpp(send, 0x114, 0xf, 0xf, true);  // row_shr:4, lane am - 4
-                    asm volatile("" : "+v"(up4), "+v"(dn4));
-                    const uint32_t recv = (uint32_t)(low ? up4 : dn4);
-                    const uint32_t word = low ? (h16 | (recv << 16)) : (recv | (l16 << 16));
-                    const uint32_t off = part + 16u * (uint32_t)(2 * t + (am >> 3)) + 4u * (uint32_t)(am & 3);
-                    if (st) *reinterpret_cast<LP_GLOBAL uint32_t*>(row + off) = word;
-                }
-                shi = row_sum16(shi);
-                slo = row_sum16(slo);
-                if (st && am == 0)
-                    reinterpret_cast<LP_GLOBAL float2*>(row + (size_t)ngp * 128)[g] = make_float2(-136.0f * shi + -136.0f * slo, 0.0f);
-            }
-        }
-    } else {
-        float* out = dptr<float>(a.out);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 16 * (2 * mt + wm) + 4 * akb + i;
-                if (m >= G.mvalid) continue;
-                float* orow = out + (size_t)(G.x.p0 + G.m0 + m) * G.NR;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int r = G.n0 + 64 * wn + 16 * t + am;
-                    if (r < G.NR) orow[r] = acc[mt][t][i];
-                }
-            }
-        }
-    }
+// 2^d as fp16 bits for d in [-127, 0] (0 below 2^-24).
+__device__ __forceinline__ uint32_t f16_pow2(int d) {
+    return d >= -14 ? (uint32_t)(d + 15) << 10 : d >= -24 ? 1u << (d + 24) : 0u;
 }
 
 template <int MODE, int RS>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const LayerView& L = a.L;
-    const int k = L.top_k;
     // XCD-aware order: workgroup w runs on XCD w % 8, so XCD x takes the
     // contiguous range [x C, x C + C) of the live (tile, row block) items,
-    // row blocks innermost: the 128 tokens' A tile and the expert's weight
-    // blocks are then fetched into one XCD's L2 and reused there.
-    const int count = dptr<const int>(a.W.meta)[2];
+    // row blocks innermost: the 128 tokens' images and the expert's weight
+    // rows are then fetched into one XCD's L2 and reused there.
+    const int count = uni(dptr<const int>(a.W.meta)[2]);
     const int live = count * a.nblocks;
     const int C = (live + kXcds - 1) / kXcds;
-    const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const int item = xcd * C + j;
-    if (j >= C || item >= live) return;
+    const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
+    const int item = xcd * C + jx;
+    if (jx >= C || item >= live) return;
     const int ti = item / a.nblocks, nb = item - ti * a.nblocks;
-    const int tv = dptr<const int>(a.tiles)[ti];
-    GemmTile G;
-    G.x = load_entry(a.W.et, tv >> 16);
-    G.m0 = (tv & 0xffff) * kGemmBM;
-    G.mvalid = min(kGemmBM, G.x.ntok - G.m0);
-    G.K = MODE == 0 ? L.hidden : L.inter;
-    G.NR = MODE == 0 ? L.inter : L.hidden;
-    G.ng = G.K >> 5;
-    G.ngp = frag_ngp(G.K);
-    G.n0 = nb * (MODE == 0 ? kGemmBN / 2 : kGemmBN);
-    const int tid = threadIdx.x;
-    if (G.x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
-        if (tid == 0 && nb == 0) atomicOr(dptr<int>(a.W.meta) + 1, kErrMissingExpert);
+    const int tv = uni(dptr<const int>(a.tiles)[ti]);
+    ExpertEntry x = load_entry(a.W.et, tv >> 16);
+    x.p0 = uni(x.p0);
+    x.ntok = uni(x.ntok);
+    const int m0 = (tv & 0xffff) * kGemmBM;
+    const int mvalid = min(kGemmBM, x.ntok - m0);
+    const int K = MODE == 0 ? L.hidden : L.inter;
+    const int NR = MODE == 0 ? L.inter : L.hidden;
+    const int ng = K >> 5, nst = frag_ngp(K) >> 1;
+    const int gpr = ng >> RS;                         // scales per weight row
+    const int nch = act_chunks(L.inter);
+    const int n0 = nb * (MODE == 0 ? kActChunk : kGemmBN);  // gate/up: first act column; down: first row
+    const uint32_t rowbytes = (uint32_t)himage_bytes(K);
+    const int tid = threadIdx.x, lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA targets stay scalar
+    int* meta = dptr<int>(a.W.meta);
+    if (x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
+        if (tid == 0 && nb == 0) atomicOr(meta + 1, kErrMissingExpert);
         if (MODE == 0) {
-            // zero act: the tile's two sub-groups of each token row's image
-            // (both parts, and the seeds)
+            // the tile's four sub-groups of each token's act image (256
+            // contiguous bytes) and its chunk exponent
             uint8_t* img = dptr<uint8_t>(a.out);
-            const int ngp = frag_ngp(G.NR);
-            const size_t ib = (size_t)image_bytes(G.NR);
-            for (int e = tid; e < G.mvalid * 18; e += blockDim.x) {
-                // item (m, sub-group gi, w): w < 8 one 16-byte quarter of
-                // part w >> 2, w = 8 the seeds
-                const int m = e / 18, q = e - m * 18, gi = q / 9, w = q - gi * 9;
-                const int g = (G.n0 >> 5) + gi;
-                if (g >= (G.NR >> 5)) continue;
-                uint8_t* row = img + (size_t)(G.x.p0 + G.m0 + m) * ib;
-                if (w < 8)
-                    reinterpret_cast<uint4*>(row + (size_t)((w >> 2) * ngp + g) * 64)[w & 3] = make_uint4(0u, 0u, 0u, 0u);
-                else
-                    reinterpret_cast<float2*>(row + (size_t)ngp * 128)[g] = make_float2(0.0f, 0.0f);
+            const size_t ob = (size_t)himage_bytes(NR);
+            for (int e = tid; e < mvalid * 16; e += blockDim.x) {
+                const int m = e >> 4, q = e & 15;
+                reinterpret_cast<uint4*>(img + (size_t)(x.p0 + m0 + m) * ob + (size_t)(n0 >> 5) * 64)[q] =
+                    make_uint4(0u, 0u, 0u, 0u);
             }
+            for (int m = tid; m < mvalid; m += blockDim.x)
+                dptr<int>(a.W.act)[(size_t)(x.p0 + m0 + m) * nch + nb] = kExpNone;
         } else {
-            const int cols = kGemmBN;
             float* out = dptr<float>(a.out);
-            for (int e = tid; e < G.mvalid * cols; e += blockDim.x) {
-                const int m = e / cols, r = G.n0 + e - m * cols;
-                if (r < G.NR) out[(size_t)(G.x.p0 + G.m0 + m) * G.NR + r] = 0.0f;
+            for (int e = tid; e < mvalid * kGemmBN; e += blockDim.x) {
+                const int m = e / kGemmBN, r = n0 + e - m * kGemmBN;
+                if (r < NR) out[(size_t)(x.p0 + m0 + m) * NR + r] = 0.0f;
             }
         }
         return;
     }
-    G.off0 = MODE == 0 ? L.gate_off : L.down_off;
-    G.off1 = MODE == 0 ? L.up_off : L.down_off;
-    const uint64_t ib = (uint64_t)image_bytes(G.K);
-    // the tile rows' image addresses (rows past the block repeat its last
-    // token) and whether any of them carries a lo part
-    int lo = MODE == 1;
+
+    // --- the tile's token rows: image offsets, exponents (down: per-chunk shifts) ---
+    uint32_t* rows_l = reinterpret_cast<uint32_t*>(g_lds + kGemmLdsRows);
+    int* exp_l = reinterpret_cast<int*>(g_lds + kGemmLdsExp);
+    int8_t* shift_l = reinterpret_cast<int8_t*>(g_lds + kGemmLdsShift);
     if (tid < kGemmBM) {
-        const int pos = G.x.p0 + G.m0 + min(tid, G.mvalid - 1);
+        // rows past the block repeat its last token
+        const int pos = x.p0 + m0 + min(tid, mvalid - 1);
         if (MODE == 0) {
-            const int tok = dptr<const int>(a.W.perm)[pos] / k;
-            reinterpret_cast<uint64_t*>(g_lds + kGemmLdsRows)[tid] = a.a_img + (uint64_t)tok * ib;
-            lo = dptr<const int>(a.W.xlo)[tok] != 0;
+            const int tok = dptr<const int>(a.W.perm)[pos] / L.top_k;
+            rows_l[tid] = (uint32_t)tok * rowbytes;
+            exp_l[tid] = dptr<const int>(a.W.xexp)[tok];
         } else {
-            reinterpret_cast<uint64_t*>(g_lds + kGemmLdsRows)[tid] = a.a_img + (uint64_t)pos * ib;
+            rows_l[tid] = (uint32_t)pos * rowbytes;
+            const int* ae = dptr<const int>(a.W.act) + (size_t)pos * nch;
+            int mx = kExpNone;
+            for (int c = 0; c < nch; ++c) mx = max(mx, ae[c]);
+            for (int c = 0; c < nch; ++c) shift_l[tid * kGemmMaxChunks + c] = (int8_t)max(ae[c] - mx, -127);
+            exp_l[tid] = mx;
         }
     }
-    if (__syncthreads_or(lo))
-        gemm_main<MODE, RS, true>(a, G);
-    else
-        gemm_main<MODE, RS, false>(a, G);
+    __syncthreads();
+
+    // --- load side: a uniform 64-bit base plus per-lane 32-bit offsets ---
+    const uint32_t lds0 = lds_base();
+    const uint64_t a_base = a.a_img;
+    const uint64_t w_base = (uint64_t)(uint32_t)uni((int)(uint32_t)x.blob) | ((uint64_t)(uint32_t)uni((int)(uint32_t)(x.blob >> 32)) << 32);
+    // tokens: copy u of the wave takes tile tokens 16 w + 8 u + (l >> 3), lane l
+    // filling position l & 7 of its row (word (l & 7) ^ tok_swz); copies whose
+    // eight tokens are all past the block are skipped
+    const int ndma = max(0, min(2, (mvalid - 16 * wave + 7) >> 3));
+    uint32_t t_off[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int tt = 16 * wave + 8 * u + (lane >> 3);
+        t_off[u] = rows_l[tt] + (uint32_t)(((lane & 7) ^ tok_swz(tt & 15)) * 16);
+    }
+    // weights: LDS row rho = 32 w + (l >> 1) (MFMA tile (rho >> 4) & 1, row
+    // rho & 15), lane l filling piece l & 1, i.e. sub-group 2 st + h
+    auto mat_row = [&](int t, int r) {
+        return min(MODE == 0 ? n0 + 16 * wave + act_col(r) : n0 + 32 * wave + 16 * t + r, NR - 1);
+    };
+    auto region = [&](int t) { return (uint32_t)(MODE == 0 ? (t ? L.up_off : L.gate_off) : L.down_off); };
+    const uint32_t sbytes = (uint32_t)NR * (uint32_t)gpr * 2u;
+    const int d_t = lane >> 5, d_r = (lane >> 1) & 15;
+    const int d_h = (lane & 1) ^ w_swz(d_r);
+    const uint32_t w_row = region(d_t) + sbytes + (uint32_t)mat_row(d_t, d_r) * (uint32_t)ng * 16u;
+    const uint32_t s_row = (uint32_t)mat_row(d_t, d_r) * (uint32_t)gpr;  // the row's first scale
+    const uint32_t s_reg = region(d_t) + 16u * (uint32_t)(lane & 1);
+
+    // Pipeline step i (i = -4 .. nst - 5 before and in the main loop) issues
+    // the token rows of stage i + 3 and the weight rows of stage i + 4 (with
+    // the scale window of stages i + 4 .. i + 7 when i + 4 is a multiple of
+    // 4): weights run one stage ahead of the tokens, so that stage st's
+    // MFMAs can share the wave with the decode of stage st + 1's weights.
+    auto issue_tok = [&](int st) {
+        const int slot = st & (kGemmSlots - 1);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (u < ndma)
+                dma16(a_base + (uint64_t)st * 128, t_off[u], lds0 + slot * kGemmSlotT + (16 * wave + 8 * u) * 128);
+    };
+    auto issue_w = [&](int st) {
+        const int slot = st & (kGemmSlots - 1);
+        const uint32_t sg = (uint32_t)min(2 * st + d_h, ng - 1);
+        dma16(w_base, w_row + sg * 16u, lds0 + kGemmLdsW + slot * kGemmSlotW + wave * 1024);
+        if ((st & 3) == 0) {
+            // the window starts at the 8-aligned scale index at or below the
+            // row's first scale of stages st .. st + 3: 16 scales cover them
+            const uint32_t c0 = (s_row + (uint32_t)((8 * (st >> 2)) >> RS)) & ~7u;
+            dma16(w_base, s_reg + c0 * 2u, lds0 + kGemmLdsS + ((st >> 2) & 1) * kGemmSlotS + wave * 1024);
+        }
+    };
+    auto issue_step = [&](int i) {
+        if (i + 3 >= 0 && i + 3 < nst) issue_tok(i + 3);
+        if (i + 4 < nst) issue_w(i + 4);
+    };
+    // loads step i issues (this wave)
+    auto nloads = [&](int i) {
+        return (i + 3 >= 0 && i + 3 < nst ? ndma : 0) + (i + 4 < nst ? 1 + ((i + 4) % 4 == 0 ? 1 : 0) : 0);
+    };
+
+    // --- read side: lane (r, kb) of the MFMAs ---
+    const int r = lane & 15, kb = lane >> 4;
+    int t_rd[2];  // token r's word 2 kb + j of a stage
+#pragma unroll
+    for (int j = 0; j < 2; ++j) t_rd[j] = r * 128 + (((2 * kb + j) ^ tok_swz(r)) * 16);
+    int w_rd[2];
+    uint32_t rsb[2];  // the row's first scale index
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int rho = 32 * wave + 16 * t + r;
+        w_rd[t] = rho * 32 + (((kb >> 1) ^ w_swz(rho)) * 16) + 8 * (kb & 1);
+        rsb[t] = (uint32_t)mat_row(t, r) * (uint32_t)gpr;
+    }
+    // valid 16-token tiles, rounded up to even (the loop comes in four
+    // unrolled forms; a tile past the block computes on stale rows, unstored)
+    const int nmt2 = min(8, (((mvalid + 15) >> 4) + 1) & ~1);
+
+    f32x4_t acc[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) acc[t][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Stage st's weight words and scale bits (LDS) of the lane's two row
+    // tiles; decode turns them into the MFMA operands (wd[j][t]: step j, row
+    // tile t), zero past the last sub-group.
+    auto read_w = [&](int st, uint2 (&wv)[2], uint32_t (&sv)[2]) {
+        const int slot = st & (kGemmSlots - 1);
+        const uint8_t* wb = g_lds + kGemmLdsW + slot * kGemmSlotW;
+        const int sg = 2 * st + (kb >> 1);
+        const int q = st >> 2;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            wv[t] = *reinterpret_cast<const uint2*>(wb + w_rd[t]);
+            const uint32_t c0 = (rsb[t] + (uint32_t)((8 * q) >> RS)) & ~7u;
+            const uint32_t pos = rsb[t] + (uint32_t)(sg >> RS) - c0;
+            const int rho = 32 * wave + 16 * t + r;
+            sv[t] = *reinterpret_cast<const uint16_t*>(g_lds + kGemmLdsS + (q & 1) * kGemmSlotS + rho * 32 + 2 * pos);
+        }
+    };
+    auto decode = [&](int st, const uint2 (&wv)[2], const uint32_t (&sv)[2], f16x8_t (&wd)[2][2]) {
+        const bool live = 2 * st + (kb >> 1) < ng;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t sb = live ? sv[t] : 0u;
+            const f16x2_t sc = __builtin_bit_cast(f16x2_t, sb | (sb << 16));
+            wd[0][t] = q4_word_to_f16x8(wv[t].x, sc);
+            wd[1][t] = q4_word_to_f16x8(wv[t].y, sc);
+        }
+    };
+
+    // Stage st's MFMAs with stage st + 1's weights read and decoded between
+    // them (wd: stage st's decoded weights in, stage st + 1's out; past the
+    // last stage the decode reads a stale slot and is not used).
+    auto compute = [&](auto nm_c, int st, f16x8_t (&wd)[2][2]) {
+        constexpr int NM = decltype(nm_c)::value;
+        const uint8_t* tb = g_lds + (st & (kGemmSlots - 1)) * kGemmSlotT;
+        // the next stage's weight reads first: its decode waits on them
+        const int sn = min(st + 1, nst - 1);
+        uint2 wv[2];
+        uint32_t sv[2];
+        read_w(sn, wv, sv);
+        __builtin_amdgcn_sched_barrier(0);
+        uint4 bt[2][NM];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) bt[j][mt] = *reinterpret_cast<const uint4*>(tb + mt * 2048 + t_rd[j]);
+        f16x8_t wn[2][2];
+        decode(sn, wv, sv, wn);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const f16x8_t b = __builtin_bit_cast(f16x8_t, bt[j][mt]);
+                acc[0][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wd[j][0], b, acc[0][mt], 0, 0, 0);
+                acc[1][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wd[j][1], b, acc[1][mt], 0, 0, 0);
+            }
+        // order: the token reads, then each MFMA followed by two vector
+        // instructions of the next stage's decode
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NM, 0);
+#pragma unroll
+        for (int i = 0; i < 4 * NM; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) wd[j][t] = wn[j][t];
+    };
+
+    // down: stage st's act chunk in LDS times 2^(chunk exponent - row
+    // exponent), 32 bytes of one token per thread
+    auto rescale = [&](int st) {
+        const int tt = tid >> 2;
+        const int d = shift_l[tt * kGemmMaxChunks + (st >> 1)];
+        if (tt >= mvalid || d == 0) return;
+        const uint32_t f = f16_pow2(d);
+        const f16x2_t f2 = __builtin_bit_cast(f16x2_t, f | (f << 16));
+        uint4* p = reinterpret_cast<uint4*>(g_lds + (st & (kGemmSlots - 1)) * kGemmSlotT + tt * 128 + (tid & 3) * 32);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint4 v = p[h];
+            v.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.x) * f2);
+            v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.y) * f2);
+            v.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.z) * f2);
+            v.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.w) * f2);
+            p[h] = v;
+        }
+    };
+
+    // Token rows of stage st sit in slot st % 4, its weight rows too, its
+    // scale window in window slot (st / 4) % 2.  Loads complete in issue
+    // order, so "step i's loads have landed" is "at most the loads of the
+    // steps after it are outstanding".  Main-loop step st (after the barrier
+    // that puts every wave past stage st - 1, whose slots it refills) needs
+    // stage st's tokens and stage st + 1's weights: gate/up waits for step st
+    // - 3.  Down also rescales stage st + 1's tokens during step st, so it
+    // waits for step st - 2; the next barrier publishes the rescale.
+    auto run = [&](auto nm_c) {
+        for (int i = -4; i < 0; ++i) issue_step(i);
+        f16x8_t wd[2][2];
+        {
+            // stage 0's weights (step -4) and, for down, its tokens (step -3)
+            wait_loads(MODE == 0 ? nloads(-3) + nloads(-2) + nloads(-1) : nloads(-2) + nloads(-1));
+            stage_barrier();
+            uint2 wv[2];
+            uint32_t sv[2];
+            read_w(0, wv, sv);
+            decode(0, wv, sv, wd);
+            if (MODE == 1) rescale(0);
+        }
+        for (int st = 0; st < nst; ++st) {
+            wait_loads(MODE == 0 ? nloads(st - 2) + nloads(st - 1) : nloads(st - 1));
+            stage_barrier();
+            issue_step(st);
+            if (MODE == 1 && st + 1 < nst) rescale(st + 1);
+            compute(nm_c, st, wd);
+        }
+    };
+    switch (nmt2) {
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 4: run(std::integral_constant<int, 4>{}); break;
+        case 6: run(std::integral_constant<int, 6>{}); break;
+        default: run(std::integral_constant<int, 8>{}); break;
+    }
+
+    // --- epilogues: lane (r, kb) holds C rows 4 kb + i of token 16 mt + r ---
+    if constexpr (MODE == 0) {
+        // act = silu(gate) * up at the x rows' scale; the tile's 128 columns
+        // of each token get the exponent of their largest magnitude (over the
+        // four lane groups, then the eight waves through LDS, reusing the
+        // token slots), then go out as fp16 image words: lane group kb's four
+        // columns are half kb & 1 of word kb >> 1 of the wave's 16 columns.
+        const int I = NR;
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(g_lds);  // [128 tokens][8 waves]
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+            const int tt = 16 * mt + r;
+            const int ex = exp_l[tt];
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = n0 + 16 * wave + act_col(4 * kb + i);
+                const float g = __builtin_ldexpf(acc[0][mt][i], ex), u = __builtin_ldexpf(acc[1][mt][i], ex);
+                const float v = col < I ? g / (1.0f + expf(-g)) * u : 0.0f;
+                acc[0][mt][i] = v;
+                m = fmaxf(m, fabsf(v));
+            }
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            if (kb == 0) red[tt * 8 + wave] = m;
+        }
+        __syncthreads();
+        uint8_t* img = dptr<uint8_t>(a.out);
+        const size_t ob = (size_t)himage_bytes(I);
+        const uint32_t woff = (uint32_t)((n0 + 16 * wave) >> 5) * 64u + 32u * (uint32_t)(wave & 1) + 8u * (uint32_t)kb;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+            const int tt = 16 * mt + r;
+            if (tt >= mvalid) continue;
+            const float4 r0 = *reinterpret_cast<const float4*>(red + tt * 8);
+            const float4 r1 = *reinterpret_cast<const float4*>(red + tt * 8 + 4);
+            const float M = fmaxf(fmaxf(fmaxf(r0.x, r0.y), fmaxf(r0.z, r0.w)), fmaxf(fmaxf(r1.x, r1.y), fmaxf(r1.z, r1.w)));
+            const int ae = M > 0.0f ? h16_exp(M) : kExpNone;
+            uint32_t h[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                h[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(acc[0][mt][i], -ae));
+            const int p = x.p0 + m0 + tt;
+            *reinterpret_cast<uint2*>(img + (size_t)p * ob + woff) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            if (wave == 0 && kb == 0) dptr<int>(a.W.act)[(size_t)p * nch + nb] = ae;
+        }
+    } else {
+        float* out = dptr<float>(a.out);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+            const int tt = 16 * mt + r;
+            if (tt >= mvalid) continue;
+            const int ex = exp_l[tt];
+            float* orow = out + (size_t)(x.p0 + m0 + tt) * NR;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int row = n0 + 32 * wave + 16 * t + 4 * kb;
+                if (row < NR)
+                    *reinterpret_cast<float4*>(orow + row) =
+                        make_float4(__builtin_ldexpf(acc[t][mt][0], ex), __builtin_ldexpf(acc[t][mt][1], ex),
+                                    __builtin_ldexpf(acc[t][mt][2], ex), __builtin_ldexpf(acc[t][mt][3], ex));
+            }
+        }
+    }
 }
 
 #define LP_BY_RS(group, call)          \
@@ -633,13 +622,13 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_tiles(const GemmArgs a
     if (tid == 0) dptr<int>(a.W.meta)[2] = min(base, a.max_tiles);
 }
 
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) lp_gemm_gateup(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(512) lp_gemm_gateup(const GemmArgs a) {
 #define LP_G(rs) gemm_body<0, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G
 }
 
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) lp_gemm_down(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(512) lp_gemm_down(const GemmArgs a) {
 #define LP_G(rs) gemm_body<1, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G

@@ -60,54 +60,6 @@ __device__ __forceinline__ T load_agent(const LP_GLOBAL T* p) {
 // ---------------------------------------------------------------------------
 namespace {
 
-// Token t's bf16 image (the prefill GEMM's A operand) from its row staged in
-// LDS, by the whole workgroup, and its lo flag (W.xlo[t]): thread u takes
-// sub-group u / 4, columns 8 (u % 4) .. 8 (u % 4) + 7, writes their bf16
-// parts, and the four threads of a sub-group add their part sums by quad
-// permutations ((s0 + s1) + (s2 + s3); the seed's rounding may differ from
-// the sequential sum of write_image_group in the last place).
-__device__ __forceinline__ void write_image_lds(const RouteArgs& a, int t, const float* row) {
-    const int H = a.L.hidden, ng = H >> 5, ngp = frag_ngp(H);
-    uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-    bool lo_any = false;
-    for (int u = threadIdx.x; u < 4 * ngp; u += blockDim.x) {  // whole quads together
-        const int g = u >> 2, d = u & 3;
-        float v[8];
-        if (g < ng) {
-            const float4 f0 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8);
-            const float4 f1 = *reinterpret_cast<const float4*>(row + g * 32 + d * 8 + 4);
-            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
-            v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-        }
-        uint32_t hi[8], lo[8];
-        float shi = 0.0f, slo = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            hi[i] = f32_to_bf16_rne(v[i]);
-            lo[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hi[i]));
-            shi += bf16_to_f32(hi[i]);
-            slo += bf16_to_f32(lo[i]);
-        }
-        shi = shi + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(shi), 0xb1, 0xf, 0xf, false));
-        shi = shi + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(shi), 0x4e, 0xf, 0xf, false));
-        slo = slo + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(slo), 0xb1, 0xf, 0xf, false));
-        slo = slo + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(slo), 0x4e, 0xf, 0xf, false));
-        const uint4 h4 = make_uint4(hi[0] | (hi[4] << 16), hi[1] | (hi[5] << 16), hi[2] | (hi[6] << 16),
-                                    hi[3] | (hi[7] << 16));
-        const uint4 l4 = make_uint4(lo[0] | (lo[4] << 16), lo[1] | (lo[5] << 16), lo[2] | (lo[6] << 16),
-                                    lo[3] | (lo[7] << 16));
-        reinterpret_cast<uint4*>(img + (size_t)g * 64)[d] = h4;
-        reinterpret_cast<uint4*>(img + (size_t)ngp * 64 + (size_t)g * 64)[d] = l4;
-        if (d == 0) reinterpret_cast<float2*>(img + (size_t)ngp * 128)[g] = make_float2(-136.0f * shi + -136.0f * slo, 0.0f);
-        lo_any |= (l4.x | l4.y | l4.z | l4.w) != 0u;
-    }
-    lo_any = __syncthreads_or(lo_any);
-    if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo_any ? 1 : 0;
-}
-
 // Token t's digit image (the grouped kernels' A operand) from its row staged
 // in LDS, by the whole workgroup: the four threads of a sub-group take eight
 // columns each, share the sub-group's largest magnitude and their sum of xq
@@ -161,19 +113,16 @@ __device__ __forceinline__ void write_image(const RouteArgs& a, int t) {
         uint8_t* img = dptr<uint8_t>(a.W.xd) + (size_t)t * dimage_bytes(H);
         for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) write_dimage_group(row, H, g, img);
     }
-    if (a.make_xf & kImgBf16) {
-        uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-        bool lo = false;
-        for (int g = threadIdx.x; g < frag_ngp(H); g += blockDim.x) lo |= write_image_group(row, H, g, img);
-        lo = __syncthreads_or(lo);
-        if (threadIdx.x == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
-    }
+    if (a.make_xf & kImgF16)
+        write_h16_image(row, H, dptr<uint8_t>(a.W.xf) + (size_t)t * himage_bytes(H), dptr<int>(a.W.xexp) + t);
 }
 
 // Token t's images from its row staged in LDS.
 __device__ __forceinline__ void write_images_lds(const RouteArgs& a, int t, const float* row) {
     if (a.make_xf & kImgDigits) write_dimage_lds(a, t, row);
-    if (a.make_xf & kImgBf16) write_image_lds(a, t, row);
+    if (a.make_xf & kImgF16)
+        write_h16_image(row, a.L.hidden, dptr<uint8_t>(a.W.xf) + (size_t)t * himage_bytes(a.L.hidden),
+                        dptr<int>(a.W.xexp) + t);
 }
 
 
@@ -395,7 +344,8 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_router(const RouteArgs 
 
 // Images of x alone (callers that route from their own logits, and the
 // large-batch router): one wave per token, lane l converting sub-groups l,
-// l + 64, ...; W.xlo[t] from a wave vote.  Grid (ceil(T / 4)), 256 threads.
+// l + 64, ... (digits) or 16-byte words l, l + 64, ... (fp16, after the row's
+// largest magnitude), and W.xexp[t].  Grid (ceil(T / 4)), 256 threads.
 extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs a) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.T) return;
@@ -405,12 +355,10 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs 
         uint8_t* img = dptr<uint8_t>(a.W.xd) + (size_t)t * dimage_bytes(H);
         for (int g = lane; g < frag_ngp(H); g += 64) write_dimage_group(row, H, g, img);
     }
-    if (a.make_xf & kImgBf16) {
-        uint8_t* img = dptr<uint8_t>(a.W.xf) + (size_t)t * image_bytes(H);
-        bool lo = false;
-        for (int g = lane; g < frag_ngp(H); g += 64) lo |= write_image_group(row, H, g, img);
-        lo = __any(lo);
-        if (lane == 0) dptr<int>(a.W.xlo)[t] = lo ? 1 : 0;
+    if (a.make_xf & kImgF16) {
+        const int e = h16_exp(row_absmax_wave(row, H, lane, 64));
+        write_h16_words(row, H, e, dptr<uint8_t>(a.W.xf) + (size_t)t * himage_bytes(H), lane, 64);
+        if (lane == 0) dptr<int>(a.W.xexp)[t] = e;
     }
 }
 

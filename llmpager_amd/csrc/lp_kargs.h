@@ -64,10 +64,16 @@ LPK_HD constexpr int dimage_bytes(int cols) { return 76 * frag_ngp(cols); }
 LPK_HD constexpr int dimage_seed_off(int ngp) { return 64 * ngp; }
 LPK_HD constexpr int dimage_sigma_off(int ngp) { return 72 * ngp; }
 
-// A token row's bf16 fragment image, the A operand of the prefill GEMM: part
-// 0 (bf16(x)) and part 1 (bf16(x - bf16(x))) as [ngp][64 B] blocks, then
-// [ngp][2] f32 seeds (-136 * the parts' sum over the sub-group, 0).
-LPK_HD constexpr int image_bytes(int cols) { return 136 * frag_ngp(cols); }
+// A token row's fp16 image, the token operand of the prefill GEMM: x * 2^-e
+// rounded to fp16 (RNE) as [ngp][4][8] halves, where 16-byte word j of
+// sub-group g holds columns 32 g + 8 j + (0, 4, 1, 5, 2, 6, 3, 7) (the order
+// in which a q4 weight word unpacks), zero padding sub-groups past the last.
+// The row's exponent e is kept beside it: x rows one per token (W.xexp, max
+// |x| 2^-e in [2^14, 2^15)), act rows one per kActChunk columns (W.act).
+LPK_HD constexpr int himage_bytes(int cols) { return 64 * frag_ngp(cols); }
+constexpr int kActChunk = 128;       // act columns per exponent (one gate/up row block)
+LPK_HD constexpr int act_chunks(int cols) { return frag_ngp(cols) >> 2; }
+constexpr int kExpNone = -1024;      // exponent of an all-zero chunk
 
 // The grouped kernels read a one-chunk tile's scales from a per-wave LDS
 // window (filled by 16-byte copies of whole scale lines) when the group is 32
@@ -258,17 +264,17 @@ struct Workspace {
     uint64_t uniq;       // i32 [E] experts with picks, ascending
     uint64_t meta;       // i32 [16]: [0] = unique count, [1] = error flags
     uint64_t et;         // ExpertEntry [E]
-    uint64_t act;        // f32 [T * k, I] expert-major activations
+    uint64_t act;        // f32 [T * k, I] expert-major activations; prefill GEMM: i32 [T * k][act_chunks(I)] act image exponents
     uint64_t y;          // f32 [T * k, H] expert-major expert outputs
-    uint64_t xf;         // [T] bf16 images of the layer input for the prefill GEMM (image_bytes(H) each)
+    uint64_t xf;         // [T] fp16 images of the layer input for the prefill GEMM (himage_bytes(H) each)
     uint64_t xd;         // [T] digit images of the layer input for the grouped kernels (dimage_bytes(H) each)
     uint64_t sh_et;      // shared MLP: shared_entries(T) ExpertEntry (consecutive tokens)
     uint64_t sh_perm;    // shared MLP: i32 [T], t
     uint64_t sh_act;     // shared MLP: f32 [T, shared_inter]
     uint64_t sh_y;       // shared MLP: f32 [T, H]
     uint64_t tiles;      // prefill GEMM: i32 tile list
-    uint64_t actimg;     // prefill GEMM: [T*k] images of act rows (image_bytes(I) each)
-    uint64_t xlo;        // i32 [T]: 1 when token t's image in xf has a non-zero lo part
+    uint64_t actimg;     // prefill GEMM: [T*k] fp16 images of act rows (himage_bytes(I) each)
+    uint64_t xexp;       // prefill GEMM: i32 [T], token t's image exponent in xf
     uint64_t disp;       // multi-block dispatch: i32 [nb][E] counts, [nb][E] first positions, [E] entries
 };
 
@@ -277,7 +283,7 @@ struct Workspace {
 // one entry of all T tokens above 64.
 LPK_HD constexpr int shared_entries(int T) { return T <= 64 ? (T + kEntryToks - 1) / kEntryToks : 1; }
 
-constexpr int kImgBf16 = 1;    // RouteArgs::make_xf bits
+constexpr int kImgF16 = 1;     // RouteArgs::make_xf bits
 constexpr int kImgDigits = 2;
 
 struct RouteArgs {
@@ -285,7 +291,7 @@ struct RouteArgs {
     Workspace W;
     uint64_t x;          // f32 [T, H]
     int32_t T;
-    int32_t make_xf;     // router: also write images of x: kImgBf16 into W.xf, kImgDigits into W.xd
+    int32_t make_xf;     // router: also write images of x: kImgF16 into W.xf (+ W.xexp), kImgDigits into W.xd
     uint64_t sync;       // fused routing: kSyncWords arrival counters, zero between launches
 };
 
@@ -340,33 +346,37 @@ LPK_HD constexpr int bal_lds_bytes(int hidden, int window_steps, int waves) {
 constexpr int kCombWaves = 8;
 constexpr int kCombShWaves = 2;
 
-// Prefill grouped GEMM (lp_gemm.hip).
+// Prefill grouped GEMM (lp_gemm.hip).  A tile is 128 tokens x 256 weight
+// rows (gate/up: 128 act columns, their gate and up rows), 8 waves; K runs
+// in stages of 64 columns.
 constexpr int kGemmBM = 128;           // tokens per tile
-constexpr int kGemmBN = 128;           // weight rows per tile (gate/up: 64 gate + the same 64 up)
+constexpr int kGemmBN = 256;           // weight rows per tile
+constexpr int kGemmWaves = 8;
 constexpr int kGemmMinPairsPerExpert = 16;  // the experts path switches to the GEMM at this average
 constexpr int kXcds = 8;               // MI355X: workgroup w is dispatched to XCD w % 8
+constexpr int kGemmMaxChunks = 64;     // act chunks per row the down GEMM's LDS table holds (I <= 8192)
 
-// GEMM LDS.  K is consumed one 32-column sub-group per pipeline stage; the
-// activation blocks come per stage (three slots: loads run two stages ahead),
-// the weight nibbles per kGemmBGroups sub-groups (64 bytes of each row) and
-// the scales per kGemmSGroups sub-groups, each in two slots.  Every read is
-// one base register plus an immediate offset below 64 KiB.
-constexpr int kGemmASlots = 3;
-constexpr int kGemmBGroups = 4;
-constexpr int kGemmSGroups = 8;
-constexpr int kGemmSlotA = 2 * kGemmBM * 64;                   // [part][token][64 B]
-constexpr int kGemmSlotB = kGemmBN * kGemmBGroups * 16;        // [row][4 x 16 B]
-constexpr int kGemmSlotS = kGemmBN * 32;                       // [row][16 f16 scales]
-constexpr int kGemmLdsB = kGemmASlots * kGemmSlotA;            // 49,152
-constexpr int kGemmLdsS = kGemmLdsB + 2 * kGemmSlotB;
-constexpr int kGemmLdsRows = kGemmLdsS + 2 * kGemmSlotS;
-constexpr int kGemmLds = kGemmLdsRows + kGemmBM * 8;           // + the tile rows' image addresses
+// GEMM LDS.  Token rows (128 B of each of the 128 tokens per stage) and weight
+// rows (32 B of each of the 256 rows per stage) in four slots each, loads
+// three stages ahead; scale windows (16 f16 of each row, every 4 stages) in
+// two; then the tile's row table, exponents and the down GEMM's per-(token,
+// chunk) exponent shifts.
+constexpr int kGemmSlots = 4;
+constexpr int kGemmSlotT = kGemmBM * 128;                      // 16 KiB
+constexpr int kGemmSlotW = kGemmBN * 32;                       // 8 KiB
+constexpr int kGemmSlotS = kGemmBN * 32;                       // 8 KiB
+constexpr int kGemmLdsW = kGemmSlots * kGemmSlotT;             // 65,536
+constexpr int kGemmLdsS = kGemmLdsW + kGemmSlots * kGemmSlotW; // 98,304
+constexpr int kGemmLdsRows = kGemmLdsS + 2 * kGemmSlotS;       // 114,688: u32 image offset per tile row
+constexpr int kGemmLdsExp = kGemmLdsRows + kGemmBM * 4;        // i32 exponent per tile row
+constexpr int kGemmLdsShift = kGemmLdsExp + kGemmBM * 4;       // i8 [128][kGemmMaxChunks]
+constexpr int kGemmLds = kGemmLdsShift + kGemmBM * kGemmMaxChunks;  // 123,904
 
 struct GemmArgs {
     LayerView L;
     Workspace W;
-    uint64_t a_img;      // A images: gate/up = W.xf (token rows through perm); down = act images
-    uint64_t out;        // gate/up: act images [T*k] (image_bytes(I) each); down: y f32 [T*k, H]
+    uint64_t a_img;      // token images: gate/up = W.xf (token rows through perm); down = W.actimg
+    uint64_t out;        // gate/up: act images [T*k] (himage_bytes(I) each); down: y f32 [T*k, H]
     uint64_t tiles;      // i32 [max_tiles]: (expert entry << 16) | token block; count in meta[2]
     int32_t T;
     int32_t max_tiles;

@@ -812,14 +812,15 @@ int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cac
 // experts average kGemmMinPairsPerExpert (token, pick) pairs.
 static bool use_gemm(const lp_moe_layer_desc* d, int T) {
     const long pairs = (long)T * d->top_k;
-    return pairs >= (long)kGemmMinPairsPerExpert * std::min<long>(d->experts, pairs);
+    return pairs >= (long)kGemmMinPairsPerExpert * std::min<long>(d->experts, pairs) &&
+           act_chunks(d->inter) <= kGemmMaxChunks;
 }
 
-// The images of x a layer's expert kernels read: bf16 images for the prefill
+// The images of x a layer's expert kernels read: fp16 images for the prefill
 // GEMM, digit images for the grouped kernels (every shared MLP included).
 static int image_kinds(const lp_moe_layer_desc* d, int T) {
     const bool gemm = use_gemm(d, T);
-    return (gemm ? kImgBf16 : 0) | (!gemm || d->shared_blob ? kImgDigits : 0);
+    return (gemm ? kImgF16 : 0) | (!gemm || d->shared_blob ? kImgDigits : 0);
 }
 
 static int gemm_max_tiles(const lp_moe_layer_desc* d, int T) {
@@ -854,9 +855,10 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->uniq = take(E * 4);
     out->meta = take(64);
     out->et = take(E * sizeof(ExpertEntry));
-    out->act = take(use_gemm(d, T) ? 0 : t * k * I * 4);  // the prefill GEMM writes act as images (actimg)
+    // the prefill GEMM writes act as fp16 images (actimg), their chunk exponents here
+    out->act = take(use_gemm(d, T) ? t * k * (uint64_t)act_chunks((int)I) * 4 : t * k * I * 4);
     out->y = take(t * k * H * 4);
-    out->xf = take(use_gemm(d, T) ? t * (uint64_t)image_bytes((int)H) : 0);
+    out->xf = take(use_gemm(d, T) ? t * (uint64_t)himage_bytes((int)H) : 0);
     out->xd = take(t * (uint64_t)dimage_bytes((int)H));
     const bool sh = d->shared_blob != 0;
     const uint64_t Is = sh ? (uint64_t)d->shared_inter : 0;
@@ -866,8 +868,8 @@ int lp_moe_ws_layout_get(const lp_moe_layer_desc* d, int T, lp_moe_ws_layout* ou
     out->sh_y = take(sh ? t * H * 4 : 0);
     const bool gemm = use_gemm(d, T);
     out->tiles = take(gemm ? (uint64_t)gemm_max_tiles(d, T) * 4 : 0);
-    out->actimg = take(gemm ? t * k * (uint64_t)image_bytes((int)I) : 0);
-    out->xlo = take(t * 4);
+    out->actimg = take(gemm ? t * k * (uint64_t)himage_bytes((int)I) : 0);
+    out->xexp = take(t * 4);
     out->disp = take(T > kTopkDispatchMaxT ? (2 * ((t + kDispTok - 1) / kDispTok) + 1) * E * 4 : 0);
     out->total = o;
     return LP_OK;
@@ -963,7 +965,7 @@ static void fill_views(const lp_moe_layer_desc* d, uint64_t ws, int T, LayerView
     W->sh_y = ws + lay.sh_y;
     W->tiles = ws + lay.tiles;
     W->actimg = ws + lay.actimg;
-    W->xlo = ws + lay.xlo;
+    W->xexp = ws + lay.xexp;
     W->disp = ws + lay.disp;
 }
 
@@ -1281,8 +1283,8 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d0, uint64_t x, uint
     if (!wave && use_gemm(d, T)) {
         if ((size_t)kGemmLds > c->max_lds) return fail(LP_E_UNSUPPORTED, "GEMM stages exceed the LDS");
         // the GEMM loads address images and weights as 32-bit offsets from a base
-        const uint64_t img_span = std::max((uint64_t)T * image_bytes(d->hidden),
-                                           (uint64_t)T * d->top_k * image_bytes(d->inter));
+        const uint64_t img_span = std::max((uint64_t)T * himage_bytes(d->hidden),
+                                           (uint64_t)T * d->top_k * himage_bytes(d->inter));
         if (img_span >= (1ull << 32) || d->slot_span >= (1ull << 32))
             return fail(LP_E_UNSUPPORTED, "prefill GEMM: activation images or expert slots of 4 GiB or more");
         GemmArgs gm{};
@@ -1292,16 +1294,16 @@ static int experts_impl(lp_ctx* c, const lp_moe_layer_desc* d0, uint64_t x, uint
         gm.tiles = ga.W.tiles;
         gm.max_tiles = gemm_max_tiles(d, T);
         if (int r = launch(c, kGemmTiles, dim3(1), dim3(256), 0, s, gm)) return r;
-        // gate/up writes act as the down GEMM's bf16 fragment images
+        // gate/up writes act as the down GEMM's fp16 images (+ chunk exponents in W.act)
         gm.a_img = ga.W.xf;
         gm.out = ga.W.actimg;
-        gm.nblocks = (d->inter + kGemmBN / 2 - 1) / (kGemmBN / 2);
-        if (int r = launch(c, kGemmGateup, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
+        gm.nblocks = act_chunks(d->inter);
+        if (int r = launch(c, kGemmGateup, dim3(gemm_grid(gm)), dim3(kGemmWaves * 64), 0, s, gm))
             return r;
         gm.a_img = ga.W.actimg;
         gm.out = ga.W.y;
         gm.nblocks = (d->hidden + kGemmBN - 1) / kGemmBN;
-        if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(256), 0, s, gm))
+        if (int r = launch(c, kGemmDown, dim3(gemm_grid(gm)), dim3(kGemmWaves * 64), 0, s, gm))
             return r;
     } else {
         // one token: down and combine in one launch (after the shared MLP,

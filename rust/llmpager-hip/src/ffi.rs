@@ -105,7 +105,7 @@ pub struct lp_moe_ws_layout {
     pub sh_y: u64,
     pub tiles: u64,
     pub actimg: u64,
-    pub xlo: u64,
+    pub xexp: u64,
     pub disp: u64,
     pub total: u64,
 }

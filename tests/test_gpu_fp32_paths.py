@@ -110,7 +110,7 @@ def test_stack_config1_inplace(cuda, T):
 
 def test_gemm_layer_fp32_activations(cuda):
     # 256 tokens x top-8 over 128 experts (16 pairs per expert on average):
-    # the grouped MFMA GEMM path, with fp32 x so gate/up runs its lo part
+    # the grouped MFMA GEMM path (fp16 operands) on fp32 x
     T, H, E = 256, 2048, 128
     L = DeviceLayer(cuda, H=H, I=768, E=E, k=8, group=32, seed=51)
     x = fp32_normal(T * H, 51).reshape(T, H)
@@ -122,12 +122,13 @@ def test_gemm_layer_fp32_activations(cuda):
     L.layer.forward(dx, dh, T, ws)
     got = cuda.download(dh, (T, H), np.float32)
     glog = cuda.download(ws + lay.logits, (T, E), np.float32)
-    xlo = cuda.download(ws + lay.xlo, (T,), np.int32)
+    xexp = cuda.download(ws + lay.xexp, (T,), np.int32)
     status = L.layer.status(ws, T)
     for p in (ws, dx, dh):
         cuda.free_device(p)
     assert status[1] == 0
-    assert xlo.min() == 1
+    m = np.abs(x).max(axis=1)
+    assert np.array_equal(xexp, np.frexp(m)[1] - 15)
     want = O.moe_layer(L.oracle_desc(), L.oracle_blobs(), x, h.copy(), logits_in=glog, threads=8)[0]
     assert rel_l2(got - h, want - h) <= 1e-3
     L.free()

@@ -75,57 +75,44 @@ def test_gemm_layer_config3(cuda):
     L.free()
 
 
-def _bf16_rne(v: np.ndarray) -> np.ndarray:
-    b = v.astype(np.float32).view(np.uint32).astype(np.uint64)
-    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint32)
+def h16_images(x: np.ndarray, ngp: int) -> tuple[np.ndarray, np.ndarray]:
+    """Restatement of the prefill GEMM's fp16 token images: per row e =
+    frexp(max |x|) - 15 (0 for a zero row), x 2^-e rounded to fp16, padded to
+    ngp 32-column sub-groups, each 16-byte word holding columns 8 j + (0, 4,
+    1, 5, 2, 6, 3, 7) of its sub-group."""
+    T, H = x.shape
+    m = np.abs(x).max(axis=1)
+    e = np.where(m > 0, np.frexp(m)[1] - 15, 0).astype(np.int32)
+    xp = np.zeros((T, 32 * ngp), np.float32)
+    xp[:, :H] = x
+    h = np.ldexp(xp.astype(np.float64), -e[:, None]).astype(np.float16)
+    order = np.array([0, 4, 1, 5, 2, 6, 3, 7])
+    h = h.reshape(T, ngp, 4, 8)[:, :, :, order].reshape(T, ngp * 32)
+    return h.view(np.uint8), e
 
 
-def _bf16_f32(h: np.ndarray) -> np.ndarray:
-    return (h.astype(np.uint32) << 16).view(np.float32)
-
-
-def test_route_bf16_images(cuda):
-    # Routing a large batch (T > 64) writes x's bf16 images for the prefill
-    # GEMM: per 32-column sub-group the parts hi = bf16(x), lo = bf16(x - hi) in
-    # fragment order (word w of 16-byte quarter d pairs columns 8d + w and
-    # 8d + w + 4), the seed -136 sum(hi) - 136 sum(lo) and 0, zero padding
-    # sub-groups (H = 320: ten sub-groups, twelve in the image), and each
-    # token's lo flag (tokens of even index bf16-valued: flag 0).
+def test_route_f16_images(cuda):
+    # Routing a large batch (T > 64) writes x's fp16 images for the prefill
+    # GEMM: byte-exact against h16_images, zero padding sub-groups (H = 320:
+    # ten sub-groups, twelve in the image), each row's exponent in xexp; rows
+    # scaled by powers of ten (and one zero row) move the exponent.
     T, H = 100, 320
     L = DeviceLayer(cuda, H=H, I=192, E=8, k=3, group=32, seed=24, router_std=0.05)
     x = np.random.default_rng(5).standard_normal((T, H)).astype(np.float32)
-    x[0::2] = _bf16_f32(_bf16_rne(x[0::2]))
+    x *= (10.0 ** np.random.default_rng(6).integers(-6, 7, T)).astype(np.float32)[:, None]
+    x[3] = 0.0
     lay = lp.ws_layout(L.desc, T)
     assert lay.tiles != lay.actimg, "this shape must take the GEMM path"
     ws = cuda.alloc_device(lay.total)
     dx = cuda.upload(x)
     L.layer.route(dx, T, ws)
     cuda.sync()
-    ib = 136 * 12
-    img = cuda.download(ws + lay.xf, (T, ib), np.uint8)
-    xlo = cuda.download(ws + lay.xlo, (T,), np.int32)
+    img = cuda.download(ws + lay.xf, (T, 64 * 12), np.uint8)
+    xexp = cuda.download(ws + lay.xexp, (T,), np.int32)
     for p in (ws, dx):
         cuda.free_device(p)
     L.free()
-    ngp = 12
-    xp = np.zeros((T, 32 * ngp), np.float32)
-    xp[:, :H] = x
-    hi = _bf16_rne(xp)
-    lo = _bf16_rne(xp - _bf16_f32(hi))
-    # fragment order: within each 8-column quarter, word w = col w | col w + 4 << 16
-    def words(p):
-        q = p.reshape(T, ngp, 4, 2, 4)  # [t, g, d, half, w]
-        return (q[:, :, :, 0, :] | (q[:, :, :, 1, :] << 16)).astype(np.uint32).reshape(T, ngp * 16)
-    got_hi = img[:, :ngp * 64].copy().view(np.uint32)
-    got_lo = img[:, ngp * 64:ngp * 128].copy().view(np.uint32)
-    assert np.array_equal(got_hi, words(hi))
-    assert np.array_equal(got_lo, words(lo))
-    seeds = img[:, ngp * 128:].copy().view(np.float32).reshape(T, ngp, 2)
-    shi = _bf16_f32(hi).reshape(T, ngp, 32).astype(np.float64).sum(axis=2)
-    slo = _bf16_f32(lo).reshape(T, ngp, 32).astype(np.float64).sum(axis=2)
-    want = -136.0 * shi - 136.0 * slo
-    scale = 136.0 * np.abs(_bf16_f32(hi)).reshape(T, ngp, 32).astype(np.float64).sum(axis=2) + 1e-30
-    assert np.all(np.abs(seeds[:, :, 0] - want) <= 4e-6 * scale)
-    assert np.all(seeds[:, :, 1] == 0.0)
-    assert np.all(seeds[:, 10:, 0] == 0.0)
-    assert np.array_equal(xlo, (np.arange(T) % 2).astype(np.int32))
+    want, we = h16_images(x, 12)
+    assert np.array_equal(xexp, we)
+    assert np.array_equal(img, want)
+    assert np.all(img[:, 64 * 10:] == 0) and np.all(img[3] == 0)

@@ -4,9 +4,10 @@ The grouped decode kernels multiply digit images: per 32-column sub-group,
 16-bit fixed point against the sub-group's own largest magnitude m (two int8
 digits, sigma = m / 32639), so a sub-group that holds an outlier beside
 N(0, 1) values keeps those small values only to within sigma / 2.  The
-prefill GEMM reads bf16 hi + lo images instead.  Residual streams have such
-columns, so these tests put a few outliers of |x| 100..1000 into random
-sub-groups of every token, and scale whole token rows by 30 and 1/30:
+prefill GEMM reads fp16 images scaled per token row instead.  Residual
+streams have such columns, so these tests put a few outliers of |x|
+100..1000 into random sub-groups of every token, and scale whole token rows
+by 30 and 1/30:
 
   - the device's digit images of x are byte-exact against the restatement
     of the per-sub-group rule (tests/_digits.py);
