@@ -73,24 +73,6 @@ __device__ __forceinline__ uint32_t lds_base() {
 // "every load issued before the last n has landed".
 #define LP_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
 
-__device__ __forceinline__ void wait_loads(int n) {
-    switch (n) {
-        case 0: LP_WAIT_VM_LGKM0(0); break;
-        case 1: LP_WAIT_VM_LGKM0(1); break;
-        case 2: LP_WAIT_VM_LGKM0(2); break;
-        case 3: LP_WAIT_VM_LGKM0(3); break;
-        case 4: LP_WAIT_VM_LGKM0(4); break;
-        case 5: LP_WAIT_VM_LGKM0(5); break;
-        case 6: LP_WAIT_VM_LGKM0(6); break;
-        case 7: LP_WAIT_VM_LGKM0(7); break;
-        case 8: LP_WAIT_VM_LGKM0(8); break;
-        case 9: LP_WAIT_VM_LGKM0(9); break;
-        case 10: LP_WAIT_VM_LGKM0(10); break;
-        case 11: LP_WAIT_VM_LGKM0(11); break;
-        default: LP_WAIT_VM_LGKM0(12); break;
-    }
-}
-
 // s_barrier as a compiler-level memory fence too: no LDS access or load moves
 // across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
@@ -134,6 +116,15 @@ __device__ __forceinline__ uint32_t f16_pow2(int d) {
     return d >= -14 ? (uint32_t)(d + 15) << 10 : d >= -24 ? 1u << (d + 24) : 0u;
 }
 
+// Waves per tile and the copies each issues per stage: RT MFMA row tiles
+// (16 rows each) per wave; tokens in copies of 8 rows x 128 B, weights and
+// scale windows in copies of 32 rows x 32 B.
+constexpr int RT = kGemmRowTiles;
+constexpr int kWaves = kGemmWaves;
+constexpr int NTD = kGemmBM / kWaves / 8;  // token copies per wave per stage
+constexpr int NWD = 16 * RT / 32;          // weight (and scale) copies per wave per stage
+static_assert(kWaves * 16 * RT == kGemmBN && NTD >= 1 && NWD >= 1, "GEMM tile shape");
+
 template <int MODE, int RS>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const LayerView& L = a.L;
@@ -162,7 +153,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const int n0 = nb * (MODE == 0 ? kActChunk : kGemmBN);  // gate/up: first act column; down: first row
     const uint32_t rowbytes = (uint32_t)himage_bytes(K);
     const int tid = threadIdx.x, lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: DMA targets stay scalar
+    const int wave = uni(tid >> 6);  // uniform: DMA targets stay scalar
     int* meta = dptr<int>(a.W.meta);
     if (x.blob == 0) {  // a routed expert without a slot: flag it, contribute zeros
         if (tid == 0 && nb == 0) atomicOr(meta + 1, kErrMissingExpert);
@@ -210,63 +201,75 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     }
     __syncthreads();
 
+    // --- rows: wave w owns the tile's weight rows 16 RT w .. 16 RT (w + 1) -
+    // 1, MFMA row tiles t = 0 .. RT - 1 (row 16 t + r).  Gate/up: the wave's
+    // 8 RT act columns n0 + 8 RT w .. in gate tiles 0 .. RT / 2 - 1 and the
+    // same in up tiles RT / 2 .. RT - 1 ---
+    constexpr int RH = RT / 2;
+    auto mat_row = [&](int t, int r) {
+        return min(MODE == 0 ? n0 + 8 * RT * wave + 16 * (t % RH) + act_col(r) : n0 + 16 * RT * wave + 16 * t + r,
+                   NR - 1);
+    };
+    auto region = [&](int t) { return (uint32_t)(MODE == 0 ? (t >= RH ? L.up_off : L.gate_off) : L.down_off); };
+    const uint32_t sbytes = (uint32_t)NR * (uint32_t)gpr * 2u;
+
     // --- load side: a uniform 64-bit base plus per-lane 32-bit offsets ---
     const uint32_t lds0 = lds_base();
     const uint64_t a_base = a.a_img;
     const uint64_t w_base = (uint64_t)(uint32_t)uni((int)(uint32_t)x.blob) | ((uint64_t)(uint32_t)uni((int)(uint32_t)(x.blob >> 32)) << 32);
-    // tokens: copy u of the wave takes tile tokens 16 w + 8 u + (l >> 3), lane l
-    // filling position l & 7 of its row (word (l & 7) ^ tok_swz); copies whose
-    // eight tokens are all past the block are skipped
-    const int ndma = max(0, min(2, (mvalid - 16 * wave + 7) >> 3));
-    uint32_t t_off[2];
+    // tokens: copy u of the wave takes tile tokens 8 (NTD w + u) + (l >> 3),
+    // lane l filling position l & 7 of its row (word (l & 7) ^ tok_swz); every
+    // wave issues all its copies (rows past the block repeat its last token),
+    // so the main loop's wait counts are constants
+    uint32_t t_off[NTD];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int tt = 16 * wave + 8 * u + (lane >> 3);
+    for (int u = 0; u < NTD; ++u) {
+        const int tt = 8 * (NTD * wave + u) + (lane >> 3);
         t_off[u] = rows_l[tt] + (uint32_t)(((lane & 7) ^ tok_swz(tt & 15)) * 16);
     }
-    // weights: LDS row rho = 32 w + (l >> 1) (MFMA tile (rho >> 4) & 1, row
-    // rho & 15), lane l filling piece l & 1, i.e. sub-group 2 st + h
-    auto mat_row = [&](int t, int r) {
-        return min(MODE == 0 ? n0 + 16 * wave + act_col(r) : n0 + 32 * wave + 16 * t + r, NR - 1);
-    };
-    auto region = [&](int t) { return (uint32_t)(MODE == 0 ? (t ? L.up_off : L.gate_off) : L.down_off); };
-    const uint32_t sbytes = (uint32_t)NR * (uint32_t)gpr * 2u;
-    const int d_t = lane >> 5, d_r = (lane >> 1) & 15;
+    // weights and scale windows: copy u of the wave fills LDS rows 16 RT w +
+    // 32 u + (l >> 1) (tile 2 u + (l >> 5), row (l >> 1) & 15), lane l piece
+    // l & 1 (weights: sub-group 2 st + ((l & 1) ^ w_swz); scales: half l & 1
+    // of the 16-scale window)
+    const int d_r = (lane >> 1) & 15;
     const int d_h = (lane & 1) ^ w_swz(d_r);
-    const uint32_t w_row = region(d_t) + sbytes + (uint32_t)mat_row(d_t, d_r) * (uint32_t)ng * 16u;
-    const uint32_t s_row = (uint32_t)mat_row(d_t, d_r) * (uint32_t)gpr;  // the row's first scale
-    const uint32_t s_reg = region(d_t) + 16u * (uint32_t)(lane & 1);
-
-    // Pipeline step i (i = -4 .. nst - 5 before and in the main loop) issues
-    // the token rows of stage i + 3 and the weight rows of stage i + 4 (with
-    // the scale window of stages i + 4 .. i + 7 when i + 4 is a multiple of
-    // 4): weights run one stage ahead of the tokens, so that stage st's
-    // MFMAs can share the wave with the decode of stage st + 1's weights.
-    auto issue_tok = [&](int st) {
-        const int slot = st & (kGemmSlots - 1);
+    uint32_t w_row[NWD], s_row[NWD], s_reg[NWD];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-            if (u < ndma)
-                dma16(a_base + (uint64_t)st * 128, t_off[u], lds0 + slot * kGemmSlotT + (16 * wave + 8 * u) * 128);
+    for (int u = 0; u < NWD; ++u) {
+        const int t = 2 * u + (lane >> 5);
+        w_row[u] = region(t) + sbytes + (uint32_t)mat_row(t, d_r) * (uint32_t)ng * 16u;
+        s_row[u] = (uint32_t)mat_row(t, d_r) * (uint32_t)gpr;  // the row's first scale
+        s_reg[u] = region(t) + 16u * (uint32_t)(lane & 1);
+    }
+
+    // Pipeline step i issues the token rows of stage i + 3 (NTD loads) and
+    // the weight rows of stage i + 4 (NWD, plus NWD for the scale window of
+    // stages i + 4 .. i + 7 when i + 4 is a multiple of 4): weights run one
+    // stage ahead of the tokens, so that stage st's MFMAs share the wave
+    // with the decode of stage st + 1's weights.  Slots are compile-time
+    // (stage % 4).
+    auto issue_tok = [&](auto slot_c, int st) {
+        constexpr int SLOT = decltype(slot_c)::value;
+        const uint64_t base = a_base + (uint64_t)st * 128;
+#pragma unroll
+        for (int u = 0; u < NTD; ++u) dma16(base, t_off[u], lds0 + SLOT * kGemmSlotT + 8 * (NTD * wave + u) * 128);
     };
-    auto issue_w = [&](int st) {
-        const int slot = st & (kGemmSlots - 1);
+    auto issue_w = [&](auto slot_c, int st) {
+        constexpr int SLOT = decltype(slot_c)::value;
         const uint32_t sg = (uint32_t)min(2 * st + d_h, ng - 1);
-        dma16(w_base, w_row + sg * 16u, lds0 + kGemmLdsW + slot * kGemmSlotW + wave * 1024);
-        if ((st & 3) == 0) {
+#pragma unroll
+        for (int u = 0; u < NWD; ++u)
+            dma16(w_base, w_row[u] + sg * 16u, lds0 + kGemmLdsW + SLOT * kGemmSlotW + (NWD * wave + u) * 1024);
+        if constexpr (SLOT == 0) {
             // the window starts at the 8-aligned scale index at or below the
             // row's first scale of stages st .. st + 3: 16 scales cover them
-            const uint32_t c0 = (s_row + (uint32_t)((8 * (st >> 2)) >> RS)) & ~7u;
-            dma16(w_base, s_reg + c0 * 2u, lds0 + kGemmLdsS + ((st >> 2) & 1) * kGemmSlotS + wave * 1024);
+            const int q = st >> 2;
+#pragma unroll
+            for (int u = 0; u < NWD; ++u) {
+                const uint32_t c0 = (s_row[u] + (uint32_t)((8 * q) >> RS)) & ~7u;
+                dma16(w_base, s_reg[u] + c0 * 2u, lds0 + kGemmLdsS + (q & 1) * kGemmSlotS + (NWD * wave + u) * 1024);
+            }
         }
-    };
-    auto issue_step = [&](int i) {
-        if (i + 3 >= 0 && i + 3 < nst) issue_tok(i + 3);
-        if (i + 4 < nst) issue_w(i + 4);
-    };
-    // loads step i issues (this wave)
-    auto nloads = [&](int i) {
-        return (i + 3 >= 0 && i + 3 < nst ? ndma : 0) + (i + 4 < nst ? 1 + ((i + 4) % 4 == 0 ? 1 : 0) : 0);
     };
 
     // --- read side: lane (r, kb) of the MFMAs ---
@@ -274,45 +277,46 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     int t_rd[2];  // token r's word 2 kb + j of a stage
 #pragma unroll
     for (int j = 0; j < 2; ++j) t_rd[j] = r * 128 + (((2 * kb + j) ^ tok_swz(r)) * 16);
-    int w_rd[2];
-    uint32_t rsb[2];  // the row's first scale index
+    int w_rd[RT], s_rd[RT];
+    uint32_t rsb[RT];  // the row's first scale index
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int rho = 32 * wave + 16 * t + r;
+    for (int t = 0; t < RT; ++t) {
+        const int rho = 16 * RT * wave + 16 * t + r;
         w_rd[t] = rho * 32 + (((kb >> 1) ^ w_swz(rho)) * 16) + 8 * (kb & 1);
+        s_rd[t] = rho * 32;
         rsb[t] = (uint32_t)mat_row(t, r) * (uint32_t)gpr;
     }
     // valid 16-token tiles, rounded up to even (the loop comes in four
     // unrolled forms; a tile past the block computes on stale rows, unstored)
     const int nmt2 = min(8, (((mvalid + 15) >> 4) + 1) & ~1);
 
-    f32x4_t acc[2][8];
+    f32x4_t acc[RT][8];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) acc[t][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Stage st's weight words and scale bits (LDS) of the lane's two row
-    // tiles; decode turns them into the MFMA operands (wd[j][t]: step j, row
-    // tile t), zero past the last sub-group.
-    auto read_w = [&](int st, uint2 (&wv)[2], uint32_t (&sv)[2]) {
-        const int slot = st & (kGemmSlots - 1);
-        const uint8_t* wb = g_lds + kGemmLdsW + slot * kGemmSlotW;
-        const int sg = 2 * st + (kb >> 1);
+    // Stage st's weight words and scale bits (LDS) of the lane's RT row
+    // tiles (SLOT = st % 4); decode turns them into the MFMA operands
+    // (wd[j][t]: step j, row tile t), zero past the last sub-group.  Within a
+    // window the lane's scale sits at ((rsb + 8 q >> RS) & 7) + ((2 (st % 4) +
+    // (kb >> 1)) >> RS).
+    auto read_w = [&](auto slot_c, int st, uint2 (&wv)[RT], uint32_t (&sv)[RT]) {
+        constexpr int SLOT = decltype(slot_c)::value;
+        const uint8_t* wb = g_lds + kGemmLdsW + SLOT * kGemmSlotW;
         const int q = st >> 2;
+        const uint8_t* sb = g_lds + kGemmLdsS + (q & 1) * kGemmSlotS;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < RT; ++t) {
             wv[t] = *reinterpret_cast<const uint2*>(wb + w_rd[t]);
-            const uint32_t c0 = (rsb[t] + (uint32_t)((8 * q) >> RS)) & ~7u;
-            const uint32_t pos = rsb[t] + (uint32_t)(sg >> RS) - c0;
-            const int rho = 32 * wave + 16 * t + r;
-            sv[t] = *reinterpret_cast<const uint16_t*>(g_lds + kGemmLdsS + (q & 1) * kGemmSlotS + rho * 32 + 2 * pos);
+            const uint32_t pos = ((rsb[t] + (uint32_t)((8 * q) >> RS)) & 7u) + (uint32_t)((2 * SLOT + (kb >> 1)) >> RS);
+            sv[t] = *reinterpret_cast<const uint16_t*>(sb + s_rd[t] + 2 * pos);
         }
     };
-    auto decode = [&](int st, const uint2 (&wv)[2], const uint32_t (&sv)[2], f16x8_t (&wd)[2][2]) {
+    auto decode = [&](int st, const uint2 (&wv)[RT], const uint32_t (&sv)[RT], f16x8_t (&wd)[2][RT]) {
         const bool live = 2 * st + (kb >> 1) < ng;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < RT; ++t) {
             const uint32_t sb = live ? sv[t] : 0u;
             const f16x2_t sc = __builtin_bit_cast(f16x2_t, sb | (sb << 16));
             wd[0][t] = q4_word_to_f16x8(wv[t].x, sc);
@@ -320,58 +324,61 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         }
     };
 
-    // Stage st's MFMAs with stage st + 1's weights read and decoded between
-    // them (wd: stage st's decoded weights in, stage st + 1's out; past the
-    // last stage the decode reads a stale slot and is not used).
-    auto compute = [&](auto nm_c, int st, f16x8_t (&wd)[2][2]) {
+    // Stage st's MFMAs (slot SLOT) with stage st + 1's weights read and
+    // decoded between them (wd: stage st's decoded weights in, stage st + 1's
+    // out; past the last stage the decode reads a stale slot, unused).
+    auto compute = [&](auto nm_c, auto slot_c, int st, f16x8_t (&wd)[2][RT]) {
         constexpr int NM = decltype(nm_c)::value;
-        const uint8_t* tb = g_lds + (st & (kGemmSlots - 1)) * kGemmSlotT;
+        constexpr int SLOT = decltype(slot_c)::value;
+        const uint8_t* tb = g_lds + SLOT * kGemmSlotT;
         // the next stage's weight reads first: its decode waits on them
-        const int sn = min(st + 1, nst - 1);
-        uint2 wv[2];
-        uint32_t sv[2];
-        read_w(sn, wv, sv);
+        uint2 wv[RT];
+        uint32_t sv[RT];
+        read_w(std::integral_constant<int, (SLOT + 1) & 3>{}, st + 1, wv, sv);
         __builtin_amdgcn_sched_barrier(0);
         uint4 bt[2][NM];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int mt = 0; mt < NM; ++mt) bt[j][mt] = *reinterpret_cast<const uint4*>(tb + mt * 2048 + t_rd[j]);
-        f16x8_t wn[2][2];
-        decode(sn, wv, sv, wn);
+        f16x8_t wn[2][RT];
+        decode(st + 1, wv, sv, wn);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int mt = 0; mt < NM; ++mt) {
                 const f16x8_t b = __builtin_bit_cast(f16x8_t, bt[j][mt]);
-                acc[0][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wd[j][0], b, acc[0][mt], 0, 0, 0);
-                acc[1][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wd[j][1], b, acc[1][mt], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < RT; ++t)
+                    acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wd[j][t], b, acc[t][mt], 0, 0, 0);
             }
-        // order: the token reads, then each MFMA followed by two vector
-        // instructions of the next stage's decode
+        // order: the token reads, then each MFMA followed by (at most) two
+        // vector instructions of the next stage's decode
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * NM, 0);
 #pragma unroll
-        for (int i = 0; i < 4 * NM; ++i) {
+        for (int i = 0; i < 2 * RT * NM; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int t = 0; t < 2; ++t) wd[j][t] = wn[j][t];
+            for (int t = 0; t < RT; ++t) wd[j][t] = wn[j][t];
     };
 
     // down: stage st's act chunk in LDS times 2^(chunk exponent - row
-    // exponent), 32 bytes of one token per thread
-    auto rescale = [&](int st) {
-        const int tt = tid >> 2;
+    // exponent), 128 / TPT bytes of one token per thread
+    constexpr int TPT = 64 * kWaves / kGemmBM;  // threads per token
+    auto rescale = [&](auto slot_c, int st) {
+        constexpr int SLOT = decltype(slot_c)::value;
+        const int tt = tid / TPT;
         const int d = shift_l[tt * kGemmMaxChunks + (st >> 1)];
         if (tt >= mvalid || d == 0) return;
         const uint32_t f = f16_pow2(d);
         const f16x2_t f2 = __builtin_bit_cast(f16x2_t, f | (f << 16));
-        uint4* p = reinterpret_cast<uint4*>(g_lds + (st & (kGemmSlots - 1)) * kGemmSlotT + tt * 128 + (tid & 3) * 32);
+        uint4* p = reinterpret_cast<uint4*>(g_lds + SLOT * kGemmSlotT + tt * 128 + (tid % TPT) * (128 / TPT));
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 8 / TPT; ++h) {
             uint4 v = p[h];
             v.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.x) * f2);
             v.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, v.y) * f2);
@@ -384,31 +391,67 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     // Token rows of stage st sit in slot st % 4, its weight rows too, its
     // scale window in window slot (st / 4) % 2.  Loads complete in issue
     // order, so "step i's loads have landed" is "at most the loads of the
-    // steps after it are outstanding".  Main-loop step st (after the barrier
-    // that puts every wave past stage st - 1, whose slots it refills) needs
-    // stage st's tokens and stage st + 1's weights: gate/up waits for step st
-    // - 3.  Down also rescales stage st + 1's tokens during step st, so it
-    // waits for step st - 2; the next barrier publishes the rescale.
+    // steps after it are outstanding": step i issues NTD + NWD loads, NWD more
+    // when i is a multiple of 4, while i + 4 < nst.  Main-loop step st (after
+    // the barrier that puts every wave past stage st - 1, whose slots it
+    // refills) needs stage st's tokens and stage st + 1's weights, i.e. step
+    // st - 3, so steps st - 2 and st - 1 may stay outstanding.  Down also
+    // rescales stage st + 1's tokens during step st, so it waits for those
+    // (step st - 2's token loads); the next barrier publishes the rescale.
+    // The last three steps wait for everything.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    auto step = [&](auto nm_c, auto slot_c, int st, f16x8_t (&wd)[2][RT]) {
+        constexpr int U = decltype(slot_c)::value;
+        constexpr int OUT = (MODE == 0 ? 2 * (NTD + NWD) : NTD + 2 * NWD) + NWD * ((U == 1) + (U == 2));
+        if (st + 3 < nst) {
+            LP_WAIT_VM_LGKM0(OUT);
+        } else {
+            LP_WAIT_VM_LGKM0(0);
+        }
+        stage_barrier();
+        if (st + 3 < nst) issue_tok(std::integral_constant<int, (U + 3) & 3>{}, st + 3);
+        if (st + 4 < nst) issue_w(slot_c, st + 4);
+        if (MODE == 1 && st + 1 < nst) rescale(std::integral_constant<int, (U + 1) & 3>{}, st + 1);
+        compute(nm_c, slot_c, st, wd);
+    };
     auto run = [&](auto nm_c) {
-        for (int i = -4; i < 0; ++i) issue_step(i);
-        f16x8_t wd[2][2];
+        // steps -4 .. -1 (weights of stage 0 with its window: 2 NWD loads;
+        // then per stage NTD token loads and NWD weight loads)
+        issue_w(I0{}, 0);
+        issue_tok(I0{}, 0);
+        if (nst > 1) issue_w(I1{}, 1);
+        if (nst > 1) issue_tok(I1{}, 1);
+        if (nst > 2) issue_w(I2{}, 2);
+        if (nst > 2) issue_tok(I2{}, 2);
+        if (nst > 3) issue_w(I3{}, 3);
+        f16x8_t wd[2][RT];
         {
             // stage 0's weights (step -4) and, for down, its tokens (step -3)
-            wait_loads(MODE == 0 ? nloads(-3) + nloads(-2) + nloads(-1) : nloads(-2) + nloads(-1));
+            if (nst > 3) {
+                LP_WAIT_VM_LGKM0(MODE == 0 ? 3 * (NTD + NWD) : 3 * NWD + 2 * NTD);
+            } else {
+                LP_WAIT_VM_LGKM0(0);
+            }
             stage_barrier();
-            uint2 wv[2];
-            uint32_t sv[2];
-            read_w(0, wv, sv);
+            uint2 wv[RT];
+            uint32_t sv[RT];
+            read_w(I0{}, 0, wv, sv);
             decode(0, wv, sv, wd);
-            if (MODE == 1) rescale(0);
+            if (MODE == 1) rescale(I0{}, 0);
         }
-        for (int st = 0; st < nst; ++st) {
-            wait_loads(MODE == 0 ? nloads(st - 2) + nloads(st - 1) : nloads(st - 1));
-            stage_barrier();
-            issue_step(st);
-            if (MODE == 1 && st + 1 < nst) rescale(st + 1);
-            compute(nm_c, st, wd);
+        int st = 0;
+        for (; st + 4 <= nst; st += 4) {
+            step(nm_c, I0{}, st, wd);
+            step(nm_c, I1{}, st + 1, wd);
+            step(nm_c, I2{}, st + 2, wd);
+            step(nm_c, I3{}, st + 3, wd);
         }
+        if (st < nst) step(nm_c, I0{}, st, wd);
+        if (st + 1 < nst) step(nm_c, I1{}, st + 1, wd);
+        if (st + 2 < nst) step(nm_c, I2{}, st + 2, wd);
     };
     switch (nmt2) {
         case 2: run(std::integral_constant<int, 2>{}); break;
@@ -419,49 +462,67 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
     // --- epilogues: lane (r, kb) holds C rows 4 kb + i of token 16 mt + r ---
     if constexpr (MODE == 0) {
-        // act = silu(gate) * up at the x rows' scale; the tile's 128 columns
-        // of each token get the exponent of their largest magnitude (over the
-        // four lane groups, then the eight waves through LDS, reusing the
-        // token slots), then go out as fp16 image words: lane group kb's four
-        // columns are half kb & 1 of word kb >> 1 of the wave's 16 columns.
+        // act = silu(gate) * up at the x rows' scale (gate tile h with up tile
+        // h + RT / 2: act columns n0 + 8 RT w + 16 h + act_col(4 kb + i)); the
+        // tile's 128 columns of each token get the exponent of their largest
+        // magnitude (over the four lane groups, then the waves through LDS,
+        // reusing the token slots), then go out as fp16 image words: lane
+        // group kb's four columns of tile h are half kb & 1 of word kb >> 1 of
+        // the 16 columns from column c = n0 + 8 RT w + 16 h, i.e. at byte 64
+        // (c / 32) + 2 (c % 32) + 8 kb of the row.
         const int I = NR;
         __syncthreads();
-        float* red = reinterpret_cast<float*>(g_lds);  // [128 tokens][8 waves]
+        float* red = reinterpret_cast<float*>(g_lds);  // [128 tokens][kWaves]
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) {
             const int tt = 16 * mt + r;
             const int ex = exp_l[tt];
             float m = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int col = n0 + 16 * wave + act_col(4 * kb + i);
-                const float g = __builtin_ldexpf(acc[0][mt][i], ex), u = __builtin_ldexpf(acc[1][mt][i], ex);
-                const float v = col < I ? g / (1.0f + expf(-g)) * u : 0.0f;
-                acc[0][mt][i] = v;
-                m = fmaxf(m, fabsf(v));
-            }
+            for (int h = 0; h < RH; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int col = n0 + 8 * RT * wave + 16 * h + act_col(4 * kb + i);
+                    const float g = __builtin_ldexpf(acc[h][mt][i], ex), u = __builtin_ldexpf(acc[h + RH][mt][i], ex);
+                    // silu with the hardware exp2 and reciprocal: a few ulp
+                    // of fp32, far below the fp16 rounding that follows
+                    const float e = __builtin_amdgcn_exp2f(-1.44269504f * g);
+                    const float v = col < I ? g * __builtin_amdgcn_rcpf(1.0f + e) * u : 0.0f;
+                    acc[h][mt][i] = v;
+                    m = fmaxf(m, fabsf(v));
+                }
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
-            if (kb == 0) red[tt * 8 + wave] = m;
+            if (kb == 0) red[tt * kWaves + wave] = m;
         }
         __syncthreads();
         uint8_t* img = dptr<uint8_t>(a.out);
         const size_t ob = (size_t)himage_bytes(I);
-        const uint32_t woff = (uint32_t)((n0 + 16 * wave) >> 5) * 64u + 32u * (uint32_t)(wave & 1) + 8u * (uint32_t)kb;
+        auto woff = [&](int h) {
+            const int c = n0 + 8 * RT * wave + 16 * h;
+            return (uint32_t)(c >> 5) * 64u + 2u * (uint32_t)(c & 31) + 8u * (uint32_t)kb;
+        };
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) {
             const int tt = 16 * mt + r;
             if (tt >= mvalid) continue;
-            const float4 r0 = *reinterpret_cast<const float4*>(red + tt * 8);
-            const float4 r1 = *reinterpret_cast<const float4*>(red + tt * 8 + 4);
-            const float M = fmaxf(fmaxf(fmaxf(r0.x, r0.y), fmaxf(r0.z, r0.w)), fmaxf(fmaxf(r1.x, r1.y), fmaxf(r1.z, r1.w)));
-            const int ae = M > 0.0f ? h16_exp(M) : kExpNone;
-            uint32_t h[4];
+            float M = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                h[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(acc[0][mt][i], -ae));
+            for (int w4 = 0; w4 < kWaves; w4 += 4) {
+                const float4 rv = *reinterpret_cast<const float4*>(red + tt * kWaves + w4);
+                M = fmaxf(M, fmaxf(fmaxf(rv.x, rv.y), fmaxf(rv.z, rv.w)));
+            }
+            const int ae = M > 0.0f ? h16_exp(M) : kExpNone;
             const int p = x.p0 + m0 + tt;
-            *reinterpret_cast<uint2*>(img + (size_t)p * ob + woff) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+#pragma unroll
+            for (int h = 0; h < RH; ++h) {
+                uint32_t hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    hv[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(acc[h][mt][i], -ae));
+                *reinterpret_cast<uint2*>(img + (size_t)p * ob + woff(h)) =
+                    make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+            }
             if (wave == 0 && kb == 0) dptr<int>(a.W.act)[(size_t)p * nch + nb] = ae;
         }
     } else {
@@ -473,8 +534,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
             const int ex = exp_l[tt];
             float* orow = out + (size_t)(x.p0 + m0 + tt) * NR;
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int row = n0 + 32 * wave + 16 * t + 4 * kb;
+            for (int t = 0; t < RT; ++t) {
+                const int row = n0 + 16 * RT * wave + 16 * t + 4 * kb;
                 if (row < NR)
                     *reinterpret_cast<float4*>(orow + row) =
                         make_float4(__builtin_ldexpf(acc[t][mt][0], ex), __builtin_ldexpf(acc[t][mt][1], ex),
@@ -622,13 +683,13 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_tiles(const GemmArgs a
     if (tid == 0) dptr<int>(a.W.meta)[2] = min(base, a.max_tiles);
 }
 
-extern "C" __global__ void __launch_bounds__(512) lp_gemm_gateup(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(64 * kGemmWaves) lp_gemm_gateup(const GemmArgs a) {
 #define LP_G(rs) gemm_body<0, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G
 }
 
-extern "C" __global__ void __launch_bounds__(512) lp_gemm_down(const GemmArgs a) {
+extern "C" __global__ void __launch_bounds__(64 * kGemmWaves) lp_gemm_down(const GemmArgs a) {
 #define LP_G(rs) gemm_body<1, rs>(a)
     LP_BY_RS(a.L.group, LP_G)
 #undef LP_G

@@ -347,11 +347,12 @@ constexpr int kCombWaves = 8;
 constexpr int kCombShWaves = 2;
 
 // Prefill grouped GEMM (lp_gemm.hip).  A tile is 128 tokens x 256 weight
-// rows (gate/up: 128 act columns, their gate and up rows), 8 waves; K runs
-// in stages of 64 columns.
+// rows (gate/up: 128 act columns, their gate and up rows), kGemmWaves waves of
+// kGemmRowTiles 16-row MFMA tiles; K runs in stages of 64 columns.
 constexpr int kGemmBM = 128;           // tokens per tile
 constexpr int kGemmBN = 256;           // weight rows per tile
-constexpr int kGemmWaves = 8;
+constexpr int kGemmRowTiles = 2;      // 16-row MFMA tiles per wave
+constexpr int kGemmWaves = kGemmBN / (16 * kGemmRowTiles);
 constexpr int kGemmMinPairsPerExpert = 16;  // the experts path switches to the GEMM at this average
 constexpr int kXcds = 8;               // MI355X: workgroup w is dispatched to XCD w % 8
 constexpr int kGemmMaxChunks = 64;     // act chunks per row the down GEMM's LDS table holds (I <= 8192)
