@@ -233,7 +233,7 @@ PREFILL_T = 2048
 DISPATCH_KERNELS = ("lp_moe_topk", "lp_moe_disp_count", "lp_moe_disp_scan", "lp_moe_disp_scatter")
 PREFILL_KERNELS = ("lp_moe_router", "lp_gemm_router", *DISPATCH_KERNELS, "lp_moe_ximage", "lp_gemm_tiles",
                    "lp_gemm_gateup", "lp_gemm_down", "lp_moe_combine")
-MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 / bf16 MFMA
 
 
 def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
@@ -244,9 +244,9 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
 
     The logits are the device router's own (lp_moe_route on the chunk), biased
     once on the host and kept resident; a step is lp_moe_route_logits (top-k
-    + dispatch from those logits) + lp_moe_experts (activation images, the
-    grouped MFMA GEMMs, combine into the residual), and the router GEMV's
-    measured time over the same chunk is added to it for tok/s."""
+    + dispatch from those logits) + lp_moe_experts (fp16 activation images,
+    the grouped fp16 MFMA GEMMs, combine into the residual), and the router
+    GEMV's measured time over the same chunk is added to it for tok/s."""
     import llmpager_amd as lp
     T = PREFILL_T
     span = align(lp.blob_bytes(H, I, G))
@@ -333,7 +333,7 @@ def run_prefill(cuda, s, steps: int, warmup: int) -> dict:
         kernels_avg_us={k: v * 1e3 for k, v in avg.items()},
     )
     log(f"prefill T={T}: {res['tok_s']:.0f} tok/s, {step_ms:.3f} ms/layer, GEMMs "
-        f"{gemm_tf:.0f} TFLOP/s ({100 * res['gemm']['mfma_util']:.1f}% of bf16 MFMA), gate/up "
+        f"{gemm_tf:.0f} TFLOP/s ({100 * res['gemm']['mfma_util']:.1f}% of fp16 MFMA), gate/up "
         f"{gu_ms * 1e3:.1f} us, down {dn_ms * 1e3:.1f} us, dispatch {res['dispatch_us']:.1f} us, "
         f"combine {res['combine_us']:.1f} us, top expert {res['top_expert_share']:.3f} of picks")
     return res
