@@ -376,14 +376,43 @@ extern "C" __global__ void __launch_bounds__(256) lp_moe_ximage(const RouteArgs 
 namespace {
 
 // Top-k of token t by the calling wave, PER candidates per lane (expert
-// i = lane + 64 q); sv is the wave's LDS row (kMaxExperts floats; the
-// winners' table uses its first 5 * kMaxTopK words).  The in-order sum of the
-// softmax runs as a chain of adds over v_readlane values.  The k winners
-// come from a radix select on the ordered keys (the largest threshold with
-// at least k keys at or above it; keys equal to it taken lowest id first),
-// each winner's place in the stable descending order is its count of
-// winners ahead of it, and lane j then finishes pick j: no sequential
-// pick loop.
+// i = lane + 64 q); sv is the wave's LDS row (kMaxExperts floats).  The
+// in-order sum of the softmax: the exponentials go to sv and every lane
+// reads them back (broadcast reads) and folds them in id order, a chain of
+// adds on registers.  The k winners, already in the stable descending order,
+// come one per round (select_rounds) on the ordered keys of p_i = e_i / z
+// (sigmoid: of s_i + bias_i).  Ranking by e_i instead, while z is folded,
+// would differ where two different e_i divide to one p_i; overlapping the two
+// chains and checking for such ties after cost as much as it saved.  Pick r
+// lands in lane r, which then finishes it.
+template <int NR, int PER>
+__device__ __forceinline__ int select_rounds(uint32_t (&key)[PER]) {
+    // live keys are >= 1; 0 marks no expert (and a taken one).  Round r: the
+    // largest key left, the lowest id holding it (ids lane + 64 q: the first
+    // non-empty ballot, its lowest lane), that key cleared; lane r keeps the
+    // id.  Rounds past the live keys leave garbage in lanes past them.
+    const int lane = lane_id();
+    int pk = -1;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        uint32_t mx = key[0];
+#pragma unroll
+        for (int q = 1; q < PER; ++q) mx = key[q] > mx ? key[q] : mx;
+        mx = wave_max_u32(mx);
+        int win = -1;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const uint64_t b = __ballot(key[q] == mx);
+            if (win < 0 && b != 0ull) win = 64 * q + (int)__builtin_ctzll(b);  // uniform
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (lane + 64 * q == win) key[q] = 0u;
+        if (lane == r) pk = win;
+    }
+    return pk;
+}
+
 template <int PER>
 __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv, int* ids_l, int* cnt_l) {
     const int lane = lane_id();
@@ -391,6 +420,7 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
     const LP_GLOBAL float* lg = gptr<float>(a.W.logits) + (size_t)t * E;
     const uint64_t tabv = exp2tab_lane();  // glibc's 2^(i/32) table, one entry per lane
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    constexpr int kZ = 8;  // float4 reads of sv in flight per fold batch
     uint32_t key[PER];
     float val[PER], v[PER];
 #pragma unroll
@@ -400,6 +430,17 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
         key[q] = 0u;
         val[q] = 0.0f;
     }
+    const int n = k < E ? k : E;
+    // the value of expert p (its lane's val); every lane must call it
+    auto pick_val = [&](int p) {
+        float pv = 0.0f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const float vq = __int_as_float(__builtin_amdgcn_ds_bpermute((p & 63) * 4, __float_as_int(val[q])));
+            if ((p >> 6) == q) pv = vq;
+        }
+        return pv;
+    };
     if (a.L.gating == 0) {
         uint32_t mk = 0u;  // max over the ordered keys = the largest logit (f32::MIN start)
 #pragma unroll
@@ -413,25 +454,25 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
             const float ex = expf_glibc_wave(v[q] - m, tabv);  // every lane takes part
             v[q] = lane + 64 * q < E ? ex : 0.0f;
         }
-        // z = e_0 + e_1 + ... in id order, from -0.0 (the reference's fold):
-        // a chain of adds over lane values read with v_readlane
+        // z = e_0 + e_1 + ... in id order, from -0.0 (the reference's fold).
+        // sv holds e_i for i < 64 PER (+0.0 past E); folding those trailing
+        // zeros changes nothing once the first term is in (z is then >= +0,
+        // and z + 0 = z), so the fold runs over whole batches of 4 kZ.
+#pragma unroll
+        for (int q = 0; q < PER; ++q) sv[lane + 64 * q] = v[q];
+        wave_sync_lds();
         float z = -0.0f;
-        if (PER <= 4 && (E & 63) == 0) {
+        const int nz = PER <= 2 ? 64 * PER : (E + 4 * kZ - 1) / (4 * kZ) * (4 * kZ);
+        for (int c = 0; c < nz; c += 4 * kZ) {
+            float4 f[kZ];
 #pragma unroll
-            for (int q = 0; q < PER; ++q) {
-                if (64 * q >= E) break;  // uniform
+            for (int u = 0; u < kZ; ++u) f[u] = *reinterpret_cast<const float4*>(sv + c + 4 * u);
 #pragma unroll
-                for (int l = 0; l < 64; ++l)
-                    z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < PER; ++q) {
-                if (64 * q >= E) break;  // uniform
-                const int n = E - 64 * q;
-#pragma unroll 8
-                for (int l = 0; l < 64; ++l)
-                    if (l < n) z = z + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+            for (int u = 0; u < kZ; ++u) {
+                z = z + f[u].x;
+                z = z + f[u].y;
+                z = z + f[u].z;
+                z = z + f[u].w;
             }
         }
 #pragma unroll
@@ -454,64 +495,20 @@ __device__ __forceinline__ void topk_token(const RouteArgs& a, int t, float* sv,
             }
         }
     }
-    // live keys are >= 1 (ordered_key(-inf) = 0x007fffff); 0 marks no expert
-    const int n = k < E ? k : E;
-    uint32_t thr = 0u;
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = thr | (1u << bit);
-        int c = 0;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) c += __popcll(__ballot(key[q] >= cand));
-        if (c >= n) thr = cand;
-    }
-    int need = n;
-#pragma unroll
-    for (int q = 0; q < PER; ++q) need -= __popcll(__ballot(key[q] > thr));
-    uint32_t* wk = reinterpret_cast<uint32_t*>(sv);
-    int* wi = reinterpret_cast<int*>(sv) + kMaxTopK;
-    float* wv = sv + 2 * kMaxTopK;
-    int eq_before = 0, slot0 = 0;
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        const uint64_t eq = __ballot(key[q] == thr);
-        const bool win = key[q] > thr || (key[q] == thr && eq_before + __popcll(eq & below) < need);
-        eq_before += __popcll(eq);
-        const uint64_t wm = __ballot(win);
-        if (win) {
-            const int s = slot0 + __popcll(wm & below);  // winners in id order
-            wk[s] = key[q];
-            wi[s] = lane + 64 * q;
-            wv[s] = val[q];
-        }
-        slot0 += __popcll(wm);
-    }
-    wave_sync_lds();
-    // winner j (id order) in lane j; its place in the stable descending
-    // order from the other winners read across lanes, then every lane
-    // pushed to its place (lanes n.. keep theirs: a permutation)
+    // live keys are >= 1 (ordered_key(-inf) = 0x007fffff), n at most the live keys
+    const int pk = n <= 8 ? select_rounds<8>(key) : select_rounds<kMaxTopK>(key);
+    // pick j in lane j (its value fetched from the winner's lane); the sum of
+    // the picks in pick order, from -0.0
     const bool inn = lane < n;
-    const uint32_t kj = inn ? wk[lane] : 0u;
-    const int ij = inn ? wi[lane] : 0;
-    const float vj = inn ? wv[lane] : 0.0f;
-    int rank = lane;
-    if (inn) {
-        rank = 0;
-#pragma unroll
-        for (int s = 0; s < kMaxTopK; ++s) {
-            if (s < n) {  // uniform
-                const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)kj, s);
-                const int is = __builtin_amdgcn_readlane(ij, s);
-                rank += (ks > kj || (ks == kj && is < ij)) ? 1 : 0;
-            }
-        }
-    }
-    // pick j in lane j; the sum of the picks in pick order, from -0.0
-    const int pk = __builtin_amdgcn_ds_permute(rank * 4, ij);
-    const int pv = __builtin_amdgcn_ds_permute(rank * 4, __float_as_int(vj));
+    const float pv = pick_val(pk);  // every lane: the permutes read from any lane
     const int my_pick = inn ? pk : -1;
-    const float my_val = inn ? __int_as_float(pv) : 0.0f;
+    const float my_val = inn ? pv : 0.0f;
     float s = -0.0f;
-    for (int j = 0; j < n; ++j) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), j));
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+        if (j >= n) break;  // uniform
+        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), j));
+    }
     float wj = my_val;
     bool keep = inn;
     if (a.L.gating == 0) {
@@ -746,61 +743,89 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     }
 }
 
-// dispatch_all's tables for at most kDispatchWaveMaxPicks picks (at most
-// 64), by one wave and no barrier:
+// dispatch_all's tables for at most kDispatchWaveMaxPicks picks, by one
+// wave and no barrier:
 // lane p holds pick p = t k + j (valid when j < cnt[t]); its position in the
 // expert-major order is the number of valid picks with a smaller expert id
 // plus those with the same id and a smaller pick index (stable by token, as
-// dispatch_all), found by one pass over the picks with lane reads.  The
-// expert table, gs, uniq, inv and perm are then written from registers.
+// dispatch_all), found by one pass over the picks.  The picks' ids, tokens
+// and ranks reach every lane through scr (the wave's own 3 MP words of LDS,
+// broadcast reads into registers: no scalar registers per pick); lanes past
+// the picks hold an id above every expert.  The expert table, gs, uniq, inv
+// and perm are then written from registers.  Waves w = 0 .. nw - 1 of the
+// workgroup call it together, each with its own scr: wave 0 writes every
+// table but gs, which the other waves write, 64 entries each in turn (wave
+// 0 too when it is alone).
 __device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids_in, const int* cnt_in,
-                                              const int* slots_in) {
+                                              const int* slots_in, int* scr, int w, int nw) {
     const int lane = lane_id();
     const int E = a.L.experts, k = a.L.top_k, T = a.T;
-    const int P = T * k;  // <= 64
+    constexpr int MP = kDispatchWaveMaxPicks;
+    const int P = T * k;  // <= MP
     const int t = lane / k, j = lane - t * k;
     const bool inb = lane < P;
     const int c = inb ? cnt_in[t] : 0;
     const bool valid = inb && j < c;
     const int e = valid ? ids_in[lane] : 0x7fffffff;
-    int less = 0, before = 0, same = 0;  // valid picks: smaller id; same id and earlier; same id
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(e, q);
-        less += eq < e;
-        before += eq == e && q < lane;
-        same += eq == e;
+    static_assert(MP % 4 == 0 && MP <= 64, "picks read back as int4");
+    if (lane < MP) {
+        scr[lane] = e;
+        scr[MP + lane] = t;
+    }
+    wave_sync_lds();
+    int eqv[MP], tv[MP];
+#pragma unroll
+    for (int q = 0; q < MP; q += 4) {
+        const int4 x = *reinterpret_cast<const int4*>(scr + q);
+        eqv[q] = x.x, eqv[q + 1] = x.y, eqv[q + 2] = x.z, eqv[q + 3] = x.w;
+    }
+    // gs[x] = valid picks with an expert id below x, for x = 0 .. E
+    if (w > 0 || nw == 1) {
+        LP_GLOBAL int* gs = gptr_w<int>(a.W.gs);
+        const int gw = nw == 1 ? 0 : w - 1, ng = nw == 1 ? 1 : nw - 1;
+        for (int x0 = 64 * gw; x0 <= E; x0 += 64 * ng) {
+            const int x = x0 + lane;
+            int below = 0;
+#pragma unroll
+            for (int q = 0; q < MP; ++q) below += eqv[q] < x;
+            if (x <= E) gs[x] = below;
+        }
+        if (w > 0) return;
+    }
+#pragma unroll
+    for (int q = 0; q < MP; q += 4) {
+        const int4 y = *reinterpret_cast<const int4*>(scr + MP + q);
+        tv[q] = y.x, tv[q + 1] = y.y, tv[q + 2] = y.z, tv[q + 3] = y.w;
+    }
+    // valid picks: smaller id; same id and earlier; same id.  tok[r]: the
+    // token of the expert's pick of rank r (r < kEntryToks), met in lane order.
+    int less = 0, before = 0, same = 0;
+    int tok[kEntryToks] = {-1, -1, -1, -1};
+#pragma unroll
+    for (int q = 0; q < MP; ++q) {
+        const bool eq = eqv[q] == e;
+        less += eqv[q] < e;
+        before += eq && q < lane;
+#pragma unroll
+        for (int r = 0; r < kEntryToks; ++r)
+            if (eq && same == r) tok[r] = tv[q];
+        same += eq;
     }
     const bool first = valid && before == 0;  // the expert's first pick
-    const uint64_t firsts = __ballot(first);
-    const int U = __popcll(firsts);
-    // the expert's index in the unique list, and (first lanes) its first
-    // four tokens from the picks of rank 0..3
+    const int U = __popcll(__ballot(first));
+    // the expert's index in the unique list: the first picks with a smaller id
+    if (lane < MP) scr[2 * MP + lane] = first ? e : 0x7fffffff;
+    wave_sync_lds();
     int uidx = 0;
-    int tok[kEntryToks] = {-1, -1, -1, -1};
-    for (int q = 0; q < P; ++q) {
-        const int eq = __builtin_amdgcn_readlane(e, q);
-        const bool fq = (firsts >> q) & 1ull;
-        uidx += fq && eq < e;
-        if (eq == e) {
-            const int rq = __builtin_amdgcn_readlane(before, q);
-            const int tq = q / k;
 #pragma unroll
-            for (int r = 0; r < kEntryToks; ++r)
-                if (rq == r) tok[r] = tq;
-        }
+    for (int q = 0; q < MP; q += 4) {
+        const int4 f = *reinterpret_cast<const int4*>(scr + 2 * MP + q);
+        uidx += (f.x < e) + (f.y < e) + (f.z < e) + (f.w < e);
     }
     LP_GLOBAL int* perm = gptr_w<int>(a.W.perm);
     LP_GLOBAL int* inv = gptr_w<int>(a.W.inv);
     if (inb) inv[lane] = valid ? less + before : -1;
     if (valid) perm[less + before] = lane;
-    // gs[x] = valid picks with an expert id below x, for x = 0 .. E
-    LP_GLOBAL int* gs = gptr_w<int>(a.W.gs);
-    for (int x0 = 0; x0 <= E; x0 += 64) {
-        const int x = x0 + lane;
-        int below = 0;
-        for (int q = 0; q < P; ++q) below += __builtin_amdgcn_readlane(e, q) < x;
-        if (x <= E) gs[x] = below;
-    }
     LP_GLOBAL ExpertEntry* et = gptr_w<ExpertEntry>(a.W.et);
     if (first) {
         gptr_w<int>(a.W.uniq)[uidx] = e;
@@ -1112,7 +1137,8 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         // workgroup
         __syncthreads();
         if (a.T * a.L.top_k <= kDispatchWaveMaxPicks) {
-            if (wave == 0) dispatch_wave(a, ids_l, cnt_l, slots_l);
+            dispatch_wave(a, ids_l, cnt_l, slots_l, reinterpret_cast<int*>(sm) + wave * kMaxExperts, wave,
+                          (int)(blockDim.x >> 6));
         } else {
             dispatch_all(a, sm, ids_l, cnt_l, slots_l, false);
         }

@@ -320,6 +320,47 @@ def test_routing_bit_exact_softmax(cuda, E, k):
     L.free()
 
 
+def _division_tie_logits() -> np.ndarray:
+    """A 128-expert row whose 8th and 9th experts (ids 15 < 37, logits one ulp
+    apart) have different exponentials, e_37 > e_15, that divide by z to one
+    probability: softmax ranks them by id (15 first) where the exponentials
+    alone would take 37.  Replays a seeded search (found at draw 3827)."""
+    E = 128
+    rng = np.random.default_rng(1)
+    for _ in range(3828):
+        v = np.full(E, -3.0, np.float32) + (rng.standard_normal(E) * 0.1).astype(np.float32)
+        top = rng.choice(E, 7, replace=False)
+        v[top] = (3.0 + rng.random(7)).astype(np.float32)
+        rest = [i for i in range(E) if i not in top]
+        a, b = sorted(rng.choice(rest, 2, replace=False))
+        x = np.float32(rng.uniform(0.5, 2.5))
+        v[a] = x
+        v[b] = np.nextafter(x, np.float32(10), dtype=np.float32)
+    m = v.max()
+    e = np.array([O.expf(float(np.float32(vi - m))) for vi in v], np.float32)
+    z = np.float32(-0.0)
+    for ei in e:
+        z = np.float32(z + ei)
+    assert (a, b) == (15, 37) and e[b] > e[a] and np.float32(e[a] / z) == np.float32(e[b] / z)
+    return v
+
+
+def test_routing_division_tie(cuda):
+    # Softmax ranks by the probabilities, not the exponentials: on this row
+    # the two orders pick different 8th experts (a tie after the division).
+    v = _division_tie_logits()
+    wi, ww = O.top_k_softmax(v, 8, True)
+    assert 15 in wi and 37 not in wi
+    L = DeviceLayer(cuda, H=128, I=64, E=128, k=8, group=32, seed=2)
+    logits = np.stack([v, v[::-1].copy(), v])
+    ids, wts, cnt = _route_logits(cuda, L, logits)
+    for t in range(3):
+        wi, ww = O.top_k_softmax(logits[t], 8, True)
+        assert cnt[t] == len(wi) and np.array_equal(ids[t, :cnt[t]], wi), t
+        assert np.array_equal(wts[t, :cnt[t]].view(np.uint32), ww.view(np.uint32)), t
+    L.free()
+
+
 def test_routing_bit_exact_sigmoid(cuda):
     E, k = 64, 6
     rng = np.random.default_rng(77)
