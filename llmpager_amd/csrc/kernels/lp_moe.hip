@@ -743,99 +743,89 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
     }
 }
 
-// dispatch_all's tables for at most kDispatchWaveMaxPicks picks, by one
-// wave and no barrier:
-// lane p holds pick p = t k + j (valid when j < cnt[t]); its position in the
-// expert-major order is the number of valid picks with a smaller expert id
-// plus those with the same id and a smaller pick index (stable by token, as
-// dispatch_all), found by one pass over the picks.  The picks' ids, tokens
-// and ranks reach every lane through scr (the wave's own 3 MP words of LDS,
-// broadcast reads into registers: no scalar registers per pick); lanes past
-// the picks hold an id above every expert.  The expert table, gs, uniq, inv
-// and perm are then written from registers.  Waves w = 0 .. nw - 1 of the
-// workgroup call it together, each with its own scr: wave 0 writes every
-// table but gs, which the other waves write, 64 entries each in turn (wave
-// 0 too when it is alone).
-__device__ __forceinline__ void dispatch_wave(const RouteArgs& a, const int* ids_in, const int* cnt_in,
+// dispatch_all's tables for at most 64 picks (lane p: pick p = t k + j,
+// valid when j < cnt[t]), by the waves of one workgroup and no barrier.
+// Pick p's key is e * 64 + p (an id above every expert's for the others):
+// its position in the expert-major order, stable by token as dispatch_all's,
+// is the number of smaller keys.  The keys reach every lane of a wave
+// through its scr (the wave's own 192 words of LDS: broadcast reads into
+// registers), and wave 0 writes the sorted keys and tokens back to scr, so
+// lane u reads position u's pick, whether it starts its expert's run, the run
+// length (the next start, from a ballot) and the run's first tokens.  Waves
+// w = 0 .. nw - 1 call it together: wave 0 writes every table but gs, which
+// the other waves write, 64 entries each in turn (wave 0 too when alone).
+__device__ __forceinline__ int below_count(const int* bk, int nb, int key) {
+    // keys bk[0 .. 16 nb) (all >= 0) against key: how many are smaller
+    int n = 0;
+    for (int b = 0; b < nb; ++b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int4 x = *reinterpret_cast<const int4*>(bk + 16 * b + 4 * i);
+            n += (int)(((uint32_t)(x.x - key) >> 31) + ((uint32_t)(x.y - key) >> 31) +
+                       ((uint32_t)(x.z - key) >> 31) + ((uint32_t)(x.w - key) >> 31));
+        }
+    }
+    return n;
+}
+
+__device__ __forceinline__ void dispatch_keys(const RouteArgs& a, const int* ids_in, const int* cnt_in,
                                               const int* slots_in, int* scr, int w, int nw) {
     const int lane = lane_id();
     const int E = a.L.experts, k = a.L.top_k, T = a.T;
-    constexpr int MP = kDispatchWaveMaxPicks;
-    const int P = T * k;  // <= MP
+    const int P = T * k;  // <= 64
     const int t = lane / k, j = lane - t * k;
     const bool inb = lane < P;
     const int c = inb ? cnt_in[t] : 0;
     const bool valid = inb && j < c;
-    const int e = valid ? ids_in[lane] : 0x7fffffff;
-    static_assert(MP % 4 == 0 && MP <= 64, "picks read back as int4");
-    if (lane < MP) {
-        scr[lane] = e;
-        scr[MP + lane] = t;
-    }
+    const int e = valid ? ids_in[lane] : 0;
+    constexpr int kNone = 0x7fffffff;
+    const int key = valid ? (e << 6) | lane : kNone;
+    scr[lane] = key;
     wave_sync_lds();
-    int eqv[MP], tv[MP];
-#pragma unroll
-    for (int q = 0; q < MP; q += 4) {
-        const int4 x = *reinterpret_cast<const int4*>(scr + q);
-        eqv[q] = x.x, eqv[q + 1] = x.y, eqv[q + 2] = x.z, eqv[q + 3] = x.w;
-    }
-    // gs[x] = valid picks with an expert id below x, for x = 0 .. E
+    const int nb = (P + 15) >> 4;  // blocks of 16 keys to compare
     if (w > 0 || nw == 1) {
+        // gs[x] = valid picks with an expert id below x = keys below x * 64
         LP_GLOBAL int* gs = gptr_w<int>(a.W.gs);
         const int gw = nw == 1 ? 0 : w - 1, ng = nw == 1 ? 1 : nw - 1;
         for (int x0 = 64 * gw; x0 <= E; x0 += 64 * ng) {
             const int x = x0 + lane;
-            int below = 0;
-#pragma unroll
-            for (int q = 0; q < MP; ++q) below += eqv[q] < x;
+            const int below = below_count(scr, nb, x << 6);
             if (x <= E) gs[x] = below;
         }
         if (w > 0) return;
     }
-#pragma unroll
-    for (int q = 0; q < MP; q += 4) {
-        const int4 y = *reinterpret_cast<const int4*>(scr + MP + q);
-        tv[q] = y.x, tv[q + 1] = y.y, tv[q + 2] = y.z, tv[q + 3] = y.w;
+    const int pos = below_count(scr, nb, key);
+    const int nv = __popcll(__ballot(valid));
+    if (valid) {
+        scr[64 + pos] = key;
+        scr[128 + pos] = t;
     }
-    // valid picks: smaller id; same id and earlier; same id.  tok[r]: the
-    // token of the expert's pick of rank r (r < kEntryToks), met in lane order.
-    int less = 0, before = 0, same = 0;
-    int tok[kEntryToks] = {-1, -1, -1, -1};
-#pragma unroll
-    for (int q = 0; q < MP; ++q) {
-        const bool eq = eqv[q] == e;
-        less += eqv[q] < e;
-        before += eq && q < lane;
-#pragma unroll
-        for (int r = 0; r < kEntryToks; ++r)
-            if (eq && same == r) tok[r] = tv[q];
-        same += eq;
-    }
-    const bool first = valid && before == 0;  // the expert's first pick
-    const int U = __popcll(__ballot(first));
-    // the expert's index in the unique list: the first picks with a smaller id
-    if (lane < MP) scr[2 * MP + lane] = first ? e : 0x7fffffff;
+    if (inb) gptr_w<int>(a.W.inv)[lane] = valid ? pos : -1;
     wave_sync_lds();
-    int uidx = 0;
-#pragma unroll
-    for (int q = 0; q < MP; q += 4) {
-        const int4 f = *reinterpret_cast<const int4*>(scr + 2 * MP + q);
-        uidx += (f.x < e) + (f.y < e) + (f.z < e) + (f.w < e);
-    }
-    LP_GLOBAL int* perm = gptr_w<int>(a.W.perm);
-    LP_GLOBAL int* inv = gptr_w<int>(a.W.inv);
-    if (inb) inv[lane] = valid ? less + before : -1;
-    if (valid) perm[less + before] = lane;
+    // lane u: dispatch position u
+    const int u = lane;
+    const bool live = u < nv;
+    const int ku = live ? scr[64 + u] : kNone;
+    const int eu = ku >> 6;
+    const int kp = u > 0 && live ? scr[64 + u - 1] : kNone;
+    const bool first = live && (u == 0 || (kp >> 6) != eu);
+    const uint64_t F = __ballot(first);
+    const int U = __popcll(F);
+    const uint64_t below = u == 0 ? 0ull : (~0ull >> (64 - u));
+    const int uidx = __popcll(F & below);
+    if (live) gptr_w<int>(a.W.perm)[u] = ku & 63;
     LP_GLOBAL ExpertEntry* et = gptr_w<ExpertEntry>(a.W.et);
     if (first) {
-        gptr_w<int>(a.W.uniq)[uidx] = e;
-        const int slot = slots_in[e];
+        const uint64_t later = F & ~below & ~(1ull << u);  // starts after u
+        const int ntok = (later ? (int)__builtin_ctzll(later) : nv) - u;
+        gptr_w<int>(a.W.uniq)[uidx] = eu;
+        const int slot = slots_in[eu];
         ExpertEntry x;
         x.blob = slot >= 0 ? a.L.arena_base + (uint64_t)slot * a.L.slot_span : 0ull;
-        x.p0 = less;
-        x.ntok = same;
+        x.p0 = u;
+        x.ntok = ntok;
 #pragma unroll
-        for (int r = 0; r < kEntryToks; ++r) x.tok[r] = tok[r];
+        for (int r = 0; r < kEntryToks; ++r) x.tok[r] = r < ntok ? scr[128 + u + r] : -1;
         et[uidx] = x;
     }
     const int maxu = min(P, E);
@@ -1136,8 +1126,8 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         // from LDS alone; up to 16 picks one wave builds them, more take the
         // workgroup
         __syncthreads();
-        if (a.T * a.L.top_k <= kDispatchWaveMaxPicks) {
-            dispatch_wave(a, ids_l, cnt_l, slots_l, reinterpret_cast<int*>(sm) + wave * kMaxExperts, wave,
+        if (a.T * a.L.top_k <= kDispatchKeysMaxPicks) {
+            dispatch_keys(a, ids_l, cnt_l, slots_l, reinterpret_cast<int*>(sm) + wave * kMaxExperts, wave,
                           (int)(blockDim.x >> 6));
         } else {
             dispatch_all(a, sm, ids_l, cnt_l, slots_l, false);

@@ -18,7 +18,7 @@ constexpr int kWave = 64;              // CDNA wavefront
 constexpr int kGroupedWaves = 4;       // waves per workgroup in the grouped kernels
 constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x32)
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
-constexpr int kDispatchWaveMaxPicks = 16;  // a single token block of at most this many picks: one-wave dispatch
+constexpr int kDispatchKeysMaxPicks = 64;  // a single token block of at most this many picks: dispatch by sort keys
 constexpr int kRouteEPW = 1;           // fused routing: router experts per wave (8 waves per workgroup)
 constexpr int kRouteXLds = 64 * 1024;  // fused routing: LDS for staged token rows (H <= 16384)
 constexpr int kSyncSlots = 64;         // launch slots of the context's arrival counters

@@ -80,7 +80,7 @@ def test_layer_small(cuda, group, T):
 @pytest.mark.parametrize("T", [1, 5, 40])
 def test_layer_top16(cuda, T):
     # top-16 of 64 experts: the combine sums each token's picks in two
-    # blocks of 8; T = 1 puts 16 picks in the one-wave dispatch.
+    # blocks of 8; T = 1 puts 16 picks in the sort-key dispatch.
     L = DeviceLayer(cuda, H=256, I=64, E=64, k=16, group=32, seed=9, router_std=0.2)
     x, h, g = _run_layer(cuda, L, T, seed=50 + T)
     _check_layer(L, x, h, g, T)
@@ -104,7 +104,7 @@ def test_layer_sigmoid_dropped_picks(cuda):
 @pytest.mark.parametrize("T", [1, 2, 8, 9, 32, 64])
 def test_layer_config1(cuda, T):
     # Qwen3-30B-A3B shape: H2048, E128, top-8, I768, q4 g32, softmax + renorm.
-    # T = 2: the one-wave dispatch at its 16-pick limit; 9: two token blocks;
+    # T = 8: the sort-key dispatch at its 64-pick limit; 9: two token blocks;
     # 64: the largest fused-routing batch, balanced kernels at their bound.
     L = DeviceLayer(cuda, H=2048, I=768, E=128, k=8, group=32, seed=0)
     x, h, g = _run_layer(cuda, L, T, seed=T)
