@@ -662,11 +662,7 @@ extern "C" __global__ void __launch_bounds__(256) lp_gemm_tiles(const GemmArgs a
     for (int u0 = 0; u0 < nu; u0 += 256) {
         const int u = u0 + tid;
         const int nb = u < nu ? (load_entry(a.W.et, u).ntok + kGemmBM - 1) / kGemmBM : 0;
-        int x = nb;  // inclusive scan over the workgroup
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
+        const int x = wave_incl_scan(nb);  // inclusive scan over the workgroup
         if (lane == 63) sh[wave] = x;
         __syncthreads();
         int wb = 0, tot = 0;

@@ -579,11 +579,7 @@ namespace {
 // Exclusive scan of one int per thread over the workgroup (<= 16 waves).
 __device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
     const int lane = lane_id(), wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int x = v;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+    const int x = wave_incl_scan(v);
     if (lane == 63) sh[wave] = x;
     __syncthreads();
     int wbase = 0, tot = 0;
@@ -676,16 +672,11 @@ __device__ __forceinline__ void dispatch_all(const RouteArgs& a, uint8_t* sm, co
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + lane;
             const int c = e < E ? __popc(mlo[e]) + __popc(mhi[e]) : 0;
-            int x = c;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(x, o, 64);
-                if (lane >= o) x += y;
-            }
+            const int x = wave_incl_scan(c);
             const uint64_t f = __ballot(c > 0);
             if (e < E) gsl[e] = run + x - c;
             if (c > 0) uniq_l[urun + __popcll(f & below)] = e;
-            run += __shfl(x, 63, 64);
+            run += __builtin_amdgcn_readlane(x, 63);
             urun += __popcll(f);
         }
         if (lane == 0) {
@@ -1082,8 +1073,8 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
     __shared__ int flag;
     static_assert(kMaxExperts <= 2 * 512, "two slot-table entries per thread");
     const int wave = threadIdx.x >> 6, tid = threadIdx.x;
-    const int b = blockIdx.y, t0 = b * kRouterTokBlock;
-    const int nt = min(kRouterTokBlock, a.T - t0);
+    const int b = blockIdx.y, t0 = b * a.tok_block;
+    const int nt = min(a.tok_block, a.T - t0);
     // the slot table comes in with the router weights (every workgroup:
     // which one dispatches is known only at the end)
     const int E = a.L.experts;
@@ -1134,7 +1125,7 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         }
         return;
     }
-    if (!last_arrival(cnt + 8, gridDim.y, &flag)) return;
+    if (!last_arrival(cnt + 16, gridDim.y, &flag)) return;
     dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l, true);
 }
 
@@ -1428,12 +1419,7 @@ __device__ __forceinline__ bool bal_plan(const GroupedArgs& a, uint8_t* lds, int
         ent[tid] = x;
         ng = (x.ntok + kBalToks - 1) / kBalToks;
     }
-    int inc = ng * Re;  // units, prefix-summed
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += o;
-    }
+    const int inc = wave_incl_scan(ng * Re);  // units, prefix-summed
     if (lane == 63) tot[wave] = inc;
     __syncthreads();
     int before = 0, N = 0;

@@ -18,11 +18,12 @@ constexpr int kWave = 64;              // CDNA wavefront
 constexpr int kGroupedWaves = 4;       // waves per workgroup in the grouped kernels
 constexpr int kTileRows = 16;          // weight rows per MFMA tile (N of 16x16x32)
 constexpr int kRouterTokBlock = 8;     // tokens per router wave pass
+constexpr int kRouteTokBlockMulti = 4;  // fused routing past one block: tokens per block (at most 16 blocks)
 constexpr int kDispatchKeysMaxPicks = 64;  // a single token block of at most this many picks: dispatch by sort keys
 constexpr int kRouteEPW = 1;           // fused routing: router experts per wave (8 waves per workgroup)
 constexpr int kRouteXLds = 64 * 1024;  // fused routing: LDS for staged token rows (H <= 16384)
 constexpr int kSyncSlots = 64;         // launch slots of the context's arrival counters
-constexpr int kSyncWords = 16;         // counters per slot: [b] token block b, [8] every block
+constexpr int kSyncWords = 32;         // counters per slot: [b] token block b (b < 16), [16] every block
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
@@ -293,6 +294,8 @@ struct RouteArgs {
     int32_t T;
     int32_t make_xf;     // router: also write images of x: kImgF16 into W.xf (+ W.xexp), kImgDigits into W.xd
     uint64_t sync;       // fused routing: kSyncWords arrival counters, zero between launches
+    int32_t tok_block;   // fused routing: tokens per block (grid y = ceil(T / tok_block))
+    int32_t pad0;
 };
 
 struct GroupedArgs {

@@ -1054,8 +1054,11 @@ int lp_moe_route(lp_ctx* c, const lp_moe_layer_desc* d, uint64_t x, int T, uint6
         return fail(LP_E_UNSUPPORTED, "lp_moe_route: more than " + std::to_string(kSyncSlots) +
                                           " streams have routed through this context");
     ra.sync = reinterpret_cast<uint64_t>(c->sync) + (uint64_t)slot * kSyncWords * 4;
+    // one block of up to kRouterTokBlock tokens, else blocks of
+    // kRouteTokBlockMulti: twice the workgroups, each staging half the rows
+    ra.tok_block = T <= kRouterTokBlock ? kRouterTokBlock : kRouteTokBlockMulti;
     dim3 g((unsigned)((d->experts + 8 * kRouteEPW - 1) / (8 * kRouteEPW)),
-           (unsigned)((T + kRouterTokBlock - 1) / kRouterTokBlock));
+           (unsigned)((T + ra.tok_block - 1) / ra.tok_block));
     return launch(c, d->experts <= 128 ? kRouteFused128 : kRouteFused, g, dim3(512), 0, s, ra);
 }
 
