@@ -1101,7 +1101,7 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         }
     };
     int* cnt = dptr<int>(a.sync);
-    const int order = arrival_order(cnt + b, gridDim.x, &flag);
+    const int order = arrival_order(cnt + kSyncStride * b, gridDim.x, &flag);
     if (order != (int)gridDim.x - 1) {
         images(order, gridDim.x - 1);
         return;
@@ -1125,7 +1125,7 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
         }
         return;
     }
-    if (!last_arrival(cnt + 16, gridDim.y, &flag)) return;
+    if (!last_arrival(cnt + kSyncStride * 16, gridDim.y, &flag)) return;
     dispatch_all(a, sm, dptr<const int>(a.W.ids), dptr<const int>(a.W.cnt), slots_l, true);
 }
 

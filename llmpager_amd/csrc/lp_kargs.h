@@ -23,7 +23,8 @@ constexpr int kDispatchKeysMaxPicks = 64;  // a single token block of at most th
 constexpr int kRouteEPW = 1;           // fused routing: router experts per wave (8 waves per workgroup)
 constexpr int kRouteXLds = 64 * 1024;  // fused routing: LDS for staged token rows (H <= 16384)
 constexpr int kSyncSlots = 64;         // launch slots of the context's arrival counters
-constexpr int kSyncWords = 32;         // counters per slot: [b] token block b (b < 16), [16] every block
+constexpr int kSyncStride = 32;        // words between arrival counters (one 128-byte line each)
+constexpr int kSyncWords = 17 * kSyncStride;  // counters per slot: [b] token block b (b < 16), [16] every block
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
