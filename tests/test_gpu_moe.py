@@ -453,11 +453,15 @@ def test_route_sequence(cuda):
 
 
 @pytest.mark.parametrize("E,k,T", [(8, 2, 64), (4, 2, 1), (64, 6, 17), (128, 8, 32), (300, 16, 5),
-                                   (300, 16, 64), (1024, 16, 64), (1024, 16, 7)])
+                                   (300, 16, 64), (1024, 16, 64), (1024, 16, 7), (8, 8, 8), (4, 2, 8),
+                                   (16, 4, 6)])
 def test_route_one_launch_tables(cuda, E, k, T):
     # The one-launch routing's tables at its sizes (T <= 64): one token block
     # (picks from LDS) and several (picks from memory), up to 1024 picks and
     # the largest expert count; 8 experts x 64 tokens put 16 picks on each.
+    # One block of at most 64 picks is placed by sort keys: every token on
+    # every expert (8 x 8 x 8: runs of 8, the entry naming the first 4),
+    # four picks per expert (4 x 2 x 8), and a ragged mix (16 x 4 x 6).
     # A permuted slot table, so each entry's blob shows which slot it read.
     slots = np.random.default_rng(E + k).permutation(E).astype(np.int32)
     L = DeviceLayer(cuda, H=256, I=64, E=E, k=k, group=32, seed=6, router_std=0.05, slots=slots)
