@@ -324,15 +324,25 @@ extern "C" __global__ void __launch_bounds__(256) lp_attn_combine(const AttnArgs
 //           flight while this chunk's softmax and context are computed);
 //   softmax per head over the chunk, the running max and sum rescaled;
 //   context ctx[h][d] += sum_r p[h][r] row_r[d]: the same MFMA with the
-//           probabilities (hi + lo) as A and the chunk, stored transposed
-//           in LDS during the score pass, as B (each wave a quarter of the
-//           c_dim columns).
+//           probabilities (hi + lo) as A and the chunk as B (each wave a
+//           quarter of the c_dim columns): the rows go to LDS as they are
+//           (one 16-byte store per lane and step during the score pass) and
+//           the B operand comes back column-wise through the transposing
+//           LDS read (ds_read_b64_tr_b16: each 16-lane group reads a 4-row x
+//           16-column block, lane i receiving column i's four values).
 // The cache rows are read once from HBM.  Each split ends with a partial
 // record {max[16], sum[16], acc[16][c_dim]}; lp_mla_combine merges them.
 // ---------------------------------------------------------------------------
 namespace {
 
 __device__ __forceinline__ uint32_t pack_bf16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+// e^x for the batched MLA's softmax (x <= 0 there): the hardware base-2
+// exponential of x log2(e), within a few ulp (the bf16 cache bounds the
+// result's precision far below that); -inf gives 0.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 // hi / lo bf16 images of eight fp32 values, element order = value order
 __device__ __forceinline__ void split8(const float (&v)[8], uint4& hi, uint4& lo) {
@@ -362,8 +372,10 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
     const int tpw = CD >> 6;  // 16-column tiles per wave (a quarter of c_dim)
     uint4* qhi = reinterpret_cast<uint4*>(lds);
     uint4* qlo = qhi + STEPS * 64;
-    uint8_t* ct = lds + 2 * STEPS * 1024;  // transposed chunk: [CD][kMlaColStride]
-    float* sl = reinterpret_cast<float*>(ct + CD * kMlaColStride);  // [16][64]
+    const int rsb = mla_row_bytes(CD);
+    uint8_t* ct = lds + 2 * STEPS * 1024;  // the chunk's first c_dim columns: [kMlaRows][rsb]
+    const uint32_t ct_addr = lds_addr_of(ct);
+    float* sl = reinterpret_cast<float*>(ct + kMlaRows * rsb);  // [16][64]
     // a length past the cache is cut to the cache (rows beyond max_seq
     // belong to the next sequence, or to no allocation at all)
     const int seq = min(dptr<const int>(a.seq_lens)[b], a.max_seq);
@@ -392,7 +404,7 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
     // so the next chunk's loads go into the same registers at that point
     auto chunk = [&](uint4 (&Bc)[STEPS], int c) {
         // scores of rows 16 wave + n; the chunk's first c_dim columns stored
-        // transposed (column-major, 64 rows per column) for the context pass
+        // row by row for the context pass
         f32x4_t s4 = {0.0f, 0.0f, 0.0f, 0.0f};
         const int rl = 16 * wave + n;
 #pragma unroll
@@ -400,15 +412,7 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
             s4 = mfma_bf16(qhi[j * 64 + lane], Bc[j], s4);
             s4 = mfma_bf16(qlo[j * 64 + lane], Bc[j], s4);
             const int col = 32 * j + 8 * kb;
-            if (col < CD) {
-                uint16_t* dst = reinterpret_cast<uint16_t*>(ct + (size_t)col * kMlaColStride) + rl;
-                const uint32_t w4[4] = {Bc[j].x, Bc[j].y, Bc[j].z, Bc[j].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    dst[(2 * i) * (kMlaColStride / 2)] = (uint16_t)(w4[i] & 0xffffu);
-                    dst[(2 * i + 1) * (kMlaColStride / 2)] = (uint16_t)(w4[i] >> 16);
-                }
-            }
+            if (col < CD) *reinterpret_cast<uint4*>(ct + (size_t)rl * rsb + col * 2) = Bc[j];
         }
         if (c + 1 < nchunks) load_chunk(Bc, c + 1);
         const bool rvalid = p0 + c * kMlaRows + rl < p1;
@@ -429,11 +433,11 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
         mx = fmaxf(mx, shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
         const bool none = m_new == -INFINITY;  // every row so far masked
-        const float alpha = none ? 1.0f : expf(m_run - m_new);
+        const float alpha = none ? 1.0f : exp_hw(m_run - m_new);
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            sv[t] = none ? 0.0f : expf(sv[t] - m_new);
+            sv[t] = none ? 0.0f : exp_hw(sv[t] - m_new);
             ps += sv[t];
         }
         ps += shfl_xor(ps, 16);
@@ -451,16 +455,29 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
             for (int i = 0; i < 8; ++i) v8[i] = sv[8 * s + i];
             split8(v8, phi[s], plo[s]);
         }
-        // context over this wave's columns
+        // context over this wave's columns: lane (n, kb) needs rows
+        // 32 s + 8 kb .. + 7 of column n; lane i of group kb points the
+        // transposing read at row 32 s + 8 kb + i / 4, columns 4 (i % 4) .. + 3
+        // of the 16-column tile (and 4 rows further for the second half)
+        const int li = lane & 15;
 #pragma unroll
         for (int t = 0; t < kMlaMaxC / 64; ++t) {
             if (t < tpw) {  // uniform
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[t][v] *= av[v];
-                const int col = wave * (CD >> 2) + 16 * t + n;
+                const int col0 = wave * (CD >> 2) + 16 * t;
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const uint4 bt = *reinterpret_cast<const uint4*>(ct + (size_t)col * kMlaColStride + (32 * s + 8 * kb) * 2);
+                    const uint32_t pa = ct_addr + (uint32_t)((32 * s + 8 * kb + (li >> 2)) * rsb) +
+                                        (uint32_t)((col0 + 4 * (li & 3)) * 2);
+                    const v4i16_t r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        reinterpret_cast<__attribute__((address_space(3))) v4i16_t*>((uintptr_t)pa));
+                    const v4i16_t r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        reinterpret_cast<__attribute__((address_space(3))) v4i16_t*>((uintptr_t)(pa + 4u * rsb)));
+                    const uint4 bt = make_uint4(pack_bf16((uint16_t)r0[0], (uint16_t)r0[1]),
+                                                pack_bf16((uint16_t)r0[2], (uint16_t)r0[3]),
+                                                pack_bf16((uint16_t)r1[0], (uint16_t)r1[1]),
+                                                pack_bf16((uint16_t)r1[2], (uint16_t)r1[3]));
                     acc[t] = mfma_bf16(phi[s], bt, acc[t]);
                     acc[t] = mfma_bf16(plo[s], bt, acc[t]);
                 }

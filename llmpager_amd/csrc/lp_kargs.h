@@ -202,11 +202,14 @@ constexpr int kMlaRows = 64;        // cache rows per chunk (4 waves x 16)
 constexpr int kMlaMaxQk = 640;
 constexpr int kMlaMaxC = 512;
 constexpr int kMlaMaxSplits = 256;  // splits per sequence (the merge keeps one weight per split in LDS)
-constexpr int kMlaColStride = 144;  // bytes per column of the transposed chunk: 64 rows + pad, 16-byte aligned
+// Bytes per row of the chunk staged in LDS: c_dim bf16 and 32 bytes of pad,
+// so that the four rows one 16-lane group of a transposing read touches
+// start 8 banks apart.
+LPK_HD constexpr int mla_row_bytes(int c_dim) { return 2 * c_dim + 32; }
 // LDS: the query images (hi and lo bf16 in MFMA A order, 2 x qk/32 x 1 KB),
-// the transposed chunk (c_dim x kMlaColStride) and the scores (16 x 64 f32).
+// the chunk's rows (kMlaRows x mla_row_bytes) and the scores (16 x 64 f32).
 LPK_HD constexpr int mla_lds_bytes(int qk_dim, int c_dim) {
-    return 2 * (qk_dim / 32) * 1024 + c_dim * kMlaColStride + 16 * kMlaRows * 4;
+    return 2 * (qk_dim / 32) * 1024 + kMlaRows * mla_row_bytes(c_dim) + 16 * kMlaRows * 4;
 }
 // Floats of one partial record: max[16], sum[16], acc[16][c_dim].
 LPK_HD constexpr int mla_part_floats(int c_dim) { return 32 + 16 * c_dim; }
