@@ -1114,8 +1114,8 @@ __device__ __forceinline__ void route_fused_body(const RouteArgs& a) {
                  one ? cnt_l : nullptr);
     if (one) {
         // ranked by this workgroup: no second arrival, and the tables come
-        // from LDS alone; up to 16 picks one wave builds them, more take the
-        // workgroup
+        // from LDS alone; up to kDispatchKeysMaxPicks picks are placed by
+        // sort keys, more by dispatch_all
         __syncthreads();
         if (a.T * a.L.top_k <= kDispatchKeysMaxPicks) {
             dispatch_keys(a, ids_l, cnt_l, slots_l, reinterpret_cast<int*>(sm) + wave * kMaxExperts, wave,
