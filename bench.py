@@ -610,6 +610,8 @@ def run_shared(cuda, s, batches, steps: int, warmup: int) -> dict:
 
 
 # Workload config 5's attention half: MLA absorbed decode over bf16 latent KV.
+# Qwen3-30B-A3B's attention block and vocabulary (the whole decode step)
+S_HEADS, S_KV_HEADS, S_HEAD_DIM, S_VOCAB, S_MAX_SEQ = 32, 4, 128, 151936, 4096
 M_HEADS, M_QK, M_C, M_CTX = 16, 576, 512, 4096
 
 
@@ -796,6 +798,103 @@ def _rounded(d):
     return round(d, 4) if isinstance(d, float) else d
 
 
+def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) -> dict:
+    """Config 2's model as one whole decode step of one token (the reference's
+    Decoder::step, decode.rs:263-363, llmpager_amd.step): per layer the
+    attention block (bf16 q/k/v/o for 32 query and 4 KV heads of 128, q/k
+    norms, rope, the fp16 KV cache, attention over pos + 1 positions) and the
+    resident MoE layer, then the final norm and the 151,936-row bf16 lm_head.
+    Random-init attention and lm_head weights (N(0, 0.02) bf16; one host copy
+    uploaded into every layer's own buffers, so no layer's weights are
+    another's), the KV caches filled with a small constant.  The step is
+    recorded once at position `pos` (lp_graph_capture_begin / end) and
+    replayed; a timed step is the replay plus the logits' readback and the
+    host argmax, as the reference's greedy step does; the replays alone are
+    timed too.  Per-kernel times come from one eager step with events."""
+    import llmpager_amd as lp
+    from llmpager_amd.step import AttnWeights, DecodeStep, StepShape
+    S = StepShape(hidden=H, heads=S_HEADS, kv_heads=S_KV_HEADS, head_dim=S_HEAD_DIM, vocab=S_VOCAB,
+                  max_seq=S_MAX_SEQ)
+    qd, kd = S.heads * S.head_dim, S.kv_heads * S.head_dim
+    shapes = dict(q=qd * H, k=kd * H, v=kd * H, o=H * qd)
+    host = {k: lp.synth_bf16(n, 0.02, 0, 2000 + i) for i, (k, n) in enumerate(shapes.items())}
+    ones_h = np.ones(H, np.float32)
+    ones_d = np.ones(S.head_dim, np.float32)
+    allocs = []
+
+    def up(a):
+        p = cuda.upload(a, s)
+        allocs.append(p)
+        return p
+    attn = [AttnWeights(q=up(host["q"]), k=up(host["k"]), v=up(host["v"]), o=up(host["o"]), input_ln=up(ones_h),
+                        q_norm=up(ones_d), k_norm=up(ones_d), post_ln=up(ones_h)) for _ in range(LAYERS)]
+    lm = up(lp.synth_bf16(S.vocab * H, 0.02, 0, 2100))
+    fn = up(ones_h)
+    ws_bytes = stack.stack.ws_bytes(1)
+    ws = cuda.alloc_device(ws_bytes)
+    allocs.append(ws)
+    # the embedding gather reads one row: the lm_head's table serves as it
+    step = DecodeStep(cuda, S, attn, stack.layers, lm, fn, lm, ws, ws_bytes)
+    for c in step.kcache + step.vcache:
+        cuda.memset_async(c, 0x20, 2 * kd * S.max_seq, s)  # fp16 0x2020: 0.0083
+    cuda.sync_stream(s)
+    weight_bytes = LAYERS * 2 * sum(shapes.values()) + 2 * S.vocab * H
+    kv_bytes = LAYERS * 2 * 2 * kd * (pos + 1)
+    # one eager step with events: per-kernel times
+    step.run(7, pos, s)
+    cuda.sync_stream(s)
+    cuda.profile(True)
+    cuda.profile_reset()
+    step.run(7, pos, s)
+    cuda.sync_stream(s)
+    names = ["lp_bf16_row_to_f32", "lp_rmsnorm", "lp_bf16_gemv", "lp_rope", "lp_kv_append_f16", "lp_attn_split_f16",
+             "lp_attn_combine", "lp_add", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_gateup_bal",
+             "lp_moe_gateup_bal8", "lp_moe_down_comb", "lp_moe_down_comb16"]
+    kern = {}
+    for n in names:
+        ms, cnt = cuda.profile_read(n)
+        if cnt:
+            kern[n] = {"launches": int(cnt), "us": ms * 1000.0}
+    cuda.profile(False)
+    moe_us = sum(v["us"] for k, v in kern.items() if k.startswith("lp_moe"))
+    g = step.capture(7, pos, s)
+    e0, e1 = cuda.event(), cuda.event()
+    for _ in range(warmup):
+        g.launch(s)
+    cuda.sync_stream(s)
+    cuda.record_event(e0, s)
+    for _ in range(steps):
+        g.launch(s)
+    cuda.record_event(e1, s)
+    cuda.sync_stream(s)
+    graph_ms = cuda.elapsed_ms(e0, e1) / steps
+    best = None
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.launch(s)
+        logits = cuda.download(step.logits, (S.vocab,), np.float32, s)
+        best = int(np.argmax(logits))
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    g.close()
+    for e in (e0, e1):
+        cuda.destroy_event(e)
+    step.free()
+    for p in allocs:
+        cuda.free_device(p)
+    out = {
+        "position": pos, "layers": LAYERS, "tok_s": 1000.0 / wall_ms, "ms_per_step": wall_ms,
+        "graph_ms_per_step": graph_ms, "graph_tok_s": 1000.0 / graph_ms,
+        "weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
+        "hbm_gbps_graph": (weight_bytes + kv_bytes) / (graph_ms * 1e-3) / 1e9,
+        "moe_us_per_step": moe_us, "attn_and_head_us_per_step": sum(v["us"] for v in kern.values()) - moe_us,
+        "kernels": kern, "argmax": best,
+    }
+    log(f"decode step B=1 at position {pos}: {out['tok_s']:.1f} tok/s ({wall_ms:.3f} ms with the logits' readback "
+        f"and argmax; graph replay {graph_ms:.3f} ms), MoE {moe_us / 1000:.3f} ms + attention, norms and lm_head "
+        f"{out['attn_and_head_us_per_step'] / 1000:.3f} ms of kernel time (eager step with events)")
+    return out
+
+
 def main() -> int:
     global LAYERS
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -815,6 +914,8 @@ def main() -> int:
     ap.add_argument("--no-mla", action="store_true", help="skip the config-5 MLA attention leg")
     ap.add_argument("--mla-only", action="store_true")
     ap.add_argument("--shared-only", action="store_true")
+    ap.add_argument("--no-step", action="store_true", help="skip the whole decode step leg (attention + MoE)")
+    ap.add_argument("--step-only", action="store_true")
     ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
     ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
     a = ap.parse_args()
@@ -838,18 +939,20 @@ def main() -> int:
     cuda.sync()
     cuda.free_device(ca)
     cuda.free_device(cb)
-    mla = None if a.no_mla or a.paged_only or a.prefill_only or a.shared_only else run_mla(cuda, s, (1, 16), a.steps)
+    other = a.paged_only or a.prefill_only or a.shared_only or a.step_only
+    mla = None if a.no_mla or other else run_mla(cuda, s, (1, 16), a.steps)
     if a.mla_only:
         print(json.dumps({"mla": _rounded(mla)}), flush=True)
         cuda.close()
         return 0
-    prefill = None if a.no_prefill or a.paged_only or a.shared_only else run_prefill(cuda, s, a.steps, a.warmup)
+    prefill = (None if a.no_prefill or a.paged_only or a.shared_only or a.step_only
+               else run_prefill(cuda, s, a.steps, a.warmup))
     if a.prefill_only:
         print(json.dumps({"prefill": prefill}), flush=True)
         cuda.close()
         return 0
-    paged = None if a.no_paged or a.shared_only else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
-    shared = None if a.no_shared or a.paged_only else run_shared(cuda, s, (1, 16), a.steps, a.warmup)
+    paged = None if a.no_paged or a.shared_only or a.step_only else run_paged(cuda, s, a.paged_layers, a.paged_tokens, P_SLOTS)
+    shared = None if a.no_shared or a.paged_only or a.step_only else run_shared(cuda, s, (1, 16), a.steps, a.warmup)
     if a.shared_only:
         print(json.dumps({"shared": _rounded(shared)}), flush=True)
         cuda.close()
@@ -859,7 +962,12 @@ def main() -> int:
         cuda.close()
         return 0
     log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
-    stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu else 2)
+    stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu or a.step_only else 2)
+    dstep = None if a.no_step else run_step(cuda, s, stack, a.steps, a.warmup)
+    if a.step_only:
+        print(json.dumps({"decode_step": _rounded(dstep)}), flush=True)
+        cuda.close()
+        return 0
     results = {}
     for B in batches:
         results[B] = run_batch(cuda, stack, B, a.steps, a.warmup)
@@ -907,6 +1015,7 @@ def main() -> int:
         "paged": None if paged is None else _rounded(paged),
         "shared": None if shared is None else _rounded(shared),
         "mla": None if mla is None else _rounded(mla),
+        "decode_step": None if dstep is None else _rounded(dstep),
         "batches": {str(b): {k: (round(v, 4) if isinstance(v, float) else v)
                              for k, v in r.items() if k not in ("dominant", "kernels_avg_us")}
                     | {"gateup_gbps": round(r["dominant"]["gbps"], 1),

@@ -316,6 +316,18 @@ int lp_moe_stack_forward(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_lay
 typedef struct lp_graph lp_graph;
 int lp_moe_stack_capture(lp_ctx* ctx, const lp_moe_layer_desc* layers, int n_layers, uint64_t h, int T,
                          uint64_t workspace, uint64_t ws_bytes, lp_stream s, lp_graph** out);
+/* The general form (no counterpart in the reference, whose decode step,
+ * decode.rs:263-363, issues each launch from the host every step): every
+ * launch this library makes on s between lp_graph_capture_begin and
+ * lp_graph_capture_end (the 1:1 kernels of the attention block, fused MoE
+ * layers, stacks through lp_moe_stack_forward) becomes one graph, with the
+ * arguments given then (a decode step at one position replays at that
+ * position).  The graph owns a set of routing arrival counters as
+ * lp_moe_stack_capture's does.  One capture per context at a time; s must be
+ * a created stream; copies, memsets and synchronisation are not allowed in
+ * between, and lp_moe_stack_capture is refused. */
+int lp_graph_capture_begin(lp_ctx* ctx, lp_stream s);
+int lp_graph_capture_end(lp_ctx* ctx, lp_stream s, lp_graph** out);
 int lp_graph_launch(lp_ctx* ctx, lp_graph* g, lp_stream s);
 void lp_graph_destroy(lp_graph* g);
 /* lp_moe_forward without a workspace argument and without any allocation:

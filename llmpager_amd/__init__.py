@@ -129,6 +129,8 @@ def _sig(lib):
         "lp_moe_forward_noalloc": (i32, [vp, P(LayerDesc), u64, u64, i32, vp]),
         "lp_moe_stack_forward": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, u64, vp]),
         "lp_moe_stack_capture": (i32, [vp, P(LayerDesc), i32, u64, i32, u64, u64, vp, P(vp)]),
+        "lp_graph_capture_begin": (i32, [vp, vp]),
+        "lp_graph_capture_end": (i32, [vp, vp, P(vp)]),
         "lp_graph_launch": (i32, [vp, vp, vp]),
         "lp_graph_destroy": (None, [vp]),
         "lp_noalloc_scratch_bytes": (u64, []),
@@ -321,6 +323,16 @@ class Cuda:
 
     def destroy_stream(self, s: int) -> None:
         _check(lib().lp_stream_destroy(self.ctx, s))
+
+    def capture_begin(self, s: int) -> None:
+        """Record every launch this library makes on stream s (lp_graph_capture_begin)."""
+        _check(lib().lp_graph_capture_begin(self.ctx, s))
+
+    def capture_end(self, s: int) -> "Graph":
+        """The launches recorded since capture_begin, as one graph (lp_graph_capture_end)."""
+        g = C.c_void_p()
+        _check(lib().lp_graph_capture_end(self.ctx, s, C.byref(g)))
+        return Graph(self, g.value)
 
     def event(self) -> int:
         e = C.c_void_p()

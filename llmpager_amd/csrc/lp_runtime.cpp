@@ -197,6 +197,7 @@ struct lp_ctx {
     bool sync_graph[kSyncSlots] = {};         // slot i belongs to a graph (sync_owner unused)
     hipStream_t cap_stream = nullptr;         // a capture in progress on this stream ...
     int cap_slot = -1;                        // ... routes through this (the graph's) slot
+    bool cap_prof = false;                    // lp_graph_capture_begin: the profiling switch to restore
     // decode gate/up through lp_moe_gateup_bal (LLMPAGER_HIP_GATEUP_BAL=0 at
     // lp_init turns it off, for comparison)
     bool gateup_bal = true;
@@ -1432,6 +1433,12 @@ int lp_moe_stack_capture(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layer
     if (!s) return fail(LP_E_INVALID, "lp_moe_stack_capture: the null stream cannot be captured");
     if (int r = lp_moe_workspace_check(layers, n_layers, T, ws, ws_bytes))
         return fail(r, "lp_moe_stack_capture: " + g_err);
+    {
+        std::lock_guard<std::mutex> g(c->sync_mu);
+        if (c->cap_slot >= 0)
+            return fail(LP_E_INVALID, "lp_moe_stack_capture: a capture is in progress (inside one, use "
+                                      "lp_moe_stack_forward)");
+    }
     // the graph's own arrival counters (routing in the captured launches)
     const int slot = graph_slot_take(c, s);
     if (slot < 0)
@@ -1457,6 +1464,65 @@ int lp_moe_stack_capture(lp_ctx* c, const lp_moe_layer_desc* layers, int n_layer
         if (g) (void)hipGraphDestroy(g);
         graph_slot_free(c, slot);
         return r != LP_OK ? fail(r, err) : hip_fail(e, "hipStreamEndCapture");
+    }
+    lp_graph* G = new lp_graph();
+    G->graph = g;
+    G->ctx = c;
+    G->slot = slot;
+    const hipError_t ie = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        lp_graph_destroy(G);
+        return hip_fail(ie, "hipGraphInstantiate");
+    }
+    *out = G;
+    return LP_OK;
+}
+
+// The general capture: whatever the library launches on s between begin
+// and end (1:1 kernels, fused layers, stacks) becomes one graph, which owns
+// a routing counter slot as lp_moe_stack_capture's graphs do.
+int lp_graph_capture_begin(lp_ctx* c, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (!s) return fail(LP_E_INVALID, "lp_graph_capture_begin: the null stream cannot be captured");
+    {
+        std::lock_guard<std::mutex> g(c->sync_mu);
+        if (c->cap_slot >= 0) return fail(LP_E_INVALID, "lp_graph_capture_begin: a capture is already in progress");
+    }
+    const int slot = graph_slot_take(c, s);
+    if (slot < 0)
+        return fail(LP_E_UNSUPPORTED, "lp_graph_capture_begin: every slot of arrival counters is taken (" +
+                                          std::to_string(kSyncSlots) + " streams and graphs)");
+    c->cap_prof = c->prof;
+    c->prof = false;  // no profiling events inside the graph
+    const hipError_t e = hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        c->prof = c->cap_prof;
+        capture_end(c);
+        graph_slot_free(c, slot);
+        return hip_fail(e, "hipStreamBeginCapture");
+    }
+    return LP_OK;
+}
+
+int lp_graph_capture_end(lp_ctx* c, lp_stream s, lp_graph** out) {
+    if (int r = check_ctx(c)) return r;
+    if (!out) return fail(LP_E_INVALID, "lp_graph_capture_end: null out");
+    *out = nullptr;
+    int slot;
+    {
+        std::lock_guard<std::mutex> g(c->sync_mu);
+        if (c->cap_slot < 0 || c->cap_stream != (hipStream_t)s)
+            return fail(LP_E_INVALID, "lp_graph_capture_end: no capture in progress on this stream");
+        slot = c->cap_slot;
+    }
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture((hipStream_t)s, &g);
+    c->prof = c->cap_prof;
+    capture_end(c);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        graph_slot_free(c, slot);
+        return hip_fail(e, "hipStreamEndCapture");
     }
     lp_graph* G = new lp_graph();
     G->graph = g;

@@ -270,6 +270,8 @@ extern "C" {
         ctx: *mut lp_ctx, layers: *const lp_moe_layer_desc, n_layers: c_int, h: u64, t: c_int, ws: u64,
         ws_bytes: u64, s: lp_stream, out: *mut *mut lp_graph,
     ) -> c_int;
+    pub fn lp_graph_capture_begin(ctx: *mut lp_ctx, s: lp_stream) -> c_int;
+    pub fn lp_graph_capture_end(ctx: *mut lp_ctx, s: lp_stream, out: *mut *mut lp_graph) -> c_int;
     pub fn lp_graph_launch(ctx: *mut lp_ctx, g: *mut lp_graph, s: lp_stream) -> c_int;
     pub fn lp_graph_destroy(g: *mut lp_graph);
     pub fn lp_moe_forward_noalloc(

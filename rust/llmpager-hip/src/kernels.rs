@@ -16,7 +16,7 @@ pub struct Kernels {
     _priv: (),
 }
 
-/// A captured HIP graph of a layer stack (`lp_moe_stack_capture`).
+/// A captured HIP graph (`lp_moe_stack_capture`, `lp_graph_capture_end`).
 pub struct Graph {
     g: *mut ffi::lp_graph,
 }
@@ -307,6 +307,19 @@ impl Kernels {
             )
         };
         check(rc, "stack_capture")?;
+        Ok(Graph { g })
+    }
+
+    /// Start recording every launch made on `stream` (a whole decode step:
+    /// the attention block's kernels and the MoE layers) into one graph.
+    pub fn capture_begin(&self, cuda: &Cuda, stream: CUstream) -> Result<()> {
+        check(unsafe { ffi::lp_graph_capture_begin(cuda.ctx, stream) }, "capture_begin")
+    }
+
+    /// End the recording started by [`Self::capture_begin`].
+    pub fn capture_end(&self, cuda: &Cuda, stream: CUstream) -> Result<Graph> {
+        let mut g = std::ptr::null_mut();
+        check(unsafe { ffi::lp_graph_capture_end(cuda.ctx, stream, &mut g) }, "capture_end")?;
         Ok(Graph { g })
     }
 
