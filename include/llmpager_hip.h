@@ -136,6 +136,33 @@ int lp_attn_decode(lp_ctx* ctx, uint64_t q, uint64_t kcache, uint64_t vcache, ui
 /* bf16_row (kernels.rs:294-306; decode.cu:328-339): out[:n] = f32(table[row, :n]). */
 int lp_bf16_row(lp_ctx* ctx, uint64_t table, int row, int n, uint64_t out, lp_stream s);
 
+/* ---- the fused decode step ------------------------------------------------
+ * No reference counterparts: each entry point does the arithmetic of launches
+ * that Decoder::step (decode.rs:275-301) issues one by one, in one launch. */
+
+/* rmsnorm + bf16_gemv (decode.rs:282-285, 359-360): y_i = W_i . rmsnorm(x, ln)
+ * for up to three bf16 [rows_i, cols] matrices sharing x [cols] (rows1 = 0
+ * and rows2 = 0 leave them out; ln = 0 skips the norm: y_i = W_i . x).
+ * cols a multiple of 8, at most 4096; x and the matrices 16-byte aligned. */
+int lp_rmsnorm_gemv(lp_ctx* ctx, uint64_t x, uint64_t ln, float eps, int cols, uint64_t w0, int rows0,
+                    uint64_t y0, uint64_t w1, int rows1, uint64_t y1, uint64_t w2, int rows2, uint64_t y2,
+                    lp_stream s);
+/* bf16_gemv + add + rmsnorm (decode.rs:296-301): h[rows] += W . x (W bf16
+ * [rows, cols]), then hn = rmsnorm(h, ln).  Same limits on cols as above.
+ * Uses the stream's arrival counters (launches that overlap on one stream's
+ * slot are not allowed; launches on one stream run in order). */
+int lp_gemv_add_rmsnorm(lp_ctx* ctx, uint64_t w, uint64_t x, int rows, int cols, uint64_t h, uint64_t ln,
+                        float eps, uint64_t hn, lp_stream s);
+/* Per-head rmsnorm of q [heads, 128] with q_norm and of k [kv_heads, 128]
+ * with k_norm (0: none), NeoX rope of both at pos, kv_append of k and v into
+ * fp16 caches [kv_heads, max_seq, 128] at pos, and attn_decode over
+ * positions 0..pos into out [heads, 128] (decode.rs:283-294).  q, k and v
+ * are read only; scratch [heads, max_seq] f32.  heads / kv_heads in
+ * {1, 2, 4, 8, 16}, kv_heads <= 16. */
+int lp_attn_fused(lp_ctx* ctx, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
+                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch, int heads,
+                  int kv_heads, int head_dim, int pos, int max_seq, float scale, lp_stream s);
+
 /* ---- MLA absorbed decode: kernels::Kernels (kernels.rs; mla.cu) ----------- */
 
 /* mla_rope (kernels.rs:311-330; mla.cu:22-45): pairs (2i, 2i+1) of the

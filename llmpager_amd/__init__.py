@@ -112,6 +112,10 @@ def _sig(lib):
         "lp_rope": (i32, [vp, u64, i32, i32, i32, f32, vp]),
         "lp_attn_decode": (i32, [vp, u64, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, i32, vp]),
         "lp_bf16_row": (i32, [vp, u64, i32, i32, u64, vp]),
+        "lp_rmsnorm_gemv": (i32, [vp, u64, u64, f32, i32, u64, i32, u64, u64, i32, u64, u64, i32, u64, vp]),
+        "lp_gemv_add_rmsnorm": (i32, [vp, u64, u64, i32, i32, u64, u64, f32, u64, vp]),
+        "lp_attn_fused": (i32, [vp, u64, u64, u64, u64, u64, f32, f32, u64, u64, u64, u64, i32, i32, i32, i32, i32,
+                                f32, vp]),
         "lp_mla_rope": (i32, [vp, u64, i32, i32, i32, i32, i32, u64, f32, vp]),
         "lp_mla_attn_decode": (i32, [vp, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
         "lp_bf16_gemv_batch": (i32, [vp, u64, u64, u64, i32, u64, i32, i32, i32, i32, vp]),
@@ -462,6 +466,30 @@ class Kernels:
 
     def bf16_row(self, table: int, row: int, n: int, out: int, stream=None) -> None:
         _check(lib().lp_bf16_row(self.cuda.ctx, table, row, n, out, stream))
+
+    # the fused decode step (no kernels.rs counterparts: each is several of
+    # the launches above in one, lp_step.hip)
+    def rmsnorm_gemv(self, x: int, ln: int, eps: float, cols: int, mats, stream=None) -> None:
+        """y_i = W_i . rmsnorm(x, ln) for mats = [(w, rows, y), ...] (one to
+        three matrices sharing x; ln = 0: no norm)."""
+        m = list(mats) + [(0, 0, 0)] * (3 - len(mats))
+        if not 1 <= len(mats) <= 3:
+            raise ValueError("rmsnorm_gemv takes one to three matrices")
+        _check(lib().lp_rmsnorm_gemv(self.cuda.ctx, x, ln, eps, cols, m[0][0], m[0][1], m[0][2], m[1][0], m[1][1],
+                                     m[1][2], m[2][0], m[2][1], m[2][2], stream))
+
+    def gemv_add_rmsnorm(self, w: int, x: int, rows: int, cols: int, h: int, ln: int, eps: float, hn: int,
+                         stream=None) -> None:
+        """h += W . x, then hn = rmsnorm(h, ln)."""
+        _check(lib().lp_gemv_add_rmsnorm(self.cuda.ctx, w, x, rows, cols, h, ln, eps, hn, stream))
+
+    def attn_fused(self, q: int, k: int, v: int, q_norm: int, k_norm: int, eps: float, rope_base: float, kcache: int,
+                   vcache: int, out: int, scratch: int, heads: int, kv_heads: int, head_dim: int, pos: int,
+                   max_seq: int, scale: float, stream=None) -> None:
+        """Per-head q / k RMSNorm, RoPE, the fp16 KV append at pos and GQA
+        decode attention over positions 0..pos (q, k, v read only)."""
+        _check(lib().lp_attn_fused(self.cuda.ctx, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, out,
+                                   scratch, heads, kv_heads, head_dim, pos, max_seq, scale, stream))
 
     # MLA absorbed decode (kernels.rs, mla.cu)
     def mla_rope(self, x: int, n_vecs: int, stride: int, offset: int, half: int, pos: int, inv_freq: int,

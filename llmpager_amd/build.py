@@ -2,7 +2,8 @@
 
 Outputs (under llmpager_amd/lib/):
   lp_basic.hsaco, lp_moe.hsaco,
-  lp_gemm.hsaco, lp_attn.hsaco    kernels, hipcc --genco --offload-arch=gfx950
+  lp_gemm.hsaco, lp_attn.hsaco,
+  lp_step.hsaco                   kernels, hipcc --genco --offload-arch=gfx950
   libllmpager_hip.so              host runtime (g++), loads the code objects
                                   with hipModuleLoad at lp_init
 
@@ -23,7 +24,7 @@ OUT = os.path.join(HERE, "lib")
 ROOT = os.path.dirname(HERE)
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip", "lp_gemm.hip", "lp_attn.hip"]
+KERNEL_SOURCES = ["lp_basic.hip", "lp_moe.hip", "lp_gemm.hip", "lp_attn.hip", "lp_step.hip"]
 HOST_SOURCES = ["lp_runtime.cpp", "lp_synth.cpp", "lp_cache.cpp", "lp_pager.cpp", "lp_pack.cpp"]
 HOST_HIP_SOURCES = ["lp_noalloc.hip"]
 

@@ -24,7 +24,13 @@ constexpr int kRouteEPW = 1;           // fused routing: router experts per wave
 constexpr int kRouteXLds = 64 * 1024;  // fused routing: LDS for staged token rows (H <= 16384)
 constexpr int kSyncSlots = 64;         // launch slots of the context's arrival counters
 constexpr int kSyncStride = 32;        // words between arrival counters (one 128-byte line each)
-constexpr int kSyncWords = 17 * kSyncStride;  // counters per slot: [b] token block b (b < 16), [16] every block
+// counters per slot: routing's [b] token block b (b < 16) and [16] every
+// block, then the fused decode step's (kStepSyncAttn + g: attention's KV
+// head g, kStepSyncGemv: the output projection)
+constexpr int kAttnFusedMaxKvHeads = 16;
+constexpr int kStepSyncAttn = 17 * kSyncStride;
+constexpr int kStepSyncGemv = kStepSyncAttn + kAttnFusedMaxKvHeads * kSyncStride;
+constexpr int kSyncWords = kStepSyncGemv + kSyncStride;
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
@@ -113,6 +119,41 @@ struct SiluMulArgs {                // kernels.rs:224-236
 struct Bf16GemvArgs {               // kernels.rs:202-222
     uint64_t w, x, y;
     int32_t rows, cols;
+};
+
+// The fused decode step (no reference counterpart: each fuses launches that
+// decode.rs:275-301 issues one by one).
+// y_i = W_i . rmsnorm(x, ln) (ln 0: W_i . x) for up to three bf16 [rows_i,
+// cols] matrices sharing the input; cols a multiple of 8, at most
+// kFusedGemvMaxCols.
+constexpr int kFusedGemvMaxCols = 4096;
+struct RmsNormGemvArgs {
+    uint64_t x, ln;
+    uint64_t w0, w1, w2, y0, y1, y2;
+    int32_t rows0, rows1, rows2, cols;
+    float eps;
+    int32_t pad0;
+};
+// h[rows] += W . x (W bf16 [rows, cols]), then hn = rmsnorm(h, ln); rows at
+// most kFusedGemvMaxRows
+constexpr int kFusedGemvMaxRows = 4096;
+struct GemvAddRmsNormArgs {
+    uint64_t w, x, h, ln, hn, sync;
+    int32_t rows, cols;
+    float eps;
+    int32_t pad0;
+};
+// Per-head q / k RMSNorm, NeoX RoPE, the fp16 KV append at pos and GQA
+// decode attention over pos + 1 positions, head_dim 128; `cps` chunks of 64
+// positions per split; partial records {max, sum, acc[128]} at scratch +
+// head * scratch_stride + split * 130 floats when splits > 1.
+constexpr int kAttnFusedMaxSplits = 32;
+struct AttnFusedArgs {
+    uint64_t q, k, v, q_norm, k_norm;
+    uint64_t kcache, vcache, out, scratch, sync;
+    int32_t kv_heads, pos, max_seq, splits, cps, scratch_stride;
+    float eps, rope_base, scale;
+    int32_t pad0;
 };
 
 struct AddArgs {                    // kernels.rs:239-250

@@ -101,6 +101,19 @@ enum Fn {
     kAttnCombine,
     kMlaSplit,
     kMlaCombine,
+    kRmsNormGemv1,
+    kRmsNormGemv2,
+    kRmsNormGemv4,
+    kRmsNormGemv8,
+    kGemvAddRmsNorm1,
+    kGemvAddRmsNorm2,
+    kGemvAddRmsNorm4,
+    kGemvAddRmsNorm8,
+    kAttnFusedG1,
+    kAttnFusedG2,
+    kAttnFusedG4,
+    kAttnFusedG8,
+    kAttnFusedG16,
     kNumFns
 };
 
@@ -138,10 +151,18 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_attn.hsaco", "lp_strided_copy"},  {"lp_attn.hsaco", "lp_attn_split_f32"},
     {"lp_attn.hsaco", "lp_attn_split_f16"}, {"lp_attn.hsaco", "lp_attn_combine"},
     {"lp_attn.hsaco", "lp_mla_split"},     {"lp_attn.hsaco", "lp_mla_combine"},
+    {"lp_step.hsaco", "lp_rmsnorm_gemv_c1"}, {"lp_step.hsaco", "lp_rmsnorm_gemv_c2"},
+    {"lp_step.hsaco", "lp_rmsnorm_gemv_c4"}, {"lp_step.hsaco", "lp_rmsnorm_gemv_c8"},
+    {"lp_step.hsaco", "lp_gemv_add_rmsnorm_c1"}, {"lp_step.hsaco", "lp_gemv_add_rmsnorm_c2"},
+    {"lp_step.hsaco", "lp_gemv_add_rmsnorm_c4"}, {"lp_step.hsaco", "lp_gemv_add_rmsnorm_c8"},
+    {"lp_step.hsaco", "lp_attn_fused_g1"}, {"lp_step.hsaco", "lp_attn_fused_g2"},
+    {"lp_step.hsaco", "lp_attn_fused_g4"}, {"lp_step.hsaco", "lp_attn_fused_g8"},
+    {"lp_step.hsaco", "lp_attn_fused_g16"},
 };
 
-const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco", "lp_attn.hsaco"};
-constexpr int kNumModules = 4;
+const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco", "lp_attn.hsaco",
+                                "lp_step.hsaco"};
+constexpr int kNumModules = 5;
 
 std::string library_dir() {
     Dl_info info;
@@ -805,6 +826,112 @@ int lp_mla_attn_decode_batch(lp_ctx* c, uint64_t q, uint64_t cache, uint64_t cac
     if (int r = launch(c, kMlaSplit, dim3((unsigned)a.splits, (unsigned)batch), dim3(256), lds, s, a)) return r;
     return launch(c, kMlaCombine, dim3((unsigned)heads, (unsigned)batch, (unsigned)(c_dim / 64)), dim3(256), 0, s,
                   a);
+}
+
+// ---- the fused decode step (lp_step.hip) ------------------------------------------
+
+static int sync_slot(lp_ctx* c, lp_stream s);
+
+static uint64_t sync_words(lp_ctx* c, int slot) {
+    return reinterpret_cast<uint64_t>(c->sync) + (uint64_t)slot * kSyncWords * 4;
+}
+
+// the 8-column chunks per lane of a fused GEMV: 1, 2, 4 or 8 (cols <= 4096)
+static int gemv_cpl(int cols) {
+    const int cpl = (cols + 511) / 512;
+    return cpl <= 1 ? 1 : cpl <= 2 ? 2 : cpl <= 4 ? 4 : 8;
+}
+
+static int gemv_index(int cpl) { return cpl == 1 ? 0 : cpl == 2 ? 1 : cpl == 4 ? 2 : 3; }
+
+int lp_rmsnorm_gemv(lp_ctx* c, uint64_t x, uint64_t ln, float eps, int cols, uint64_t w0, int rows0, uint64_t y0,
+                    uint64_t w1, int rows1, uint64_t y1, uint64_t w2, int rows2, uint64_t y2, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (cols <= 0 || rows0 <= 0 || rows1 < 0 || rows2 < 0 || (rows2 > 0 && rows1 == 0))
+        return fail(LP_E_INVALID, "rmsnorm_gemv: empty shape");
+    if (cols % 8 || cols > kFusedGemvMaxCols)
+        return fail(LP_E_UNSUPPORTED, "rmsnorm_gemv: cols must be a multiple of 8, at most " +
+                                          std::to_string(kFusedGemvMaxCols));
+    if (x % 16 || w0 % 16 || (rows1 && w1 % 16) || (rows2 && w2 % 16))
+        return fail(LP_E_UNSUPPORTED, "rmsnorm_gemv: x and the matrices must be 16-byte aligned");
+    if ((ln && ln % 16) || !x || !w0 || !y0 || (rows1 && (!w1 || !y1)) || (rows2 && (!w2 || !y2)))
+        return fail(LP_E_INVALID, "rmsnorm_gemv: null or misaligned pointer");
+    const long total = (long)rows0 + rows1 + rows2;
+    if (total > (long)INT32_MAX - 8) return fail(LP_E_UNSUPPORTED, "rmsnorm_gemv: too many rows");
+    RmsNormGemvArgs a{};
+    a.x = x;
+    a.ln = ln;
+    a.w0 = w0, a.w1 = w1, a.w2 = w2;
+    a.y0 = y0, a.y1 = y1, a.y2 = y2;
+    a.rows0 = rows0, a.rows1 = rows1, a.rows2 = rows2;
+    a.cols = cols;
+    a.eps = eps;
+    const Fn f = (Fn)(kRmsNormGemv1 + gemv_index(gemv_cpl(cols)));
+    return launch(c, f, dim3((unsigned)((total + 7) / 8)), dim3(256), 0, s, a);
+}
+
+int lp_gemv_add_rmsnorm(lp_ctx* c, uint64_t w, uint64_t x, int rows, int cols, uint64_t h, uint64_t ln, float eps,
+                        uint64_t hn, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (rows <= 0 || cols <= 0) return fail(LP_E_INVALID, "gemv_add_rmsnorm: empty shape");
+    if (rows > kFusedGemvMaxRows)
+        return fail(LP_E_UNSUPPORTED, "gemv_add_rmsnorm: at most " + std::to_string(kFusedGemvMaxRows) + " rows");
+    if (cols % 8 || cols > kFusedGemvMaxCols)
+        return fail(LP_E_UNSUPPORTED, "gemv_add_rmsnorm: cols must be a multiple of 8, at most " +
+                                          std::to_string(kFusedGemvMaxCols));
+    if (!w || !x || !h || !ln || !hn || w % 16 || x % 16)
+        return fail(LP_E_INVALID, "gemv_add_rmsnorm: null pointer, or w / x not 16-byte aligned");
+    const int slot = sync_slot(c, s);
+    if (slot < 0)
+        return fail(LP_E_UNSUPPORTED, "gemv_add_rmsnorm: more than " + std::to_string(kSyncSlots) +
+                                          " streams use this context's arrival counters");
+    GemvAddRmsNormArgs a{};
+    a.w = w, a.x = x, a.h = h, a.ln = ln, a.hn = hn;
+    a.sync = sync_words(c, slot);
+    a.rows = rows, a.cols = cols;
+    a.eps = eps;
+    const Fn f = (Fn)(kGemvAddRmsNorm1 + gemv_index(gemv_cpl(cols)));
+    return launch(c, f, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
+}
+
+int lp_attn_fused(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
+                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch, int heads,
+                  int kv_heads, int head_dim, int pos, int max_seq, float scale, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+        return fail(LP_E_INVALID, "attn_fused: heads must be a multiple of kv_heads");
+    const int group = heads / kv_heads;
+    if (head_dim != 128 || kv_heads > kAttnFusedMaxKvHeads || group > 16 || (group & (group - 1)))
+        return fail(LP_E_UNSUPPORTED, "attn_fused: head_dim 128, at most " + std::to_string(kAttnFusedMaxKvHeads) +
+                                          " kv heads, 1, 2, 4, 8 or 16 query heads per kv head");
+    if (pos < 0 || pos >= max_seq) return fail(LP_E_INVALID, "attn_fused: need 0 <= pos < max_seq");
+    // buffer offsets reach 63 rows past the last position (int32 bytes)
+    if ((uint64_t)(max_seq + 64) * head_dim * 2 >= (1ull << 31))
+        return fail(LP_E_UNSUPPORTED, "attn_fused: each kv head's cache must be under 2 GiB");
+    if (!q || !k || !v || !kcache || !vcache || !out || kcache % 16 || vcache % 16 || q % 4 || k % 4 || v % 4)
+        return fail(LP_E_INVALID, "attn_fused: null pointer, or caches not 16-byte aligned");
+    const int chunks = (pos + 64) / 64;
+    const int by_scratch = max_seq / (head_dim + 2);
+    int splits = std::min(chunks, std::min(kAttnFusedMaxSplits, by_scratch));
+    if (splits < 1) splits = 1;
+    const int cps = (chunks + splits - 1) / splits;
+    splits = (chunks + cps - 1) / cps;
+    if (splits > 1 && !scratch) return fail(LP_E_INVALID, "attn_fused: null scratch");
+    AttnFusedArgs a{};
+    a.q = q, a.k = k, a.v = v, a.q_norm = q_norm, a.k_norm = k_norm;
+    a.kcache = kcache, a.vcache = vcache, a.out = out, a.scratch = scratch;
+    a.kv_heads = kv_heads, a.pos = pos, a.max_seq = max_seq, a.splits = splits, a.cps = cps;
+    a.scratch_stride = max_seq;
+    a.eps = eps, a.rope_base = rope_base, a.scale = scale;
+    if (splits > 1) {
+        const int slot = sync_slot(c, s);
+        if (slot < 0)
+            return fail(LP_E_UNSUPPORTED, "attn_fused: more than " + std::to_string(kSyncSlots) +
+                                              " streams use this context's arrival counters");
+        a.sync = sync_words(c, slot);
+    }
+    const int gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : group == 8 ? 3 : 4;
+    return launch(c, (Fn)(kAttnFusedG1 + gi), dim3((unsigned)splits, (unsigned)kv_heads), dim3(256), 0, s, a);
 }
 
 // ---- fused MoE layer --------------------------------------------------------------

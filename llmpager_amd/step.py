@@ -17,7 +17,19 @@ Every launch goes to one stream with no host synchronisation, so a step can
 be recorded once (Cuda.capture_begin / capture_end) and replayed.  The
 attention matrices are bf16 (the reference's default core dtype,
 decode.rs:25-39 with core_q4 off) and the KV cache fp16 (its default,
-decode.rs:151)."""
+decode.rs:151).
+
+Two launch sequences compute the step: the reference's own, one launch per
+kernels.rs call (fused=False), and the fused one (fused=True, the default
+where the shape allows it: head_dim 128, an fp16 cache, 1, 2, 4, 8 or 16
+query heads per KV head, at most 16 KV heads, hidden and heads x head_dim
+at most 4096), three launches per attention block:
+
+    rmsnorm_gemv       q, k, v = W_{q,k,v} rmsnorm(h, input_ln)
+    attn_fused         q / k norms, rope, kv_append, attention -> a
+    gemv_add_rmsnorm   h += W_o a; hn = rmsnorm(h, post_ln)
+
+and rmsnorm_gemv again for the final norm and the lm_head."""
 from __future__ import annotations
 
 from dataclasses import dataclass
@@ -36,6 +48,14 @@ class StepShape:
     eps: float = 1e-6
     rope_theta: float = 1e6
     kv_f16: bool = True
+
+
+def fusable(S: StepShape) -> bool:
+    """Whether the fused launches (lp_attn_fused, lp_rmsnorm_gemv,
+    lp_gemv_add_rmsnorm) take this shape."""
+    g = S.heads // S.kv_heads if S.kv_heads else 0
+    return (S.head_dim == 128 and S.kv_f16 and S.heads % S.kv_heads == 0 and g in (1, 2, 4, 8, 16)
+            and S.kv_heads <= 16 and S.hidden % 8 == 0 and S.hidden <= 4096 and S.heads * S.head_dim <= 4096)
 
 
 @dataclass
@@ -58,7 +78,7 @@ class DecodeStep:
     (with its workspace for one token: `ws`, `ws_bytes`)."""
 
     def __init__(self, cuda, shape: StepShape, attn: list[AttnWeights], moe: list, embed: int,
-                 final_norm: int, lm_head: int, ws: int, ws_bytes: int):
+                 final_norm: int, lm_head: int, ws: int, ws_bytes: int, fused: bool | None = None):
         import llmpager_amd as lp
         assert len(attn) == len(moe)
         self.cuda, self.shape, self.attn, self.moe = cuda, shape, attn, moe
@@ -67,6 +87,10 @@ class DecodeStep:
         self.K = lp.Kernels(cuda)
         S = shape
         qd, kd = S.heads * S.head_dim, S.kv_heads * S.head_dim
+        can_fuse = fusable(S)
+        if fused and not can_fuse:
+            raise ValueError(f"the fused step does not take this shape: {S}")
+        self.fused = can_fuse if fused is None else fused
         cb = (2 if S.kv_f16 else 4) * kd * S.max_seq
         self.allocs = []
 
@@ -89,6 +113,18 @@ class DecodeStep:
         if not 0 <= pos < S.max_seq:
             raise ValueError(f"position {pos} exceeds max_seq {S.max_seq}")
         K.bf16_row(self.embed, token, hid, self.h, s)
+        scale = 1.0 / float(np.sqrt(S.head_dim))
+        if self.fused:
+            for l, (w, layer) in enumerate(zip(self.attn, self.moe)):
+                K.rmsnorm_gemv(self.h, w.input_ln, S.eps, hid, [(w.q, qd, self.q), (w.k, kd, self.k),
+                                                                (w.v, kd, self.v)], s)
+                K.attn_fused(self.q, self.k, self.v, w.q_norm, w.k_norm, S.eps, S.rope_theta, self.kcache[l],
+                             self.vcache[l], self.att, self.scratch, S.heads, S.kv_heads, S.head_dim, pos,
+                             S.max_seq, scale, s)
+                K.gemv_add_rmsnorm(w.o, self.att, hid, qd, self.h, w.post_ln, S.eps, self.hn, s)
+                layer.forward(self.hn, self.h, 1, self.ws, s, ws_bytes=self.ws_bytes)
+            K.rmsnorm_gemv(self.h, self.final_norm, S.eps, hid, [(self.lm_head, S.vocab, self.logits)], s)
+            return
         for l, (w, layer) in enumerate(zip(self.attn, self.moe)):
             K.rmsnorm(self.h, w.input_ln, self.hn, 1, hid, S.eps, s)
             K.bf16_gemv(w.q, self.hn, self.q, qd, hid, s)
@@ -101,7 +137,7 @@ class DecodeStep:
             K.kv_append(self.k, self.v, self.kcache[l], self.vcache[l], S.kv_heads, S.head_dim, pos, S.max_seq,
                         S.kv_f16, s)
             K.attn_decode(self.q, self.kcache[l], self.vcache[l], self.att, self.scratch, S.heads, S.kv_heads,
-                          S.head_dim, pos + 1, S.max_seq, 1.0 / float(np.sqrt(S.head_dim)), S.kv_f16, s)
+                          S.head_dim, pos + 1, S.max_seq, scale, S.kv_f16, s)
             K.bf16_gemv(w.o, self.att, self.proj, hid, qd, s)
             K.add(self.h, self.proj, hid, s)
             K.rmsnorm(self.h, w.post_ln, self.hn, 1, hid, S.eps, s)

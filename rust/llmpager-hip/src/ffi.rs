@@ -214,6 +214,19 @@ extern "C" {
         kv_heads: c_int, head_dim: c_int, seq_len: c_int, max_seq: c_int, scale: f32, f16: c_int, s: lp_stream,
     ) -> c_int;
     pub fn lp_bf16_row(ctx: *mut lp_ctx, table: u64, row: c_int, n: c_int, out: u64, s: lp_stream) -> c_int;
+    pub fn lp_rmsnorm_gemv(
+        ctx: *mut lp_ctx, x: u64, ln: u64, eps: f32, cols: c_int, w0: u64, rows0: c_int, y0: u64, w1: u64,
+        rows1: c_int, y1: u64, w2: u64, rows2: c_int, y2: u64, s: lp_stream,
+    ) -> c_int;
+    pub fn lp_gemv_add_rmsnorm(
+        ctx: *mut lp_ctx, w: u64, x: u64, rows: c_int, cols: c_int, h: u64, ln: u64, eps: f32, hn: u64,
+        s: lp_stream,
+    ) -> c_int;
+    pub fn lp_attn_fused(
+        ctx: *mut lp_ctx, q: u64, k: u64, v: u64, q_norm: u64, k_norm: u64, eps: f32, rope_base: f32,
+        kcache: u64, vcache: u64, out: u64, scratch: u64, heads: c_int, kv_heads: c_int, head_dim: c_int,
+        pos: c_int, max_seq: c_int, scale: f32, s: lp_stream,
+    ) -> c_int;
     pub fn lp_mla_rope(
         ctx: *mut lp_ctx, x: u64, n_vecs: c_int, stride: c_int, offset: c_int, half: c_int, pos: c_int,
         inv_freq: u64, mscale: f32, s: lp_stream,

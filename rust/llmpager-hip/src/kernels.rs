@@ -5,7 +5,7 @@
 //! line each replaces).  The fused MoE layer entries (`moe_*`, `stack_*`)
 //! have no reference method: they replace the per-expert sequence the
 //! reference's decode loop issues (`decode.rs:734-790`).
-use anyhow::Result;
+use anyhow::{bail, Result};
 
 use crate::driver::{CUdeviceptr, CUstream, Cuda};
 use crate::ffi::{self, check, lp_moe_layer_desc, lp_moe_ws_layout};
@@ -131,6 +131,53 @@ impl Kernels {
         &self, cuda: &Cuda, table: CUdeviceptr, row: i32, n: i32, out: CUdeviceptr, stream: CUstream,
     ) -> Result<()> {
         check(unsafe { ffi::lp_bf16_row(cuda.ctx, table, row, n, out, stream) }, "bf16_row")
+    }
+
+    /// `y_i = W_i . rmsnorm(x, ln)` for one to three bf16 matrices `(w, rows, y)`
+    /// sharing `x` (`ln` 0: no norm).  No `kernels.rs` counterpart: the
+    /// rmsnorm and bf16_gemv launches of `decode.rs:282-285, 359-360` in one.
+    #[allow(clippy::too_many_arguments)]
+    pub fn rmsnorm_gemv(
+        &self, cuda: &Cuda, x: CUdeviceptr, ln: CUdeviceptr, eps: f32, cols: i32,
+        mats: &[(CUdeviceptr, i32, CUdeviceptr)], stream: CUstream,
+    ) -> Result<()> {
+        if mats.is_empty() || mats.len() > 3 {
+            bail!("rmsnorm_gemv takes one to three matrices");
+        }
+        let m = |i: usize| mats.get(i).copied().unwrap_or((0, 0, 0));
+        let (a, b, c) = (m(0), m(1), m(2));
+        let rc = unsafe {
+            ffi::lp_rmsnorm_gemv(cuda.ctx, x, ln, eps, cols, a.0, a.1, a.2, b.0, b.1, b.2, c.0, c.1, c.2, stream)
+        };
+        check(rc, "rmsnorm_gemv")
+    }
+
+    /// `h += W . x`, then `hn = rmsnorm(h, ln)` (`decode.rs:296-301` in one launch).
+    #[allow(clippy::too_many_arguments)]
+    pub fn gemv_add_rmsnorm(
+        &self, cuda: &Cuda, w: CUdeviceptr, x: CUdeviceptr, rows: i32, cols: i32, h: CUdeviceptr,
+        ln: CUdeviceptr, eps: f32, hn: CUdeviceptr, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe { ffi::lp_gemv_add_rmsnorm(cuda.ctx, w, x, rows, cols, h, ln, eps, hn, stream) };
+        check(rc, "gemv_add_rmsnorm")
+    }
+
+    /// Per-head q / k rmsnorm, rope, the fp16 KV append at `pos` and GQA decode
+    /// attention over `pos + 1` positions (`decode.rs:283-294` in one launch).
+    #[allow(clippy::too_many_arguments)]
+    pub fn attn_fused(
+        &self, cuda: &Cuda, q: CUdeviceptr, k: CUdeviceptr, v: CUdeviceptr, q_norm: CUdeviceptr,
+        k_norm: CUdeviceptr, eps: f32, rope_base: f32, kcache: CUdeviceptr, vcache: CUdeviceptr, out: CUdeviceptr,
+        scratch: CUdeviceptr, heads: i32, kv_heads: i32, head_dim: i32, pos: i32, max_seq: i32, scale: f32,
+        stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_attn_fused(
+                cuda.ctx, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, out, scratch, heads, kv_heads,
+                head_dim, pos, max_seq, scale, stream,
+            )
+        };
+        check(rc, "attn_fused")
     }
 
     #[allow(clippy::too_many_arguments)]
