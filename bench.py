@@ -808,9 +808,12 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) 
     uploaded into every layer's own buffers, so no layer's weights are
     another's), the KV caches filled with a small constant.  The step is
     recorded once at position `pos` (lp_graph_capture_begin / end) and
-    replayed; a timed step is the replay plus the logits' readback and the
-    host argmax, as the reference's greedy step does; the replays alone are
-    timed too.  Per-kernel times come from one eager step with events."""
+    replayed; a timed step is the replay plus the logits' readback (into
+    page-locked memory) and the host argmax, as the reference's greedy step
+    does; the replays alone are timed too.  Per-kernel times come from one
+    eager step with events.  Both launch sequences are measured: the fused
+    one (three launches per attention block) and the reference's own (one
+    launch per kernels.rs call)."""
     import llmpager_amd as lp
     from llmpager_amd.step import AttnWeights, DecodeStep, StepShape
     S = StepShape(hidden=H, heads=S_HEADS, kv_heads=S_KV_HEADS, head_dim=S_HEAD_DIM, vocab=S_VOCAB,
@@ -833,66 +836,84 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) 
     ws_bytes = stack.stack.ws_bytes(1)
     ws = cuda.alloc_device(ws_bytes)
     allocs.append(ws)
-    # the embedding gather reads one row: the lm_head's table serves as it
-    step = DecodeStep(cuda, S, attn, stack.layers, lm, fn, lm, ws, ws_bytes)
-    for c in step.kcache + step.vcache:
-        cuda.memset_async(c, 0x20, 2 * kd * S.max_seq, s)  # fp16 0x2020: 0.0083
-    cuda.sync_stream(s)
     weight_bytes = LAYERS * 2 * sum(shapes.values()) + 2 * S.vocab * H
     kv_bytes = LAYERS * 2 * 2 * kd * (pos + 1)
-    # one eager step with events: per-kernel times
-    step.run(7, pos, s)
-    cuda.sync_stream(s)
-    cuda.profile(True)
-    cuda.profile_reset()
-    step.run(7, pos, s)
-    cuda.sync_stream(s)
+    moe_bytes = LAYERS * (K * EXPERT_BYTES + ROUTER_BYTES + ACT_BYTES)  # one token: k distinct experts
+    pinned = cuda.alloc_pinned(4 * S.vocab)
+    logits = np.ctypeslib.as_array(C.cast(pinned, C.POINTER(C.c_float)), (S.vocab,))
     names = ["lp_bf16_row_to_f32", "lp_rmsnorm", "lp_bf16_gemv", "lp_rope", "lp_kv_append_f16", "lp_attn_split_f16",
              "lp_attn_combine", "lp_add", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_gateup_bal",
              "lp_moe_gateup_bal8", "lp_moe_down_comb", "lp_moe_down_comb16", "lp_rmsnorm_gemv_c4",
              "lp_attn_fused_g8", "lp_gemv_add_rmsnorm_c8"]
-    kern = {}
-    for n in names:
-        ms, cnt = cuda.profile_read(n)
-        if cnt:
-            kern[n] = {"launches": int(cnt), "us": ms * 1000.0}
-    cuda.profile(False)
-    moe_us = sum(v["us"] for k, v in kern.items() if k.startswith("lp_moe"))
-    g = step.capture(7, pos, s)
-    e0, e1 = cuda.event(), cuda.event()
-    for _ in range(warmup):
-        g.launch(s)
-    cuda.sync_stream(s)
-    cuda.record_event(e0, s)
-    for _ in range(steps):
-        g.launch(s)
-    cuda.record_event(e1, s)
-    cuda.sync_stream(s)
-    graph_ms = cuda.elapsed_ms(e0, e1) / steps
-    best = None
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.launch(s)
-        logits = cuda.download(step.logits, (S.vocab,), np.float32, s)
-        best = int(np.argmax(logits))
-    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
-    g.close()
-    for e in (e0, e1):
-        cuda.destroy_event(e)
-    step.free()
+
+    def measure(fused: bool) -> dict:
+        # the embedding gather reads one row: the lm_head's table serves as it
+        step = DecodeStep(cuda, S, attn, stack.layers, lm, fn, lm, ws, ws_bytes, fused=fused)
+        for c in step.kcache + step.vcache:
+            cuda.memset_async(c, 0x20, 2 * kd * S.max_seq, s)  # fp16 0x2020: 0.0083
+        cuda.sync_stream(s)
+        # one eager step with events: per-kernel times
+        step.run(7, pos, s)
+        cuda.sync_stream(s)
+        cuda.profile(True)
+        cuda.profile_reset()
+        step.run(7, pos, s)
+        cuda.sync_stream(s)
+        kern = {}
+        for n in names:
+            ms, cnt = cuda.profile_read(n)
+            if cnt:
+                kern[n] = {"launches": int(cnt), "us": ms * 1000.0}
+        cuda.profile(False)
+        moe_us = sum(v["us"] for k, v in kern.items() if k.startswith("lp_moe"))
+        g = step.capture(7, pos, s)
+        e0, e1 = cuda.event(), cuda.event()
+        for _ in range(warmup):
+            g.launch(s)
+        cuda.sync_stream(s)
+        cuda.record_event(e0, s)
+        for _ in range(steps):
+            g.launch(s)
+        cuda.record_event(e1, s)
+        cuda.sync_stream(s)
+        graph_ms = cuda.elapsed_ms(e0, e1) / steps
+        best = None
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.launch(s)
+            cuda.dtoh_ptr_async(pinned, step.logits, 4 * S.vocab, s)
+            cuda.sync_stream(s)
+            best = int(np.argmax(logits))
+        wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+        g.close()
+        for e in (e0, e1):
+            cuda.destroy_event(e)
+        step.free()
+        return {
+            "fused": fused, "tok_s": 1000.0 / wall_ms, "ms_per_step": wall_ms,
+            "graph_ms_per_step": graph_ms, "graph_tok_s": 1000.0 / graph_ms,
+            "launches_per_step": sum(v["launches"] for v in kern.values()),
+            "hbm_gbps_graph": (weight_bytes + kv_bytes + moe_bytes) / (graph_ms * 1e-3) / 1e9,
+            "moe_us_per_step": moe_us, "attn_and_head_us_per_step": sum(v["us"] for v in kern.values()) - moe_us,
+            "kernels": kern, "argmax": best,
+        }
+
+    fused = measure(True)
+    ref_seq = measure(False)
+    cuda.free_pinned(pinned)
     for p in allocs:
         cuda.free_device(p)
-    out = {
-        "position": pos, "layers": LAYERS, "tok_s": 1000.0 / wall_ms, "ms_per_step": wall_ms,
-        "graph_ms_per_step": graph_ms, "graph_tok_s": 1000.0 / graph_ms,
-        "weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
-        "hbm_gbps_graph": (weight_bytes + kv_bytes) / (graph_ms * 1e-3) / 1e9,
-        "moe_us_per_step": moe_us, "attn_and_head_us_per_step": sum(v["us"] for v in kern.values()) - moe_us,
-        "kernels": kern, "argmax": best,
-    }
-    log(f"decode step B=1 at position {pos}: {out['tok_s']:.1f} tok/s ({wall_ms:.3f} ms with the logits' readback "
-        f"and argmax; graph replay {graph_ms:.3f} ms), MoE {moe_us / 1000:.3f} ms + attention, norms and lm_head "
-        f"{out['attn_and_head_us_per_step'] / 1000:.3f} ms of kernel time (eager step with events)")
+    out = dict(fused)
+    out.update({"position": pos, "layers": LAYERS, "attn_weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
+                "moe_bytes": moe_bytes,
+                "reference_launch_sequence": {k: ref_seq[k] for k in ("tok_s", "ms_per_step", "graph_ms_per_step",
+                                                                      "launches_per_step", "argmax")}})
+    for r in (fused, ref_seq):
+        log(f"decode step B=1 at position {pos} ({'fused' if r['fused'] else 'one launch per kernels.rs call'}, "
+            f"{r['launches_per_step']} launches): {r['tok_s']:.1f} tok/s ({r['ms_per_step']:.3f} ms with the logits' "
+            f"readback and argmax; graph replay {r['graph_ms_per_step']:.3f} ms, {r['hbm_gbps_graph']:.0f} GB/s), "
+            f"MoE {r['moe_us_per_step'] / 1000:.3f} ms + attention, norms and lm_head "
+            f"{r['attn_and_head_us_per_step'] / 1000:.3f} ms of kernel time (eager step with events)")
     return out
 
 

@@ -357,6 +357,9 @@ class Cuda:
         assert dst.flags["C_CONTIGUOUS"]
         _check(lib().lp_dtoh_async(self.ctx, _ptr(dst), src, dst.nbytes, stream))
 
+    def dtoh_ptr_async(self, dst_ptr: int, src: int, nbytes: int, stream: int | None = None) -> None:
+        _check(lib().lp_dtoh_async(self.ctx, dst_ptr, src, nbytes, stream))
+
     def dtod_async(self, dst: int, src: int, nbytes: int, stream: int | None = None) -> None:
         _check(lib().lp_dtod_async(self.ctx, dst, src, nbytes, stream))
 
