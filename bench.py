@@ -844,7 +844,7 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) 
     names = ["lp_bf16_row_to_f32", "lp_rmsnorm", "lp_bf16_gemv", "lp_rope", "lp_kv_append_f16", "lp_attn_split_f16",
              "lp_attn_combine", "lp_add", "lp_moe_route_fused", "lp_moe_route_fused128", "lp_moe_gateup_bal",
              "lp_moe_gateup_bal8", "lp_moe_down_comb", "lp_moe_down_comb16", "lp_rmsnorm_gemv_c4",
-             "lp_attn_fused_g8", "lp_gemv_add_rmsnorm_c8"]
+             "lp_attn_fused_g8", "lp_gemv_add_rmsnorm_c8", "lp_attn_block_g8"]
 
     def measure(fused: bool) -> dict:
         # the embedding gather reads one row: the lm_head's table serves as it

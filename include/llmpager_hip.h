@@ -162,6 +162,15 @@ int lp_gemv_add_rmsnorm(lp_ctx* ctx, uint64_t w, uint64_t x, int rows, int cols,
 int lp_attn_fused(lp_ctx* ctx, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
                   float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch, int heads,
                   int kv_heads, int head_dim, int pos, int max_seq, float scale, lp_stream s);
+/* lp_attn_fused into att, then h[hidden] += W_o . att (W_o bf16 [hidden,
+ * heads * 128]) and hn = rmsnorm(h, post_ln), in one launch (decode.rs:
+ * 283-301): the o projection's workgroups load W_o while the attention
+ * runs.  hidden and heads * 128 at most 4096.  Uses the stream's arrival
+ * counters, like lp_gemv_add_rmsnorm. */
+int lp_attn_block(lp_ctx* ctx, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
+                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t att, uint64_t scratch, int heads,
+                  int kv_heads, int head_dim, int pos, int max_seq, float scale, uint64_t wo, uint64_t h,
+                  uint64_t post_ln, uint64_t hn, int hidden, lp_stream s);
 
 /* ---- MLA absorbed decode: kernels::Kernels (kernels.rs; mla.cu) ----------- */
 

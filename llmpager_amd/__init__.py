@@ -116,6 +116,8 @@ def _sig(lib):
         "lp_gemv_add_rmsnorm": (i32, [vp, u64, u64, i32, i32, u64, u64, f32, u64, vp]),
         "lp_attn_fused": (i32, [vp, u64, u64, u64, u64, u64, f32, f32, u64, u64, u64, u64, i32, i32, i32, i32, i32,
                                 f32, vp]),
+        "lp_attn_block": (i32, [vp, u64, u64, u64, u64, u64, f32, f32, u64, u64, u64, u64, i32, i32, i32, i32, i32,
+                                f32, u64, u64, u64, u64, i32, vp]),
         "lp_mla_rope": (i32, [vp, u64, i32, i32, i32, i32, i32, u64, f32, vp]),
         "lp_mla_attn_decode": (i32, [vp, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
         "lp_bf16_gemv_batch": (i32, [vp, u64, u64, u64, i32, u64, i32, i32, i32, i32, vp]),
@@ -493,6 +495,15 @@ class Kernels:
         decode attention over positions 0..pos (q, k, v read only)."""
         _check(lib().lp_attn_fused(self.cuda.ctx, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, out,
                                    scratch, heads, kv_heads, head_dim, pos, max_seq, scale, stream))
+
+    def attn_block(self, q: int, k: int, v: int, q_norm: int, k_norm: int, eps: float, rope_base: float, kcache: int,
+                   vcache: int, att: int, scratch: int, heads: int, kv_heads: int, head_dim: int, pos: int,
+                   max_seq: int, scale: float, wo: int, h: int, post_ln: int, hn: int, hidden: int,
+                   stream=None) -> None:
+        """attn_fused into att, then h += W_o . att and hn = rmsnorm(h, post_ln), in one launch."""
+        _check(lib().lp_attn_block(self.cuda.ctx, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, att,
+                                   scratch, heads, kv_heads, head_dim, pos, max_seq, scale, wo, h, post_ln, hn, hidden,
+                                   stream))
 
     # MLA absorbed decode (kernels.rs, mla.cu)
     def mla_rope(self, x: int, n_vecs: int, stride: int, offset: int, half: int, pos: int, inv_freq: int,

@@ -45,6 +45,26 @@ __device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
     return *flag;
 }
 
+// One more completed part at *cnt once this workgroup's stores have
+// completed (every thread calls it).
+__device__ __forceinline__ void signal(int* cnt, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(cnt, 1);
+}
+
+// Wait until *cnt reaches target (every thread calls it), polling with
+// agent-scope loads.  The counted parts come from workgroups of lower index
+// in the same launch, dispatched before this one on its XCD; the wait is
+// bounded all the same (kSpinMax polls of about a microsecond each).
+constexpr int kSpinMax = 1 << 15;
+__device__ __forceinline__ void wait_count(int* cnt, int target) {
+    if (threadIdx.x == 0) {
+        for (int it = 0; it < kSpinMax && load_agent(cnt) < target; ++it) __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o >= 1; o >>= 1) v += shfl_xor(v, o);
     return v;
@@ -293,8 +313,11 @@ __device__ __forceinline__ float row16_max(float v) {
     return fmaxf(v, dpp<0x128>(v));
 }
 
+// The attention output leaves by agent-scope stores when another workgroup
+// of the launch reads it (done != null); the workgroup that completes a KV
+// head's output then adds one to *done.
 template <int G>
-__device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a) {
+__device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a, int sp, int g, int* done) {
     constexpr int STEPS = kHd / 32;
     __shared__ __align__(16) float qf[G][kHd];
     __shared__ __align__(16) uint4 qb[2][STEPS][64];
@@ -307,7 +330,6 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a) {
     __shared__ int flag;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     const int n = lane & 15, kb = lane >> 4;
-    const int g = blockIdx.y, sp = blockIdx.x;
     const int pos = a.pos, seq = pos + 1;
     const int nch = (seq + 63) >> 6;
     const int c0 = sp * a.cps, c1 = min(nch, c0 + a.cps);
@@ -510,7 +532,7 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a) {
     __syncthreads();
     float* out = reinterpret_cast<float*>(a.out);
     float* scr = reinterpret_cast<float*>(a.scratch);
-    constexpr int kRec = kHd + 2;
+    constexpr int kRec = kAttnFusedRec;
     for (int o = tid; o < G * kHd; o += 256) {
         const int hh = o / kHd, d = o % kHd;
         float M = -INFINITY;
@@ -525,48 +547,60 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a) {
         }
         const size_t head = (size_t)g * G + hh;
         if (a.splits == 1) {
-            out[head * kHd + d] = A / L;
+            if (done)
+                store_agent(out + head * kHd + d, A / L);
+            else
+                out[head * kHd + d] = A / L;
         } else {
             float* rec = scr + head * a.scratch_stride + (size_t)sp * kRec;
-            store_agent(rec + 2 + d, A);
+            store_agent(rec + d, A);
             if (d == 0) {
-                store_agent(rec, M);
-                store_agent(rec + 1, L);
+                store_agent(rec + kHd, M);
+                store_agent(rec + kHd + 1, L);
             }
         }
     }
-    if (a.splits == 1) return;
+    if (a.splits == 1) {
+        if (done) signal(done, &flag);
+        return;
+    }
     int* cnt = reinterpret_cast<int*>(a.sync) + kStepSyncAttn + kSyncStride * g;
     if (arrival_order(cnt, a.splits, &flag) != a.splits - 1) return;
-    // ---- the last split of head group g merges the records.  Every load is
-    // issued at once: the {max, sum} pairs (32 lanes per head, lane s holding
-    // split s) and each thread's accumulators (outputs tid + 256 i) of up to
-    // 16 splits; the weights e^(m_s - M) / sum_s e^(m_s - M) l_s then go
-    // through LDS to the threads that need them.
+    // ---- the last split of head group g merges the records.  They were
+    // written in this launch with agent-scope stores and nothing on this XCD
+    // has read them since the launch began, so plain loads see them.  Every
+    // load is issued at once: the {max, sum} pairs (32 lanes per head, lane s
+    // holding split s) and each thread's accumulators (4 dimensions of one
+    // head: 16-byte loads) of up to 16 splits; the weights e^(m_s - M) /
+    // sum_s e^(m_s - M) l_s then go through LDS to the threads that need them.
     const int S = a.splits;
-    constexpr int kOut = G * kHd / 256 > 0 ? G * kHd / 256 : 1;
+    constexpr int kOut = G * kHd / 4 / 256 > 0 ? G * kHd / 4 / 256 : 1;
     constexpr int kWP = (G + 7) / 8;
     float mr[kWP], lr[kWP];
 #pragma unroll
     for (int p = 0; p < kWP; ++p) {
         const int hh = 8 * p + (tid >> 5), s = tid & 31;
         const bool on = hh < G && s < S;
-        const float* rec = scr + ((size_t)g * G + (hh < G ? hh : 0)) * a.scratch_stride + (size_t)s * kRec;
-        mr[p] = on ? load_agent(rec) : -INFINITY;
-        lr[p] = on ? load_agent(rec + 1) : 0.0f;
+        const float* rec = scr + ((size_t)g * G + (hh < G ? hh : 0)) * a.scratch_stride + (size_t)s * kRec + kHd;
+        float2 ml = make_float2(-INFINITY, 0.0f);
+        if (on) ml = *gptr<float2>(reinterpret_cast<uint64_t>(rec));
+        mr[p] = ml.x;
+        lr[p] = ml.y;
     }
-    float num[kOut];
+    float4 num[kOut];
 #pragma unroll
-    for (int i = 0; i < kOut; ++i) num[i] = 0.0f;
+    for (int i = 0; i < kOut; ++i) num[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int s0 = 0; s0 < S; s0 += 16) {
-        float v[16][kOut];
+        float4 v[16][kOut];
 #pragma unroll
         for (int k = 0; k < 16; ++k)
 #pragma unroll
             for (int i = 0; i < kOut; ++i) {
-                const int o = tid + 256 * i, hh = o / kHd, d = o % kHd;
-                const float* rec = scr + ((size_t)g * G + hh) * a.scratch_stride + (size_t)(s0 + k) * kRec + 2 + d;
-                v[k][i] = s0 + k < S && o < G * kHd ? load_agent(rec) : 0.0f;
+                const int o = tid + 256 * i, hh = o >> 5, d4 = o & 31;
+                const float* rec = scr + ((size_t)g * G + (hh < G ? hh : 0)) * a.scratch_stride +
+                                   (size_t)(s0 + k) * kRec + 4 * d4;
+                v[k][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (s0 + k < S && hh < G) v[k][i] = *gptr<float4>(reinterpret_cast<uint64_t>(rec));
             }
         if (s0 == 0) {
 #pragma unroll
@@ -585,23 +619,39 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a) {
         for (int k = 0; k < 16; ++k)
 #pragma unroll
             for (int i = 0; i < kOut; ++i) {
-                const int o = tid + 256 * i;
-                if (s0 + k < S && o < G * kHd)
-                    num[i] = __builtin_fmaf(mw[(o / kHd) * kAttnFusedMaxSplits + s0 + k], v[k][i], num[i]);
+                const int hh = (tid + 256 * i) >> 5;
+                if (s0 + k < S && hh < G) {
+                    const float wt = mw[hh * kAttnFusedMaxSplits + s0 + k];
+                    num[i].x = __builtin_fmaf(wt, v[k][i].x, num[i].x);
+                    num[i].y = __builtin_fmaf(wt, v[k][i].y, num[i].y);
+                    num[i].z = __builtin_fmaf(wt, v[k][i].z, num[i].z);
+                    num[i].w = __builtin_fmaf(wt, v[k][i].w, num[i].w);
+                }
             }
     }
 #pragma unroll
     for (int i = 0; i < kOut; ++i) {
-        const int o = tid + 256 * i;
-        if (o < G * kHd) out[((size_t)g * G + o / kHd) * kHd + o % kHd] = num[i];
+        const int o = tid + 256 * i, hh = o >> 5, d4 = o & 31;
+        if (hh < G) {
+            float* po = out + ((size_t)g * G + hh) * kHd + 4 * d4;
+            if (done) {
+                store_agent(po, num[i].x);
+                store_agent(po + 1, num[i].y);
+                store_agent(po + 2, num[i].z);
+                store_agent(po + 3, num[i].w);
+            } else {
+                *reinterpret_cast<float4*>(po) = num[i];
+            }
+        }
     }
+    if (done) signal(done, &flag);
 }
 
 }  // namespace
 
 #define LP_ATTN_FUSED(G)                                                                             \
     extern "C" __global__ void __launch_bounds__(256) lp_attn_fused_g##G(const AttnFusedArgs a) {  \
-        attn_fused_body<G>(a);                                                                       \
+        attn_fused_body<G>(a, blockIdx.x, blockIdx.y, nullptr);                                      \
     }
 LP_ATTN_FUSED(1)
 LP_ATTN_FUSED(2)
@@ -609,3 +659,86 @@ LP_ATTN_FUSED(4)
 LP_ATTN_FUSED(8)
 LP_ATTN_FUSED(16)
 #undef LP_ATTN_FUSED
+
+// ---------------------------------------------------------------------------
+// The attention block's tail in one launch: lp_attn_fused on workgroups
+// [0, n_attn) (split s of KV head g at s + splits g), then the o projection,
+// the residual add and the post-attention norm (lp_gemv_add_rmsnorm) on the
+// workgroups after them.  Those start by loading their rows of W_o, which do
+// not depend on the attention, then wait for the attention's KV heads to be
+// complete (a counter) and read its output with agent-scope loads.  The last
+// of them resets the counter.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kBlockCpl = kFusedGemvMaxCols / 512;
+
+template <int G>
+__device__ __forceinline__ void attn_block_body(const AttnBlockArgs& b) {
+    const AttnFusedArgs& a = b.at;
+    int* sync = reinterpret_cast<int*>(a.sync);
+    if ((int)blockIdx.x < b.n_attn) {
+        attn_fused_body<G>(a, blockIdx.x % a.splits, blockIdx.x / a.splits, sync + kStepSyncDone);
+        return;
+    }
+    __shared__ float red[4];
+    __shared__ int flag;
+    constexpr int CPL = kBlockCpl;
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const int r0 = ((blockIdx.x - b.n_attn) * 4 + wave) * kGemvRowsPerWave;
+    uint4 w[kGemvRowsPerWave][CPL];
+#pragma unroll
+    for (int r = 0; r < kGemvRowsPerWave; ++r)
+        load_row<CPL>(b.wo + (uint64_t)(r0 + r) * b.cols * 2, b.cols, r0 + r < b.rows, w[r]);
+    float hr[kGemvRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kGemvRowsPerWave; ++r) hr[r] = r0 + r < b.rows ? reinterpret_cast<const float*>(b.h)[r0 + r] : 0.0f;
+    wait_count(sync + kStepSyncDone, a.kv_heads);
+    // the attention output: written in this launch with agent-scope stores,
+    // and nothing on this XCD read it before they completed, so plain loads
+    // see it
+    float x[CPL][8];
+    load_vec<CPL>(a.out, b.cols, x);
+    float* h = reinterpret_cast<float*>(b.h);
+#pragma unroll
+    for (int r = 0; r < kGemvRowsPerWave; ++r) {
+        const float y = row_dot<CPL>(w[r], x);
+        if (lane == 0 && r0 + r < b.rows) store_agent(h + r0 + r, hr[r] + y);
+    }
+    const int n_o = (int)gridDim.x - b.n_attn;
+    if (arrival_order(sync + kStepSyncGemv, n_o, &flag) != n_o - 1) return;
+    // every workgroup has passed its wait: the counter starts the next launch at zero
+    if (threadIdx.x == 0) store_agent(sync + kStepSyncDone, 0);
+    constexpr int kPer = kFusedGemvMaxRows / 256;
+    const float* ln = reinterpret_cast<const float*>(b.ln);
+    float hv[kPer], gv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        hv[k] = i < b.rows ? load_agent(h + i) : 0.0f;
+        gv[k] = i < b.rows ? ln[i] : 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) ss = __builtin_fmaf(hv[k], hv[k], ss);
+    const float inv = 1.0f / sqrtf(block_sum4(ss, red) / (float)b.rows + a.eps);
+    float* hn = reinterpret_cast<float*>(b.hn);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < b.rows) hn[i] = hv[k] * inv * gv[k];
+    }
+}
+
+}  // namespace
+
+#define LP_ATTN_BLOCK(G)                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) lp_attn_block_g##G(const AttnBlockArgs a) {  \
+        attn_block_body<G>(a);                                                                       \
+    }
+LP_ATTN_BLOCK(1)
+LP_ATTN_BLOCK(2)
+LP_ATTN_BLOCK(4)
+LP_ATTN_BLOCK(8)
+LP_ATTN_BLOCK(16)
+#undef LP_ATTN_BLOCK

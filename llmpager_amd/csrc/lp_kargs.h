@@ -30,7 +30,8 @@ constexpr int kSyncStride = 32;        // words between arrival counters (one 12
 constexpr int kAttnFusedMaxKvHeads = 16;
 constexpr int kStepSyncAttn = 17 * kSyncStride;
 constexpr int kStepSyncGemv = kStepSyncAttn + kAttnFusedMaxKvHeads * kSyncStride;
-constexpr int kSyncWords = kStepSyncGemv + kSyncStride;
+constexpr int kStepSyncDone = kStepSyncGemv + kSyncStride;  // lp_attn_block: KV heads complete
+constexpr int kSyncWords = kStepSyncDone + kSyncStride;
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
@@ -145,15 +146,26 @@ struct GemvAddRmsNormArgs {
 };
 // Per-head q / k RMSNorm, NeoX RoPE, the fp16 KV append at pos and GQA
 // decode attention over pos + 1 positions, head_dim 128; `cps` chunks of 64
-// positions per split; partial records {max, sum, acc[128]} at scratch +
-// head * scratch_stride + split * 130 floats when splits > 1.
+// positions per split; partial records {acc[128], max, sum, 2 unused} at
+// scratch + head * scratch_stride + split * kAttnFusedRec floats when
+// splits > 1.
 constexpr int kAttnFusedMaxSplits = 32;
+constexpr int kAttnFusedRec = 128 + 4;
 struct AttnFusedArgs {
     uint64_t q, k, v, q_norm, k_norm;
     uint64_t kcache, vcache, out, scratch, sync;
     int32_t kv_heads, pos, max_seq, splits, cps, scratch_stride;
     float eps, rope_base, scale;
     int32_t pad0;
+};
+
+// lp_attn_fused on workgroups [0, n_attn) (at.out the attention output),
+// then h[rows] += W_o . out (W_o bf16 [rows, cols]) and hn = rmsnorm(h, ln)
+// on the workgroups after them
+struct AttnBlockArgs {
+    AttnFusedArgs at;
+    uint64_t wo, h, ln, hn;
+    int32_t rows, cols, n_attn, pad0;
 };
 
 struct AddArgs {                    // kernels.rs:239-250

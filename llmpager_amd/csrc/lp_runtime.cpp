@@ -114,6 +114,11 @@ enum Fn {
     kAttnFusedG4,
     kAttnFusedG8,
     kAttnFusedG16,
+    kAttnBlockG1,
+    kAttnBlockG2,
+    kAttnBlockG4,
+    kAttnBlockG8,
+    kAttnBlockG16,
     kNumFns
 };
 
@@ -158,6 +163,9 @@ const FnSpec kSpecs[kNumFns] = {
     {"lp_step.hsaco", "lp_attn_fused_g1"}, {"lp_step.hsaco", "lp_attn_fused_g2"},
     {"lp_step.hsaco", "lp_attn_fused_g4"}, {"lp_step.hsaco", "lp_attn_fused_g8"},
     {"lp_step.hsaco", "lp_attn_fused_g16"},
+    {"lp_step.hsaco", "lp_attn_block_g1"}, {"lp_step.hsaco", "lp_attn_block_g2"},
+    {"lp_step.hsaco", "lp_attn_block_g4"}, {"lp_step.hsaco", "lp_attn_block_g8"},
+    {"lp_step.hsaco", "lp_attn_block_g16"},
 };
 
 const char* const kModules[] = {"lp_basic.hsaco", "lp_moe.hsaco", "lp_gemm.hsaco", "lp_attn.hsaco",
@@ -894,10 +902,13 @@ int lp_gemv_add_rmsnorm(lp_ctx* c, uint64_t w, uint64_t x, int rows, int cols, u
     return launch(c, f, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
 }
 
-int lp_attn_fused(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
-                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch, int heads,
-                  int kv_heads, int head_dim, int pos, int max_seq, float scale, lp_stream s) {
-    if (int r = check_ctx(c)) return r;
+// Checks and plans lp_attn_fused: splits of whole 64-position chunks, at
+// most kAttnFusedMaxSplits and as many as the scratch holds records for; the
+// stream's counter slot when there is more than one split (or `counters`).
+static int attn_fused_plan(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm,
+                           float eps, float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out,
+                           uint64_t scratch, int heads, int kv_heads, int head_dim, int pos, int max_seq, float scale,
+                           bool counters, lp_stream s, AttnFusedArgs& a, int& gi) {
     if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
         return fail(LP_E_INVALID, "attn_fused: heads must be a multiple of kv_heads");
     const int group = heads / kv_heads;
@@ -911,27 +922,66 @@ int lp_attn_fused(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm
     if (!q || !k || !v || !kcache || !vcache || !out || kcache % 16 || vcache % 16 || q % 4 || k % 4 || v % 4)
         return fail(LP_E_INVALID, "attn_fused: null pointer, or caches not 16-byte aligned");
     const int chunks = (pos + 64) / 64;
-    const int by_scratch = max_seq / (head_dim + 2);
+    // records are read 16 bytes at a time: each head's row of the scratch
+    // starts at a multiple of 4 floats
+    const int stride = max_seq & ~3;
+    const int by_scratch = stride / kAttnFusedRec;
     int splits = std::min(chunks, std::min(kAttnFusedMaxSplits, by_scratch));
     if (splits < 1) splits = 1;
     const int cps = (chunks + splits - 1) / splits;
     splits = (chunks + cps - 1) / cps;
-    if (splits > 1 && !scratch) return fail(LP_E_INVALID, "attn_fused: null scratch");
-    AttnFusedArgs a{};
+    if (splits > 1 && (!scratch || scratch % 16))
+        return fail(LP_E_INVALID, "attn_fused: the scratch must be 16-byte aligned");
+    a = AttnFusedArgs{};
     a.q = q, a.k = k, a.v = v, a.q_norm = q_norm, a.k_norm = k_norm;
     a.kcache = kcache, a.vcache = vcache, a.out = out, a.scratch = scratch;
     a.kv_heads = kv_heads, a.pos = pos, a.max_seq = max_seq, a.splits = splits, a.cps = cps;
-    a.scratch_stride = max_seq;
+    a.scratch_stride = stride;
     a.eps = eps, a.rope_base = rope_base, a.scale = scale;
-    if (splits > 1) {
+    if (splits > 1 || counters) {
         const int slot = sync_slot(c, s);
         if (slot < 0)
             return fail(LP_E_UNSUPPORTED, "attn_fused: more than " + std::to_string(kSyncSlots) +
                                               " streams use this context's arrival counters");
         a.sync = sync_words(c, slot);
     }
-    const int gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : group == 8 ? 3 : 4;
-    return launch(c, (Fn)(kAttnFusedG1 + gi), dim3((unsigned)splits, (unsigned)kv_heads), dim3(256), 0, s, a);
+    gi = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : group == 8 ? 3 : 4;
+    return LP_OK;
+}
+
+int lp_attn_fused(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
+                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t out, uint64_t scratch, int heads,
+                  int kv_heads, int head_dim, int pos, int max_seq, float scale, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    AttnFusedArgs a;
+    int gi = 0;
+    if (int r = attn_fused_plan(c, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, out, scratch, heads,
+                                kv_heads, head_dim, pos, max_seq, scale, false, s, a, gi))
+        return r;
+    return launch(c, (Fn)(kAttnFusedG1 + gi), dim3((unsigned)a.splits, (unsigned)kv_heads), dim3(256), 0, s, a);
+}
+
+int lp_attn_block(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm, uint64_t k_norm, float eps,
+                  float rope_base, uint64_t kcache, uint64_t vcache, uint64_t att, uint64_t scratch, int heads,
+                  int kv_heads, int head_dim, int pos, int max_seq, float scale, uint64_t wo, uint64_t h,
+                  uint64_t post_ln, uint64_t hn, int hidden, lp_stream s) {
+    if (int r = check_ctx(c)) return r;
+    const int cols = heads * head_dim;
+    if (hidden <= 0 || hidden > kFusedGemvMaxRows || cols > kFusedGemvMaxCols)
+        return fail(LP_E_UNSUPPORTED, "attn_block: hidden and heads x head_dim at most " +
+                                          std::to_string(kFusedGemvMaxRows));
+    if (!wo || !h || !post_ln || !hn || wo % 16)
+        return fail(LP_E_INVALID, "attn_block: null pointer, or W_o not 16-byte aligned");
+    AttnBlockArgs b{};
+    int gi = 0;
+    if (int r = attn_fused_plan(c, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, att, scratch, heads,
+                                kv_heads, head_dim, pos, max_seq, scale, true, s, b.at, gi))
+        return r;
+    b.wo = wo, b.h = h, b.ln = post_ln, b.hn = hn;
+    b.rows = hidden, b.cols = cols;
+    b.n_attn = b.at.splits * kv_heads;
+    const unsigned n_o = (unsigned)((hidden + 7) / 8);
+    return launch(c, (Fn)(kAttnBlockG1 + gi), dim3((unsigned)b.n_attn + n_o), dim3(256), 0, s, b);
 }
 
 // ---- fused MoE layer --------------------------------------------------------------

@@ -23,11 +23,12 @@ Two launch sequences compute the step: the reference's own, one launch per
 kernels.rs call (fused=False), and the fused one (fused=True, the default
 where the shape allows it: head_dim 128, an fp16 cache, 1, 2, 4, 8 or 16
 query heads per KV head, at most 16 KV heads, hidden and heads x head_dim
-at most 4096), three launches per attention block:
+at most 4096), two launches per attention block:
 
     rmsnorm_gemv       q, k, v = W_{q,k,v} rmsnorm(h, input_ln)
-    attn_fused         q / k norms, rope, kv_append, attention -> a
-    gemv_add_rmsnorm   h += W_o a; hn = rmsnorm(h, post_ln)
+    attn_block         q / k norms, rope, kv_append, attention -> a; then
+                       h += W_o a and hn = rmsnorm(h, post_ln) (attn_fused and
+                       gemv_add_rmsnorm in one launch)
 
 and rmsnorm_gemv again for the final norm and the lm_head."""
 from __future__ import annotations
@@ -118,10 +119,9 @@ class DecodeStep:
             for l, (w, layer) in enumerate(zip(self.attn, self.moe)):
                 K.rmsnorm_gemv(self.h, w.input_ln, S.eps, hid, [(w.q, qd, self.q), (w.k, kd, self.k),
                                                                 (w.v, kd, self.v)], s)
-                K.attn_fused(self.q, self.k, self.v, w.q_norm, w.k_norm, S.eps, S.rope_theta, self.kcache[l],
+                K.attn_block(self.q, self.k, self.v, w.q_norm, w.k_norm, S.eps, S.rope_theta, self.kcache[l],
                              self.vcache[l], self.att, self.scratch, S.heads, S.kv_heads, S.head_dim, pos,
-                             S.max_seq, scale, s)
-                K.gemv_add_rmsnorm(w.o, self.att, hid, qd, self.h, w.post_ln, S.eps, self.hn, s)
+                             S.max_seq, scale, w.o, self.h, w.post_ln, self.hn, hid, s)
                 layer.forward(self.hn, self.h, 1, self.ws, s, ws_bytes=self.ws_bytes)
             K.rmsnorm_gemv(self.h, self.final_norm, S.eps, hid, [(self.lm_head, S.vocab, self.logits)], s)
             return

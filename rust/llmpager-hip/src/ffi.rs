@@ -227,6 +227,12 @@ extern "C" {
         kcache: u64, vcache: u64, out: u64, scratch: u64, heads: c_int, kv_heads: c_int, head_dim: c_int,
         pos: c_int, max_seq: c_int, scale: f32, s: lp_stream,
     ) -> c_int;
+    pub fn lp_attn_block(
+        ctx: *mut lp_ctx, q: u64, k: u64, v: u64, q_norm: u64, k_norm: u64, eps: f32, rope_base: f32,
+        kcache: u64, vcache: u64, att: u64, scratch: u64, heads: c_int, kv_heads: c_int, head_dim: c_int,
+        pos: c_int, max_seq: c_int, scale: f32, wo: u64, h: u64, post_ln: u64, hn: u64, hidden: c_int,
+        s: lp_stream,
+    ) -> c_int;
     pub fn lp_mla_rope(
         ctx: *mut lp_ctx, x: u64, n_vecs: c_int, stride: c_int, offset: c_int, half: c_int, pos: c_int,
         inv_freq: u64, mscale: f32, s: lp_stream,

@@ -180,6 +180,24 @@ impl Kernels {
         check(rc, "attn_fused")
     }
 
+    /// `attn_fused` into `att`, then `h += W_o . att` and `hn = rmsnorm(h, post_ln)`
+    /// in one launch (`decode.rs:283-301`).
+    #[allow(clippy::too_many_arguments)]
+    pub fn attn_block(
+        &self, cuda: &Cuda, q: CUdeviceptr, k: CUdeviceptr, v: CUdeviceptr, q_norm: CUdeviceptr,
+        k_norm: CUdeviceptr, eps: f32, rope_base: f32, kcache: CUdeviceptr, vcache: CUdeviceptr, att: CUdeviceptr,
+        scratch: CUdeviceptr, heads: i32, kv_heads: i32, head_dim: i32, pos: i32, max_seq: i32, scale: f32,
+        wo: CUdeviceptr, h: CUdeviceptr, post_ln: CUdeviceptr, hn: CUdeviceptr, hidden: i32, stream: CUstream,
+    ) -> Result<()> {
+        let rc = unsafe {
+            ffi::lp_attn_block(
+                cuda.ctx, q, k, v, q_norm, k_norm, eps, rope_base, kcache, vcache, att, scratch, heads, kv_heads,
+                head_dim, pos, max_seq, scale, wo, h, post_ln, hn, hidden, stream,
+            )
+        };
+        check(rc, "attn_block")
+    }
+
     #[allow(clippy::too_many_arguments)]
     pub fn mla_rope(
         &self, cuda: &Cuda, x: CUdeviceptr, n_vecs: i32, stride: i32, offset: i32, half: i32, pos: i32,

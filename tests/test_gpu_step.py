@@ -5,8 +5,8 @@ lm_head) against the oracle's composition of the same functions in the
 order of decode.rs:263-363, over several positions; the step recorded once
 with lp_graph_capture_begin / lp_graph_capture_end, whose replay equals the
 eager step bit for bit; and each fused launch (lp_rmsnorm_gemv,
-lp_gemv_add_rmsnorm, lp_attn_fused) against the oracle functions it
-combines, at the test shapes and at Qwen3-30B-A3B's.
+lp_gemv_add_rmsnorm, lp_attn_fused, lp_attn_block) against the oracle
+functions it combines, at the test shapes and at Qwen3-30B-A3B's.
 
 Tolerances: the logits within rel-L2 1e-3 of the oracle's (the MoE layers'
 own bound); the fused launches with the reference's check (worst |got -
@@ -241,6 +241,52 @@ def test_attn_fused(cuda, K, heads, kvh, pos, ms, norms):
         cuda.free_device(p)
 
 
+@pytest.mark.parametrize("heads,kvh,pos,ms,hidden", [
+    (32, 4, 1023, 4096, 2048),  # Qwen3-30B-A3B: 16 splits merged, then the o projection
+    (4, 2, 5, 16, 256),          # one split per KV head: each signals on its own
+    (32, 2, 200, 1024, 1000),    # 16 query heads per KV head; hidden not a multiple of 8 rows
+])
+def test_attn_block(cuda, K, heads, kvh, pos, ms, hidden):
+    # attention then h += W_o att, hn = rmsnorm(h, post_ln) in one launch,
+    # twice in a row on one stream (its counters reset themselves)
+    hd = 128
+    rng = np.random.default_rng(heads + pos)
+    qn = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    ln = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    wo = lp.synth_bf16(hidden * heads * hd, 0.05, 7, 1)
+    kc, vc = _f16(_rnd(rng, kvh * ms * hd)), _f16(_rnd(rng, kvh * ms * hd))
+    dqn, dkn, dln, dwo = cuda.upload(qn), cuda.upload(kn), cuda.upload(ln), cuda.upload(wo)
+    dkc, dvc = cuda.upload(kc), cuda.upload(vc)
+    datt, dscr, dhn = cuda.alloc_device(4 * heads * hd), cuda.alloc_device(4 * heads * ms), cuda.alloc_device(4 * hidden)
+    scale = 1.0 / np.sqrt(hd)
+    s = cuda.stream()
+    for it, p in enumerate((pos, pos + 1)):
+        q, k, v, h = _rnd(rng, heads * hd), _rnd(rng, kvh * hd), _rnd(rng, kvh * hd), _rnd(rng, hidden)
+        dq, dk, dv, dh = cuda.upload(q), cuda.upload(k), cuda.upload(v), cuda.upload(h)
+        K.attn_block(dq, dk, dv, dqn, dkn, 1e-6, 1e6, dkc, dvc, datt, dscr, heads, kvh, hd, p, ms, scale, dwo, dh,
+                     dln, dhn, hidden, s)
+        cuda.sync_stream(s)
+        qq = O.rope(O.rmsnorm(q, qn, heads, hd, 1e-6), heads, hd, p, 1e6)
+        kk = O.rope(O.rmsnorm(k, kn, kvh, hd, 1e-6), kvh, hd, p, 1e6)
+        kc, vc = O.kv_append(kk, v, kc, vc, kvh, hd, p, ms, True)
+        att = O.attn_decode(qq, kc, vc, heads, kvh, hd, p + 1, ms, scale, True)
+        got_att = cuda.download(datt, (heads * hd,), np.float32)
+        assert worst_rel(got_att, att) <= 1e-3, it
+        # the rest from the kernel's own attention output and caches, so the
+        # bound is the o projection's and the norm's
+        kc = cuda.download(dkc, (kvh * ms * hd,), np.uint16)
+        vc = cuda.download(dvc, (kvh * ms * hd,), np.uint16)
+        want_h = O.add(h, O.bf16_gemv(wo, got_att, hidden, heads * hd))
+        assert worst_rel(cuda.download(dh, (hidden,), np.float32), want_h) <= 1e-4, it
+        assert worst_rel(cuda.download(dhn, (hidden,), np.float32), O.rmsnorm(want_h, ln, 1, hidden, 1e-6)) <= 1e-4, it
+        for d in (dq, dk, dv, dh):
+            cuda.free_device(d)
+    cuda.destroy_stream(s)
+    for d in (dqn, dkn, dln, dwo, dkc, dvc, datt, dscr, dhn):
+        cuda.free_device(d)
+
+
 def test_fused_launches_refuse_what_they_do_not_take(cuda, K):
     d = cuda.alloc_device(1 << 16)
     with pytest.raises(lp.LpError):   # head_dim 64
@@ -253,4 +299,6 @@ def test_fused_launches_refuse_what_they_do_not_take(cuda, K):
         K.rmsnorm_gemv(d, 0, 1e-6, 4104, [(d, 1, d)])
     with pytest.raises(lp.LpError):   # columns not a multiple of 8
         K.gemv_add_rmsnorm(d, d, 8, 100, d, d, 1e-6, d)
+    with pytest.raises(lp.LpError):   # heads x head_dim past 4096
+        K.attn_block(d, d, d, 0, 0, 1e-6, 1e6, d, d, d, d, 64, 4, 128, 0, 16, 0.125, d, d, d, d, 2048)
     cuda.free_device(d)
