@@ -798,7 +798,7 @@ def _rounded(d):
     return round(d, 4) if isinstance(d, float) else d
 
 
-def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) -> dict:
+def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023, graph: bool = True) -> dict:
     """Config 2's model as one whole decode step of one token (the reference's
     Decoder::step, decode.rs:263-363, llmpager_amd.step): per layer the
     attention block (bf16 q/k/v/o for 32 query and 4 KV heads of 128, q/k
@@ -813,7 +813,8 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) 
     does; the replays alone are timed too.  Per-kernel times come from one
     eager step with events.  Both launch sequences are measured: the fused
     one (three launches per attention block) and the reference's own (one
-    launch per kernels.rs call)."""
+    launch per kernels.rs call).  graph=False times eager steps instead of
+    replays (for profilers that do not follow graph launches)."""
     import llmpager_amd as lp
     from llmpager_amd.step import AttnWeights, DecodeStep, StepShape
     S = StepShape(hidden=H, heads=S_HEADS, kv_heads=S_KV_HEADS, head_dim=S_HEAD_DIM, vocab=S_VOCAB,
@@ -866,31 +867,33 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023) 
                 kern[n] = {"launches": int(cnt), "us": ms * 1000.0}
         cuda.profile(False)
         moe_us = sum(v["us"] for k, v in kern.items() if k.startswith("lp_moe"))
-        g = step.capture(7, pos, s)
+        g = step.capture(7, pos, s) if graph else None
+        one = (lambda: g.launch(s)) if graph else (lambda: step.run(7, pos, s))
         e0, e1 = cuda.event(), cuda.event()
         for _ in range(warmup):
-            g.launch(s)
+            one()
         cuda.sync_stream(s)
         cuda.record_event(e0, s)
         for _ in range(steps):
-            g.launch(s)
+            one()
         cuda.record_event(e1, s)
         cuda.sync_stream(s)
         graph_ms = cuda.elapsed_ms(e0, e1) / steps
         best = None
         t0 = time.perf_counter()
         for _ in range(steps):
-            g.launch(s)
+            one()
             cuda.dtoh_ptr_async(pinned, step.logits, 4 * S.vocab, s)
             cuda.sync_stream(s)
             best = int(np.argmax(logits))
         wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
-        g.close()
+        if g is not None:
+            g.close()
         for e in (e0, e1):
             cuda.destroy_event(e)
         step.free()
         return {
-            "fused": fused, "tok_s": 1000.0 / wall_ms, "ms_per_step": wall_ms,
+            "fused": fused, "graph": graph, "tok_s": 1000.0 / wall_ms, "ms_per_step": wall_ms,
             "graph_ms_per_step": graph_ms, "graph_tok_s": 1000.0 / graph_ms,
             "launches_per_step": sum(v["launches"] for v in kern.values()),
             "hbm_gbps_graph": (weight_bytes + kv_bytes + moe_bytes) / (graph_ms * 1e-3) / 1e9,
@@ -938,6 +941,7 @@ def main() -> int:
     ap.add_argument("--shared-only", action="store_true")
     ap.add_argument("--no-step", action="store_true", help="skip the whole decode step leg (attention + MoE)")
     ap.add_argument("--step-only", action="store_true")
+    ap.add_argument("--step-eager", action="store_true", help="time the decode step's eager launches, not a graph")
     ap.add_argument("--paged-layers", type=int, default=P_LAYERS)
     ap.add_argument("--paged-tokens", type=int, default=P_TOKENS)
     a = ap.parse_args()
@@ -985,7 +989,7 @@ def main() -> int:
         return 0
     log(f"building the {LAYERS}-layer resident stack ({LAYERS * E} experts)")
     stack = Stack(cuda, s, LAYERS, keep_host=0 if a.no_cpu or a.step_only else 2)
-    dstep = None if a.no_step else run_step(cuda, s, stack, a.steps, a.warmup)
+    dstep = None if a.no_step else run_step(cuda, s, stack, a.steps, a.warmup, graph=not a.step_eager)
     if a.step_only:
         print(json.dumps({"decode_step": _rounded(dstep)}), flush=True)
         cuda.close()
