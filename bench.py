@@ -903,11 +903,15 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023, 
 
     fused = measure(True)
     ref_seq = measure(False)
+    waits_given_up = cuda.step_errors()
+    if waits_given_up:
+        log(f"decode step: {waits_given_up} bounded waits gave up (results invalid)")
     cuda.free_pinned(pinned)
     for p in allocs:
         cuda.free_device(p)
     out = dict(fused)
-    out.update({"position": pos, "layers": LAYERS, "attn_weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
+    out.update({"position": pos, "layers": LAYERS, "waits_given_up": waits_given_up,
+                "attn_weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
                 "moe_bytes": moe_bytes,
                 "reference_launch_sequence": {k: ref_seq[k] for k in ("tok_s", "ms_per_step", "graph_ms_per_step",
                                                                       "launches_per_step", "argmax")}})

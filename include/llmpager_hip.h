@@ -171,6 +171,12 @@ int lp_attn_block(lp_ctx* ctx, uint64_t q, uint64_t k, uint64_t v, uint64_t q_no
                   float rope_base, uint64_t kcache, uint64_t vcache, uint64_t att, uint64_t scratch, int heads,
                   int kv_heads, int head_dim, int pos, int max_seq, float scale, uint64_t wo, uint64_t h,
                   uint64_t post_ln, uint64_t hn, int hidden, lp_stream s);
+/* The o projection's wait in lp_attn_block is bounded (about 30 ms): one
+ * that gives up counts itself and lets the launch end with a wrong result
+ * instead of hanging.  This waits for the device, returns the count since the
+ * last call in *timeouts (0 normally) and clears it, with the fused step's
+ * counters of each stream that had one. */
+int lp_step_errors_sync(lp_ctx* ctx, int32_t* timeouts);
 
 /* ---- MLA absorbed decode: kernels::Kernels (kernels.rs; mla.cu) ----------- */
 

@@ -118,6 +118,7 @@ def _sig(lib):
                                 f32, vp]),
         "lp_attn_block": (i32, [vp, u64, u64, u64, u64, u64, f32, f32, u64, u64, u64, u64, i32, i32, i32, i32, i32,
                                 f32, u64, u64, u64, u64, i32, vp]),
+        "lp_step_errors_sync": (i32, [vp, P(i32)]),
         "lp_mla_rope": (i32, [vp, u64, i32, i32, i32, i32, i32, u64, f32, vp]),
         "lp_mla_attn_decode": (i32, [vp, u64, u64, u64, u64, i32, i32, i32, i32, i32, f32, vp]),
         "lp_bf16_gemv_batch": (i32, [vp, u64, u64, u64, i32, u64, i32, i32, i32, i32, vp]),
@@ -393,6 +394,13 @@ class Cuda:
 
     def sync(self) -> None:
         _check(lib().lp_sync(self.ctx))
+
+    def step_errors(self) -> int:
+        """Waits of the fused decode step that gave up since the last call
+        (lp_step_errors_sync; 0 normally)."""
+        n = C.c_int32()
+        _check(lib().lp_step_errors_sync(self.ctx, C.byref(n)))
+        return n.value
 
     # measurement (lp_profile_*)
     def profile(self, enable: bool) -> None:

@@ -56,11 +56,19 @@ __device__ __forceinline__ void signal(int* cnt, int* flag) {
 // Wait until *cnt reaches target (every thread calls it), polling with
 // agent-scope loads.  The counted parts come from workgroups of lower index
 // in the same launch, dispatched before this one on its XCD; the wait is
-// bounded all the same (kSpinMax polls of about a microsecond each).
-constexpr int kSpinMax = 1 << 15;
-__device__ __forceinline__ void wait_count(int* cnt, int target) {
+// bounded all the same (spin_max polls of about a microsecond each): one
+// that gives up adds one to *err (the host reads it with
+// lp_step_errors_sync) and goes on, so every wave still ends.
+__device__ __forceinline__ void wait_count(int* cnt, int target, int* err, int spin_max) {
     if (threadIdx.x == 0) {
-        for (int it = 0; it < kSpinMax && load_agent(cnt) < target; ++it) __builtin_amdgcn_s_sleep(2);
+        int it = 0;
+        while (load_agent(cnt) < target) {
+            if (++it >= spin_max) {
+                atomicAdd(err, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
     }
     __syncthreads();
 }
@@ -693,7 +701,7 @@ __device__ __forceinline__ void attn_block_body(const AttnBlockArgs& b) {
     float hr[kGemvRowsPerWave];
 #pragma unroll
     for (int r = 0; r < kGemvRowsPerWave; ++r) hr[r] = r0 + r < b.rows ? reinterpret_cast<const float*>(b.h)[r0 + r] : 0.0f;
-    wait_count(sync + kStepSyncDone, a.kv_heads);
+    wait_count(sync + kStepSyncDone, a.kv_heads, sync + kStepSyncErr, b.spin_max);
     // the attention output: written in this launch with agent-scope stores,
     // and nothing on this XCD read it before they completed, so plain loads
     // see it

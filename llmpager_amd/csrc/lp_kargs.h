@@ -31,7 +31,8 @@ constexpr int kAttnFusedMaxKvHeads = 16;
 constexpr int kStepSyncAttn = 17 * kSyncStride;
 constexpr int kStepSyncGemv = kStepSyncAttn + kAttnFusedMaxKvHeads * kSyncStride;
 constexpr int kStepSyncDone = kStepSyncGemv + kSyncStride;  // lp_attn_block: KV heads complete
-constexpr int kSyncWords = kStepSyncDone + kSyncStride;
+constexpr int kStepSyncErr = kStepSyncDone + kSyncStride;   // waits that gave up (lp_step_errors_sync)
+constexpr int kSyncWords = kStepSyncErr + kSyncStride;
 constexpr int kMaxTopK = 16;           // largest top_k the device router accepts
 constexpr int kMaxExperts = 1024;      // largest expert count the device router accepts
 constexpr int kTopkFusedMaxT = 8;      // largest T routed by the one-workgroup top-k + dispatch kernel
@@ -162,10 +163,11 @@ struct AttnFusedArgs {
 // lp_attn_fused on workgroups [0, n_attn) (at.out the attention output),
 // then h[rows] += W_o . out (W_o bf16 [rows, cols]) and hn = rmsnorm(h, ln)
 // on the workgroups after them
+constexpr int kStepSpinMax = 1 << 15;  // polls (about a microsecond each) before the wait gives up
 struct AttnBlockArgs {
     AttnFusedArgs at;
     uint64_t wo, h, ln, hn;
-    int32_t rows, cols, n_attn, pad0;
+    int32_t rows, cols, n_attn, spin_max;
 };
 
 struct AddArgs {                    // kernels.rs:239-250

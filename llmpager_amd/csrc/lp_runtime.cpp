@@ -227,6 +227,7 @@ struct lp_ctx {
     hipStream_t cap_stream = nullptr;         // a capture in progress on this stream ...
     int cap_slot = -1;                        // ... routes through this (the graph's) slot
     bool cap_prof = false;                    // lp_graph_capture_begin: the profiling switch to restore
+    int step_spin = kStepSpinMax;             // polls before lp_attn_block's wait gives up
     // decode gate/up through lp_moe_gateup_bal (LLMPAGER_HIP_GATEUP_BAL=0 at
     // lp_init turns it off, for comparison)
     bool gateup_bal = true;
@@ -346,6 +347,8 @@ int lp_init(int device, const char* hsaco_dir, lp_ctx** out) {
     c->cus = prop.multiProcessorCount;
     c->max_lds = prop.sharedMemPerBlock;
     if (const char* e = std::getenv("LLMPAGER_HIP_GATEUP_BAL")) c->gateup_bal = std::atoi(e) != 0;
+    // tests only: a smaller bound on the fused step's waits, to exercise giving up
+    if (const char* e = std::getenv("LLMPAGER_HIP_STEP_SPIN")) c->step_spin = std::max(1, std::min(kStepSpinMax, std::atoi(e)));
     if (const char* e = std::getenv("LLMPAGER_HIP_BAL_WAVES")) {
         // The balanced kernels run at kBalWaves waves only: a 16-wave build
         // of lp_moe_gateup_bal faulted and was never fixed, so no other
@@ -980,6 +983,7 @@ int lp_attn_block(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm
     b.wo = wo, b.h = h, b.ln = post_ln, b.hn = hn;
     b.rows = hidden, b.cols = cols;
     b.n_attn = b.at.splits * kv_heads;
+    b.spin_max = c->step_spin;
     const unsigned n_o = (unsigned)((hidden + 7) / 8);
     return launch(c, (Fn)(kAttnBlockG1 + gi), dim3((unsigned)b.n_attn + n_o), dim3(256), 0, s, b);
 }
@@ -1746,6 +1750,28 @@ int lp_moe_status_sync(lp_ctx* c, uint64_t ws, uint64_t ws_bytes, const lp_moe_l
     HIPCHK(hipStreamSynchronize((hipStream_t)s));
     if (unique_count) *unique_count = meta[0];
     if (error_flags) *error_flags = meta[1];
+    return LP_OK;
+}
+
+int lp_step_errors_sync(lp_ctx* c, int32_t* timeouts) {
+    if (int r = check_ctx(c)) return r;
+    HIPCHK(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> g(c->sync_mu);
+    int32_t total = 0;
+    for (int i = 0; i < kSyncSlots; ++i) {
+        int32_t* w = c->sync + (size_t)i * kSyncWords + kStepSyncErr;
+        int32_t v = 0;
+        HIPCHK(hipMemcpy(&v, w, 4, hipMemcpyDeviceToHost));
+        if (v) {
+            // a wait that gave up may have let a counter be reset before its
+            // last arrivals: every launch has ended, so zero the slot's
+            // fused-step counters along with the count
+            total += v;
+            int32_t* step = c->sync + (size_t)i * kSyncWords + kStepSyncAttn;
+            HIPCHK(hipMemset(step, 0, (size_t)(kSyncWords - kStepSyncAttn) * 4));
+        }
+    }
+    if (timeouts) *timeouts = total;
     return LP_OK;
 }
 

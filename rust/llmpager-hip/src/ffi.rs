@@ -233,6 +233,7 @@ extern "C" {
         pos: c_int, max_seq: c_int, scale: f32, wo: u64, h: u64, post_ln: u64, hn: u64, hidden: c_int,
         s: lp_stream,
     ) -> c_int;
+    pub fn lp_step_errors_sync(ctx: *mut lp_ctx, timeouts: *mut i32) -> c_int;
     pub fn lp_mla_rope(
         ctx: *mut lp_ctx, x: u64, n_vecs: c_int, stride: c_int, offset: c_int, half: c_int, pos: c_int,
         inv_freq: u64, mscale: f32, s: lp_stream,

@@ -110,6 +110,7 @@ def test_decode_step_against_oracle_and_graph(cuda, hd, fused, max_seq, position
             assert np.array_equal(cuda.download(step.logits, (S.vocab,), np.float32), got[-1])
     finally:
         g.close()
+    assert cuda.step_errors() == 0
     cuda.destroy_stream(s)
     step.free()
     for p in allocs:
@@ -282,9 +283,46 @@ def test_attn_block(cuda, K, heads, kvh, pos, ms, hidden):
         assert worst_rel(cuda.download(dhn, (hidden,), np.float32), O.rmsnorm(want_h, ln, 1, hidden, 1e-6)) <= 1e-4, it
         for d in (dq, dk, dv, dh):
             cuda.free_device(d)
+    assert cuda.step_errors() == 0  # no wait of the o projection gave up
     cuda.destroy_stream(s)
     for d in (dqn, dkn, dln, dwo, dkc, dvc, datt, dscr, dhn):
         cuda.free_device(d)
+
+
+def test_attn_block_wait_that_gives_up_is_reported(cuda):
+    # a context whose bound on the o projection's wait is one poll (set from
+    # the host): the long attention at pos 4095 outlasts it, the wait gives
+    # up, the launch still ends, and lp_step_errors_sync reports it and clears
+    # the counters; a context with the normal bound then computes correctly
+    import os
+    hd, heads, kvh, ms, hidden, pos = 128, 32, 4, 4096, 2048, 4095
+    rng = np.random.default_rng(5)
+    q, k, v, h = _rnd(rng, heads * hd), _rnd(rng, kvh * hd), _rnd(rng, kvh * hd), _rnd(rng, hidden)
+    wo = lp.synth_bf16(hidden * heads * hd, 0.05, 7, 2)
+    kc = _f16(_rnd(rng, kvh * ms * hd))
+    scale = 1.0 / np.sqrt(hd)
+    os.environ["LLMPAGER_HIP_STEP_SPIN"] = "1"
+    try:
+        c1 = lp.Cuda(0)
+    finally:
+        del os.environ["LLMPAGER_HIP_STEP_SPIN"]
+    for c, given_up in ((c1, True), (cuda, False)):
+        K2 = lp.Kernels(c)
+        ones = c.upload(np.ones(hidden, np.float32))
+        bufs = [c.upload(a) for a in (q, k, v, wo, kc, kc.copy(), h.copy())]
+        dq, dk, dv, dwo, dkc, dvc, dh = bufs
+        datt, dscr, dhn = c.alloc_device(4 * heads * hd), c.alloc_device(4 * heads * ms), c.alloc_device(4 * hidden)
+        K2.attn_block(dq, dk, dv, 0, 0, 1e-6, 1e6, dkc, dvc, datt, dscr, heads, kvh, hd, pos, ms, scale, dwo, dh,
+                      ones, dhn, hidden)
+        n = c.step_errors()
+        assert (n > 0) == given_up, n
+        if not given_up:
+            got = c.download(datt, (heads * hd,), np.float32)
+            want_h = O.add(h, O.bf16_gemv(wo, got, hidden, heads * hd))
+            assert worst_rel(c.download(dh, (hidden,), np.float32), want_h) <= 1e-4
+        for p in (*bufs, datt, dscr, dhn, ones):
+            c.free_device(p)
+    c1.close()
 
 
 def test_fused_launches_refuse_what_they_do_not_take(cuda, K):
