@@ -151,3 +151,26 @@ def test_bf16_gemv_batch_closed_form():
     got = O.bf16_gemv_batch(w, rows * cols, x, 0, rows, rows, cols, batch).reshape(batch, rows)
     want = _bf16_val(w).astype(np.float64).reshape(batch, rows, cols) @ x.astype(np.float64)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 8), (33, 2048), (5, 4096), (3, 37)])
+def test_bf16_gemv_closed_form(rows, cols):
+    # y = W x against float64 (each product of a bf16 weight and an fp32
+    # value is exact in float64), within the fp32 chain's rounding bound
+    # n * 2^-24 * sum |w x|; then the special cases that are exact in fp32
+    rng = np.random.default_rng(rows * cols)
+    w = _bf16(_rnd(rng, rows * cols))
+    x = _rnd(rng, cols)
+    got = O.bf16_gemv(w, x, rows, cols).astype(np.float64)
+    wf = _bf16_val(w).astype(np.float64).reshape(rows, cols)
+    want = wf @ x.astype(np.float64)
+    bound = cols * 2.0 ** -24 * (np.abs(wf) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+    # a one-hot row picks one column exactly; a zero row gives 0; a row of
+    # 1.0 over small integers sums exactly
+    w2 = np.zeros((3, cols), np.uint16)
+    w2[0, cols // 2] = 0x3F80  # bf16 1.0
+    w2[2, :] = 0x3F80
+    xi = (np.arange(cols) % 7).astype(np.float32)
+    y2 = O.bf16_gemv(w2.reshape(-1), xi, 3, cols)
+    assert y2[0] == xi[cols // 2] and y2[1] == 0.0 and y2[2] == float(xi.sum())
