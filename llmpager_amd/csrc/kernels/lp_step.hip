@@ -141,8 +141,7 @@ __device__ __forceinline__ float row_dot(const uint4 (&w)[CPL], const float (&x)
     return wave_sum(acc);
 }
 
-constexpr int kGemvRowsPerWave = 2;
-constexpr int kGemvRowsPerBlock = 4 * kGemvRowsPerWave;
+constexpr int kGemvRowsPerWave = kFusedGemvRowsPerWave;
 
 // rows [seg0 | seg1 | seg2] of RmsNormGemvArgs: the matrix, output and local
 // row of global row r (uniform across the wave)
@@ -693,14 +692,14 @@ __device__ __forceinline__ void attn_block_body(const AttnBlockArgs& b) {
     __shared__ int flag;
     constexpr int CPL = kBlockCpl;
     const int wave = threadIdx.x >> 6, lane = lane_id();
-    const int r0 = ((blockIdx.x - b.n_attn) * 4 + wave) * kGemvRowsPerWave;
-    uint4 w[kGemvRowsPerWave][CPL];
+    const int r0 = ((blockIdx.x - b.n_attn) * 4 + wave) * kBlockRowsPerWave;
+    uint4 w[kBlockRowsPerWave][CPL];
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r)
+    for (int r = 0; r < kBlockRowsPerWave; ++r)
         load_row<CPL>(b.wo + (uint64_t)(r0 + r) * b.cols * 2, b.cols, r0 + r < b.rows, w[r]);
-    float hr[kGemvRowsPerWave];
+    float hr[kBlockRowsPerWave];
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r) hr[r] = r0 + r < b.rows ? reinterpret_cast<const float*>(b.h)[r0 + r] : 0.0f;
+    for (int r = 0; r < kBlockRowsPerWave; ++r) hr[r] = r0 + r < b.rows ? reinterpret_cast<const float*>(b.h)[r0 + r] : 0.0f;
     wait_count(sync + kStepSyncDone, a.kv_heads, sync + kStepSyncErr, b.spin_max);
     // the attention output: written in this launch with agent-scope stores,
     // and nothing on this XCD read it before they completed, so plain loads
@@ -709,7 +708,7 @@ __device__ __forceinline__ void attn_block_body(const AttnBlockArgs& b) {
     load_vec<CPL>(a.out, b.cols, x);
     float* h = reinterpret_cast<float*>(b.h);
 #pragma unroll
-    for (int r = 0; r < kGemvRowsPerWave; ++r) {
+    for (int r = 0; r < kBlockRowsPerWave; ++r) {
         const float y = row_dot<CPL>(w[r], x);
         if (lane == 0 && r0 + r < b.rows) store_agent(h + r0 + r, hr[r] + y);
     }

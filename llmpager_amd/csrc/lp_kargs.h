@@ -129,6 +129,8 @@ struct Bf16GemvArgs {               // kernels.rs:202-222
 // cols] matrices sharing the input; cols a multiple of 8, at most
 // kFusedGemvMaxCols.
 constexpr int kFusedGemvMaxCols = 4096;
+constexpr int kFusedGemvRowsPerWave = 2;  // rows per wave (4 waves per workgroup)
+constexpr int kBlockRowsPerWave = 4;      // lp_attn_block's o projection
 struct RmsNormGemvArgs {
     uint64_t x, ln;
     uint64_t w0, w1, w2, y0, y1, y2;

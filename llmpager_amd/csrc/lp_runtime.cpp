@@ -878,7 +878,8 @@ int lp_rmsnorm_gemv(lp_ctx* c, uint64_t x, uint64_t ln, float eps, int cols, uin
     a.cols = cols;
     a.eps = eps;
     const Fn f = (Fn)(kRmsNormGemv1 + gemv_index(gemv_cpl(cols)));
-    return launch(c, f, dim3((unsigned)((total + 7) / 8)), dim3(256), 0, s, a);
+    constexpr int rpb = 4 * kFusedGemvRowsPerWave;
+    return launch(c, f, dim3((unsigned)((total + rpb - 1) / rpb)), dim3(256), 0, s, a);
 }
 
 int lp_gemv_add_rmsnorm(lp_ctx* c, uint64_t w, uint64_t x, int rows, int cols, uint64_t h, uint64_t ln, float eps,
@@ -902,7 +903,8 @@ int lp_gemv_add_rmsnorm(lp_ctx* c, uint64_t w, uint64_t x, int rows, int cols, u
     a.rows = rows, a.cols = cols;
     a.eps = eps;
     const Fn f = (Fn)(kGemvAddRmsNorm1 + gemv_index(gemv_cpl(cols)));
-    return launch(c, f, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, s, a);
+    constexpr int rpb = 4 * kFusedGemvRowsPerWave;
+    return launch(c, f, dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, a);
 }
 
 // Checks and plans lp_attn_fused: splits of whole 64-position chunks, at
@@ -984,7 +986,7 @@ int lp_attn_block(lp_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t q_norm
     b.rows = hidden, b.cols = cols;
     b.n_attn = b.at.splits * kv_heads;
     b.spin_max = c->step_spin;
-    const unsigned n_o = (unsigned)((hidden + 7) / 8);
+    const unsigned n_o = (unsigned)((hidden + 4 * kBlockRowsPerWave - 1) / (4 * kBlockRowsPerWave));
     return launch(c, (Fn)(kAttnBlockG1 + gi), dim3((unsigned)b.n_attn + n_o), dim3(256), 0, s, b);
 }
 
