@@ -2,7 +2,7 @@
 // reference's Decoder::step (crates/llmpager-run/src/decode.rs:275-301)
 // issues rmsnorm, three bf16_gemv, two per-head rmsnorm, two rope, kv_append,
 // attn_decode, bf16_gemv, add and rmsnorm per layer, each a launch of its own
-// (decode.cu:17-339).  Here the same arithmetic is three launches:
+// (decode.cu:17-339).  Here the same arithmetic is these launches:
 //
 //   lp_rmsnorm_gemv      y_i = W_i . rmsnorm(x, ln) for up to three bf16
 //                        matrices sharing the input (q / k / v; the lm_head)
@@ -10,10 +10,14 @@
 //                        appended to the fp16 caches, GQA decode attention
 //   lp_gemv_add_rmsnorm  h += W . a, then hn = rmsnorm(h, ln) (the o
 //                        projection, the residual add and the next norm)
+//   lp_attn_block        the last two in one launch (two per attention block
+//                        with lp_rmsnorm_gemv)
 //
 // Work is handed between workgroups of one launch the way the fused routing
 // kernel does it: agent-scope stores, a relaxed arrival counter in the
-// stream's counter slot that the last arrival resets, agent-scope loads.
+// stream's counter slot that the last arrival resets, then loads that see
+// the stores (agent-scope loads, or plain loads of data that nothing on the
+// reading XCD has read since the launch began).
 #include "lp_device.h"
 
 using namespace lp;
@@ -47,7 +51,7 @@ __device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
 
 // One more completed part at *cnt once this workgroup's stores have
 // completed (every thread calls it).
-__device__ __forceinline__ void signal(int* cnt, int* flag) {
+__device__ __forceinline__ void signal(int* cnt) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) atomicAdd(cnt, 1);
@@ -568,7 +572,7 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a, int sp, 
         }
     }
     if (a.splits == 1) {
-        if (done) signal(done, &flag);
+        if (done) signal(done);
         return;
     }
     int* cnt = reinterpret_cast<int*>(a.sync) + kStepSyncAttn + kSyncStride * g;
@@ -651,7 +655,7 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a, int sp, 
             }
         }
     }
-    if (done) signal(done, &flag);
+    if (done) signal(done);
 }
 
 }  // namespace
