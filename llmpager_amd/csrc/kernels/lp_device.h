@@ -68,6 +68,45 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v;
 }
 
+// Hand-offs between workgroups of one launch: stores that write through to
+// agent scope, loads at agent scope, a count of completed parts and a
+// bounded wait for it.
+template <typename T>
+__device__ __forceinline__ void agent_store(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T agent_load(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One more completed part at *cnt once this workgroup's stores have
+// completed (every thread calls it).
+__device__ __forceinline__ void signal_count(int* cnt) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(cnt, 1);
+}
+
+// Wait until *cnt reaches target (every thread calls it), polling with
+// agent-scope loads.  The counted parts come from workgroups of lower index
+// in the same launch, dispatched before this one on its XCD; the wait is
+// bounded all the same (spin_max polls of about a microsecond each): one
+// that gives up adds one to *err and goes on, so every wave still ends.
+__device__ __forceinline__ void wait_count(int* cnt, int target, int* err, int spin_max) {
+    if (threadIdx.x == 0) {
+        int it = 0;
+        while (agent_load(cnt) < target) {
+            if (++it >= spin_max) {
+                atomicAdd(err, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return wave_reduce_u32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
 }

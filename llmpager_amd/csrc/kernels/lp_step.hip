@@ -25,15 +25,6 @@ using namespace lpk;
 
 namespace {
 
-template <typename T>
-__device__ __forceinline__ void store_agent(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T load_agent(const T* p) {
-    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // One arrival at *cnt per workgroup (every thread calls it); returns the
 // workgroup's arrival order, n - 1 for the last, which resets the counter.
 // Each wave first waits until its own stores have completed.
@@ -47,34 +38,6 @@ __device__ __forceinline__ int arrival_order(int* cnt, int n, int* flag) {
     }
     __syncthreads();
     return *flag;
-}
-
-// One more completed part at *cnt once this workgroup's stores have
-// completed (every thread calls it).
-__device__ __forceinline__ void signal(int* cnt) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(cnt, 1);
-}
-
-// Wait until *cnt reaches target (every thread calls it), polling with
-// agent-scope loads.  The counted parts come from workgroups of lower index
-// in the same launch, dispatched before this one on its XCD; the wait is
-// bounded all the same (spin_max polls of about a microsecond each): one
-// that gives up adds one to *err (the host reads it with
-// lp_step_errors_sync) and goes on, so every wave still ends.
-__device__ __forceinline__ void wait_count(int* cnt, int target, int* err, int spin_max) {
-    if (threadIdx.x == 0) {
-        int it = 0;
-        while (load_agent(cnt) < target) {
-            if (++it >= spin_max) {
-                atomicAdd(err, 1);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-    }
-    __syncthreads();
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -222,7 +185,7 @@ __device__ __forceinline__ void gemv_add_rmsnorm_body(const GemvAddRmsNormArgs& 
     for (int r = 0; r < kGemvRowsPerWave; ++r) {
         const float y = row_dot<CPL>(w[r], x);
         // the residual add (decode.cu:44-53 with s = 1: a[i] + b[i])
-        if (lane == 0 && r0 + r < a.rows) store_agent(h + r0 + r, h[r0 + r] + y);
+        if (lane == 0 && r0 + r < a.rows) agent_store(h + r0 + r, h[r0 + r] + y);
     }
     int* cnt = reinterpret_cast<int*>(a.sync) + kStepSyncGemv;
     if (arrival_order(cnt, gridDim.x, &flag) != (int)gridDim.x - 1) return;
@@ -234,7 +197,7 @@ __device__ __forceinline__ void gemv_add_rmsnorm_body(const GemvAddRmsNormArgs& 
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = threadIdx.x + 256 * k;
-        hv[k] = i < a.rows ? load_agent(h + i) : 0.0f;
+        hv[k] = i < a.rows ? agent_load(h + i) : 0.0f;
         gv[k] = i < a.rows ? ln[i] : 0.0f;
     }
     float ss = 0.0f;
@@ -559,20 +522,20 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a, int sp, 
         const size_t head = (size_t)g * G + hh;
         if (a.splits == 1) {
             if (done)
-                store_agent(out + head * kHd + d, A / L);
+                agent_store(out + head * kHd + d, A / L);
             else
                 out[head * kHd + d] = A / L;
         } else {
             float* rec = scr + head * a.scratch_stride + (size_t)sp * kRec;
-            store_agent(rec + d, A);
+            agent_store(rec + d, A);
             if (d == 0) {
-                store_agent(rec + kHd, M);
-                store_agent(rec + kHd + 1, L);
+                agent_store(rec + kHd, M);
+                agent_store(rec + kHd + 1, L);
             }
         }
     }
     if (a.splits == 1) {
-        if (done) signal(done);
+        if (done) signal_count(done);
         return;
     }
     int* cnt = reinterpret_cast<int*>(a.sync) + kStepSyncAttn + kSyncStride * g;
@@ -646,16 +609,16 @@ __device__ __forceinline__ void attn_fused_body(const AttnFusedArgs& a, int sp, 
         if (hh < G) {
             float* po = out + ((size_t)g * G + hh) * kHd + 4 * d4;
             if (done) {
-                store_agent(po, num[i].x);
-                store_agent(po + 1, num[i].y);
-                store_agent(po + 2, num[i].z);
-                store_agent(po + 3, num[i].w);
+                agent_store(po, num[i].x);
+                agent_store(po + 1, num[i].y);
+                agent_store(po + 2, num[i].z);
+                agent_store(po + 3, num[i].w);
             } else {
                 *reinterpret_cast<float4*>(po) = num[i];
             }
         }
     }
-    if (done) signal(done);
+    if (done) signal_count(done);
 }
 
 }  // namespace
@@ -714,19 +677,19 @@ __device__ __forceinline__ void attn_block_body(const AttnBlockArgs& b) {
 #pragma unroll
     for (int r = 0; r < kBlockRowsPerWave; ++r) {
         const float y = row_dot<CPL>(w[r], x);
-        if (lane == 0 && r0 + r < b.rows) store_agent(h + r0 + r, hr[r] + y);
+        if (lane == 0 && r0 + r < b.rows) agent_store(h + r0 + r, hr[r] + y);
     }
     const int n_o = (int)gridDim.x - b.n_attn;
     if (arrival_order(sync + kStepSyncGemv, n_o, &flag) != n_o - 1) return;
     // every workgroup has passed its wait: the counter starts the next launch at zero
-    if (threadIdx.x == 0) store_agent(sync + kStepSyncDone, 0);
+    if (threadIdx.x == 0) agent_store(sync + kStepSyncDone, 0);
     constexpr int kPer = kFusedGemvMaxRows / 256;
     const float* ln = reinterpret_cast<const float*>(b.ln);
     float hv[kPer], gv[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = threadIdx.x + 256 * k;
-        hv[k] = i < b.rows ? load_agent(h + i) : 0.0f;
+        hv[k] = i < b.rows ? agent_load(h + i) : 0.0f;
         gv[k] = i < b.rows ? ln[i] : 0.0f;
     }
     float ss = 0.0f;
