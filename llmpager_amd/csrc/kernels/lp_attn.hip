@@ -485,23 +485,24 @@ __device__ __forceinline__ void mla_split_body(const MlaBatchArgs& a) {
         }
         __syncthreads();  // the chunk's LDS is free for the next one
     };
-    // the first chunk's rows are in flight while the query images are made
+    // the query's loads first, then the first chunk's rows: the loads retire
+    // in order, so the query images are made while the rows are in flight
     uint4 B0[STEPS];
-    if (nchunks > 0) load_chunk(B0, 0);
     {
         constexpr int kUnits = (STEPS * 64 + 255) / 256;  // query pieces per thread
-        const float* q = dptr<const float>(a.q) + (size_t)b * H * QK;
+        const uint64_t q = a.q + (uint64_t)b * H * QK * 4;
         float4 v4[kUnits][2];
 #pragma unroll
         for (int r = 0; r < kUnits; ++r) {
             const int u = tid + 256 * r, j = u >> 6, l = u & 63, m = l & 15, k8 = l >> 4;
             v4[r][0] = v4[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if (u < STEPS * 64 && m < H) {
-                const float4* src = reinterpret_cast<const float4*>(q + (size_t)m * QK + 32 * j + 8 * k8);
+                const LP_GLOBAL float4* src = gptr<float4>(q + ((uint64_t)m * QK + 32 * j + 8 * k8) * 4);
                 v4[r][0] = src[0];
                 v4[r][1] = src[1];
             }
         }
+        if (nchunks > 0) load_chunk(B0, 0);
 #pragma unroll
         for (int r = 0; r < kUnits; ++r) {
             const int u = tid + 256 * r;
