@@ -26,7 +26,7 @@ from llmpager_amd.step import AttnWeights, DecodeStep, StepShape
 pytestmark = pytest.mark.gpu
 
 
-def _build(cuda, S: StepShape, NL: int, seed: int, fused=None):
+def _build(cuda, S: StepShape, NL: int, seed: int, fused=None, moe_shape=None):
     rng = np.random.default_rng(seed)
     H, qd, kd = S.hidden, S.heads * S.head_dim, S.kv_heads * S.head_dim
     host, attn, moe, allocs = [], [], [], []
@@ -44,7 +44,8 @@ def _build(cuda, S: StepShape, NL: int, seed: int, fused=None):
                  post_ln=(1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
         host.append(w)
         attn.append(AttnWeights(**{k: up(v) for k, v in w.items()}))
-        moe.append(DeviceLayer(cuda, H=H, I=64, E=8, k=2, group=32, seed=seed + l, layer=l, router_std=0.1))
+        ms = moe_shape or dict(I=64, E=8, k=2, group=32, router_std=0.1)
+        moe.append(DeviceLayer(cuda, H=H, seed=seed + l, layer=l, **ms))
     embed = lp.synth_bf16(S.vocab * H, 1.0, seed, 900)
     lm = lp.synth_bf16(S.vocab * H, 0.05, seed, 901)
     fn = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
@@ -110,6 +111,40 @@ def test_decode_step_against_oracle_and_graph(cuda, hd, fused, max_seq, position
             assert np.array_equal(cuda.download(step.logits, (S.vocab,), np.float32), got[-1])
     finally:
         g.close()
+    assert cuda.step_errors() == 0
+    cuda.destroy_stream(s)
+    step.free()
+    for p in allocs:
+        cuda.free_device(p)
+    for L in moe:
+        L.free()
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_step_bench_shape(cuda, fused):
+    # one layer at the shape the bench's decode step runs (Qwen3-30B-A3B:
+    # hidden 2048, 32 query and 4 KV heads of 128, fp16 cache; the config-2
+    # MoE layer, E128 / top-8 / I768 / g32), at positions 0, 1 and 1023 (the
+    # bench's: 16 splits merged by the fused attention), against the oracle's
+    # composition of decode.rs:263-363
+    S = StepShape(hidden=2048, heads=32, kv_heads=4, head_dim=128, vocab=1024, max_seq=2048)
+    step, W, moe, allocs = _build(cuda, S, NL=1, seed=47, fused=fused,
+                                  moe_shape=dict(I=768, E=128, k=8, group=32, router_std=0.02))
+    assert step.fused == fused
+    kd = S.kv_heads * S.head_dim
+    z = np.zeros(kd * S.max_seq, np.uint16)
+    for c in step.kcache + step.vcache:
+        cuda.htod_async(c, z)
+    cuda.sync()
+    caches = [(z.copy(), z.copy())]
+    s = cuda.stream()
+    for pos, tok in zip((0, 1, 1023), (3, 1000, 77)):
+        print(f"step bench shape fused={fused} pos={pos}", flush=True)
+        step.run(tok, pos, s)
+        cuda.sync_stream(s)
+        got = cuda.download(step.logits, (S.vocab,), np.float32)
+        want = _oracle_step(S, W, moe, caches, tok, pos)
+        assert rel_l2(got, want) <= 1e-3, (pos, rel_l2(got, want))
     assert cuda.step_errors() == 0
     cuda.destroy_stream(s)
     step.free()
