@@ -910,7 +910,10 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023, 
     for p in allocs:
         cuda.free_device(p)
     out = dict(fused)
+    # both launch sequences compute the same step: at full size their greedy
+    # tokens must agree (the parity tests pin the logits at smaller sizes)
     out.update({"position": pos, "layers": LAYERS, "waits_given_up": waits_given_up,
+                "argmax_agrees": fused["argmax"] == ref_seq["argmax"],
                 "attn_weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
                 "moe_bytes": moe_bytes,
                 "reference_launch_sequence": {k: ref_seq[k] for k in ("tok_s", "ms_per_step", "graph_ms_per_step",
@@ -921,6 +924,8 @@ def run_step(cuda, s, stack: "Stack", steps: int, warmup: int, pos: int = 1023, 
             f"readback and argmax; graph replay {r['graph_ms_per_step']:.3f} ms, {r['hbm_gbps_graph']:.0f} GB/s), "
             f"MoE {r['moe_us_per_step'] / 1000:.3f} ms + attention, norms and lm_head "
             f"{r['attn_and_head_us_per_step'] / 1000:.3f} ms of kernel time (eager step with events)")
+    log(f"decode step: greedy token {fused['argmax']} (fused) and {ref_seq['argmax']} (one launch per call): "
+        f"{'agree' if out['argmax_agrees'] else 'DIFFER'}")
     return out
 
 
