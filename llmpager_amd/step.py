@@ -59,6 +59,16 @@ def fusable(S: StepShape) -> bool:
             and S.kv_heads <= 16 and S.hidden % 8 == 0 and S.hidden <= 4096 and S.heads * S.head_dim <= 4096)
 
 
+def check_step(S: StepShape, token: int, pos: int) -> None:
+    """A step's token and position must lie inside the embedding table and
+    the KV cache: the row lookup (lp_bf16_row, as kernels.rs's) and the cache
+    append take them unchecked."""
+    if not 0 <= token < S.vocab:
+        raise ValueError(f"token {token} outside the vocabulary of {S.vocab}")
+    if not 0 <= pos < S.max_seq:
+        raise ValueError(f"position {pos} exceeds max_seq {S.max_seq}")
+
+
 @dataclass
 class AttnWeights:
     """One layer's attention block: bf16 [rows, cols] matrices, f32 norm
@@ -111,8 +121,7 @@ class DecodeStep:
         """The launches of one step (token at position pos) on stream."""
         S, K, s = self.shape, self.K, stream
         hid, qd, kd = S.hidden, S.heads * S.head_dim, S.kv_heads * S.head_dim
-        if not 0 <= pos < S.max_seq:
-            raise ValueError(f"position {pos} exceeds max_seq {S.max_seq}")
+        check_step(S, token, pos)
         K.bf16_row(self.embed, token, hid, self.h, s)
         scale = 1.0 / float(np.sqrt(S.head_dim))
         if self.fused:

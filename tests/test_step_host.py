@@ -5,7 +5,7 @@ head_dim at most 4096, hidden a multiple of 8), so a shape outside them
 runs the reference's launch sequence instead of failing on the device."""
 import pytest
 
-from llmpager_amd.step import StepShape, fusable
+from llmpager_amd.step import StepShape, check_step, fusable
 
 
 @pytest.mark.parametrize("kw,ok", [
@@ -23,3 +23,17 @@ def test_fusable(kw, ok):
     assert fusable(StepShape(vocab=100, max_seq=16, **kw)) == ok
     # an fp32 cache always takes the reference's sequence
     assert not fusable(StepShape(vocab=100, max_seq=16, kv_f16=False, **kw))
+
+
+@pytest.mark.parametrize("token,pos,ok", [
+    (0, 0, True), (99, 15, True),
+    (100, 0, False), (-1, 0, False),   # outside the embedding table
+    (0, 16, False), (0, -1, False),    # outside the KV cache
+])
+def test_step_token_and_position_checked(token, pos, ok):
+    S = StepShape(hidden=256, heads=4, kv_heads=2, head_dim=128, vocab=100, max_seq=16)
+    if ok:
+        check_step(S, token, pos)
+    else:
+        with pytest.raises(ValueError):
+            check_step(S, token, pos)
